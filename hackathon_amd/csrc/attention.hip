@@ -1,0 +1,304 @@
+// Attention kernels of libc3hip.so (gfx950).
+//
+// attention_scores: the reference's FusedAttentionScores contract
+//   (c35/engine.py:1250-1380): softmax(Q K^T / divisor + mask) written as a
+//   full [B,H,S,S] fp32 tensor.  One workgroup per score row; the Q row is
+//   staged in LDS and every dot product is computed once (the reference
+//   recomputes each three times).
+//
+// flash_attention: the launch-grouped FusedAttentionScores + P.V MatMul.  A
+//   workgroup owns 64 queries of one (batch, head) (16 per wave); K and V
+//   tiles of 64 keys are staged in LDS.  Each wave computes S^T = K Q^T with
+//   v_mfma_f32_16x16x32_{f16,bf16} so that a lane holds one query's scores;
+//   the online-softmax state is then per lane and P^T feeds the O^T = V^T P^T
+//   MFMA straight from registers (both operands use the same key order, so
+//   the product is unchanged).
+#include "common.h"
+
+using namespace c3h;
+
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+
+// ------------------------------------------------------------ scores (fp32)
+constexpr int kScoreThreads = 256;
+constexpr int kMaxCachedCols = 8192;
+
+__global__ void __launch_bounds__(kScoreThreads) attention_scores_kernel(c3h_attn_scores_args a, int out_heads) {
+  extern __shared__ float smem[];
+  float* qrow = smem;               // [inner]
+  float* srow = smem + a.inner;     // [cols] when cached
+  __shared__ float red[kScoreThreads / 64];
+  const int64_t segment = blockIdx.x;
+  int64_t value = segment;
+  const int row = static_cast<int>(value % a.rows); value /= a.rows;
+  const int head = static_cast<int>(value % out_heads); value /= out_heads;
+  const int batch = static_cast<int>(value);
+  const int qb = a.q0 == 1 ? 0 : batch, qh = a.q1 == 1 ? 0 : head;
+  const int kb = a.k0 == 1 ? 0 : batch, kh = a.k1 == 1 ? 0 : head;
+  const int mb = a.m0 == 1 ? 0 : batch, mh = a.m1 == 1 ? 0 : head, mr = a.m2 == 1 ? 0 : row;
+  const int64_t qbase = ((static_cast<int64_t>(qb) * a.q1 + qh) * a.rows + row) * a.inner;
+  const int64_t kbase = (static_cast<int64_t>(kb) * a.k1 + kh) * static_cast<int64_t>(a.inner) * a.cols;
+  const int64_t mbase = ((static_cast<int64_t>(mb) * a.m1 + mh) * a.m2 + mr) * a.m3;
+  const float* mask = static_cast<const float*>(a.mask);
+  const float divisor = static_cast<const float*>(a.divisor)[0];
+  for (int i = threadIdx.x; i < a.inner; i += kScoreThreads) qrow[i] = load_as_f32(a.q, a.in_dtype, qbase + i);
+  __syncthreads();
+  const bool cached = a.cols <= kMaxCachedCols;
+  auto score = [&](int col) {
+    float s = 0.0f;
+    for (int i = 0; i < a.inner; ++i) s = fmaf(qrow[i], load_as_f32(a.kt, a.in_dtype, kbase + static_cast<int64_t>(i) * a.cols + col), s);
+    return s / divisor + mask[mbase + (a.m3 == 1 ? 0 : col)];
+  };
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float m = -INFINITY;
+  for (int col = threadIdx.x; col < a.cols; col += kScoreThreads) {
+    float s = score(col);
+    if (cached) srow[col] = s;
+    m = fmaxf(m, s);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float sum = 0.0f;
+  for (int col = threadIdx.x; col < a.cols; col += kScoreThreads) sum += expf((cached ? srow[col] : score(col)) - m);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  sum = red[0] + red[1] + red[2] + red[3];
+  float* out = static_cast<float*>(a.out) + segment * a.cols;
+  for (int col = threadIdx.x; col < a.cols; col += kScoreThreads)
+    out[col] = expf((cached ? srow[col] : score(col)) - m) / sum;
+}
+
+// ------------------------------------------------------------ flash attention
+constexpr int kD = 64;        // head dim
+constexpr int kBQ = 64;       // queries per workgroup (16 per wave)
+constexpr int kBK = 64;       // keys per tile
+constexpr int kPad = 8;       // 16-byte skew of LDS rows
+
+template <typename T> struct FlashMma;
+template <> struct FlashMma<bf16_t> {
+  typedef bf16x8 vec;
+  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct FlashMma<f16_t> {
+  typedef f16x8 vec;
+  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename T, int MASK>
+__global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
+  typedef typename FlashMma<T>::vec vec8;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBK][kD + kPad];   // [key][dim]
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[kD][kBK + kPad];   // [dim][key]
+
+  const int qtiles = (a.seq_q + kBQ - 1) / kBQ;
+  const int qt = blockIdx.x % qtiles;
+  const int bh = blockIdx.x / qtiles;
+  const int head = bh % a.heads, batch = bh / a.heads;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l16 = lane & 15, g = lane >> 4;
+
+  const uint16_t* Q = static_cast<const uint16_t*>(a.q) + batch * a.q_sb + head * a.q_sh;
+  const uint16_t* K = static_cast<const uint16_t*>(a.k) + batch * a.k_sb + head * a.k_sh;
+  const uint16_t* V = static_cast<const uint16_t*>(a.v) + batch * a.v_sb + head * a.v_sh;
+  uint16_t* O = static_cast<uint16_t*>(a.out) + batch * a.o_sb + head * a.o_sh;
+
+  // This lane's query (B operand column of S^T = K Q^T) and its Q fragment:
+  // dims 32*ks + 8*g + [0..7].
+  const int q = qt * kBQ + wave * 16 + l16;
+  const bool q_valid = q < a.seq_q;
+  vec8 qf[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    uint4 raw = {0u, 0u, 0u, 0u};
+    if (q_valid) raw = *reinterpret_cast<const uint4*>(Q + q * a.q_ss + 32 * ks + 8 * g);
+    qf[ks] = __builtin_bit_cast(vec8, raw);
+  }
+
+  f32x4 o_acc[4];  // O^T tiles: dims 16*d + 4*g + j, query l16
+#pragma unroll
+  for (int d = 0; d < 4; ++d) o_acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;  // running max of this lane's query
+  float l_part = 0.0f;      // this lane's partial row sum (its keys only)
+
+  const float* mask = static_cast<const float*>(a.mask);
+  int kend = a.seq_k;
+  if (MASK == 1) {
+    int last_q = qt * kBQ + kBQ - 1;
+    if (last_q + 1 < kend) kend = last_q + 1;
+  }
+  const int ntiles = (kend + kBK - 1) / kBK;
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int k0 = t * kBK;
+    // Stage K [key][dim] and V^T [dim][key]: 64x64 each, 16-byte vectors.
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      int e = tid + 256 * i;
+      int key = e >> 3, d0 = (e & 7) * 8;
+      uint4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
+      if (k0 + key < a.seq_k) {
+        kv = *reinterpret_cast<const uint4*>(K + (k0 + key) * a.k_ss + d0);
+        vv = *reinterpret_cast<const uint4*>(V + (k0 + key) * a.v_ss + d0);
+      }
+      *reinterpret_cast<uint4*>(&Ks[key][d0]) = kv;
+      const uint16_t* vs = reinterpret_cast<const uint16_t*>(&vv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) Vt[d0 + j][key] = vs[j];
+    }
+    __syncthreads();
+
+    // S^T tiles: keys 16*kt4 + 4*g + j (j = 0..3), query l16.
+    f32x4 s_acc[4];
+#pragma unroll
+    for (int kt4 = 0; kt4 < 4; ++kt4) {
+      s_acc[kt4] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        vec8 kf = *reinterpret_cast<const vec8*>(&Ks[16 * kt4 + l16][32 * ks + 8 * g]);
+        s_acc[kt4] = FlashMma<T>::mma(kf, qf[ks], s_acc[kt4]);
+      }
+    }
+    // Scale, mask, running max.
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kt4 = 0; kt4 < 4; ++kt4) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = k0 + 16 * kt4 + 4 * g + j;
+        float s = s_acc[kt4][j] * a.scale;
+        if (key >= a.seq_k) s = -INFINITY;
+        if (MASK == 1 && key > q) s = -INFINITY;
+        if (MASK == 2 && q_valid && key < a.seq_k) s += mask[static_cast<int64_t>(q) * a.mask_ld + key];
+        s_acc[kt4][j] = s;
+        tmax = fmaxf(tmax, s);
+      }
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float base = m_new == -INFINITY ? 0.0f : m_new;
+    const float corr = m_run == -INFINITY ? 0.0f : expf(m_run - base);
+    m_run = m_new;
+    l_part *= corr;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o_acc[d] *= corr;
+    // P^T fragments for the two 32-key halves: element i of half ks is key
+    // 32*ks + 16*(i/4) + 4*g + (i%4), i.e. s_acc[2*ks + i/4][i%4].
+    vec8 pf[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      uint16_t bits[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float p = expf(s_acc[2 * ks + i / 4][i % 4] - base);
+        l_part += p;
+        bits[i] = Elem<T>::from_f32(p).bits;
+      }
+      pf[ks] = __builtin_bit_cast(vec8, *reinterpret_cast<const uint4*>(bits));
+    }
+    // O^T += V^T P^T: A operand = V^T rows (dims 16*d + l16), keys in the
+    // same order as P^T: two runs of 4 consecutive keys.
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const uint16_t* row = &Vt[16 * d + l16][32 * ks + 4 * g];
+        uint2 lo = *reinterpret_cast<const uint2*>(row);
+        uint2 hi = *reinterpret_cast<const uint2*>(row + 16);
+        uint4 packed = {lo.x, lo.y, hi.x, hi.y};
+        o_acc[d] = FlashMma<T>::mma(__builtin_bit_cast(vec8, packed), pf[ks], o_acc[d]);
+      }
+    }
+    __syncthreads();
+  }
+
+  float l_tot = l_part + __shfl_xor(l_part, 16, 64);
+  l_tot += __shfl_xor(l_tot, 32, 64);
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  if (q_valid) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      uint16_t bits[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bits[j] = Elem<T>::from_f32(o_acc[d][j] * inv).bits;
+      *reinterpret_cast<uint2*>(O + q * a.o_ss + 16 * d + 4 * g) = *reinterpret_cast<const uint2*>(bits);
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int c3h_attention_scores(const c3h_attn_scores_args* a, void* stream) {
+  C3H_REQUIRE(a != nullptr, "attention_scores: null args");
+  C3H_REQUIRE(a->rows >= 0 && a->cols >= 1 && a->inner >= 1, "attention_scores: bad sizes");
+  C3H_REQUIRE((a->q0 == 1 || a->k0 == 1 || a->q0 == a->k0) && (a->q1 == 1 || a->k1 == 1 || a->q1 == a->k1),
+              "attention_scores: batch/head dims do not broadcast");
+  const int out0 = a->q0 > a->k0 ? a->q0 : a->k0;
+  const int out1 = a->q1 > a->k1 ? a->q1 : a->k1;
+  const int dims[4] = {out0, out1, a->rows, a->cols};
+  const int md[4] = {a->m0, a->m1, a->m2, a->m3};
+  for (int i = 0; i < 4; ++i)
+    C3H_REQUIRE(md[i] == 1 || md[i] == dims[i], "attention_scores: mask dim %d (%d) does not broadcast to %d", i,
+                md[i], dims[i]);
+  int64_t segments = static_cast<int64_t>(out0) * out1 * a->rows;
+  if (segments == 0) return C3H_OK;
+  C3H_REQUIRE(segments <= 2147483647LL, "attention_scores: too many rows");
+  size_t smem = (static_cast<size_t>(a->inner) + (a->cols <= kMaxCachedCols ? a->cols : 0)) * sizeof(float);
+  C3H_REQUIRE(smem <= 64 * 1024, "attention_scores: inner dim too large");
+  hipLaunchKernelGGL(attention_scores_kernel, dim3(static_cast<unsigned>(segments)), dim3(kScoreThreads), smem,
+                     as_stream(stream), *a, out1);
+  return launch_status("attention_scores");
+}
+
+int c3h_flash_attention(const c3h_flash_args* a, void* stream) {
+  C3H_REQUIRE(a != nullptr, "flash: null args");
+  C3H_REQUIRE(a->head_dim == kD, "flash: head_dim %d unsupported (needs 64)", a->head_dim);
+  C3H_REQUIRE(a->batch >= 0 && a->heads >= 1 && a->seq_q >= 0 && a->seq_k >= 1, "flash: bad sizes");
+  C3H_REQUIRE(a->mask_kind >= 0 && a->mask_kind <= 2, "flash: bad mask_kind");
+  C3H_REQUIRE(a->mask_kind != 2 || a->mask != nullptr, "flash: additive mask pointer missing");
+  C3H_REQUIRE(a->q_ss % 8 == 0 && a->k_ss % 8 == 0 && a->v_ss % 8 == 0 && a->q_sh % 8 == 0 && a->k_sh % 8 == 0 &&
+                  a->v_sh % 8 == 0 && a->q_sb % 8 == 0 && a->k_sb % 8 == 0 && a->v_sb % 8 == 0,
+              "flash: Q/K/V strides must be multiples of 8 elements");
+  C3H_REQUIRE(a->o_ss % 4 == 0 && a->o_sh % 4 == 0 && a->o_sb % 4 == 0, "flash: out strides must be multiples of 4");
+  C3H_REQUIRE((reinterpret_cast<uintptr_t>(a->q) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->k) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(a->v) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 7) == 0,
+              "flash: misaligned operands");
+  if (a->batch == 0 || a->seq_q == 0) return C3H_OK;
+  int64_t blocks = static_cast<int64_t>(a->batch) * a->heads * ((a->seq_q + kBQ - 1) / kBQ);
+  C3H_REQUIRE(blocks <= 2147483647LL, "flash: too many workgroups");
+  hipStream_t s = as_stream(stream);
+  dim3 grid(static_cast<unsigned>(blocks));
+#define C3H_FLASH_LAUNCH(T)                                                                            \
+  switch (a->mask_kind) {                                                                              \
+    case 0: hipLaunchKernelGGL((flash_kernel<T, 0>), grid, dim3(256), 0, s, *a); break;                \
+    case 1: hipLaunchKernelGGL((flash_kernel<T, 1>), grid, dim3(256), 0, s, *a); break;                \
+    default: hipLaunchKernelGGL((flash_kernel<T, 2>), grid, dim3(256), 0, s, *a); break;               \
+  }
+  if (a->dtype == C3H_BF16) {
+    C3H_FLASH_LAUNCH(bf16_t)
+  } else if (a->dtype == C3H_F16) {
+    C3H_FLASH_LAUNCH(f16_t)
+  } else {
+    return fail(C3H_EUNSUPPORTED, "flash: dtype %d unsupported", a->dtype);
+  }
+#undef C3H_FLASH_LAUNCH
+  return launch_status("flash_attention");
+}
+
+}  // extern "C"

@@ -1,0 +1,159 @@
+// Internal helpers shared by the libc3hip.so translation units (gfx950 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+#include "../../include/c3hip.h"
+
+namespace c3h {
+
+// Thread-local last-error message (returned by c3h_last_error()).
+void set_error(const char* fmt, ...);
+int fail(int code, const char* fmt, ...);
+
+#define C3H_HIP_CHECK(expr)                                                   \
+  do {                                                                        \
+    hipError_t err__ = (expr);                                                \
+    if (err__ != hipSuccess)                                                  \
+      return ::c3h::fail(C3H_EHIP, "%s failed: %s", #expr,                    \
+                         hipGetErrorString(err__));                           \
+  } while (0)
+
+#define C3H_REQUIRE(cond, ...)                                                \
+  do {                                                                        \
+    if (!(cond)) return ::c3h::fail(C3H_EINVAL, __VA_ARGS__);                 \
+  } while (0)
+
+// Check the launch that was just enqueued.
+inline int launch_status(const char* what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(C3H_EHIP, "%s launch failed: %s", what, hipGetErrorString(err));
+  return C3H_OK;
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int dtype_size(int dt) {
+  switch (dt) {
+    case C3H_F32: case C3H_I32: return 4;
+    case C3H_F16: case C3H_BF16: return 2;
+    case C3H_I8: case C3H_U8: case C3H_BOOL: return 1;
+    case C3H_I64: case C3H_F64: return 8;
+    default: return 0;
+  }
+}
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------
+// Device-side element conversions.  bf16 and f16 narrowing round to nearest
+// even; NaN stays NaN.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  _Float16 v;
+  __builtin_memcpy(&v, &h, 2);
+  return static_cast<float>(v);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 v = static_cast<_Float16>(f);
+  uint16_t h;
+  __builtin_memcpy(&h, &v, 2);
+  return h;
+}
+
+// Load element `i` of a buffer of runtime dtype as fp32.
+__device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
+  switch (dt) {
+    case C3H_F32: return static_cast<const float*>(p)[i];
+    case C3H_F16: return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+    case C3H_BF16: return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+    case C3H_I8: return static_cast<float>(static_cast<const int8_t*>(p)[i]);
+    case C3H_I32: return static_cast<float>(static_cast<const int32_t*>(p)[i]);
+    case C3H_I64: return static_cast<float>(static_cast<const int64_t*>(p)[i]);
+    case C3H_U8: case C3H_BOOL: return static_cast<float>(static_cast<const uint8_t*>(p)[i]);
+    case C3H_F64: return static_cast<float>(static_cast<const double*>(p)[i]);
+    default: return 0.0f;
+  }
+}
+
+__device__ __forceinline__ void store_from_f32(void* p, int dt, int64_t i, float v) {
+  switch (dt) {
+    case C3H_F32: static_cast<float*>(p)[i] = v; break;
+    case C3H_F16: static_cast<uint16_t*>(p)[i] = f32_to_f16_bits(v); break;
+    case C3H_BF16: static_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v); break;
+    case C3H_F64: static_cast<double*>(p)[i] = static_cast<double>(v); break;
+    default: break;
+  }
+}
+
+// Typed element storage used by templated kernels.
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static __device__ __forceinline__ float to_f32(float v) { return v; }
+  static __device__ __forceinline__ float from_f32(float v) { return v; }
+};
+
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+template <> struct Elem<bf16_t> {
+  static __device__ __forceinline__ float to_f32(bf16_t v) { return bf16_bits_to_f32(v.bits); }
+  static __device__ __forceinline__ bf16_t from_f32(float v) { return bf16_t{f32_to_bf16_bits(v)}; }
+};
+template <> struct Elem<f16_t> {
+  static __device__ __forceinline__ float to_f32(f16_t v) { return f16_bits_to_f32(v.bits); }
+  static __device__ __forceinline__ f16_t from_f32(float v) { return f16_t{f32_to_f16_bits(v)}; }
+};
+
+// Abramowitz & Stegun 7.1.26 rational approximation of erf (max abs error
+// about 1.5e-7), the formula the reference's unfused Erf uses.
+__device__ __forceinline__ float erf_as(float x) {
+  float s = x < 0.0f ? -1.0f : (x > 0.0f ? 1.0f : 0.0f);
+  float ax = fabsf(x);
+  float t = 1.0f / (1.0f + 0.3275911f * ax);
+  float t2 = t * t, t3 = t2 * t, t4 = t3 * t, t5 = t4 * t;
+  float poly = 0.254829592f * t + -0.284496736f * t2 + 1.421413741f * t3 +
+               -1.453152027f * t4 + 1.061405429f * t5;
+  return s * (1.0f - poly * expf(-ax * ax));
+}
+
+// One elementwise instruction on fp32 values.
+__device__ __forceinline__ float ew_apply(int op, float a, float b, float imm) {
+  switch (op) {
+    case C3H_EW_ADD: return a + b;
+    case C3H_EW_SUB: return a - b;
+    case C3H_EW_MUL: return a * b;
+    case C3H_EW_DIV: return a / b;
+    case C3H_EW_RELU: return fmaxf(a, 0.0f);
+    case C3H_EW_ERF: return erff(a);
+    case C3H_EW_ERF_AS: return erf_as(a);
+    case C3H_EW_SQRT: return sqrtf(a);
+    case C3H_EW_EXP: return expf(a);
+    case C3H_EW_RECIP: return 1.0f / a;
+    case C3H_EW_MAX: return fmaxf(a, b);
+    case C3H_EW_MIN: return fminf(a, b);
+    case C3H_EW_NEG: return -a;
+    case C3H_EW_ADD_IMM: return a + imm;
+    case C3H_EW_MUL_IMM: return a * imm;
+    case C3H_EW_COPY: return a;
+    default: return a;
+  }
+}
+
+// Register file of an elementwise program: up to 24 fp32 registers addressed
+// by uniform (kernel-argument) indices, so the switch compiles to scalar
+// branches rather than scratch memory.
+struct EwRegs {
+  float r[24];
+};
+
+}  // namespace c3h

@@ -1,0 +1,830 @@
+// Memory-bound kernel families of libc3hip.so (gfx950).  Each kernel reads
+// its inputs once and writes its outputs once; launches are sized for 256 CUs
+// (grid >= 4 x 256 workgroups where the problem allows) with coalesced,
+// 64-lane-wide access along the fastest-varying dimension.
+#include "common.h"
+
+using namespace c3h;
+
+namespace {
+
+constexpr int kBlock = 256;
+
+inline int grid_for(int64_t work, int per_thread = 1) {
+  int64_t blocks = ceil_div(ceil_div(work, per_thread), kBlock);
+  if (blocks < 1) blocks = 1;
+  if (blocks > 65536) blocks = 65536;  // grid-stride beyond this
+  return static_cast<int>(blocks);
+}
+
+// ------------------------------------------------------------------ fill
+__global__ void fill_kernel(void* out, int64_t count, int dt, double value) {
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
+    switch (dt) {
+      case C3H_I64: static_cast<int64_t*>(out)[i] = static_cast<int64_t>(value); break;
+      case C3H_I32: static_cast<int32_t*>(out)[i] = static_cast<int32_t>(value); break;
+      case C3H_I8: static_cast<int8_t*>(out)[i] = static_cast<int8_t>(value); break;
+      case C3H_U8: case C3H_BOOL: static_cast<uint8_t*>(out)[i] = static_cast<uint8_t>(value); break;
+      default: store_from_f32(out, dt, i, static_cast<float>(value)); break;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ cast
+__global__ void cast_kernel(const void* in, void* out, int64_t count, int idt, int odt) {
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
+    if (odt == C3H_I64) {
+      static_cast<int64_t*>(out)[i] = idt == C3H_I64 ? static_cast<const int64_t*>(in)[i]
+                                                     : static_cast<int64_t>(load_as_f32(in, idt, i));
+    } else if (odt == C3H_I32) {
+      static_cast<int32_t*>(out)[i] = idt == C3H_I64 ? static_cast<int32_t>(static_cast<const int64_t*>(in)[i])
+                                                     : static_cast<int32_t>(load_as_f32(in, idt, i));
+    } else {
+      store_from_f32(out, odt, i, load_as_f32(in, idt, i));
+    }
+  }
+}
+
+// ------------------------------------------------------------------ elementwise program
+// Flat mode: every input is either dense with the output's shape (stride
+// flag 1) or a single element (stride flag 0); general mode decomposes the
+// linear index over the output shape.
+template <bool kFlat>
+__global__ void __launch_bounds__(kBlock) ew_kernel(c3h_ew_args a, int64_t numel) {
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < numel; idx += stride) {
+    float r[C3H_EW_MAX_IN + C3H_EW_MAX_INST];
+    if (kFlat) {
+#pragma unroll
+      for (int j = 0; j < C3H_EW_MAX_IN; ++j)
+        if (j < a.n_in) r[j] = load_as_f32(a.in[j], a.in_dtype[j], a.stride[j][0] ? idx : 0);
+    } else {
+      int64_t off[C3H_EW_MAX_IN];
+#pragma unroll
+      for (int j = 0; j < C3H_EW_MAX_IN; ++j) off[j] = 0;
+      int64_t rem = idx;
+      for (int d = a.rank - 1; d >= 0; --d) {
+        int64_t extent = a.shape[d];
+        int64_t c = rem % extent;
+        rem /= extent;
+#pragma unroll
+        for (int j = 0; j < C3H_EW_MAX_IN; ++j) off[j] += c * a.stride[j][d];
+      }
+#pragma unroll
+      for (int j = 0; j < C3H_EW_MAX_IN; ++j)
+        if (j < a.n_in) r[j] = load_as_f32(a.in[j], a.in_dtype[j], off[j]);
+    }
+    float v = r[0];
+    for (int i = 0; i < a.n_inst; ++i) {
+      const c3h_ew_inst ins = a.inst[i];
+      v = ew_apply(ins.op, r[ins.a], r[ins.b], ins.imm);
+      r[a.n_in + i] = v;
+    }
+    store_from_f32(a.out, a.out_dtype, idx, v);
+  }
+}
+
+// Vectorized fast path: fp32 inputs (dense or scalar), fp32 output, 4
+// elements per thread per step.
+__global__ void __launch_bounds__(kBlock) ew_flat_f32x4_kernel(c3h_ew_args a, int64_t nvec) {
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t vi = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; vi < nvec; vi += stride) {
+    constexpr int R = C3H_EW_MAX_IN + C3H_EW_MAX_INST;
+    float rx[R], ry[R], rz[R], rw[R];
+#pragma unroll
+    for (int j = 0; j < C3H_EW_MAX_IN; ++j) {
+      if (j < a.n_in) {
+        const float* p = static_cast<const float*>(a.in[j]);
+        float4 t;
+        if (a.stride[j][0]) t = reinterpret_cast<const float4*>(p)[vi];
+        else { float s = p[0]; t = make_float4(s, s, s, s); }
+        rx[j] = t.x; ry[j] = t.y; rz[j] = t.z; rw[j] = t.w;
+      }
+    }
+    float4 v = make_float4(rx[0], ry[0], rz[0], rw[0]);
+    for (int i = 0; i < a.n_inst; ++i) {
+      const c3h_ew_inst ins = a.inst[i];
+      v.x = ew_apply(ins.op, rx[ins.a], rx[ins.b], ins.imm);
+      v.y = ew_apply(ins.op, ry[ins.a], ry[ins.b], ins.imm);
+      v.z = ew_apply(ins.op, rz[ins.a], rz[ins.b], ins.imm);
+      v.w = ew_apply(ins.op, rw[ins.a], rw[ins.b], ins.imm);
+      rx[a.n_in + i] = v.x; ry[a.n_in + i] = v.y; rz[a.n_in + i] = v.z; rw[a.n_in + i] = v.w;
+    }
+    reinterpret_cast<float4*>(a.out)[vi] = v;
+  }
+}
+
+// ------------------------------------------------------------------ strided copy
+template <typename T>
+__global__ void __launch_bounds__(kBlock) strided_copy_kernel(const T* __restrict__ in, T* __restrict__ out,
+                                                               c3h_copy_args a, int64_t total) {
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+    int64_t rem = idx, off = a.in_offset;
+    for (int d = a.rank - 1; d >= 0; --d) {
+      int64_t extent = a.shape[d];
+      int64_t c = rem % extent;
+      rem /= extent;
+      off += c * a.in_stride[d];
+    }
+    out[idx] = in[off];
+  }
+}
+
+// Tiled 2-D transpose for the case "innermost output dim is strided on the
+// input while another dim is unit-stride": out[b][r][c] = in[b][c][r].
+template <typename T>
+__global__ void __launch_bounds__(256) transpose_tile_kernel(const T* __restrict__ in, T* __restrict__ out,
+                                                             int64_t batch, int64_t rows, int64_t cols,
+                                                             int64_t in_b, int64_t out_b) {
+  __shared__ T tile[32][33];
+  int64_t b = blockIdx.z;
+  int64_t r0 = static_cast<int64_t>(blockIdx.y) * 32, c0 = static_cast<int64_t>(blockIdx.x) * 32;
+  int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  const T* src = in + b * in_b;
+  T* dst = out + b * out_b;
+  // in is [cols][rows] (row-major): read coalesced along rows.
+  for (int k = ty; k < 32; k += 8) {
+    int64_t c = c0 + k, r = r0 + tx;
+    if (c < cols && r < rows) tile[k][tx] = src[c * rows + r];
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    int64_t r = r0 + k, c = c0 + tx;
+    if (r < rows && c < cols) dst[r * cols + c] = tile[tx][k];
+  }
+}
+
+// ------------------------------------------------------------------ reductions
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// inner == 1: one wave per row.
+__global__ void __launch_bounds__(kBlock) reduce_rows_kernel(c3h_reduce_args a) {
+  int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + wave;
+  if (row >= a.outer) return;
+  const int64_t base = row * a.reduce;
+  float acc = a.kind == 0 ? -INFINITY : 0.0f;
+  for (int64_t i = lane; i < a.reduce; i += 64) {
+    float v = load_as_f32(a.in, a.in_dtype, base + i);
+    acc = a.kind == 0 ? fmaxf(acc, v) : acc + v;
+  }
+  acc = a.kind == 0 ? wave_max(acc) : wave_sum(acc);
+  if (a.kind == 2) acc = acc / static_cast<float>(a.reduce);
+  if (lane == 0) store_from_f32(a.out, a.out_dtype, row, acc);
+}
+
+// inner > 1: one thread per (outer, inner) column, coalesced across inner.
+__global__ void __launch_bounds__(kBlock) reduce_cols_kernel(c3h_reduce_args a) {
+  int64_t total = a.outer * a.inner;
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
+    int64_t o = t / a.inner, in = t - o * a.inner;
+    int64_t base = o * a.reduce * a.inner + in;
+    float acc = a.kind == 0 ? -INFINITY : 0.0f;
+    for (int64_t i = 0; i < a.reduce; ++i) {
+      float v = load_as_f32(a.in, a.in_dtype, base + i * a.inner);
+      acc = a.kind == 0 ? fmaxf(acc, v) : acc + v;
+    }
+    if (a.kind == 2) acc = acc / static_cast<float>(a.reduce);
+    store_from_f32(a.out, a.out_dtype, t, acc);
+  }
+}
+
+// ------------------------------------------------------------------ softmax
+__global__ void __launch_bounds__(kBlock) softmax_rows_kernel(c3h_softmax_args a) {
+  // one block per row (inner == 1)
+  __shared__ float red[kBlock / 64];
+  int64_t row = blockIdx.x;
+  int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t base = row * a.axis;
+  float m = -INFINITY;
+  for (int64_t i = threadIdx.x; i < a.axis; i += kBlock) m = fmaxf(m, load_as_f32(a.in, a.in_dtype, base + i));
+  m = wave_max(m);
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float s = 0.0f;
+  for (int64_t i = threadIdx.x; i < a.axis; i += kBlock) s += expf(load_as_f32(a.in, a.in_dtype, base + i) - m);
+  s = wave_sum(s);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  s = red[0] + red[1] + red[2] + red[3];
+  for (int64_t i = threadIdx.x; i < a.axis; i += kBlock)
+    store_from_f32(a.out, a.out_dtype, base + i, expf(load_as_f32(a.in, a.in_dtype, base + i) - m) / s);
+}
+
+__global__ void __launch_bounds__(kBlock) softmax_cols_kernel(c3h_softmax_args a) {
+  int64_t total = a.outer * a.inner;
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
+    int64_t o = t / a.inner, in = t - o * a.inner;
+    int64_t base = o * a.axis * a.inner + in;
+    float m = -INFINITY;
+    for (int64_t i = 0; i < a.axis; ++i) m = fmaxf(m, load_as_f32(a.in, a.in_dtype, base + i * a.inner));
+    float s = 0.0f;
+    for (int64_t i = 0; i < a.axis; ++i) s += expf(load_as_f32(a.in, a.in_dtype, base + i * a.inner) - m);
+    for (int64_t i = 0; i < a.axis; ++i)
+      store_from_f32(a.out, a.out_dtype, base + i * a.inner,
+                     expf(load_as_f32(a.in, a.in_dtype, base + i * a.inner) - m) / s);
+  }
+}
+
+// ------------------------------------------------------------------ layernorm
+// One wave per row; up to kCache values per lane stay in registers.
+constexpr int kLnCache = 32;
+
+__global__ void __launch_bounds__(kBlock) layernorm_kernel(c3h_layernorm_args a) {
+  int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + wave;
+  if (row >= a.rows) return;
+  const int64_t base = row * a.cols;
+  const float* scale = static_cast<const float*>(a.scale);
+  const float* bias = static_cast<const float*>(a.bias);
+  const bool cached = a.cols <= 64 * kLnCache;
+  float vals[kLnCache];
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kLnCache; ++j) {
+    int64_t c = lane + 64 * j;
+    float v = 0.0f;
+    if (cached && c < a.cols) {
+      v = load_as_f32(a.x, a.x_dtype, base + c);
+      if (a.residual) v += load_as_f32(a.residual, a.x_dtype, base + c);
+    }
+    vals[j] = v;
+    sum += v;
+  }
+  if (!cached) {
+    for (int64_t c = lane; c < a.cols; c += 64) {
+      float v = load_as_f32(a.x, a.x_dtype, base + c);
+      if (a.residual) v += load_as_f32(a.residual, a.x_dtype, base + c);
+      sum += v;
+    }
+  }
+  const float mean = wave_sum(sum) / static_cast<float>(a.cols);
+  float sq = 0.0f;
+  if (cached) {
+#pragma unroll
+    for (int j = 0; j < kLnCache; ++j) {
+      int64_t c = lane + 64 * j;
+      if (c < a.cols) { float d = vals[j] - mean; sq += d * d; }
+    }
+  } else {
+    for (int64_t c = lane; c < a.cols; c += 64) {
+      float v = load_as_f32(a.x, a.x_dtype, base + c);
+      if (a.residual) v += load_as_f32(a.residual, a.x_dtype, base + c);
+      float d = v - mean;
+      sq += d * d;
+    }
+  }
+  const float var = wave_sum(sq) / static_cast<float>(a.cols);
+  const float inv_std = 1.0f / sqrtf(var + a.epsilon);
+  if (cached) {
+#pragma unroll
+    for (int j = 0; j < kLnCache; ++j) {
+      int64_t c = lane + 64 * j;
+      if (c < a.cols) {
+        float y = (vals[j] - mean) * inv_std * scale[c];
+        if (bias) y += bias[c];
+        store_from_f32(a.out, a.out_dtype, base + c, y);
+      }
+    }
+  } else {
+    for (int64_t c = lane; c < a.cols; c += 64) {
+      float v = load_as_f32(a.x, a.x_dtype, base + c);
+      if (a.residual) v += load_as_f32(a.residual, a.x_dtype, base + c);
+      float y = (v - mean) * inv_std * scale[c];
+      if (bias) y += bias[c];
+      store_from_f32(a.out, a.out_dtype, base + c, y);
+    }
+  }
+  if (lane == 0) {
+    if (a.mean_out) static_cast<float*>(a.mean_out)[row] = mean;
+    if (a.invstd_out) static_cast<float*>(a.invstd_out)[row] = inv_std;
+  }
+}
+
+// ------------------------------------------------------------------ batchnorm / fold
+__global__ void batchnorm_kernel(c3h_batchnorm_args a) {
+  int64_t total = a.n * a.c * a.hw;
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const float* x = static_cast<const float*>(a.x);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+    int64_t ch = (i / a.hw) % a.c;
+    float sc = static_cast<const float*>(a.scale)[ch];
+    float bi = static_cast<const float*>(a.bias)[ch];
+    float mu = static_cast<const float*>(a.mean)[ch];
+    float va = static_cast<const float*>(a.var)[ch];
+    static_cast<float*>(a.out)[i] = (x[i] - mu) / sqrtf(va + a.epsilon) * sc + bi;
+  }
+}
+
+__global__ void bn_fold_kernel(c3h_bnfold_args a) {
+  int64_t total = a.out_channels * a.per_channel;
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+    int64_t o = i / a.per_channel;
+    float f = a.scale[o] / sqrtf(a.var[o] + a.epsilon);
+    a.w_out[i] = a.w[i] * f;
+    if (i - o * a.per_channel == 0) {
+      float cb = a.conv_bias ? a.conv_bias[o] : 0.0f;
+      a.b_out[o] = (cb - a.mean[o]) * f + a.bias[o];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ gather
+// One thread per 16-byte chunk (or element when rows are not 16B multiples).
+template <typename V>
+__global__ void __launch_bounds__(kBlock) gather_kernel(c3h_gather_args a, int64_t row_vecs) {
+  int64_t total = a.outer * a.n_indices * row_vecs;
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const V* data = static_cast<const V*>(a.data);
+  V* out = static_cast<V*>(a.out);
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
+    int64_t v = t % row_vecs;
+    int64_t r = t / row_vecs;
+    int64_t i = r % a.n_indices;
+    int64_t o = r / a.n_indices;
+    int64_t idx = a.indices[i];
+    if (idx < 0) idx += a.axis_dim;
+    if (idx < 0 || idx >= a.axis_dim) {
+      if (a.error_flag) *a.error_flag = 1;
+      out[t] = V{};
+      continue;
+    }
+    out[t] = data[(o * a.axis_dim + idx) * row_vecs + v];
+  }
+}
+
+// ------------------------------------------------------------------ argmax
+// One 256-thread block per row; NaN counts as the maximum (NumPy rule) and
+// ties resolve to the lowest index.
+__device__ __forceinline__ bool better(float v, int64_t i, float bv, int64_t bi) {
+  bool vn = v != v, bn = bv != bv;
+  if (vn || bn) {
+    if (vn && bn) return i < bi;
+    return vn;
+  }
+  return v > bv || (v == bv && i < bi);
+}
+
+template <bool kVec>
+__global__ void __launch_bounds__(kBlock) argmax_kernel(c3h_argmax_args a) {
+  __shared__ float sv[kBlock];
+  __shared__ int64_t si[kBlock];
+  int64_t row = blockIdx.x;
+  const int64_t base = row * a.cols;
+  float bv = -INFINITY;
+  int64_t bi = a.cols;  // sentinel above every real index
+  if (kVec) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(a.in) + base);
+    for (int64_t c4 = threadIdx.x; c4 < a.cols / 4; c4 += kBlock) {
+      float4 v = p[c4];
+      int64_t c = c4 * 4;
+      if (better(v.x, c, bv, bi)) { bv = v.x; bi = c; }
+      if (better(v.y, c + 1, bv, bi)) { bv = v.y; bi = c + 1; }
+      if (better(v.z, c + 2, bv, bi)) { bv = v.z; bi = c + 2; }
+      if (better(v.w, c + 3, bv, bi)) { bv = v.w; bi = c + 3; }
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) {
+      float v = load_as_f32(a.in, a.in_dtype, base + c);
+      if (better(v, c, bv, bi)) { bv = v; bi = c; }
+    }
+  }
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = kBlock / 2; s > 0; s >>= 1) {
+    if (threadIdx.x < s) {
+      float ov = sv[threadIdx.x + s];
+      int64_t oi = si[threadIdx.x + s];
+      if (better(ov, oi, sv[threadIdx.x], si[threadIdx.x])) { sv[threadIdx.x] = ov; si[threadIdx.x] = oi; }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) a.out[row] = si[0] < a.cols ? si[0] : 0;
+}
+
+// ------------------------------------------------------------------ im2col
+__global__ void __launch_bounds__(kBlock) im2col_kernel(c3h_im2col_args a) {
+  const int64_t cols = static_cast<int64_t>(a.c) * a.kh * a.kw;
+  const int64_t total = static_cast<int64_t>(a.n) * a.ho * a.wo * cols;
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
+    int64_t col = t % cols, row = t / cols;
+    int kw_i = static_cast<int>(col % a.kw);
+    int kh_i = static_cast<int>((col / a.kw) % a.kh);
+    int ci = static_cast<int>(col / (static_cast<int64_t>(a.kw) * a.kh));
+    int wo_i = static_cast<int>(row % a.wo);
+    int ho_i = static_cast<int>((row / a.wo) % a.ho);
+    int ni = static_cast<int>(row / (static_cast<int64_t>(a.wo) * a.ho));
+    int hi = ho_i * a.sh - a.pad_top + kh_i * a.dh;
+    int wi = wo_i * a.sw - a.pad_left + kw_i * a.dw;
+    float v = 0.0f;
+    if (hi >= 0 && hi < a.h && wi >= 0 && wi < a.w)
+      v = load_as_f32(a.x, a.dtype, ((static_cast<int64_t>(ni) * a.c + ci) * a.h + hi) * a.w + wi);
+    store_from_f32(a.out, a.dtype, t, v);
+  }
+}
+
+// ------------------------------------------------------------------ layout NCHW <-> NHWC
+// Small-channel path: one thread per pixel, channels (padded) in order.
+__global__ void __launch_bounds__(kBlock) nchw_to_nhwc_small_kernel(c3h_layout_args a) {
+  const int64_t hw = static_cast<int64_t>(a.h) * a.w;
+  const int64_t total = static_cast<int64_t>(a.n) * hw;
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < total; p += stride) {
+    int64_t ni = p / hw, s = p - ni * hw;
+    for (int c = 0; c < a.c_pad; ++c) {
+      float v = c < a.c ? load_as_f32(a.in, a.in_dtype, (ni * a.c + c) * hw + s) : 0.0f;
+      store_from_f32(a.out, a.out_dtype, p * a.c_pad + c, v);
+    }
+  }
+}
+
+// Tiled path: per image, [C][HW] <-> [HW][Cpad] through a 32x33 LDS tile.
+__global__ void __launch_bounds__(256) layout_tile_kernel(c3h_layout_args a) {
+  __shared__ float tile[32][33];
+  const int64_t hw = static_cast<int64_t>(a.h) * a.w;
+  int64_t ni = blockIdx.z;
+  int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  if (a.direction == 0) {  // NCHW -> NHWC: tile over (c, s)
+    int64_t s0 = static_cast<int64_t>(blockIdx.x) * 32, c0 = static_cast<int64_t>(blockIdx.y) * 32;
+    for (int k = ty; k < 32; k += 8) {
+      int64_t c = c0 + k, s = s0 + tx;
+      tile[k][tx] = (c < a.c && s < hw) ? load_as_f32(a.in, a.in_dtype, (ni * a.c + c) * hw + s) : 0.0f;
+    }
+    __syncthreads();
+    for (int k = ty; k < 32; k += 8) {
+      int64_t s = s0 + k, c = c0 + tx;
+      if (s < hw && c < a.c_pad) store_from_f32(a.out, a.out_dtype, (ni * hw + s) * a.c_pad + c, tile[tx][k]);
+    }
+  } else {  // NHWC(c_pad) -> NCHW
+    int64_t s0 = static_cast<int64_t>(blockIdx.x) * 32, c0 = static_cast<int64_t>(blockIdx.y) * 32;
+    for (int k = ty; k < 32; k += 8) {
+      int64_t s = s0 + k, c = c0 + tx;
+      tile[k][tx] = (s < hw && c < a.c) ? load_as_f32(a.in, a.in_dtype, (ni * hw + s) * a.c_pad + c) : 0.0f;
+    }
+    __syncthreads();
+    for (int k = ty; k < 32; k += 8) {
+      int64_t c = c0 + k, s = s0 + tx;
+      if (c < a.c && s < hw) store_from_f32(a.out, a.out_dtype, (ni * a.c + c) * hw + s, tile[tx][k]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ weight packing
+__global__ void __launch_bounds__(kBlock) pack_conv_weight_kernel(c3h_pack_args a) {
+  const int64_t total = static_cast<int64_t>(a.o) * a.k_stride;
+  const int64_t k_real = static_cast<int64_t>(a.kh) * a.kw_pack * a.c_pack;
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
+    int64_t o = t / a.k_stride, k = t - o * a.k_stride;
+    float v = 0.0f;
+    if (k < k_real) {
+      int c = static_cast<int>(k % a.c_pack);
+      int tap = static_cast<int>(k / a.c_pack);
+      int kwi = tap % a.kw_pack, khi = tap / a.kw_pack;
+      if (c < a.c && kwi < a.kw)
+        v = load_as_f32(a.w, a.in_dtype, ((o * a.c + c) * a.kh + khi) * a.kw + kwi);
+    }
+    store_from_f32(a.out, a.out_dtype, t, v);
+  }
+}
+
+// ------------------------------------------------------------------ maxpool
+__global__ void __launch_bounds__(kBlock) maxpool_kernel(c3h_pool_args a) {
+  const int64_t total = static_cast<int64_t>(a.n) * a.c * a.ho * a.wo;
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
+    int ci, wo_i, ho_i, ni;
+    if (a.layout == 1) {  // NHWC: channel fastest
+      ci = static_cast<int>(t % a.c);
+      int64_t p = t / a.c;
+      wo_i = static_cast<int>(p % a.wo);
+      ho_i = static_cast<int>((p / a.wo) % a.ho);
+      ni = static_cast<int>(p / (static_cast<int64_t>(a.wo) * a.ho));
+    } else {
+      wo_i = static_cast<int>(t % a.wo);
+      ho_i = static_cast<int>((t / a.wo) % a.ho);
+      ci = static_cast<int>((t / (static_cast<int64_t>(a.wo) * a.ho)) % a.c);
+      ni = static_cast<int>(t / (static_cast<int64_t>(a.wo) * a.ho * a.c));
+    }
+    float m = -INFINITY;
+    for (int i = 0; i < a.kh; ++i) {
+      int hi = ho_i * a.sh - a.pad_top + i * a.dh;
+      if (hi < 0 || hi >= a.h) continue;
+      for (int j = 0; j < a.kw; ++j) {
+        int wi = wo_i * a.sw - a.pad_left + j * a.dw;
+        if (wi < 0 || wi >= a.w) continue;
+        int64_t off = a.layout == 1
+                          ? ((static_cast<int64_t>(ni) * a.h + hi) * a.w + wi) * a.c_stride + ci
+                          : ((static_cast<int64_t>(ni) * a.c + ci) * a.h + hi) * a.w + wi;
+        m = fmaxf(m, load_as_f32(a.x, a.dtype, off));
+      }
+    }
+    int64_t o = a.layout == 1
+                    ? ((static_cast<int64_t>(ni) * a.ho + ho_i) * a.wo + wo_i) * a.c_stride + ci
+                    : t;
+    store_from_f32(a.out, a.dtype, o, m);
+  }
+}
+
+// ------------------------------------------------------------------ quantize / dequantize
+__global__ void quantize_kernel(c3h_quantize_args a) {
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < a.count; i += stride) {
+    float v = rintf(load_as_f32(a.x, a.x_dtype, i) / a.scale) + static_cast<float>(a.zero_point);
+    v = fminf(fmaxf(v, -128.0f), 127.0f);
+    a.out[i] = static_cast<int8_t>(v);
+  }
+}
+
+__global__ void dequantize_kernel(c3h_dequantize_args a) {
+  int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < a.count; i += stride)
+    store_from_f32(a.out, a.out_dtype, i, static_cast<float>(static_cast<int32_t>(a.q[i]) - a.zero_point) * a.scale);
+}
+
+bool ew_is_flat(const c3h_ew_args& a) {
+  // Flat iff every input is either dense in output order or a single element.
+  for (int j = 0; j < a.n_in; ++j) {
+    bool all_zero = true, dense = true;
+    int64_t expect = 1;
+    for (int d = a.rank - 1; d >= 0; --d) {
+      int64_t s = a.stride[j][d];
+      if (s != 0) all_zero = false;
+      if (a.shape[d] != 1 && s != expect) dense = false;
+      expect *= a.shape[d];
+    }
+    if (!(all_zero || dense)) return false;
+  }
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int c3h_fill(const c3h_fill_args* a, void* stream) {
+  C3H_REQUIRE(a && (a->out || a->count == 0), "fill: bad args");
+  if (a->count == 0) return C3H_OK;
+  C3H_REQUIRE(dtype_size(a->dtype) > 0, "fill: bad dtype %d", a->dtype);
+  hipLaunchKernelGGL(fill_kernel, dim3(grid_for(a->count)), dim3(kBlock), 0, as_stream(stream), a->out, a->count,
+                     a->dtype, a->value);
+  return launch_status("fill");
+}
+
+int c3h_cast(const c3h_cast_args* a, void* stream) {
+  C3H_REQUIRE(a && a->count >= 0, "cast: bad args");
+  if (a->count == 0) return C3H_OK;
+  C3H_REQUIRE(dtype_size(a->in_dtype) > 0 && dtype_size(a->out_dtype) > 0, "cast: bad dtype");
+  hipLaunchKernelGGL(cast_kernel, dim3(grid_for(a->count)), dim3(kBlock), 0, as_stream(stream), a->in, a->out,
+                     a->count, a->in_dtype, a->out_dtype);
+  return launch_status("cast");
+}
+
+int c3h_ew(const c3h_ew_args* a, void* stream) {
+  C3H_REQUIRE(a != nullptr, "ew: null args");
+  C3H_REQUIRE(a->n_in >= 1 && a->n_in <= C3H_EW_MAX_IN, "ew: n_in %d out of range", a->n_in);
+  C3H_REQUIRE(a->n_inst >= 1 && a->n_inst <= C3H_EW_MAX_INST, "ew: n_inst %d out of range", a->n_inst);
+  C3H_REQUIRE(a->rank >= 0 && a->rank <= C3H_MAX_RANK, "ew: rank %d out of range", a->rank);
+  for (int i = 0; i < a->n_inst; ++i) {
+    const c3h_ew_inst& ins = a->inst[i];
+    int limit = a->n_in + i;
+    C3H_REQUIRE(ins.a >= 0 && ins.a < limit && ins.b >= 0 && ins.b < limit,
+                "ew: instruction %d reads register outside [0,%d)", i, limit);
+    C3H_REQUIRE(ins.op >= 0 && ins.op <= C3H_EW_COPY, "ew: bad opcode %d", ins.op);
+  }
+  int64_t numel = 1;
+  for (int d = 0; d < a->rank; ++d) {
+    C3H_REQUIRE(a->shape[d] >= 0, "ew: negative extent");
+    numel *= a->shape[d];
+  }
+  if (numel == 0) return C3H_OK;
+  bool flat = ew_is_flat(*a);
+  bool all_f32 = a->out_dtype == C3H_F32;
+  for (int j = 0; j < a->n_in; ++j) {
+    all_f32 = all_f32 && a->in_dtype[j] == C3H_F32;
+    if (a->stride[j][a->rank ? a->rank - 1 : 0] && (reinterpret_cast<uintptr_t>(a->in[j]) & 15)) all_f32 = false;
+  }
+  if (reinterpret_cast<uintptr_t>(a->out) & 15) all_f32 = false;
+  c3h_ew_args k = *a;
+  if (flat) {
+    // Normalize flat strides to a 0/1 flag in slot 0.
+    for (int j = 0; j < k.n_in; ++j) {
+      bool any = false;
+      for (int d = 0; d < k.rank; ++d) any = any || k.stride[j][d] != 0;
+      k.stride[j][0] = any ? 1 : 0;
+    }
+    if (all_f32 && (numel & 3) == 0) {
+      hipLaunchKernelGGL(ew_flat_f32x4_kernel, dim3(grid_for(numel / 4)), dim3(kBlock), 0, as_stream(stream), k,
+                         numel / 4);
+      return launch_status("ew_flat_f32x4");
+    }
+    hipLaunchKernelGGL(ew_kernel<true>, dim3(grid_for(numel)), dim3(kBlock), 0, as_stream(stream), k, numel);
+    return launch_status("ew_flat");
+  }
+  hipLaunchKernelGGL(ew_kernel<false>, dim3(grid_for(numel)), dim3(kBlock), 0, as_stream(stream), k, numel);
+  return launch_status("ew");
+}
+
+int c3h_strided_copy(const c3h_copy_args* a, void* stream) {
+  C3H_REQUIRE(a && a->rank >= 0 && a->rank <= C3H_MAX_RANK, "strided_copy: bad rank");
+  int64_t total = 1;
+  for (int d = 0; d < a->rank; ++d) total *= a->shape[d];
+  if (total == 0) return C3H_OK;
+  hipStream_t s = as_stream(stream);
+  // Tiled transpose when the output's innermost dim is strided on the input
+  // and the second-innermost dim is unit-stride on the input.
+  if (a->rank >= 2 && a->in_stride[a->rank - 1] != 1 && a->in_stride[a->rank - 2] == 1 &&
+      a->in_stride[a->rank - 1] == a->shape[a->rank - 2] && a->in_offset == 0) {
+    int64_t rows = a->shape[a->rank - 2], cols = a->shape[a->rank - 1];
+    int64_t batch = total / (rows * cols);
+    bool batch_dense = true;
+    int64_t expect = rows * cols;
+    for (int d = a->rank - 3; d >= 0; --d) {
+      if (a->shape[d] != 1 && a->in_stride[d] != expect) batch_dense = false;
+      expect *= a->shape[d];
+    }
+    if (batch_dense && batch <= 65535) {
+      dim3 grid(static_cast<unsigned>(ceil_div(cols, 32)), static_cast<unsigned>(ceil_div(rows, 32)),
+                static_cast<unsigned>(batch));
+      switch (a->elem_bytes) {
+        case 4: hipLaunchKernelGGL(transpose_tile_kernel<uint32_t>, grid, dim3(256), 0, s,
+                                   static_cast<const uint32_t*>(a->in), static_cast<uint32_t*>(a->out), batch, rows, cols,
+                                   rows * cols, rows * cols); return launch_status("transpose_tile");
+        case 2: hipLaunchKernelGGL(transpose_tile_kernel<uint16_t>, grid, dim3(256), 0, s,
+                                   static_cast<const uint16_t*>(a->in), static_cast<uint16_t*>(a->out), batch, rows, cols,
+                                   rows * cols, rows * cols); return launch_status("transpose_tile");
+        default: break;
+      }
+    }
+  }
+  switch (a->elem_bytes) {
+    case 1: hipLaunchKernelGGL(strided_copy_kernel<uint8_t>, dim3(grid_for(total)), dim3(kBlock), 0, s,
+                               static_cast<const uint8_t*>(a->in), static_cast<uint8_t*>(a->out), *a, total); break;
+    case 2: hipLaunchKernelGGL(strided_copy_kernel<uint16_t>, dim3(grid_for(total)), dim3(kBlock), 0, s,
+                               static_cast<const uint16_t*>(a->in), static_cast<uint16_t*>(a->out), *a, total); break;
+    case 4: hipLaunchKernelGGL(strided_copy_kernel<uint32_t>, dim3(grid_for(total)), dim3(kBlock), 0, s,
+                               static_cast<const uint32_t*>(a->in), static_cast<uint32_t*>(a->out), *a, total); break;
+    case 8: hipLaunchKernelGGL(strided_copy_kernel<uint64_t>, dim3(grid_for(total)), dim3(kBlock), 0, s,
+                               static_cast<const uint64_t*>(a->in), static_cast<uint64_t*>(a->out), *a, total); break;
+    default: return fail(C3H_EINVAL, "strided_copy: elem_bytes %d unsupported", a->elem_bytes);
+  }
+  return launch_status("strided_copy");
+}
+
+int c3h_reduce(const c3h_reduce_args* a, void* stream) {
+  C3H_REQUIRE(a && a->outer >= 0 && a->reduce >= 1 && a->inner >= 1, "reduce: bad shape");
+  C3H_REQUIRE(a->kind >= 0 && a->kind <= 2, "reduce: bad kind %d", a->kind);
+  if (a->outer == 0) return C3H_OK;
+  if (a->inner == 1) {
+    int blocks = static_cast<int>(ceil_div(a->outer, kBlock / 64));
+    hipLaunchKernelGGL(reduce_rows_kernel, dim3(blocks), dim3(kBlock), 0, as_stream(stream), *a);
+  } else {
+    hipLaunchKernelGGL(reduce_cols_kernel, dim3(grid_for(a->outer * a->inner)), dim3(kBlock), 0, as_stream(stream), *a);
+  }
+  return launch_status("reduce");
+}
+
+int c3h_softmax(const c3h_softmax_args* a, void* stream) {
+  C3H_REQUIRE(a && a->outer >= 0 && a->axis >= 1 && a->inner >= 1, "softmax: bad shape");
+  if (a->outer == 0) return C3H_OK;
+  if (a->inner == 1) {
+    C3H_REQUIRE(a->outer <= 2147483647LL, "softmax: too many rows");
+    hipLaunchKernelGGL(softmax_rows_kernel, dim3(static_cast<unsigned>(a->outer)), dim3(kBlock), 0, as_stream(stream), *a);
+  } else {
+    hipLaunchKernelGGL(softmax_cols_kernel, dim3(grid_for(a->outer * a->inner)), dim3(kBlock), 0, as_stream(stream), *a);
+  }
+  return launch_status("softmax");
+}
+
+int c3h_layernorm(const c3h_layernorm_args* a, void* stream) {
+  C3H_REQUIRE(a && a->rows >= 0 && a->cols >= 1 && a->x && a->scale && a->out, "layernorm: bad args");
+  if (a->rows == 0) return C3H_OK;
+  int blocks = static_cast<int>(ceil_div(a->rows, kBlock / 64));
+  hipLaunchKernelGGL(layernorm_kernel, dim3(blocks), dim3(kBlock), 0, as_stream(stream), *a);
+  return launch_status("layernorm");
+}
+
+int c3h_batchnorm(const c3h_batchnorm_args* a, void* stream) {
+  C3H_REQUIRE(a && a->n >= 0 && a->c >= 1 && a->hw >= 1, "batchnorm: bad shape");
+  int64_t total = a->n * a->c * a->hw;
+  if (total == 0) return C3H_OK;
+  hipLaunchKernelGGL(batchnorm_kernel, dim3(grid_for(total)), dim3(kBlock), 0, as_stream(stream), *a);
+  return launch_status("batchnorm");
+}
+
+int c3h_bn_fold(const c3h_bnfold_args* a, void* stream) {
+  C3H_REQUIRE(a && a->out_channels >= 1 && a->per_channel >= 1, "bn_fold: bad shape");
+  hipLaunchKernelGGL(bn_fold_kernel, dim3(grid_for(a->out_channels * a->per_channel)), dim3(kBlock), 0,
+                     as_stream(stream), *a);
+  return launch_status("bn_fold");
+}
+
+int c3h_gather(const c3h_gather_args* a, void* stream) {
+  C3H_REQUIRE(a && a->outer >= 0 && a->axis_dim >= 1 && a->inner >= 0 && a->n_indices >= 0, "gather: bad shape");
+  int64_t row_bytes = a->inner * a->elem_bytes;
+  int64_t total_rows = a->outer * a->n_indices;
+  if (total_rows == 0 || row_bytes == 0) return C3H_OK;
+  hipStream_t s = as_stream(stream);
+  bool aligned16 = (reinterpret_cast<uintptr_t>(a->data) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 15) == 0;
+  if (row_bytes % 16 == 0 && aligned16) {
+    int64_t rv = row_bytes / 16;
+    hipLaunchKernelGGL(gather_kernel<uint4>, dim3(grid_for(total_rows * rv)), dim3(kBlock), 0, s, *a, rv);
+  } else if (row_bytes % 4 == 0) {
+    int64_t rv = row_bytes / 4;
+    hipLaunchKernelGGL(gather_kernel<uint32_t>, dim3(grid_for(total_rows * rv)), dim3(kBlock), 0, s, *a, rv);
+  } else {
+    hipLaunchKernelGGL(gather_kernel<uint8_t>, dim3(grid_for(total_rows * row_bytes)), dim3(kBlock), 0, s, *a,
+                       row_bytes);
+  }
+  return launch_status("gather");
+}
+
+int c3h_argmax(const c3h_argmax_args* a, void* stream) {
+  C3H_REQUIRE(a && a->rows >= 0 && a->cols >= 1 && a->out, "argmax: bad args");
+  if (a->rows == 0) return C3H_OK;
+  C3H_REQUIRE(a->rows <= 2147483647LL, "argmax: too many rows");
+  bool vec = a->in_dtype == C3H_F32 && (a->cols & 3) == 0 && (reinterpret_cast<uintptr_t>(a->in) & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL(argmax_kernel<true>, dim3(static_cast<unsigned>(a->rows)), dim3(kBlock), 0, as_stream(stream), *a);
+  else
+    hipLaunchKernelGGL(argmax_kernel<false>, dim3(static_cast<unsigned>(a->rows)), dim3(kBlock), 0, as_stream(stream), *a);
+  return launch_status("argmax");
+}
+
+int c3h_im2col(const c3h_im2col_args* a, void* stream) {
+  C3H_REQUIRE(a && a->n >= 0 && a->c >= 1 && a->ho >= 1 && a->wo >= 1 && a->kh >= 1 && a->kw >= 1, "im2col: bad shape");
+  int64_t total = static_cast<int64_t>(a->n) * a->ho * a->wo * a->c * a->kh * a->kw;
+  if (total == 0) return C3H_OK;
+  hipLaunchKernelGGL(im2col_kernel, dim3(grid_for(total)), dim3(kBlock), 0, as_stream(stream), *a);
+  return launch_status("im2col");
+}
+
+int c3h_layout(const c3h_layout_args* a, void* stream) {
+  C3H_REQUIRE(a && a->n >= 0 && a->c >= 1 && a->h >= 1 && a->w >= 1 && a->c_pad >= a->c, "layout: bad shape");
+  C3H_REQUIRE(a->direction == 0 || a->direction == 1, "layout: bad direction");
+  if (a->n == 0) return C3H_OK;
+  int64_t hw = static_cast<int64_t>(a->h) * a->w;
+  if (a->direction == 0 && a->c_pad <= 16) {
+    hipLaunchKernelGGL(nchw_to_nhwc_small_kernel, dim3(grid_for(a->n * hw)), dim3(kBlock), 0, as_stream(stream), *a);
+    return launch_status("layout_small");
+  }
+  C3H_REQUIRE(a->n <= 65535, "layout: batch too large for tiled path");
+  int64_t cdim = a->direction == 0 ? a->c_pad : a->c;
+  dim3 grid(static_cast<unsigned>(ceil_div(hw, 32)), static_cast<unsigned>(ceil_div(cdim, 32)),
+            static_cast<unsigned>(a->n));
+  hipLaunchKernelGGL(layout_tile_kernel, grid, dim3(256), 0, as_stream(stream), *a);
+  return launch_status("layout_tile");
+}
+
+int c3h_maxpool2d(const c3h_pool_args* a, void* stream) {
+  C3H_REQUIRE(a && a->n >= 0 && a->c >= 1 && a->ho >= 1 && a->wo >= 1, "maxpool: bad shape");
+  C3H_REQUIRE(a->layout == 0 || (a->layout == 1 && a->c_stride >= a->c), "maxpool: bad layout");
+  int64_t total = static_cast<int64_t>(a->n) * a->c * a->ho * a->wo;
+  if (total == 0) return C3H_OK;
+  hipLaunchKernelGGL(maxpool_kernel, dim3(grid_for(total)), dim3(kBlock), 0, as_stream(stream), *a);
+  return launch_status("maxpool");
+}
+
+int c3h_pack_conv_weight(const c3h_pack_args* a, void* stream) {
+  C3H_REQUIRE(a && a->o >= 1 && a->c >= 1 && a->kh >= 1 && a->kw >= 1, "pack: bad sizes");
+  C3H_REQUIRE(a->c_pack >= a->c && a->kw_pack >= a->kw, "pack: c_pack/kw_pack too small");
+  C3H_REQUIRE(a->k_stride >= static_cast<int64_t>(a->kh) * a->kw_pack * a->c_pack, "pack: k_stride too small");
+  hipLaunchKernelGGL(pack_conv_weight_kernel, dim3(grid_for(static_cast<int64_t>(a->o) * a->k_stride)), dim3(kBlock),
+                     0, as_stream(stream), *a);
+  return launch_status("pack_conv_weight");
+}
+
+int c3h_quantize(const c3h_quantize_args* a, void* stream) {
+  C3H_REQUIRE(a && a->count >= 0 && a->scale != 0.0f, "quantize: bad args");
+  if (a->count == 0) return C3H_OK;
+  hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(a->count)), dim3(kBlock), 0, as_stream(stream), *a);
+  return launch_status("quantize");
+}
+
+int c3h_dequantize(const c3h_dequantize_args* a, void* stream) {
+  C3H_REQUIRE(a && a->count >= 0, "dequantize: bad args");
+  if (a->count == 0) return C3H_OK;
+  hipLaunchKernelGGL(dequantize_kernel, dim3(grid_for(a->count)), dim3(kBlock), 0, as_stream(stream), *a);
+  return launch_status("dequantize");
+}
+
+}  // extern "C"

@@ -1,0 +1,249 @@
+"""GPU checks of the kernel families the compiled path uses directly.
+
+MFMA operand layouts, 16-bit GEMM, channels-last implicit-GEMM conv (fp32,
+bf16, f16, narrow-channel stem), flash attention, layout conversion, and the
+native timeline interpreter / hipGraph replay.  References are float64 NumPy
+on the same (rounded) inputs; tolerances are stated per test.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import graph_ref as G
+from oracle import registry_ref as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(x, dtype=None):
+    from hackathon_amd.device import DeviceArray
+
+    return DeviceArray.from_host(np.ascontiguousarray(x), dtype)
+
+
+def _bits(x, kind):
+    """Host array of 16-bit storage for kind in {'bf16','fp16'} + its float32 value."""
+    from hackathon_amd.device import f32_to_bf16
+
+    if kind == "bf16":
+        bits = f32_to_bf16(x)
+        return bits, G.round_bf16(x)
+    h = np.asarray(x, np.float32).astype(np.float16)
+    return h, h.astype(np.float32)
+
+
+def _from16(arr, kind):
+    from hackathon_amd.device import bf16_to_f32
+
+    return bf16_to_f32(arr) if kind == "bf16" else np.asarray(arr).astype(np.float32)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+@pytest.mark.parametrize("m,n,k", [(16, 16, 32), (64, 64, 64), (300, 200, 96), (1000, 64, 576), (130, 600, 520)])
+def test_gemm_16bit_matches_float64(gpu, kind, m, n, k):
+    """16x16x32 MFMA operand layout + tiling: out = A @ B^T + bias, relu, fp32 out."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import DeviceArray
+
+    rng = np.random.default_rng(m + n + k)
+    a, af = _bits(rng.standard_normal((m, k), dtype=np.float32), kind)
+    bt, bf = _bits(rng.standard_normal((n, k), dtype=np.float32), kind)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    out = DeviceArray.empty((m, n), np.float32)
+    code = _lib.BF16 if kind == "bf16" else _lib.F16
+    E.gemm(_dev(a), _dev(bt), out, m, n, k, lda=k, ldb=k, ldo=n, trans_b=1, in_dtype=code,
+           epi=E.epilogue(bias=_dev(bias), bias_mode=2, act=1))
+    ref = np.maximum(af.astype(np.float64) @ bf.astype(np.float64).T + bias, 0)
+    np.testing.assert_allclose(out.get(), ref, rtol=2e-5, atol=2e-4 * math.sqrt(k))
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+def test_gemm_16bit_out_and_program_epilogue(gpu, kind):
+    """16-bit output with a GELU program epilogue and a residual."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import DeviceArray
+
+    rng = np.random.default_rng(1)
+    m, n, k = 256, 192, 128
+    a, af = _bits(rng.standard_normal((m, k), dtype=np.float32) * 0.5, kind)
+    bt, bf = _bits(rng.standard_normal((n, k), dtype=np.float32) * 0.1, kind)
+    res, resf = _bits(rng.standard_normal((m, n), dtype=np.float32), kind)
+    code = _lib.BF16 if kind == "bf16" else _lib.F16
+    out = DeviceArray.empty((m, n), a.dtype)
+    # program: v/sqrt2 -> erf -> +1 -> x*() -> *0.5  (operands: 0=x, 1=prev, 2+j=imm[j])
+    prog = [(_lib.EW_DIV, 0, 2, 0.0), (_lib.EW_ERF, 1, 1, 0.0), (_lib.EW_ADD, 1, 3, 0.0),
+            (_lib.EW_MUL, 0, 1, 0.0), (_lib.EW_MUL, 1, 4, 0.0)]
+    E.gemm(_dev(a), _dev(bt), out, m, n, k, lda=k, ldb=k, ldo=n, trans_b=1, in_dtype=code,
+           epi=E.epilogue(residual=_dev(res), program=prog, imm=[math.sqrt(2.0), 1.0, 0.5]))
+    from scipy.special import erf
+    v = af.astype(np.float64) @ bf.astype(np.float64).T + resf
+    ref = 0.5 * v * (1 + erf(v / math.sqrt(2.0)))
+    got = _from16(out.get(), kind)
+    np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-2)
+
+
+def _conv_case(rng, n, c, h, w, o, kh, kw, s, p):
+    x = rng.standard_normal((n, c, h, w), dtype=np.float32)
+    wt = rng.standard_normal((o, c, kh, kw), dtype=np.float32) * np.float32(math.sqrt(2.0 / (c * kh * kw)))
+    b = rng.standard_normal(o, dtype=np.float32) * 0.1
+    return x, wt, b, {"kernel_shape": [kh, kw], "strides": [s, s], "pads": [p, p, p, p], "dilations": [1, 1]}
+
+
+@pytest.mark.parametrize("kind", ["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("case", [(2, 64, 14, 14, 64, 3, 3, 1, 1), (2, 64, 15, 15, 128, 3, 3, 2, 1),
+                                  (2, 128, 8, 8, 256, 1, 1, 2, 0), (1, 3, 37, 37, 64, 7, 7, 2, 3),
+                                  (3, 3, 16, 16, 64, 3, 3, 1, 1)])
+def test_conv_nhwc_implicit_gemm(gpu, kind, case):
+    """Channels-last implicit GEMM (+bias, +residual, relu) vs a float64 conv of the rounded operands."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    rng = np.random.default_rng(sum(case))
+    n, c, h, w, o, kh, kw, s, p = case
+    x, wt, b, attrs = _conv_case(rng, n, c, h, w, o, kh, kw, s, p)
+    ho, wo = (h + 2 * p - kh) // s + 1, (w + 2 * p - kw) // s + 1
+    code = {"fp32": _lib.F32, "bf16": _lib.BF16, "fp16": _lib.F16}[kind]
+    sdt = {"fp32": np.float32, "bf16": BF16, "fp16": np.float16}[kind]
+    narrow = kind != "fp32" and c < 8
+    c_pack = 4 if (kind == "fp32" or narrow) and c <= 4 else (c + 7) // 8 * 8 if kind != "fp32" else (c + 3) // 4 * 4
+    kw_pack = ((kw + 7) // 8 * 8) if narrow else kw
+    k = kh * kw_pack * c_pack
+    k_stride = k if kind == "fp32" or narrow else (k + 31) // 32 * 32
+    xd = E.to_nhwc(_dev(x), c_pack, out_dtype=sdt)
+    wp = E.pack_conv_weight(_dev(wt), c_pack, kw_pack, k_stride, out_dtype=sdt)
+    xr = x if kind == "fp32" else G.round_to(x, kind)
+    wr = wt if kind == "fp32" else G.round_to(wt, kind)
+    ref = R.conv2d(xr.astype(np.float64), wr.astype(np.float64), attrs).astype(np.float64) + b.reshape(1, o, 1, 1)
+    resid = rng.standard_normal((n, ho, wo, o), dtype=np.float32)
+    res_dev = _dev(resid) if kind == "fp32" else _dev(_bits(resid, kind)[0])
+    ref = np.maximum(ref + (resid if kind == "fp32" else _bits(resid, kind)[1]).transpose(0, 3, 1, 2), 0)
+    out = DeviceArray.empty((n, ho, wo, o), sdt)
+    a = _lib.ConvArgs()
+    a.x, a.w, a.out = xd.ptr, wp.ptr, out.ptr
+    a.n, a.c, a.h, a.w_, a.c_stride, a.c_pack, a.o = n, c, h, w, c_pack, c_pack, o
+    a.kh, a.kw, a.sh, a.sw, a.pad_top, a.pad_left, a.dh, a.dw, a.ho, a.wo = kh, kw, s, s, p, p, 1, 1, ho, wo
+    a.out_layout, a.in_dtype, a.out_dtype = 1, code, code
+    a.epi = E.epilogue(bias=_dev(b), bias_mode=2, act=1, residual=res_dev)
+    _lib.launch(a, None)
+    got = out.get()
+    got = got if kind == "fp32" else _from16(got, kind)
+    tol = 1e-4 if kind == "fp32" else 2e-2
+    np.testing.assert_allclose(got.transpose(0, 3, 1, 2), ref, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16"])
+@pytest.mark.parametrize("mask_kind", [0, 1, 2])
+@pytest.mark.parametrize("b,h,s", [(2, 3, 64), (1, 2, 200), (2, 1, 256)])
+def test_flash_attention(gpu, kind, mask_kind, b, h, s):
+    """softmax(QK^T*scale + mask) V with Q,K,V head-split views of a packed [B,S,3,H,64] buffer."""
+    from hackathon_amd import _lib
+    from hackathon_amd.device import DeviceArray
+
+    d = 64
+    rng = np.random.default_rng(b * 100 + h * 10 + s)
+    qkv = rng.standard_normal((b, s, 3, h, d), dtype=np.float32)
+    bits, val = _bits(qkv, kind)
+    dev = _dev(bits)
+    out = DeviceArray.empty((b, s, h, d), bits.dtype)  # written in [B,S,H,D] order
+    mask = np.zeros((s, s), np.float32)
+    if mask_kind == 2:
+        mask = rng.standard_normal((s, s)).astype(np.float32)
+        mask[np.triu_indices(s, 1)] = -np.inf
+    mdev = _dev(mask)
+    a = _lib.FlashArgs()
+    item = 2
+    base = dev.ptr
+    a.q, a.k, a.v = base, base + h * d * item, base + 2 * h * d * item
+    a.mask, a.out = mdev.ptr, out.ptr
+    a.batch, a.heads, a.seq_q, a.seq_k, a.head_dim = b, h, s, s, d
+    a.dtype = _lib.BF16 if kind == "bf16" else _lib.F16
+    sb, ss, sh = s * 3 * h * d, 3 * h * d, d
+    a.q_sb = a.k_sb = a.v_sb = sb
+    a.q_sh = a.k_sh = a.v_sh = sh
+    a.q_ss = a.k_ss = a.v_ss = ss
+    a.o_sb, a.o_sh, a.o_ss = s * h * d, d, h * d
+    a.mask_ld, a.scale, a.mask_kind = s, 1.0 / math.sqrt(d), mask_kind
+    _lib.launch(a, None)
+    got = _from16(out.get(), kind).transpose(0, 2, 1, 3)
+    q, k, v = (val[:, :, i].transpose(0, 2, 1, 3).astype(np.float64) for i in range(3))
+    sc = q @ k.transpose(0, 1, 3, 2) / math.sqrt(d)
+    if mask_kind == 1:
+        sc = sc + np.triu(np.full((s, s), -np.inf), 1)
+    elif mask_kind == 2:
+        sc = sc + mask
+    p = np.exp(sc - sc.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    ref = p @ v
+    tol = 2e-2 if kind == "bf16" else 5e-3
+    np.testing.assert_allclose(got, ref, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("c,c_pad,kind", [(3, 4, "bf16"), (64, 64, "fp32"), (40, 48, "fp16"), (3, 8, "fp32")])
+def test_layout_roundtrip(gpu, c, c_pad, kind):
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    x = np.random.default_rng(c).standard_normal((2, c, 9, 13)).astype(np.float32)
+    sdt = {"fp32": np.float32, "bf16": BF16, "fp16": np.float16}[kind]
+    nhwc = E.to_nhwc(_dev(x), c_pad, out_dtype=sdt)
+    host = nhwc.get()
+    val = host if kind == "fp32" else _from16(host, kind)
+    xr = x if kind == "fp32" else G.round_to(x, kind)
+    np.testing.assert_array_equal(val[..., :c], xr.transpose(0, 2, 3, 1))
+    np.testing.assert_array_equal(val[..., c:], 0)
+    back = DeviceArray.empty(x.shape, np.float32)
+    a = _lib.LayoutArgs()
+    a.in_, a.out, a.n, a.c, a.h, a.w = nhwc.ptr, back.ptr, 2, c, 9, 13
+    a.c_pad, a.direction, a.in_dtype, a.out_dtype = c_pad, 1, nhwc.code, _lib.F32
+    _lib.launch(a, None)
+    np.testing.assert_array_equal(back.get(), xr)
+
+
+def test_program_run_and_graph_replay(gpu):
+    """The native timeline interpreter and a captured hipGraph replayed 5 times."""
+    import ctypes as C
+
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import DeviceArray, Stream, synchronize
+
+    x = np.linspace(-1, 1, 4096, dtype=np.float32)
+    xd = _dev(x)
+    y = DeviceArray.empty((4096,), np.float32)
+    z = DeviceArray.empty((4096,), np.float32)
+    fill = _lib.FillArgs(out=z.ptr, count=4096, dtype=_lib.F32, value=0.0)
+    ew1 = E.ew_args([xd], [(_lib.EW_RELU, 0, 0, 0.0)], y, (4096,))
+    ew2 = E.ew_args([y, xd], [(_lib.EW_ADD, 0, 1, 0.0), (_lib.EW_MUL_IMM, 2, 2, 3.0)], z, (4096,))
+    ops = (_lib.Op * 3)()
+    for i, args in enumerate([fill, ew1, ew2]):
+        ops[i].kind = _lib.OP_KIND[type(args)]
+        ops[i].stream = 0
+        ops[i].args = C.cast(C.pointer(args), C.c_void_p)
+    s = Stream()
+    streams = (C.c_void_p * 1)(s.handle)
+    _lib.check(_lib.lib().c3h_program_run(ops, 3, streams, 1, None, 0), "program_run")
+    s.synchronize()
+    expect = (np.maximum(x, 0) + x) * 3
+    np.testing.assert_allclose(z.get(), expect, rtol=1e-6)
+    g = C.c_void_p()
+    _lib.check(_lib.lib().c3h_program_capture(ops, 3, streams, 1, None, 0, C.byref(g)), "capture")
+    for _ in range(5):
+        xd.copy_from_host(np.zeros(4096, np.float32))
+        synchronize()
+        np.testing.assert_array_equal(z.get(), expect)  # untouched until replay
+        _lib.check(_lib.lib().c3h_graph_launch(g, s.handle), "graph_launch")
+        s.synchronize()
+        np.testing.assert_array_equal(z.get(), 0)
+        xd.copy_from_host(x)
+        _lib.check(_lib.lib().c3h_graph_launch(g, s.handle), "graph_launch")
+        s.synchronize()
+        np.testing.assert_allclose(z.get(), expect, rtol=1e-6)
+    _lib.check(_lib.lib().c3h_graph_destroy(g), "graph_destroy")

