@@ -318,6 +318,14 @@ class PlannedGraphExecutor(GraphExecutor):
             hit = cache[name]
         return hit[0]
 
+    def weight_sources(self) -> Dict[str, Any]:
+        """Every model tensor by name: host payloads plus the device-resident ones.
+
+        Folded Conv+BN parameters leave `host_weights` once a planned run has
+        made them resident; the compiled engine needs them either way.
+        """
+        return {**self.host_weights, **self._resident_model_tensors}
+
     def run_planned(self, feed_dict: Dict[str, Any], plan: ExecutionPlan) -> Dict[str, DeviceArray]:
         issues = plan.validate()
         if issues:
@@ -469,7 +477,7 @@ class CrossStageReferencePipeline:
         if batch_size not in self._compiled:
             plan = self._plan_for_batch(batch_size)
             ex = self.optimized_executor
-            self._compiled[batch_size] = CompiledPlan(self.graph, plan, ex.host_weights, ex.host_constants,
+            self._compiled[batch_size] = CompiledPlan(self.graph, plan, ex.weight_sources(), ex.host_constants,
                                                       policy=self.precision)
         return self._compiled[batch_size]
 

@@ -647,7 +647,16 @@ __global__ void __launch_bounds__(kThreads) qgemm_kernel(QProblem p) {
           y = fminf(fmaxf(y, -128.0f), 127.0f);
           static_cast<int8_t*>(p.out)[o] = static_cast<int8_t>(y);
         } else {
-          const float deq = static_cast<float>(iacc) * (p.a_scale * p.b_scale[n]);
+          float deq;
+          if (p.mode == 3) {
+            // QLinearMatMul -> DequantizeLinear: the int8 y of mode 1, then (y - zy) * y_scale.
+            const float mult = (p.a_scale * p.b_scale[n]) / p.y_scale;
+            float y = rintf(static_cast<float>(iacc) * mult) + static_cast<float>(p.y_zero);
+            y = fminf(fmaxf(y, -128.0f), 127.0f);
+            deq = (y - static_cast<float>(p.y_zero)) * p.y_scale;
+          } else {
+            deq = static_cast<float>(iacc) * (p.a_scale * p.b_scale[n]);
+          }
           float res = 0.0f;
           if (p.epi.residual) res = load_as_f32(p.epi.residual, p.out_dtype, o);
           store_from_f32(p.out, p.out_dtype, o, apply_epilogue(p.epi, deq, m, n, p.n, res));
@@ -859,12 +868,12 @@ int c3h_qgemm(const c3h_qgemm_args* a, void* stream) {
   C3H_REQUIRE(a != nullptr, "qgemm: null args");
   C3H_REQUIRE(a->m >= 0 && a->n >= 0 && a->k >= 1, "qgemm: bad sizes");
   C3H_REQUIRE(a->a_zero == 0 && a->b_zero == 0, "qgemm: only symmetric (zero-point 0) operands are supported");
-  C3H_REQUIRE(a->mode >= 0 && a->mode <= 2, "qgemm: bad mode %d", a->mode);
+  C3H_REQUIRE(a->mode >= 0 && a->mode <= 3, "qgemm: bad mode %d", a->mode);
   C3H_REQUIRE(a->mode == 0 || a->b_scale != nullptr, "qgemm: b_scale required");
-  C3H_REQUIRE(a->mode != 1 || a->y_scale != 0.0f, "qgemm: y_scale must be nonzero");
+  C3H_REQUIRE((a->mode != 1 && a->mode != 3) || a->y_scale != 0.0f, "qgemm: y_scale must be nonzero");
   C3H_REQUIRE(a->k % 16 == 0 && a->lda % 16 == 0 && a->ldb % 16 == 0, "qgemm: k, lda, ldb must be multiples of 16");
   C3H_REQUIRE(aligned(a->a, 16) && aligned(a->b, 16), "qgemm: operands must be 16-byte aligned");
-  C3H_REQUIRE(a->mode != 2 || a->out_dtype == C3H_F32 || a->out_dtype == C3H_BF16 || a->out_dtype == C3H_F16,
+  C3H_REQUIRE(a->mode < 2 || a->out_dtype == C3H_F32 || a->out_dtype == C3H_BF16 || a->out_dtype == C3H_F16,
               "qgemm: dequantized output dtype must be float");
   int rc = check_epilogue(a->epi);
   if (rc) return rc;

@@ -512,7 +512,9 @@ int c3h_quantize(const c3h_quantize_args* a, void* stream);
  * (B[n,k]-zb); B packed [n][k] (transB).  mode 0: write int32 acc; mode 1:
  * requantize y = saturate(rne(acc * a_scale * b_scale[n] / y_scale) + zy)
  * to int8 (QLinearMatMul); mode 2: dequantize to float out_dtype
- * v = acc * (a_scale * b_scale[n]) then the epilogue (bias, act/program). */
+ * v = acc * (a_scale * b_scale[n]) then the epilogue (bias, act/program);
+ * mode 3: QLinearMatMul followed by DequantizeLinear(y_scale, y_zero) --
+ * the mode-1 int8 y, then v = (y - zy) * y_scale, then the epilogue. */
 typedef struct {
   const int8_t* a;
   const int8_t* b;

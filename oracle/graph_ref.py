@@ -75,6 +75,20 @@ def _elements(plan, name: str, graph, batch: int) -> int:
     return 0
 
 
+def _lookup_policy_kernel(name: str):
+    """Registry kernel for a plan step; reduced-precision names use the fp32 kernel.
+
+    The reference registry holds fp32 kernels only (kernel_registry.py:42-67
+    resolves `_f32` / `_fp32` suffixes); steps a 16-bit or W8A8 policy
+    renames (`matmul_bf16`, `fused_ew_fp16`, ...) are evaluated with the fp32
+    kernel, and run_plan applies the policy's rounding at node boundaries.
+    """
+    for suffix in ("_bf16", "_fp16", "_f16", "_fp8", "_fp4", "_int8"):
+        if name.endswith(suffix):
+            return R.lookup(name[: -len(suffix)] + "_f32")
+    return R.lookup(name)
+
+
 def run_plan(plan, graph, weights: Dict[str, np.ndarray], feed: Dict[str, np.ndarray],
              policy: str = "fp32") -> Dict[str, np.ndarray]:
     """Evaluate the plan's kernel steps in order with the registry oracle."""
@@ -96,7 +110,7 @@ def run_plan(plan, graph, weights: Dict[str, np.ndarray], feed: Dict[str, np.nda
     for k in plan.kernel_steps:
         if k.kernel_name == "constant":
             continue
-        fn = R.lookup(k.kernel_name)
+        fn = _lookup_policy_kernel(k.kernel_name)
         prof = k.precision_profile or {}
         ins = []
         for n in k.logical_inputs:
