@@ -98,21 +98,47 @@ __device__ __forceinline__ void store_from_f32(void* p, int dt, int64_t i, float
 
 // Typed element storage used by templated kernels.
 template <typename T> struct Elem;
+// load8 / store8 move 8 consecutive elements (16-byte aligned for 16-bit
+// types, 32-byte for fp32) as whole vectors.
 template <> struct Elem<float> {
   static __device__ __forceinline__ float to_f32(float v) { return v; }
   static __device__ __forceinline__ float from_f32(float v) { return v; }
+  static __device__ __forceinline__ void load8(const float* p, float* v) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  static __device__ __forceinline__ void store8(float* p, const float* v) {
+    reinterpret_cast<float4*>(p)[0] = float4{v[0], v[1], v[2], v[3]};
+    reinterpret_cast<float4*>(p)[1] = float4{v[4], v[5], v[6], v[7]};
+  }
 };
 
 struct bf16_t { uint16_t bits; };
 struct f16_t { uint16_t bits; };
-template <> struct Elem<bf16_t> {
-  static __device__ __forceinline__ float to_f32(bf16_t v) { return bf16_bits_to_f32(v.bits); }
-  static __device__ __forceinline__ bf16_t from_f32(float v) { return bf16_t{f32_to_bf16_bits(v)}; }
+
+template <typename T, float (*ToF)(uint16_t), uint16_t (*FromF)(float)>
+struct Elem16 {
+  static __device__ __forceinline__ float to_f32(T v) { return ToF(v.bits); }
+  static __device__ __forceinline__ T from_f32(float v) { return T{FromF(v)}; }
+  static __device__ __forceinline__ void load8(const T* p, float* v) {
+    const uint4 q = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = ToF(static_cast<uint16_t>(w[i] & 0xffffu));
+      v[2 * i + 1] = ToF(static_cast<uint16_t>(w[i] >> 16));
+    }
+  }
+  static __device__ __forceinline__ void store8(T* p, const float* v) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = static_cast<uint32_t>(FromF(v[2 * i])) | (static_cast<uint32_t>(FromF(v[2 * i + 1])) << 16);
+    *reinterpret_cast<uint4*>(p) = uint4{w[0], w[1], w[2], w[3]};
+  }
 };
-template <> struct Elem<f16_t> {
-  static __device__ __forceinline__ float to_f32(f16_t v) { return f16_bits_to_f32(v.bits); }
-  static __device__ __forceinline__ f16_t from_f32(float v) { return f16_t{f32_to_f16_bits(v)}; }
-};
+template <> struct Elem<bf16_t> : Elem16<bf16_t, bf16_bits_to_f32, f32_to_bf16_bits> {};
+template <> struct Elem<f16_t> : Elem16<f16_t, f16_bits_to_f32, f32_to_f16_bits> {};
 
 // Abramowitz & Stegun 7.1.26 rational approximation of erf (max abs error
 // about 1.5e-7), the formula the reference's unfused Erf uses.

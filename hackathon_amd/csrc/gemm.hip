@@ -11,6 +11,8 @@
 // tile k+1 are in flight while the MFMAs of tile k run.  Tile ids are
 // remapped so that consecutive tiles (sharing an A row panel) land on the
 // same XCD and hit its L2.
+#include <type_traits>
+
 #include "common.h"
 
 using namespace c3h;
@@ -23,10 +25,22 @@ typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 
 constexpr int kThreads = 256;
 
+// Kernel-argument view: the (single) by-value argument read in place through
+// the kernarg segment pointer (constant address space, scalar loads), so a
+// dynamically indexed epilogue program never makes the compiler copy the
+// argument struct into scratch memory.
+template <typename T>
+using KArg = __attribute__((address_space(4))) T;
+
+template <typename P>
+__device__ __forceinline__ const KArg<P>& kernel_arg() {
+  return *(const KArg<P>*)(__builtin_amdgcn_kernarg_segment_ptr());
+}
+
 // ---------------------------------------------------------------- epilogue
 // `e` is read straight from the kernel-argument segment (uniform scalar
 // loads); `bias_off` selects the batch's bias slice.
-__device__ __forceinline__ float apply_epilogue(const c3h_epilogue& e, float acc, int64_t m, int64_t n,
+__device__ __forceinline__ float apply_epilogue(const KArg<c3h_epilogue>& e, float acc, int64_t m, int64_t n,
                                                 int64_t ldb_bias, float res, int64_t bias_off = 0) {
   float v = e.alpha * acc;
   const float* bias = static_cast<const float*>(e.bias) + bias_off;
@@ -56,6 +70,67 @@ __device__ __forceinline__ float apply_epilogue(const c3h_epilogue& e, float acc
   return v;
 }
 
+// Epilogue of 8 consecutive columns n..n+7 of row m, in the same order and
+// arithmetic as apply_epilogue.  Every decision is uniform across the wave
+// and is taken once per 8 values, and bias_mode 2 reads its 8 bias values
+// as two float4 loads when they are 16-byte aligned.
+__device__ __forceinline__ void apply_epilogue8(const KArg<c3h_epilogue>& e, float* v, int64_t m, int64_t n,
+                                                int64_t ldb_bias, const float* res, int64_t bias_off) {
+  const float alpha = e.alpha, beta = e.beta;
+  if (alpha != 1.0f) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) v[c] = alpha * v[c];
+  }
+  const float* bias = static_cast<const float*>(e.bias) + bias_off;
+  const int bm = e.bias_mode;
+  if (bm == 2) {
+    float b[8];
+    if ((reinterpret_cast<uintptr_t>(bias + n) & 15) == 0) {
+      const float4 b0 = *reinterpret_cast<const float4*>(bias + n), b1 = *reinterpret_cast<const float4*>(bias + n + 4);
+      b[0] = b0.x; b[1] = b0.y; b[2] = b0.z; b[3] = b0.w; b[4] = b1.x; b[5] = b1.y; b[6] = b1.z; b[7] = b1.w;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) b[c] = bias[n + c];
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) v[c] += beta * b[c];
+  } else if (bm == 1) {
+    const float b = beta * bias[0];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) v[c] += b;
+  } else if (bm == 3) {
+    const float b = beta * bias[m];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) v[c] += b;
+  } else if (bm == 4) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) v[c] += beta * bias[m * ldb_bias + n + c];
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) v[c] += res[c];
+  if (e.act == 1) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) v[c] = fmaxf(v[c], 0.0f);
+  }
+  const int ni = e.n_inst;
+  if (ni > 0) {
+    float x[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) x[c] = v[c];
+    for (int i = 0; i < ni; ++i) {
+      const int op = e.inst[i].op, ca = e.inst[i].a, cb = e.inst[i].b;
+      const float imm = e.inst[i].imm;
+      const float ia = ca >= 2 ? e.imm[ca - 2] : 0.0f, ib = cb >= 2 ? e.imm[cb - 2] : 0.0f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float oa = ca == 0 ? x[c] : (ca == 1 ? v[c] : ia);
+        const float ob = cb == 0 ? x[c] : (cb == 1 ? v[c] : ib);
+        v[c] = ew_apply(op, oa, ob, imm);
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------- problem
 // Everything the kernels need, flattened from the gemm/conv args.
 struct Problem {
@@ -71,6 +146,10 @@ struct Problem {
   int cn, cc, ch, cw, c_stride, c_pack, kh, kw, kw_pack, sh, sw, pt, pl, dh, dw, ho, wo;
   int out_nchw;  // conv: write NCHW instead of NHWC
   int tiles_m, tiles_n;
+  // int8 GEMM (c3h_qgemm): output mode and quantization parameters
+  int qmode, y_zero;
+  float a_scale, y_scale;
+  const float* b_scale;
   c3h_epilogue epi;
 };
 
@@ -148,7 +227,7 @@ __device__ __forceinline__ void store_strip(const Problem& p, const float* stage
       if (n >= p.n) break;
       const int64_t o = m * p.ldo + n;
       const float res = resp ? Elem<TO>::to_f32(resp[o]) : 0.0f;
-      outp[o] = Elem<TO>::from_f32(apply_epilogue(p.epi, stage[row * SS + c0 + c], m, n, p.n, res, bias_off));
+      outp[o] = Elem<TO>::from_f32(apply_epilogue(kernel_arg<Problem>().epi, stage[row * SS + c0 + c], m, n, p.n, res, bias_off));
     }
   } else {
     const int64_t hw = static_cast<int64_t>(p.ho) * p.wo;
@@ -161,7 +240,7 @@ __device__ __forceinline__ void store_strip(const Problem& p, const float* stage
         const int64_t img = m / hw, pix = m - img * hw;
         const int64_t o = (img * p.n + n) * hw + pix;
         const float res = resp ? Elem<TO>::to_f32(resp[o]) : 0.0f;
-        outp[o] = Elem<TO>::from_f32(apply_epilogue(p.epi, stage[row * SS + col], m, n, p.n, res, bias_off));
+        outp[o] = Elem<TO>::from_f32(apply_epilogue(kernel_arg<Problem>().epi, stage[row * SS + col], m, n, p.n, res, bias_off));
       }
     }
   }
@@ -377,291 +456,420 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(Problem p) {
 }
 
 // =====================================================================
-// 16-bit kernel: v_mfma_f32_16x16x32_{bf16,f16}.  LDS tiles are stored
-// row-major with K contiguous (As[m][k], Bs[n][k]) plus a 16-byte skew, so a
-// lane's 8-element operand is one ds_read_b128.
+// MFMA kernel for 16-bit (v_mfma_f32_16x16x32_{bf16,f16}) and int8
+// (v_mfma_i32_16x16x64_i8, exact int32 accumulation) operands.  A tile row
+// is 128 bytes of K (64 16-bit or 128 int8 elements); LDS rows hold eight
+// 16-byte chunks XOR-swizzled by (row & 7), so a lane's MFMA operand is one
+// ds_read_b128 and 8 consecutive rows reading the same K chunk hit 8
+// distinct bank groups.  Every thread moves 16-byte vectors; since 256 % 8
+// == 0 a thread's vectors share one K chunk and step 32 rows apart.
+//
+// A operand modes:
+//   kDenseK    A[m][k] row-major (lda).
+//   kConvTap   implicit-GEMM conv with c_pack % 64 == 0: a 64-wide K tile lies
+//              inside one filter tap, so (kh, kw, c0) is uniform per tile and
+//              advanced incrementally; each row keeps its pixel base.
+//   kConv      generic implicit GEMM (c_pack % 8 == 0): per-vector tap math.
+//   kConvStem  c_pack == c_stride == 4, kw padded to 8: a vector is two taps
+//              of one input row (two 8-byte halves, each bounds-checked).
 // =====================================================================
-template <typename T> struct Mfma16;
-template <> struct Mfma16<bf16_t> {
+typedef __attribute__((ext_vector_type(4))) int i32x4;
+
+struct MmaBF16 {
   typedef bf16x8 vec;
-  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+  typedef f32x4 acc_t;
+  static constexpr int ES = 2;
+  static constexpr bool kInt = false;
+  static __device__ __forceinline__ acc_t mma(vec a, vec b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
 };
-template <> struct Mfma16<f16_t> {
+struct MmaF16 {
   typedef f16x8 vec;
-  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+  typedef f32x4 acc_t;
+  static constexpr int ES = 2;
+  static constexpr bool kInt = false;
+  static __device__ __forceinline__ acc_t mma(vec a, vec b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
 };
+struct MmaI8 {
+  typedef i32x4 vec;
+  typedef i32x4 acc_t;
+  static constexpr int ES = 1;
+  static constexpr bool kInt = true;
+  static __device__ __forceinline__ acc_t mma(vec a, vec b, acc_t c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  }
+};
 
-template <typename T, typename TO, int BM, int BN, int WM, int WN, int AM, int VEC, bool SWAP>
-__global__ void __launch_bounds__(kThreads) gemm_h_kernel(Problem p) {
-  constexpr int BK = 32;
-  constexpr int SK = BK + 8;  // 80-byte row stride
+enum AMode16 { kConvTap = 3, kConvStem = 4 };
+
+// Grouped tile order: each XCD (blockIdx % 8) owns a contiguous range of tile
+// ids, walked in column-major groups of 8 tile rows so blocks resident at
+// the same time share both A and B panels in that XCD's L2.
+__device__ __forceinline__ void tile_coords_grouped(const Problem& p, int& tm, int& tn) {
+  const int total = p.tiles_m * p.tiles_n;
+  int tile = blockIdx.x;
+  if ((total & 7) == 0) {
+    const int per = total >> 3;
+    tile = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  }
+  constexpr int G = 8;
+  const int group = tile / (G * p.tiles_n);
+  const int first_m = group * G;
+  const int gsize = min(p.tiles_m - first_m, G);
+  const int in_group = tile - group * G * p.tiles_n;
+  tm = first_m + in_group % gsize;
+  tn = in_group / gsize;
+}
+
+// Vectorized epilogue of one 16-row strip (row-major [m, n] output): each
+// lane owns 8 consecutive columns, so a row is written as WTN/8 16-byte
+// (bf16/fp16) or 32-byte (fp32) stores.  Called from a runtime loop over
+// strips: the whole wave tile is staged in LDS first, so the accumulators are
+// only ever indexed by unrolled (constant) indices.
+template <typename TO, int WTN>
+__device__ __forceinline__ void store_strip_vec(const float* stage, int lane, int64_t mrow0, int64_t ncol0,
+                                                          TO* outp, const TO* resp, int64_t bias_off, bool vec_ok) {
+  const KArg<Problem>& p = kernel_arg<Problem>();
+  constexpr int SS = WTN + 4;
+  constexpr int LPR = WTN / 8;
+  constexpr int RPP = 64 / LPR;
+  static_assert(LPR >= 1 && 64 % LPR == 0 && RPP <= 16, "strip shape");
+  const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
+  for (int pass = 0; pass < 16 / RPP; ++pass) {
+    const int row = pass * RPP + lane / LPR;
+    const int c0 = (lane % LPR) * 8;
+    const int64_t m = mrow0 + row;
+    const int64_t n = ncol0 + c0;
+    if (m >= pm || n >= pn) continue;
+    const float4 lo = *reinterpret_cast<const float4*>(stage + row * SS + c0);
+    const float4 hi = *reinterpret_cast<const float4*>(stage + row * SS + c0 + 4);
+    float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    const int64_t o = m * ldo + n;
+    if (vec_ok && n + 8 <= pn) {
+      float res[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (resp) Elem<TO>::load8(resp + o, res);
+      apply_epilogue8(p.epi, v, m, n, pn, res, bias_off);
+      Elem<TO>::store8(outp + o, v);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        if (n + c < pn) {
+          const float res = resp ? Elem<TO>::to_f32(resp[o + c]) : 0.0f;
+          outp[o + c] = Elem<TO>::from_f32(apply_epilogue(p.epi, v[c], m, n + c, pn, res, bias_off));
+        }
+      }
+    }
+  }
+}
+
+// int8 GEMM epilogue of one 16-row strip: the stage holds int32 accumulator
+// bits.  qmode 0 writes int32, 1 requantizes to int8, 2 dequantizes, 3
+// requantizes then dequantizes (QLinearMatMul -> DequantizeLinear); 2 and 3
+// continue through the float epilogue into TO.
+template <typename TO, int WTN>
+__device__ __forceinline__ void store_strip_q(const float* stage, int lane, int64_t mrow0, int64_t ncol0, TO* outp,
+                                              const TO* resp, bool vec_ok) {
+  const KArg<Problem>& p = kernel_arg<Problem>();
+  constexpr int SS = WTN + 4;
+  constexpr int LPR = WTN / 8;
+  constexpr int RPP = 64 / LPR;
+  const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
+  const int mode = p.qmode;
+  const float sa = p.a_scale, sy = p.y_scale, zy = static_cast<float>(p.y_zero);
+  const float* sb = p.b_scale;
+  for (int pass = 0; pass < 16 / RPP; ++pass) {
+    const int row = pass * RPP + lane / LPR;
+    const int c0 = (lane % LPR) * 8;
+    const int64_t m = mrow0 + row;
+    const int64_t n = ncol0 + c0;
+    if (m >= pm || n >= pn) continue;
+    const int4 lo = *reinterpret_cast<const int4*>(stage + row * SS + c0);
+    const int4 hi = *reinterpret_cast<const int4*>(stage + row * SS + c0 + 4);
+    const int acc[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    const int64_t o = m * ldo + n;
+    const bool full = vec_ok && n + 8 <= pn;
+    if constexpr (std::is_same<TO, int32_t>::value) {
+      int32_t* out = outp;
+      if (full) {
+        reinterpret_cast<int4*>(out + o)[0] = lo;
+        reinterpret_cast<int4*>(out + o)[1] = hi;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (n + c < pn) out[o + c] = acc[c];
+      }
+    } else {
+      float v[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float bsc = n + c < pn ? sb[n + c] : 0.0f;
+        if (mode == 1 || mode == 3) {
+          const float mult = (sa * bsc) / sy;
+          float y = rintf(static_cast<float>(acc[c]) * mult) + zy;
+          y = fminf(fmaxf(y, -128.0f), 127.0f);
+          v[c] = mode == 1 ? y : (y - zy) * sy;
+        } else {
+          v[c] = static_cast<float>(acc[c]) * (sa * bsc);
+        }
+      }
+      if constexpr (std::is_same<TO, int8_t>::value) {
+        int8_t* out = outp;
+        if (full) {
+          uint32_t w[2] = {0u, 0u};
+#pragma unroll
+          for (int c = 0; c < 8; ++c)
+            w[c >> 2] |= (static_cast<uint32_t>(static_cast<int8_t>(v[c])) & 0xffu) << (8 * (c & 3));
+          *reinterpret_cast<uint2*>(out + o) = uint2{w[0], w[1]};
+        } else {
+#pragma unroll
+          for (int c = 0; c < 8; ++c)
+            if (n + c < pn) out[o + c] = static_cast<int8_t>(v[c]);
+        }
+      } else if (full) {
+        float res[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (resp) Elem<TO>::load8(resp + o, res);
+        apply_epilogue8(p.epi, v, m, n, pn, res, 0);
+        Elem<TO>::store8(outp + o, v);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          if (n + c < pn) {
+            const float res = resp ? Elem<TO>::to_f32(resp[o + c]) : 0.0f;
+            outp[o + c] = Elem<TO>::from_f32(apply_epilogue(p.epi, v[c], m, n + c, pn, res, 0));
+          }
+        }
+      }
+    }
+  }
+}
+
+template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM>
+__global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
+  constexpr int ES = Mma::ES;
+  constexpr int VE = 16 / ES;        // elements per 16-byte vector
+  constexpr int BK = 128 / ES;       // elements per 128-byte tile row
+  constexpr int RB = 128;            // LDS row bytes
   constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
-  constexpr int WTN = BN / WN;
-  constexpr int kTileBytes = 2 * BM * SK * 2 + 2 * BN * SK * 2;
-  constexpr int kStageBytes = 4 * 16 * (WTN + 4) * 4;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int RSTEP = kThreads / 8;  // rows between a thread's vectors
+  constexpr int A_V = BM / RSTEP, B_V = BN / RSTEP;
+  static_assert(WM * WN == kThreads / 64, "wave grid");
+  static_assert(A_V >= 1 && B_V >= 1 && BM % RSTEP == 0 && BN % RSTEP == 0, "tile too small");
+  static_assert(AM == kDenseK || ES == 2, "conv modes are 16-bit");
+  constexpr int kTileBytes = 2 * (BM + BN) * RB;
+  constexpr int kStageBytes = (kThreads / 64) * WTM * (WTN + 4) * 4;  // whole wave tiles, 32-bit
   __shared__ __attribute__((aligned(16))) uint8_t smem[kTileBytes > kStageBytes ? kTileBytes : kStageBytes];
-  uint16_t (*As)[BM][SK] = reinterpret_cast<uint16_t (*)[BM][SK]>(smem);
-  uint16_t (*Bs)[BN][SK] = reinterpret_cast<uint16_t (*)[BN][SK]>(smem + 2 * BM * SK * 2);
-  typedef typename Mfma16<T>::vec vec8;
+  uint8_t (*As)[BM][RB] = reinterpret_cast<uint8_t (*)[BM][RB]>(smem);
+  uint8_t (*Bs)[BN][RB] = reinterpret_cast<uint8_t (*)[BN][RB]>(smem + 2 * BM * RB);
+  typedef typename Mma::vec vec;
+  typedef typename Mma::acc_t acc_t;
 
   int tm, tn;
-  tile_coords(p, tm, tn);
+  tile_coords_grouped(p, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const int64_t bz = blockIdx.z;
-  const uint16_t* A = static_cast<const uint16_t*>(p.a) + bz * p.stride_a;
-  const uint16_t* B = static_cast<const uint16_t*>(p.b) + bz * p.stride_b;
+  const uint8_t* A = static_cast<const uint8_t*>(p.a) + bz * p.stride_a * ES;
+  const uint8_t* B = static_cast<const uint8_t*>(p.b) + bz * p.stride_b * ES;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int wm = wave / WN, wn = wave % WN;
+  const int trow = tid >> 3;         // first tile row of this thread
+  const int kchunk = tid & 7;        // 16-byte K chunk of all of this thread's vectors
+  const int kc = kchunk * VE;        // ... as an element column
 
-  // Each thread moves VEC-element vectors (VEC = 8 -> 16 B, VEC = 4 -> 8 B).
-  constexpr int VPR = BK / VEC;                     // vectors per tile row
-  constexpr int A_VECS = BM * VPR / kThreads;
-  constexpr int B_VECS8 = BN * (BK / 8) / kThreads;  // B always 16-byte vectors
-  static_assert(A_VECS >= 1 && B_VECS8 >= 1, "tile too small");
-  typedef typename std::conditional<VEC == 8, uint4, uint2>::type AV;
-  AV ra[A_VECS];
-  uint4 rb[B_VECS8];
+  uint4 ra[A_V], rb[B_V];
 
-  ConvRow crow[A_VECS];
-  if (AM == kConv) {
+  // Per-row conv state (conv modes): pixel base offset, top-left input coords.
+  int64_t rbase[AM == kDenseK ? 1 : A_V];
+  int rhi[AM == kDenseK ? 1 : A_V], rwi[AM == kDenseK ? 1 : A_V];
+  ConvRow crow[AM == kConv ? A_V : 1];
+  if (AM == kConvTap || AM == kConvStem) {
 #pragma unroll
-    for (int i = 0; i < A_VECS; ++i) crow[i] = conv_row(p, m0 + (tid + kThreads * i) / VPR);
+    for (int i = 0; i < A_V; ++i) {
+      const ConvRow r = conv_row(p, m0 + trow + RSTEP * i);
+      rbase[i] = r.base;
+      rhi[i] = r.valid ? r.hi0 : -(1 << 28);  // invalid rows fail every bounds check
+      rwi[i] = r.wi0;
+    }
+  } else if (AM == kConv) {
+#pragma unroll
+    for (int i = 0; i < A_V; ++i) crow[i] = conv_row(p, m0 + trow + RSTEP * i);
   }
+  // kConvTap: the next tile's filter tap and channel base.
+  int t_kh = 0, t_kw = 0, t_c0 = 0;
 
   auto load_a = [&](int64_t k0) {
+    if (AM == kDenseK) {
+      const int64_t k = k0 + kc;
 #pragma unroll
-    for (int i = 0; i < A_VECS; ++i) {
-      int e = tid + kThreads * i;
-      int mr = e / VPR, kc = (e % VPR) * VEC;
-      int64_t m = m0 + mr, k = k0 + kc;
-      AV v = {};
-      if (AM == kDenseK) {
-        if (m < p.m && k < p.k) v = *reinterpret_cast<const AV*>(A + m * p.lda + k);
-      } else {
-        int64_t off = conv_k_offset(p, crow[i], k);
-        if (off >= 0) v = *reinterpret_cast<const AV*>(A + off);
+      for (int i = 0; i < A_V; ++i) {
+        const int64_t m = m0 + trow + RSTEP * i;
+        uint4 v = {0u, 0u, 0u, 0u};
+        if (m < p.m && k < p.k) v = *reinterpret_cast<const uint4*>(A + (m * p.lda + k) * ES);
+        ra[i] = v;
       }
-      ra[i] = v;
+    } else if (AM == kConvTap) {
+      const int dh = t_kh * p.dh, dw = t_kw * p.dw;
+      const int64_t tap_off = (static_cast<int64_t>(dh) * p.cw + dw) * p.c_stride + t_c0 + kc;
+#pragma unroll
+      for (int i = 0; i < A_V; ++i) {
+        const int hi = rhi[i] + dh, wi = rwi[i] + dw;
+        uint4 v = {0u, 0u, 0u, 0u};
+        if (static_cast<unsigned>(hi) < static_cast<unsigned>(p.ch) &&
+            static_cast<unsigned>(wi) < static_cast<unsigned>(p.cw))
+          v = *reinterpret_cast<const uint4*>(
+              A + (rbase[i] + (static_cast<int64_t>(rhi[i]) * p.cw + rwi[i]) * p.c_stride + tap_off) * ES);
+        ra[i] = v;
+      }
+    } else if (AM == kConvStem) {
+      // K order (kh, kw_pack = 8, c = 4): vector kc covers taps kw0, kw0 + 1.
+      const int64_t k = k0 + kc;
+      const int tap = static_cast<int>(k >> 2);
+      const int khi = tap >> 3, kw0 = tap & 7;
+#pragma unroll
+      for (int i = 0; i < A_V; ++i) {
+        uint2 lo = {0u, 0u}, hi2 = {0u, 0u};
+        if (k < p.k) {
+          const int hi = rhi[i] + khi * p.dh;
+          if (static_cast<unsigned>(hi) < static_cast<unsigned>(p.ch)) {
+            const int wa = rwi[i] + kw0 * p.dw, wb = wa + p.dw;
+            const int64_t rowoff = rbase[i] + static_cast<int64_t>(hi) * p.cw * 4;
+            if (kw0 < p.kw && static_cast<unsigned>(wa) < static_cast<unsigned>(p.cw))
+              lo = *reinterpret_cast<const uint2*>(A + (rowoff + static_cast<int64_t>(wa) * 4) * ES);
+            if (kw0 + 1 < p.kw && static_cast<unsigned>(wb) < static_cast<unsigned>(p.cw))
+              hi2 = *reinterpret_cast<const uint2*>(A + (rowoff + static_cast<int64_t>(wb) * 4) * ES);
+          }
+        }
+        ra[i] = uint4{lo.x, lo.y, hi2.x, hi2.y};
+      }
+    } else {
+      const int64_t k = k0 + kc;
+#pragma unroll
+      for (int i = 0; i < A_V; ++i) {
+        const int64_t off = conv_k_offset(p, crow[i], k);
+        uint4 v = {0u, 0u, 0u, 0u};
+        if (off >= 0) v = *reinterpret_cast<const uint4*>(A + off * ES);
+        ra[i] = v;
+      }
+    }
+  };
+  auto advance_tap = [&]() {
+    if (AM == kConvTap) {
+      t_c0 += BK;
+      if (t_c0 >= p.c_pack) {
+        t_c0 = 0;
+        if (++t_kw >= p.kw) {
+          t_kw = 0;
+          ++t_kh;
+        }
+      }
     }
   };
   auto load_b = [&](int64_t k0) {
+    const int64_t k = k0 + kc;
 #pragma unroll
-    for (int i = 0; i < B_VECS8; ++i) {
-      int e = tid + kThreads * i;
-      int nr = e / (BK / 8), kc = (e % (BK / 8)) * 8;
-      int64_t n = n0 + nr, k = k0 + kc;
+    for (int i = 0; i < B_V; ++i) {
+      const int64_t n = n0 + trow + RSTEP * i;
       uint4 v = {0u, 0u, 0u, 0u};
-      if (n < p.n && k < p.k) v = *reinterpret_cast<const uint4*>(B + n * p.ldb + k);
+      if (n < p.n && k < p.k) v = *reinterpret_cast<const uint4*>(B + (n * p.ldb + k) * ES);
       rb[i] = v;
     }
   };
+  // Byte offset of 16-byte chunk c of row r (XOR swizzle).
+  auto swz = [](int r, int c) { return (c ^ (r & 7)) << 4; };
   auto store_tiles = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < A_VECS; ++i) {
-      int e = tid + kThreads * i;
-      int mr = e / VPR, kc = (e % VPR) * VEC;
-      *reinterpret_cast<AV*>(&As[buf][mr][kc]) = ra[i];
+    for (int i = 0; i < A_V; ++i) {
+      const int r = trow + RSTEP * i;
+      *reinterpret_cast<uint4*>(&As[buf][r][swz(r, kchunk)]) = ra[i];
     }
 #pragma unroll
-    for (int i = 0; i < B_VECS8; ++i) {
-      int e = tid + kThreads * i;
-      int nr = e / (BK / 8), kc = (e % (BK / 8)) * 8;
-      *reinterpret_cast<uint4*>(&Bs[buf][nr][kc]) = rb[i];
+    for (int i = 0; i < B_V; ++i) {
+      const int r = trow + RSTEP * i;
+      *reinterpret_cast<uint4*>(&Bs[buf][r][swz(r, kchunk)]) = rb[i];
     }
   };
 
-  f32x4 acc[TM][TN];
+  acc_t acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
 
   const int64_t ktiles = ceil_div(p.k, BK);
   load_a(0);
   load_b(0);
+  advance_tap();
   store_tiles(0);
   __syncthreads();
-  const int lrow = lane & 15, lk = (lane >> 4) * 8;
+  const int lrow = lane & 15, lchunk = lane >> 4;
   for (int64_t kt = 0; kt < ktiles; ++kt) {
     const int cur = kt & 1;
     if (kt + 1 < ktiles) {
       load_a((kt + 1) * BK);
       load_b((kt + 1) * BK);
+      advance_tap();
     }
-    vec8 av[TM], bv[TN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-      av[i] = *reinterpret_cast<const vec8*>(&As[cur][wm * (BM / WM) + i * 16 + lrow][lk]);
+    for (int ks = 0; ks < 8; ks += 4) {  // two MFMA K steps of 64 bytes
+      vec av[TM], bv[TN];
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-      bv[j] = *reinterpret_cast<const vec8*>(&Bs[cur][wn * (BN / WN) + j * 16 + lrow][lk]);
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm * WTM + i * 16 + lrow;
+        av[i] = *reinterpret_cast<const vec*>(&As[cur][r][swz(r, ks + lchunk)]);
+      }
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TN; ++j) {
+        const int r = wn * WTN + j * 16 + lrow;
+        bv[j] = *reinterpret_cast<const vec*>(&Bs[cur][r][swz(r, ks + lchunk)]);
+      }
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = SWAP ? Mfma16<T>::mma(bv[j], av[i], acc[i][j]) : Mfma16<T>::mma(av[i], bv[j], acc[i][j]);
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = Mma::mma(av[i], bv[j], acc[i][j]);
+    }
     if (kt + 1 < ktiles) {
       store_tiles(cur ^ 1);
       __syncthreads();
     }
   }
 
-  // Epilogue: a lane holds (m = 4*(lane/16)+r, n = lane%16) of each tile
-  // (with SWAP the tile is transposed); stage 16-row strips through LDS.
+  // Epilogue: a lane holds (m = 4*(lane/16)+r, n = lane%16) of each 16x16
+  // tile.  The whole wave tile is staged in LDS (accumulators only ever
+  // indexed by unrolled constants), then stored 16 rows at a time with 8
+  // columns per lane.
   TO* outp = static_cast<TO*>(p.out) + bz * p.stride_out;
   const TO* resp = p.epi.residual ? static_cast<const TO*>(p.epi.residual) + bz * p.stride_res : nullptr;
   const int64_t bias_off = bz * p.stride_bias;
+  const bool vec_ok = !p.out_nchw && (p.ldo % 8 == 0) && (p.stride_out % 8 == 0) && (p.stride_res % 8 == 0) &&
+                      ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(p.epi.residual) & 15) == 0);
   __syncthreads();
-  float* stage = reinterpret_cast<float*>(smem) + wave * 16 * (WTN + 4);
+  float* stage = reinterpret_cast<float*>(smem) + wave * WTM * (WTN + 4);
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        if (SWAP) stage[lrow * (WTN + 4) + j * 16 + (lane >> 4) * 4 + r] = acc[i][j][r];
-        else stage[((lane >> 4) * 4 + r) * (WTN + 4) + j * 16 + lrow] = acc[i][j][r];
+        float* dst = &stage[(i * 16 + (lane >> 4) * 4 + r) * (WTN + 4) + j * 16 + lrow];
+        if constexpr (Mma::kInt) *reinterpret_cast<int*>(dst) = acc[i][j][r];
+        else *dst = acc[i][j][r];
       }
-    wave_sync_lds();
-    store_strip<TO, WTN>(p, stage, lane, m0 + wm * (BM / WM) + i * 16, n0 + wn * WTN, outp, resp, bias_off);
-    wave_sync_lds();
-  }
-}
-
-// =====================================================================
-// int8 kernel: v_mfma_i32_16x16x64_i8 with exact int32 accumulation
-// (QLinearMatMul core).  A [m][k] and B packed [n][k], both K-contiguous;
-// LDS rows of 64 bytes + 16-byte skew so a lane's 16-byte operand is one
-// ds_read_b128.
-// =====================================================================
-typedef __attribute__((ext_vector_type(4))) int i32x4;
-
-struct QProblem {
-  const int8_t* a;
-  const int8_t* b;
-  void* out;
-  int64_t m, n, k, lda, ldb, ldo;
-  float a_scale, y_scale;
-  const float* b_scale;
-  int y_zero, mode, out_dtype;
-  int tiles_m, tiles_n;
-  c3h_epilogue epi;
-};
-
-template <int BM, int BN, int WM, int WN>
-__global__ void __launch_bounds__(kThreads) qgemm_kernel(QProblem p) {
-  constexpr int BK = 64;
-  constexpr int SK = BK + 16;
-  constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
-  __shared__ __attribute__((aligned(16))) int8_t As[2][BM][SK];
-  __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN][SK];
-
-  const int total = p.tiles_m * p.tiles_n;
-  int tile = blockIdx.x;
-  if ((total & 7) == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
-  const int tm = tile / p.tiles_n, tn = tile - (tile / p.tiles_n) * p.tiles_n;
-  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int wm = wave / WN, wn = wave % WN;
-  constexpr int A_V = BM * (BK / 16) / kThreads, B_V = BN * (BK / 16) / kThreads;
-  uint4 ra[A_V], rb[B_V];
-  auto load = [&](int64_t k0) {
-#pragma unroll
-    for (int i = 0; i < A_V; ++i) {
-      int e = tid + kThreads * i, r = e / (BK / 16), c = (e % (BK / 16)) * 16;
-      int64_t m = m0 + r, k = k0 + c;
-      uint4 v = {0u, 0u, 0u, 0u};
-      if (m < p.m && k < p.k) v = *reinterpret_cast<const uint4*>(p.a + m * p.lda + k);
-      ra[i] = v;
-    }
-#pragma unroll
-    for (int i = 0; i < B_V; ++i) {
-      int e = tid + kThreads * i, r = e / (BK / 16), c = (e % (BK / 16)) * 16;
-      int64_t n = n0 + r, k = k0 + c;
-      uint4 v = {0u, 0u, 0u, 0u};
-      if (n < p.n && k < p.k) v = *reinterpret_cast<const uint4*>(p.b + n * p.ldb + k);
-      rb[i] = v;
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < A_V; ++i) {
-      int e = tid + kThreads * i, r = e / (BK / 16), c = (e % (BK / 16)) * 16;
-      *reinterpret_cast<uint4*>(&As[buf][r][c]) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_V; ++i) {
-      int e = tid + kThreads * i, r = e / (BK / 16), c = (e % (BK / 16)) * 16;
-      *reinterpret_cast<uint4*>(&Bs[buf][r][c]) = rb[i];
-    }
-  };
-  i32x4 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
-  const int64_t ktiles = ceil_div(p.k, BK);
-  load(0);
-  store(0);
-  __syncthreads();
-  const int lrow = lane & 15, lk = (lane >> 4) * 16;
-  for (int64_t kt = 0; kt < ktiles; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < ktiles) load((kt + 1) * BK);
-    i32x4 av[TM], bv[TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) av[i] = *reinterpret_cast<const i32x4*>(&As[cur][wm * (BM / WM) + i * 16 + lrow][lk]);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) bv[j] = *reinterpret_cast<const i32x4*>(&Bs[cur][wn * (BN / WN) + j * 16 + lrow][lk]);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
-    if (kt + 1 < ktiles) {
-      store(cur ^ 1);
-      __syncthreads();
-    }
-  }
-#pragma unroll
+  wave_sync_lds();
+#pragma nounroll
   for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t n = n0 + wn * (BN / WN) + j * 16 + lrow;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t m = m0 + wm * (BM / WM) + i * 16 + (lane >> 4) * 4 + r;
-        if (m >= p.m || n >= p.n) continue;
-        const int64_t o = m * p.ldo + n;
-        const int32_t iacc = acc[i][j][r];
-        if (p.mode == 0) {
-          static_cast<int32_t*>(p.out)[o] = iacc;
-        } else if (p.mode == 1) {
-          const float mult = (p.a_scale * p.b_scale[n]) / p.y_scale;
-          float y = rintf(static_cast<float>(iacc) * mult) + static_cast<float>(p.y_zero);
-          y = fminf(fmaxf(y, -128.0f), 127.0f);
-          static_cast<int8_t*>(p.out)[o] = static_cast<int8_t>(y);
-        } else {
-          float deq;
-          if (p.mode == 3) {
-            // QLinearMatMul -> DequantizeLinear: the int8 y of mode 1, then (y - zy) * y_scale.
-            const float mult = (p.a_scale * p.b_scale[n]) / p.y_scale;
-            float y = rintf(static_cast<float>(iacc) * mult) + static_cast<float>(p.y_zero);
-            y = fminf(fmaxf(y, -128.0f), 127.0f);
-            deq = (y - static_cast<float>(p.y_zero)) * p.y_scale;
-          } else {
-            deq = static_cast<float>(iacc) * (p.a_scale * p.b_scale[n]);
-          }
-          float res = 0.0f;
-          if (p.epi.residual) res = load_as_f32(p.epi.residual, p.out_dtype, o);
-          store_from_f32(p.out, p.out_dtype, o, apply_epilogue(p.epi, deq, m, n, p.n, res));
-        }
-      }
+    const int64_t mrow0 = m0 + wm * WTM + i * 16, ncol0 = n0 + wn * WTN;
+    const float* strip = stage + i * 16 * (WTN + 4);
+    if constexpr (Mma::kInt) {
+      store_strip_q<TO, WTN>(strip, lane, mrow0, ncol0, outp, resp, vec_ok);
+    } else {
+      if (p.out_nchw) store_strip<TO, WTN>(p, strip, lane, mrow0, ncol0, outp, resp, bias_off);
+      else store_strip_vec<TO, WTN>(strip, lane, mrow0, ncol0, outp, resp, bias_off, vec_ok);
     }
   }
 }
@@ -686,7 +894,7 @@ __global__ void __launch_bounds__(256) gemm_simple_kernel(Problem p) {
   float* outp = static_cast<float*>(p.out) + bz * p.stride_out;
   const int64_t o = m * p.ldo + n;
   const float res = p.epi.residual ? static_cast<const float*>(p.epi.residual)[bz * p.stride_res + o] : 0.0f;
-  outp[o] = apply_epilogue(p.epi, acc, m, n, p.n, res, bz * p.stride_bias);
+  outp[o] = apply_epilogue(kernel_arg<Problem>().epi, acc, m, n, p.n, res, bz * p.stride_bias);
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -713,28 +921,35 @@ int launch_f32(Problem p, int64_t batch, hipStream_t s) {
   return launch_status("gemm_f32");
 }
 
-template <typename T, typename TO, int AM, int VEC>
-int launch_h_shape(Problem p, int64_t batch, hipStream_t s) {
+template <typename Mma, typename TO, int AM>
+int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
   dim3 grid;
+  const int64_t sms = 256;
   if (p.n <= 64) {
     grid_of<256, 64>(p, batch, grid);
-    hipLaunchKernelGGL((gemm_h_kernel<T, TO, 256, 64, 4, 1, AM, VEC, false>), grid, dim3(kThreads), 0, s, p);
-  } else if (p.m <= 4096 || p.n <= 128) {
+    hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 256, 64, 4, 1, AM>), grid, dim3(kThreads), 0, s, p);
+  } else if (p.n <= 128 || ceil_div(p.m, 128) * ceil_div(p.n, 256) * batch < 2 * sms) {
     grid_of<128, 128>(p, batch, grid);
-    hipLaunchKernelGGL((gemm_h_kernel<T, TO, 128, 128, 2, 2, AM, VEC, false>), grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 128, 128, 2, 2, AM>), grid, dim3(kThreads), 0, s, p);
   } else {
     grid_of<128, 256>(p, batch, grid);
-    hipLaunchKernelGGL((gemm_h_kernel<T, TO, 128, 256, 2, 2, AM, VEC, false>), grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 128, 256, 2, 2, AM>), grid, dim3(kThreads), 0, s, p);
   }
-  return launch_status("gemm_h");
+  return launch_status(what);
 }
 
 // 16-bit inputs write either the same 16-bit type or fp32.
-template <typename T, int AM, int VEC>
+template <typename Mma, typename T, int AM>
 int launch_h(Problem p, int64_t batch, hipStream_t s, int in_dtype) {
-  if (p.out_dtype == C3H_F32) return launch_h_shape<T, float, AM, VEC>(p, batch, s);
-  if (p.out_dtype == in_dtype) return launch_h_shape<T, T, AM, VEC>(p, batch, s);
+  if (p.out_dtype == C3H_F32) return launch_mfma<Mma, float, AM>(p, batch, s, "gemm_h");
+  if (p.out_dtype == in_dtype) return launch_mfma<Mma, T, AM>(p, batch, s, "gemm_h");
   return fail(C3H_EUNSUPPORTED, "gemm: 16-bit inputs write fp32 or the input dtype, not %d", p.out_dtype);
+}
+
+template <int AM>
+int launch_h_any(Problem p, int64_t batch, hipStream_t s, int in_dtype) {
+  return in_dtype == C3H_BF16 ? launch_h<MmaBF16, bf16_t, AM>(p, batch, s, in_dtype)
+                              : launch_h<MmaF16, f16_t, AM>(p, batch, s, in_dtype);
 }
 
 int check_epilogue(const c3h_epilogue& e) {
@@ -803,8 +1018,7 @@ int c3h_gemm(const c3h_gemm_args* a, void* stream) {
     C3H_REQUIRE(a->k % 8 == 0 && a->lda % 8 == 0 && a->ldb % 8 == 0 && a->stride_a % 8 == 0 && a->stride_b % 8 == 0,
                 "gemm: 16-bit path needs k, lda, ldb multiples of 8");
     C3H_REQUIRE(aligned(a->a, 16) && aligned(a->b, 16), "gemm: 16-bit operands must be 16-byte aligned");
-    return a->in_dtype == C3H_BF16 ? launch_h<bf16_t, kDenseK, 8>(p, a->batch, s, a->in_dtype)
-                                   : launch_h<f16_t, kDenseK, 8>(p, a->batch, s, a->in_dtype);
+    return launch_h_any<kDenseK>(p, a->batch, s, a->in_dtype);
   }
   return fail(C3H_EUNSUPPORTED, "gemm: input dtype %d unsupported", a->in_dtype);
 }
@@ -849,8 +1063,9 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
       p.kw_pack = a->kw;
       p.k = static_cast<int64_t>(a->kh) * a->kw * a->c_pack;
       p.ldb = ceil_div(p.k, 32) * 32;  // weights padded to whole 32-wide K tiles
-      return a->in_dtype == C3H_BF16 ? launch_h<bf16_t, kConv, 8>(p, 1, s, a->in_dtype)
-                                     : launch_h<f16_t, kConv, 8>(p, 1, s, a->in_dtype);
+      // A 64-wide K tile stays inside one filter tap when c_pack % 64 == 0.
+      if (a->c_pack % 64 == 0) return launch_h_any<kConvTap>(p, 1, s, a->in_dtype);
+      return launch_h_any<kConv>(p, 1, s, a->in_dtype);
     }
     // Narrow-channel stem: c_pack = c_stride = 4, kw padded to a multiple of
     // 2 so each 32-wide K tile covers whole pixels (8-byte vectors).
@@ -858,8 +1073,7 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
     p.kw_pack = static_cast<int>(ceil_div(a->kw, 8) * 8);
     p.k = static_cast<int64_t>(a->kh) * p.kw_pack * 4;
     p.ldb = p.k;
-    return a->in_dtype == C3H_BF16 ? launch_h<bf16_t, kConv, 4>(p, 1, s, a->in_dtype)
-                                   : launch_h<f16_t, kConv, 4>(p, 1, s, a->in_dtype);
+    return launch_h_any<kConvStem>(p, 1, s, a->in_dtype);
   }
   return fail(C3H_EUNSUPPORTED, "conv2d: input dtype %d unsupported", a->in_dtype);
 }
@@ -878,24 +1092,20 @@ int c3h_qgemm(const c3h_qgemm_args* a, void* stream) {
   int rc = check_epilogue(a->epi);
   if (rc) return rc;
   if (a->m == 0 || a->n == 0) return C3H_OK;
-  QProblem p;
+  Problem p;
   memset(&p, 0, sizeof(p));
   p.a = a->a; p.b = a->b; p.out = a->out;
   p.m = a->m; p.n = a->n; p.k = a->k; p.lda = a->lda; p.ldb = a->ldb; p.ldo = a->ldo;
   p.a_scale = a->a_scale; p.y_scale = a->y_scale; p.b_scale = a->b_scale;
-  p.y_zero = a->y_zero; p.mode = a->mode; p.out_dtype = a->out_dtype;
+  p.y_zero = a->y_zero; p.qmode = a->mode; p.out_dtype = a->out_dtype;
   p.epi = a->epi;
+  p.ho = 1; p.wo = 1;
   hipStream_t s = as_stream(stream);
-  if (p.n <= 64 || p.m <= 4096) {
-    p.tiles_m = static_cast<int>(ceil_div(p.m, 128));
-    p.tiles_n = static_cast<int>(ceil_div(p.n, 64));
-    hipLaunchKernelGGL((qgemm_kernel<128, 64, 2, 2>), dim3(p.tiles_m * p.tiles_n), dim3(kThreads), 0, s, p);
-  } else {
-    p.tiles_m = static_cast<int>(ceil_div(p.m, 128));
-    p.tiles_n = static_cast<int>(ceil_div(p.n, 128));
-    hipLaunchKernelGGL((qgemm_kernel<128, 128, 2, 2>), dim3(p.tiles_m * p.tiles_n), dim3(kThreads), 0, s, p);
-  }
-  return launch_status("qgemm");
+  if (a->mode == 0) return launch_mfma<MmaI8, int32_t, kDenseK>(p, 1, s, "qgemm");
+  if (a->mode == 1) return launch_mfma<MmaI8, int8_t, kDenseK>(p, 1, s, "qgemm");
+  if (a->out_dtype == C3H_F32) return launch_mfma<MmaI8, float, kDenseK>(p, 1, s, "qgemm");
+  if (a->out_dtype == C3H_BF16) return launch_mfma<MmaI8, bf16_t, kDenseK>(p, 1, s, "qgemm");
+  return launch_mfma<MmaI8, f16_t, kDenseK>(p, 1, s, "qgemm");
 }
 
 }  // extern "C"

@@ -43,7 +43,8 @@ def _from16(arr, kind):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "fp16"])
-@pytest.mark.parametrize("m,n,k", [(16, 16, 32), (64, 64, 64), (300, 200, 96), (1000, 64, 576), (130, 600, 520)])
+@pytest.mark.parametrize("m,n,k", [(16, 16, 32), (64, 64, 64), (300, 200, 96), (1000, 64, 576), (130, 600, 520),
+                                   (77, 90, 136), (520, 1030, 1024)])
 def test_gemm_16bit_matches_float64(gpu, kind, m, n, k):
     """16x16x32 MFMA operand layout + tiling: out = A @ B^T + bias, relu, fp32 out."""
     from hackathon_amd import _lib
@@ -98,7 +99,8 @@ def _conv_case(rng, n, c, h, w, o, kh, kw, s, p):
 @pytest.mark.parametrize("kind", ["fp32", "bf16", "fp16"])
 @pytest.mark.parametrize("case", [(2, 64, 14, 14, 64, 3, 3, 1, 1), (2, 64, 15, 15, 128, 3, 3, 2, 1),
                                   (2, 128, 8, 8, 256, 1, 1, 2, 0), (1, 3, 37, 37, 64, 7, 7, 2, 3),
-                                  (3, 3, 16, 16, 64, 3, 3, 1, 1)])
+                                  (3, 3, 16, 16, 64, 3, 3, 1, 1), (2, 40, 9, 9, 70, 3, 3, 1, 1),
+                                  (1, 64, 12, 12, 64, 3, 3, 1, 2)])
 def test_conv_nhwc_implicit_gemm(gpu, kind, case):
     """Channels-last implicit GEMM (+bias, +residual, relu) vs a float64 conv of the rounded operands."""
     from hackathon_amd import _lib
@@ -247,3 +249,45 @@ def test_program_run_and_graph_replay(gpu):
         s.synchronize()
         np.testing.assert_allclose(z.get(), expect, rtol=1e-6)
     _lib.check(_lib.lib().c3h_graph_destroy(g), "graph_destroy")
+
+
+@pytest.mark.parametrize("mode,n,out_kind", [(2, 200, "fp32"), (3, 200, "fp32"), (3, 200, "bf16"), (3, 70, "fp32"),
+                                              (2, 96, "fp16")])
+def test_qgemm_fused_dequant_epilogue_bit_exact(gpu, mode, n, out_kind):
+    """Modes 2/3 (dequantize / QLinearMatMul->DequantizeLinear) + bias + residual + relu, float32 order."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    rng = np.random.default_rng(mode * 1000 + n)
+    m, k = 300, 256
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    bt = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    sa, sy = np.float32(0.02), np.float32(0.37)
+    sb = (rng.random(n) * 0.01 + 0.001).astype(np.float32)
+    bias = rng.standard_normal(n, dtype=np.float32)
+    res32 = rng.standard_normal((m, n), dtype=np.float32)
+    acc = (a.astype(np.int64) @ bt.T.astype(np.int64)).astype(np.int32)
+    if mode == 3:
+        v = R.requantize(acc, sa, sb, sy, 0).astype(np.float32) * sy
+    else:
+        v = acc.astype(np.float32) * (sa * sb)
+    code, sdt = {"fp32": (_lib.F32, np.float32), "bf16": (_lib.BF16, BF16), "fp16": (_lib.F16, np.float16)}[out_kind]
+    if out_kind == "fp32":
+        res_dev, res_used = _dev(res32), res32
+    else:
+        bits, res_used = _bits(res32, out_kind)
+        res_dev = _dev(bits)
+    want = np.maximum((v + bias) + res_used, 0).astype(np.float32)
+    out = DeviceArray.empty((m, n), sdt)
+    g = _lib.QGemmArgs()
+    ad, bd, sbd, biasd = _dev(a), _dev(bt), _dev(sb), _dev(bias)
+    g.a, g.b, g.out, g.m, g.n, g.k, g.lda, g.ldb, g.ldo = ad.ptr, bd.ptr, out.ptr, m, n, k, k, k, n
+    g.a_scale, g.y_scale, g.b_scale, g.mode, g.out_dtype = sa, sy, sbd.ptr, mode, code
+    g.epi = E.epilogue(bias=biasd, bias_mode=2, act=1, residual=res_dev)
+    _lib.launch(g, None)
+    got = out.get()
+    if out_kind == "fp32":
+        np.testing.assert_array_equal(got, want)
+    else:
+        np.testing.assert_array_equal(_from16(got, out_kind), G.round_to(want, out_kind))

@@ -387,7 +387,7 @@ def _argmax_both(x, params, rows):
     synchronize()
     ref = [np.zeros(rows, np.int64)]
     R.lookup("argmax")([x], ref, dict(params), None)
-    return out[0].get().view(np.int64)[:rows], ref[0].reshape(-1)
+    return out[0].get().view(np.int64).reshape(-1)[:rows], ref[0].reshape(-1)
 
 
 def test_argmax_ties_and_nan(gpu):
