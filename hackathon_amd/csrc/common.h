@@ -140,6 +140,25 @@ struct Elem16 {
 template <> struct Elem<bf16_t> : Elem16<bf16_t, bf16_bits_to_f32, f32_to_bf16_bits> {};
 template <> struct Elem<f16_t> : Elem16<f16_t, f16_bits_to_f32, f32_to_f16_bits> {};
 
+// 16 bytes of T <-> fp32 values (8 for 16-bit types, 4 for fp32).
+template <typename T>
+__device__ __forceinline__ void load_vec16(const T* p, float* v) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 q = *reinterpret_cast<const float4*>(p);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  } else {
+    Elem<T>::load8(p, v);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void store_vec16(T* p, const float* v) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<float4*>(p) = float4{v[0], v[1], v[2], v[3]};
+  } else {
+    Elem<T>::store8(p, v);
+  }
+}
+
 // Abramowitz & Stegun 7.1.26 rational approximation of erf (max abs error
 // about 1.5e-7), the formula the reference's unfused Erf uses.
 __device__ __forceinline__ float erf_as(float x) {

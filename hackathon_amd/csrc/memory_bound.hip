@@ -457,6 +457,35 @@ __global__ void __launch_bounds__(kBlock) nchw_to_nhwc_small_kernel(c3h_layout_a
   }
 }
 
+// NCHW fp32 -> NHWC with c_pad == 4 (network inputs: 3 channels padded to 4),
+// four consecutive pixels per thread: one float4 load per channel plane and
+// 4 pixels x 4 channels of output written as whole 16-byte vectors.
+template <typename TO>
+__global__ void __launch_bounds__(kBlock) nchw_to_nhwc_c4_kernel(c3h_layout_args a) {
+  const int64_t hw = static_cast<int64_t>(a.h) * a.w;
+  const int64_t quads = static_cast<int64_t>(a.n) * (hw / 4);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const float* in = static_cast<const float*>(a.in);
+  for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < quads; q += stride) {
+    const int64_t ni = q / (hw / 4), s = (q - ni * (hw / 4)) * 4;
+    float px[4][4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float4 v = float4{0.f, 0.f, 0.f, 0.f};
+      if (c < a.c) v = *reinterpret_cast<const float4*>(in + (ni * a.c + c) * hw + s);
+      px[0][c] = v.x; px[1][c] = v.y; px[2][c] = v.z; px[3][c] = v.w;
+    }
+    TO* out = static_cast<TO*>(a.out) + (ni * hw + s) * 4;
+#pragma unroll
+    for (int p = 0; p < 4; p += 16 / (4 * static_cast<int>(sizeof(TO)))) {
+      float v[16 / sizeof(TO)];
+#pragma unroll
+      for (int e = 0; e < static_cast<int>(16 / sizeof(TO)); ++e) v[e] = px[p + e / 4][e % 4];
+      store_vec16(out + p * 4, v);
+    }
+  }
+}
+
 // Tiled path: per image, [C][HW] <-> [HW][Cpad] through a 32x33 LDS tile.
 __global__ void __launch_bounds__(256) layout_tile_kernel(c3h_layout_args a) {
   __shared__ float tile[32][33];
@@ -575,6 +604,42 @@ bool ew_is_flat(const c3h_ew_args& a) {
     if (!(all_zero || dense)) return false;
   }
   return true;
+}
+
+// Channels-last max pool, 16 bytes of channels per thread: each of the kh*kw
+// taps is one 16-byte load, the window max is taken in fp32 with the same
+// fmaxf / -inf semantics as maxpool_kernel (exact for 16-bit inputs).
+template <typename T>
+__global__ void __launch_bounds__(kBlock) maxpool_nhwc_vec_kernel(c3h_pool_args a) {
+  constexpr int V = 16 / sizeof(T);
+  const int groups = a.c / V;
+  const int64_t total = static_cast<int64_t>(a.n) * a.ho * a.wo * groups;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
+    const int g = static_cast<int>(t % groups);
+    const int64_t pix = t / groups;
+    const int wo_i = static_cast<int>(pix % a.wo);
+    const int ho_i = static_cast<int>((pix / a.wo) % a.ho);
+    const int64_t ni = pix / (static_cast<int64_t>(a.wo) * a.ho);
+    float m[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) m[v] = -INFINITY;
+    for (int i = 0; i < a.kh; ++i) {
+      const int hi = ho_i * a.sh - a.pad_top + i * a.dh;
+      if (hi < 0 || hi >= a.h) continue;
+      for (int j = 0; j < a.kw; ++j) {
+        const int wi = wo_i * a.sw - a.pad_left + j * a.dw;
+        if (wi < 0 || wi >= a.w) continue;
+        const T* src = static_cast<const T*>(a.x) + ((ni * a.h + hi) * a.w + wi) * a.c_stride + g * V;
+        float x[V];
+        load_vec16(src, x);
+#pragma unroll
+        for (int v = 0; v < V; ++v) m[v] = fmaxf(m[v], x[v]);
+      }
+    }
+    T* dst = static_cast<T*>(a.out) + ((ni * a.ho + ho_i) * a.wo + wo_i) * a.c_stride + g * V;
+    store_vec16(dst, m);
+  }
 }
 
 }  // namespace
@@ -783,6 +848,18 @@ int c3h_layout(const c3h_layout_args* a, void* stream) {
   C3H_REQUIRE(a->direction == 0 || a->direction == 1, "layout: bad direction");
   if (a->n == 0) return C3H_OK;
   int64_t hw = static_cast<int64_t>(a->h) * a->w;
+  if (a->direction == 0 && a->c_pad == 4 && a->in_dtype == C3H_F32 && hw % 4 == 0 &&
+      (reinterpret_cast<uintptr_t>(a->in) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 15) == 0 &&
+      (a->out_dtype == C3H_F32 || a->out_dtype == C3H_BF16 || a->out_dtype == C3H_F16)) {
+    const dim3 grid(grid_for(a->n * hw / 4));
+    if (a->out_dtype == C3H_F32)
+      hipLaunchKernelGGL(nchw_to_nhwc_c4_kernel<float>, grid, dim3(kBlock), 0, as_stream(stream), *a);
+    else if (a->out_dtype == C3H_BF16)
+      hipLaunchKernelGGL(nchw_to_nhwc_c4_kernel<bf16_t>, grid, dim3(kBlock), 0, as_stream(stream), *a);
+    else
+      hipLaunchKernelGGL(nchw_to_nhwc_c4_kernel<f16_t>, grid, dim3(kBlock), 0, as_stream(stream), *a);
+    return launch_status("layout_c4");
+  }
   if (a->direction == 0 && a->c_pad <= 16) {
     hipLaunchKernelGGL(nchw_to_nhwc_small_kernel, dim3(grid_for(a->n * hw)), dim3(kBlock), 0, as_stream(stream), *a);
     return launch_status("layout_small");
@@ -800,6 +877,20 @@ int c3h_maxpool2d(const c3h_pool_args* a, void* stream) {
   C3H_REQUIRE(a->layout == 0 || (a->layout == 1 && a->c_stride >= a->c), "maxpool: bad layout");
   int64_t total = static_cast<int64_t>(a->n) * a->c * a->ho * a->wo;
   if (total == 0) return C3H_OK;
+  const int es = dtype_size(a->dtype);
+  const bool vec = a->layout == 1 && (a->dtype == C3H_F32 || a->dtype == C3H_BF16 || a->dtype == C3H_F16) &&
+                   es > 0 && (a->c * es) % 16 == 0 && (a->c_stride * es) % 16 == 0 &&
+                   (reinterpret_cast<uintptr_t>(a->x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 15) == 0;
+  if (vec) {
+    const int64_t work = total * es / 16;
+    if (a->dtype == C3H_F32)
+      hipLaunchKernelGGL(maxpool_nhwc_vec_kernel<float>, dim3(grid_for(work)), dim3(kBlock), 0, as_stream(stream), *a);
+    else if (a->dtype == C3H_BF16)
+      hipLaunchKernelGGL(maxpool_nhwc_vec_kernel<bf16_t>, dim3(grid_for(work)), dim3(kBlock), 0, as_stream(stream), *a);
+    else
+      hipLaunchKernelGGL(maxpool_nhwc_vec_kernel<f16_t>, dim3(grid_for(work)), dim3(kBlock), 0, as_stream(stream), *a);
+    return launch_status("maxpool_nhwc_vec");
+  }
   hipLaunchKernelGGL(maxpool_kernel, dim3(grid_for(total)), dim3(kBlock), 0, as_stream(stream), *a);
   return launch_status("maxpool");
 }

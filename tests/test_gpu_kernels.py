@@ -187,13 +187,16 @@ def test_flash_attention(gpu, kind, mask_kind, b, h, s):
     np.testing.assert_allclose(got, ref, rtol=tol, atol=tol)
 
 
-@pytest.mark.parametrize("c,c_pad,kind", [(3, 4, "bf16"), (64, 64, "fp32"), (40, 48, "fp16"), (3, 8, "fp32")])
-def test_layout_roundtrip(gpu, c, c_pad, kind):
+@pytest.mark.parametrize("c,c_pad,kind,hw", [(3, 4, "bf16", (9, 13)), (64, 64, "fp32", (9, 13)),
+                                             (40, 48, "fp16", (9, 13)), (3, 8, "fp32", (9, 13)),
+                                             (3, 4, "bf16", (8, 12)), (3, 4, "fp32", (6, 6)), (1, 4, "fp16", (4, 5))])
+def test_layout_roundtrip(gpu, c, c_pad, kind, hw):
     from hackathon_amd import _lib
     from hackathon_amd.c35 import engine as E
     from hackathon_amd.device import BF16, DeviceArray
 
-    x = np.random.default_rng(c).standard_normal((2, c, 9, 13)).astype(np.float32)
+    h, w = hw
+    x = np.random.default_rng(c).standard_normal((2, c, h, w)).astype(np.float32)
     sdt = {"fp32": np.float32, "bf16": BF16, "fp16": np.float16}[kind]
     nhwc = E.to_nhwc(_dev(x), c_pad, out_dtype=sdt)
     host = nhwc.get()
@@ -203,7 +206,7 @@ def test_layout_roundtrip(gpu, c, c_pad, kind):
     np.testing.assert_array_equal(val[..., c:], 0)
     back = DeviceArray.empty(x.shape, np.float32)
     a = _lib.LayoutArgs()
-    a.in_, a.out, a.n, a.c, a.h, a.w = nhwc.ptr, back.ptr, 2, c, 9, 13
+    a.in_, a.out, a.n, a.c, a.h, a.w = nhwc.ptr, back.ptr, 2, c, h, w
     a.c_pad, a.direction, a.in_dtype, a.out_dtype = c_pad, 1, nhwc.code, _lib.F32
     _lib.launch(a, None)
     np.testing.assert_array_equal(back.get(), xr)
@@ -291,3 +294,34 @@ def test_qgemm_fused_dequant_epilogue_bit_exact(gpu, mode, n, out_kind):
         np.testing.assert_array_equal(got, want)
     else:
         np.testing.assert_array_equal(_from16(got, out_kind), G.round_to(want, out_kind))
+
+
+@pytest.mark.parametrize("kind", ["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("c,c_stride,geom", [(64, 64, (3, 2, 1)), (16, 24, (3, 2, 1)), (8, 8, (2, 2, 0)), (6, 6, (3, 1, 1))])
+def test_maxpool_nhwc(gpu, kind, c, c_stride, geom):
+    """Channels-last max pool (vector and scalar paths) vs the oracle on the rounded input."""
+    from hackathon_amd import _lib
+    from hackathon_amd.device import BF16, DeviceArray
+
+    k, st, pd = geom
+    rng = np.random.default_rng(c + k)
+    n, h, w = 2, 15, 14
+    x = rng.standard_normal((n, c, h, w)).astype(np.float32)
+    xr = x if kind == "fp32" else G.round_to(x, kind)
+    attrs = {"kernel_shape": [k, k], "strides": [st, st], "pads": [pd] * 4}
+    ref = R.maxpool2d(xr, attrs)
+    ho, wo = ref.shape[2:]
+    store = np.zeros((n, h, w, c_stride), np.float32)
+    store[..., :c] = x.transpose(0, 2, 3, 1)
+    sdt = {"fp32": np.float32, "bf16": BF16, "fp16": np.float16}[kind]
+    xd = _dev(store) if kind == "fp32" else _dev(_bits(store, kind)[0])
+    out = DeviceArray.empty((n, ho, wo, c_stride), sdt)
+    a = _lib.PoolArgs()
+    a.x, a.out, a.n, a.c, a.h, a.w = xd.ptr, out.ptr, n, c, h, w
+    a.kh, a.kw, a.sh, a.sw, a.pad_top, a.pad_left, a.dh, a.dw = k, k, st, st, pd, pd, 1, 1
+    a.ho, a.wo, a.layout, a.c_stride = ho, wo, 1, c_stride
+    a.dtype = {"fp32": _lib.F32, "bf16": _lib.BF16, "fp16": _lib.F16}[kind]
+    _lib.launch(a, None)
+    got = out.get()
+    got = got if kind == "fp32" else _from16(got, kind)
+    np.testing.assert_array_equal(got[..., :c].transpose(0, 3, 1, 2), ref)
