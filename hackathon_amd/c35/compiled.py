@@ -772,6 +772,7 @@ class CompiledPlan:
             trial.absorbed = st.absorbed + [nxt.id]
             st = trial
         self.consumed.update(st.absorbed)
+        _gelu_program_to_act(st)
         return st
 
     def _fill_epi(self, e, st: "_Epi", r, alpha: float = 1.0, beta: float = 1.0, bias_mode: Optional[int] = None):
@@ -1285,6 +1286,31 @@ class CompiledPlan:
             return a
         self._emit("dequantize", build, [q], [out])
         self.vals[node.outputs[0]] = out
+
+
+def _gelu_program_to_act(st: "_Epi") -> None:
+    """Replace the decomposed-GELU program by the kernels' compiled GELU (act 2).
+
+    The program Div(x, c0) -> Erf -> Add(., c1) -> Mul(x, .) -> Mul(., c2) is
+    what the Div/Erf/Add/Mul/Mul chain of a GELU lowers to; act 2 evaluates
+    the same five operations in the same order (Add and Mul operands may come
+    in either order: they commute exactly), so results are unchanged.
+    """
+    if st.act or len(st.prog) != 5:
+        return
+    (o0, a0, b0, _), (o1, a1, _, _), (o2, a2, b2, _), (o3, a3, b3, _), (o4, a4, b4, _) = st.prog
+    if [o0, o1, o2, o3, o4] != [_lib.EW_DIV, _lib.EW_ERF, _lib.EW_ADD, _lib.EW_MUL, _lib.EW_MUL]:
+        return
+    if a0 not in (0, 1) or b0 < 2 or a1 != 1:
+        return
+    if sorted((a2, b2))[0] != 1 or max(a2, b2) < 2:
+        return
+    if sorted((a3, b3)) != [0, 1]:
+        return
+    if sorted((a4, b4))[0] != 1 or max(a4, b4) < 2:
+        return
+    c = [st.imm[b0 - 2], st.imm[max(a2, b2) - 2], st.imm[max(a4, b4) - 2]]
+    st.prog, st.imm, st.act = [], c, 2
 
 
 def _reshape_strides(shape, strides, new_shape) -> Optional[Tuple[int, ...]]:

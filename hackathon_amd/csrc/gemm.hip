@@ -37,6 +37,14 @@ __device__ __forceinline__ const KArg<P>& kernel_arg() {
   return *(const KArg<P>*)(__builtin_amdgcn_kernarg_segment_ptr());
 }
 
+// GELU as the decomposed ONNX chain Div -> Erf -> Add -> Mul -> Mul computes
+// it, operation for operation: ((x * (erf(x / c0) + c1)) * c2) with the
+// chain's constants (c0 = sqrt(2), c1 = 1, c2 = 0.5 in practice).
+__device__ __forceinline__ float gelu_erf(float x, float c0, float c1, float c2) {
+  const float t = erff(x / c0) + c1;
+  return (x * t) * c2;
+}
+
 // ---------------------------------------------------------------- epilogue
 // `e` is read straight from the kernel-argument segment (uniform scalar
 // loads); `bias_off` selects the batch's bias slice.
@@ -53,6 +61,7 @@ __device__ __forceinline__ float apply_epilogue(const KArg<c3h_epilogue>& e, flo
   }
   v += res;
   if (e.act == 1) v = fmaxf(v, 0.0f);
+  else if (e.act == 2) v = gelu_erf(v, e.imm[0], e.imm[1], e.imm[2]);
   if (e.n_inst > 0) {
     // Linear program: operand 0 = x (the value entering the program),
     // 1 = previous result, 2 + j = imm[j].  No register file, so the
@@ -108,9 +117,14 @@ __device__ __forceinline__ void apply_epilogue8(const KArg<c3h_epilogue>& e, flo
   }
 #pragma unroll
   for (int c = 0; c < 8; ++c) v[c] += res[c];
-  if (e.act == 1) {
+  const int act = e.act;
+  if (act == 1) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) v[c] = fmaxf(v[c], 0.0f);
+  } else if (act == 2) {
+    const float c0 = e.imm[0], c1 = e.imm[1], c2 = e.imm[2];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) v[c] = gelu_erf(v[c], c0, c1, c2);
   }
   const int ni = e.n_inst;
   if (ni > 0) {
@@ -955,7 +969,8 @@ int launch_h_any(Problem p, int64_t batch, hipStream_t s, int in_dtype) {
 int check_epilogue(const c3h_epilogue& e) {
   C3H_REQUIRE(e.bias_mode >= 0 && e.bias_mode <= 4, "epilogue: bad bias_mode %d", e.bias_mode);
   C3H_REQUIRE(e.bias_mode == 0 || e.bias != nullptr, "epilogue: bias_mode %d needs a bias pointer", e.bias_mode);
-  C3H_REQUIRE(e.act == 0 || e.act == 1, "epilogue: bad act %d", e.act);
+  C3H_REQUIRE(e.act >= 0 && e.act <= 2, "epilogue: bad act %d", e.act);
+  C3H_REQUIRE(e.act != 2 || e.n_imm >= 3, "epilogue: act 2 (gelu) reads imm[0..2]");
   C3H_REQUIRE(e.n_imm >= 0 && e.n_imm <= 8, "epilogue: n_imm %d out of range", e.n_imm);
   C3H_REQUIRE(e.n_inst >= 0 && e.n_inst <= C3H_EW_MAX_INST, "epilogue: n_inst %d out of range", e.n_inst);
   for (int i = 0; i < e.n_inst; ++i) {

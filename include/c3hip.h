@@ -380,7 +380,9 @@ int c3h_maxpool2d(const c3h_pool_args* a, void* stream);
  *   v += beta * bias[...]          (bias_mode: 0 none, 1 scalar, 2 per-column
  *                                   [n], 3 per-row [m], 4 full [m, n])
  *   v += residual[...]             (if residual != NULL; same layout as out)
- *   v = act(v)                     (act: 0 none, 1 relu)
+ *   v = act(v)                     (act: 0 none, 1 relu, 2 gelu as the ONNX
+ *                                   chain Div->Erf->Add->Mul->Mul computes it:
+ *                                   (v * (erf(v / imm[0]) + imm[1])) * imm[2])
  *   v = program(v)                 (n_inst > 0: a linear elementwise program;
  *                                   each instruction's operands a/b select
  *                                   0 = x (the value entering the program),

@@ -57,8 +57,9 @@ def test_gemm_16bit_matches_float64(gpu, kind, m, n, k):
     bias = rng.standard_normal(n, dtype=np.float32)
     out = DeviceArray.empty((m, n), np.float32)
     code = _lib.BF16 if kind == "bf16" else _lib.F16
+    bias_d = _dev(bias)  # kept alive until the launch completes: the epilogue holds a raw pointer
     E.gemm(_dev(a), _dev(bt), out, m, n, k, lda=k, ldb=k, ldo=n, trans_b=1, in_dtype=code,
-           epi=E.epilogue(bias=_dev(bias), bias_mode=2, act=1))
+           epi=E.epilogue(bias=bias_d, bias_mode=2, act=1))
     ref = np.maximum(af.astype(np.float64) @ bf.astype(np.float64).T + bias, 0)
     np.testing.assert_allclose(out.get(), ref, rtol=2e-5, atol=2e-4 * math.sqrt(k))
 
@@ -80,13 +81,20 @@ def test_gemm_16bit_out_and_program_epilogue(gpu, kind):
     # program: v/sqrt2 -> erf -> +1 -> x*() -> *0.5  (operands: 0=x, 1=prev, 2+j=imm[j])
     prog = [(_lib.EW_DIV, 0, 2, 0.0), (_lib.EW_ERF, 1, 1, 0.0), (_lib.EW_ADD, 1, 3, 0.0),
             (_lib.EW_MUL, 0, 1, 0.0), (_lib.EW_MUL, 1, 4, 0.0)]
-    E.gemm(_dev(a), _dev(bt), out, m, n, k, lda=k, ldb=k, ldo=n, trans_b=1, in_dtype=code,
-           epi=E.epilogue(residual=_dev(res), program=prog, imm=[math.sqrt(2.0), 1.0, 0.5]))
+    ad, btd, resd = _dev(a), _dev(bt), _dev(res)  # kept alive: the epilogue holds raw pointers
+    E.gemm(ad, btd, out, m, n, k, lda=k, ldb=k, ldo=n, trans_b=1, in_dtype=code,
+           epi=E.epilogue(residual=resd, program=prog, imm=[math.sqrt(2.0), 1.0, 0.5]))
     from scipy.special import erf
     v = af.astype(np.float64) @ bf.astype(np.float64).T + resf
     ref = 0.5 * v * (1 + erf(v / math.sqrt(2.0)))
     got = _from16(out.get(), kind)
     np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-2)
+    # The compiled GELU activation (act 2) performs the same five operations: bit-identical.
+    out2 = DeviceArray.empty((m, n), a.dtype)
+    e2 = E.epilogue(residual=resd, imm=[math.sqrt(2.0), 1.0, 0.5])
+    e2.act = 2
+    E.gemm(ad, btd, out2, m, n, k, lda=k, ldb=k, ldo=n, trans_b=1, in_dtype=code, epi=e2)
+    np.testing.assert_array_equal(out2.get().view(np.uint16), out.get().view(np.uint16))
 
 
 def _conv_case(rng, n, c, h, w, o, kh, kw, s, p):
@@ -132,7 +140,8 @@ def test_conv_nhwc_implicit_gemm(gpu, kind, case):
     a.n, a.c, a.h, a.w_, a.c_stride, a.c_pack, a.o = n, c, h, w, c_pack, c_pack, o
     a.kh, a.kw, a.sh, a.sw, a.pad_top, a.pad_left, a.dh, a.dw, a.ho, a.wo = kh, kw, s, s, p, p, 1, 1, ho, wo
     a.out_layout, a.in_dtype, a.out_dtype = 1, code, code
-    a.epi = E.epilogue(bias=_dev(b), bias_mode=2, act=1, residual=res_dev)
+    b_dev = _dev(b)  # kept alive: the epilogue holds a raw pointer
+    a.epi = E.epilogue(bias=b_dev, bias_mode=2, act=1, residual=res_dev)
     _lib.launch(a, None)
     got = out.get()
     got = got if kind == "fp32" else _from16(got, kind)
