@@ -11,6 +11,7 @@
 // tile k+1 are in flight while the MFMAs of tile k run.  Tile ids are
 // remapped so that consecutive tiles (sharing an A row panel) land on the
 // same XCD and hit its L2.
+#include <stdlib.h>
 #include <type_traits>
 
 #include "common.h"
@@ -146,6 +147,20 @@ __device__ __forceinline__ void apply_epilogue8(const KArg<c3h_epilogue>& e, flo
 }
 
 // ---------------------------------------------------------------- problem
+// Division by an invariant d for n < 2^31 (Granlund & Montgomery 1994, the
+// round-up multiplier with a 33-bit add): l = ceil(log2 d),
+// mul = floor(2^32 (2^l - d) / d) + 1, q = (mulhi(n, mul) + n) >> l.
+struct FastDiv {
+  uint32_t mul, shift;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((uint64_t{1} << l) < d) ++l;
+  const uint64_t mul = ((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1;
+  return FastDiv{static_cast<uint32_t>(mul), l};
+}
+
 // Everything the kernels need, flattened from the gemm/conv args.
 struct Problem {
   const void* a;
@@ -160,6 +175,10 @@ struct Problem {
   int cn, cc, ch, cw, c_stride, c_pack, kh, kw, kw_pack, sh, sw, pt, pl, dh, dw, ho, wo;
   int out_nchw;  // conv: write NCHW instead of NHWC
   int tiles_m, tiles_n;
+  // conv index divisors: ho*wo, wo, c_pack, kw_pack
+  FastDiv fd_hw, fd_wo, fd_cpack, fd_kwpack;
+  // byte extents of A and B (buffer-resource bounds of the pipelined kernel)
+  int64_t a_bytes, b_bytes;
   // int8 GEMM (c3h_qgemm): output mode and quantization parameters
   int qmode, y_zero;
   float a_scale, y_scale;
@@ -191,18 +210,22 @@ struct ConvRow {
   bool valid;
 };
 
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  return (__umulhi(n, f.mul) + n) >> f.shift;
+}
+
+// m < 2^31 (checked on the host): 32-bit index math with invariant divisors.
 __device__ __forceinline__ ConvRow conv_row(const Problem& p, int64_t m) {
   ConvRow r;
   r.valid = m < p.m;
-  int64_t mm = r.valid ? m : 0;
-  const int64_t hw = static_cast<int64_t>(p.ho) * p.wo;
-  int64_t img = mm / hw;
-  int64_t rem = mm - img * hw;
-  int ho = static_cast<int>(rem / p.wo);
-  int wo = static_cast<int>(rem - static_cast<int64_t>(ho) * p.wo);
-  r.base = img * static_cast<int64_t>(p.ch) * p.cw * p.c_stride;
-  r.hi0 = ho * p.sh - p.pt;
-  r.wi0 = wo * p.sw - p.pl;
+  const uint32_t mm = r.valid ? static_cast<uint32_t>(m) : 0u;
+  const uint32_t img = fdiv(mm, p.fd_hw);
+  const uint32_t rem = mm - img * static_cast<uint32_t>(p.ho * p.wo);
+  const uint32_t ho = fdiv(rem, p.fd_wo);
+  const uint32_t wo = rem - ho * static_cast<uint32_t>(p.wo);
+  r.base = static_cast<int64_t>(img) * p.ch * p.cw * p.c_stride;
+  r.hi0 = static_cast<int>(ho) * p.sh - p.pt;
+  r.wi0 = static_cast<int>(wo) * p.sw - p.pl;
   return r;
 }
 
@@ -210,14 +233,14 @@ __device__ __forceinline__ ConvRow conv_row(const Problem& p, int64_t m) {
 // padding.  K order is (kh, kw_pack, c_pack) with c fastest.
 __device__ __forceinline__ int64_t conv_k_offset(const Problem& p, const ConvRow& r, int64_t k) {
   if (!r.valid || k >= p.k) return -1;
-  int kk = static_cast<int>(k);
-  int c0 = kk % p.c_pack;
-  int tap = kk / p.c_pack;
-  int kwi = tap % p.kw_pack;
-  int khi = tap / p.kw_pack;
+  const uint32_t kk = static_cast<uint32_t>(k);
+  const uint32_t tap = fdiv(kk, p.fd_cpack);
+  const int c0 = static_cast<int>(kk - tap * static_cast<uint32_t>(p.c_pack));
+  const uint32_t khi = fdiv(tap, p.fd_kwpack);
+  const int kwi = static_cast<int>(tap - khi * static_cast<uint32_t>(p.kw_pack));
   if (kwi >= p.kw || c0 >= p.cc) return -1;
-  int hi = r.hi0 + khi * p.dh;
-  int wi = r.wi0 + kwi * p.dw;
+  const int hi = r.hi0 + static_cast<int>(khi) * p.dh;
+  const int wi = r.wi0 + kwi * p.dw;
   if (hi < 0 || hi >= p.ch || wi < 0 || wi >= p.cw) return -1;
   return r.base + (static_cast<int64_t>(hi) * p.cw + wi) * p.c_stride + c0;
 }
@@ -889,6 +912,210 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
 }
 
 // =====================================================================
+// Pipelined variant: operand tiles go straight from global memory to LDS
+// (buffer_load_dwordx4 ... lds) through S stages, so S-1 tiles are in flight
+// while one is multiplied, without staging registers.  Lane i of a DMA load
+// writes LDS bytes [16 i, 16 i + 16) from the wave's base (M0); a wave load
+// covers 8 tile rows, and each lane fetches the logical K chunk that the XOR
+// swizzle places at its slot.  Out-of-range lanes (M/N/K tails, conv
+// padding) get a byte offset beyond the buffer's num_records and so write
+// zeros.  One barrier per K tile: after it, every wave has finished the
+// previous tile, whose buffer then receives tile kt + S - 1.
+//
+// Requirements (checked on the host): A and B each below 2^31 bytes; A mode
+// kDenseK or kConvTap.
+// =====================================================================
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+constexpr uint32_t kOobOffset = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, int S>
+__global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
+  constexpr int ES = Mma::ES;
+  constexpr int VE = 16 / ES;
+  constexpr int BK = 128 / ES;
+  constexpr int RB = 128;
+  constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int GROUPS = (BM + BN) / 8;   // 8-row wave loads per stage
+  constexpr int LPW = GROUPS / 4;         // wave loads per wave per stage
+  constexpr int STAGE = (BM + BN) * RB;
+  static_assert(WM * WN == 4 && GROUPS % 4 == 0 && BM % 8 == 0, "shape");
+  static_assert(AM == kDenseK || AM == kConvTap, "dma kernel: dense or tap-uniform conv only");
+  static_assert(S >= 2 && S <= 4 && LPW * (S - 2) < 64, "stages");
+  constexpr int kStageBytes = 4 * WTM * (WTN + 4) * 4;
+  constexpr int kSmem = S * STAGE > kStageBytes ? S * STAGE : kStageBytes;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
+  typedef typename Mma::vec vec;
+  typedef typename Mma::acc_t acc_t;
+
+  int tm, tn;
+  tile_coords_grouped(p, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  // wave index via readfirstlane: provably uniform, so each DMA's LDS base
+  // (M0) is a scalar and needs no per-lane waterfall loop
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wm = wave / WN, wn = wave % WN;
+
+  const __amdgpu_buffer_rsrc_t rs_a = make_rsrc(p.a, p.a_bytes);
+  const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(p.b, p.b_bytes);
+  const int lchunk_ld = (lane & 7) ^ (lane >> 3);  // logical K chunk this lane fetches
+  const int kc = lchunk_ld * VE;
+
+  // Per load slot j (group g = wave + 4 j): row base byte offset (or -1), conv coords.
+  int64_t slot_base[LPW];
+  int slot_hi[LPW], slot_wi[LPW];
+#pragma unroll
+  for (int j = 0; j < LPW; ++j) {
+    const int g = wave + 4 * j;
+    const int r = g * 8 + (lane >> 3);
+    slot_hi[j] = 0;
+    slot_wi[j] = 0;
+    if (g < BM / 8) {
+      const int64_t m = m0 + r;
+      if (AM == kConvTap) {
+        const ConvRow cr = conv_row(p, m);
+        slot_base[j] = cr.valid ? cr.base : -1;
+        slot_hi[j] = cr.hi0;
+        slot_wi[j] = cr.wi0;
+      } else {
+        slot_base[j] = m < p.m ? m * p.lda : -1;
+      }
+    } else {
+      const int64_t n = n0 + (r - BM);
+      slot_base[j] = n < p.n ? n * p.ldb : -1;
+    }
+  }
+  int t_kh = 0, t_kw = 0, t_c0 = 0;  // kConvTap: tap of the next tile to issue
+
+  auto issue = [&](int64_t kt, int buf) {
+    const int64_t k = kt * BK + kc;
+    const bool k_ok = k < p.k;
+    const int dh = t_kh * p.dh, dw = t_kw * p.dw;
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int g = wave + 4 * j;
+      uint32_t voff = kOobOffset;
+      if (g < BM / 8) {
+        if (AM == kConvTap) {
+          const int hi = slot_hi[j] + dh, wi = slot_wi[j] + dw;
+          if (slot_base[j] >= 0 && static_cast<unsigned>(hi) < static_cast<unsigned>(p.ch) &&
+              static_cast<unsigned>(wi) < static_cast<unsigned>(p.cw))
+            voff = static_cast<uint32_t>(
+                (slot_base[j] + (static_cast<int64_t>(hi) * p.cw + wi) * p.c_stride + t_c0 + kc) * ES);
+        } else if (slot_base[j] >= 0 && k_ok) {
+          voff = static_cast<uint32_t>((slot_base[j] + k) * ES);
+        }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, (lds_void_ptr)(smem + buf * STAGE + g * 1024), 16, voff, 0,
+                                                 0, 0);
+      } else {
+        if (slot_base[j] >= 0 && k_ok) voff = static_cast<uint32_t>((slot_base[j] + k) * ES);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, (lds_void_ptr)(smem + buf * STAGE + g * 1024), 16, voff, 0,
+                                                 0, 0);
+      }
+    }
+    if (AM == kConvTap) {
+      t_c0 += BK;
+      if (t_c0 >= p.c_pack) {
+        t_c0 = 0;
+        if (++t_kw >= p.kw) {
+          t_kw = 0;
+          ++t_kh;
+        }
+      }
+    }
+  };
+
+  acc_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
+
+  const int64_t ktiles = ceil_div(p.k, BK);
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < ktiles) issue(st, st);
+  const int lrow = lane & 15, lchunk = lane >> 4;
+  for (int64_t kt = 0; kt < ktiles; ++kt) {
+    // Tiles issued after kt (at most S - 2 of them) may stay in flight.
+    const int64_t later = min(static_cast<int64_t>(S - 2), ktiles - 1 - kt);
+    if (later >= 2) wait_vmcnt<2 * LPW>();
+    else if (later == 1) wait_vmcnt<LPW>();
+    else wait_vmcnt<0>();
+    // Barrier without __syncthreads' release fence: that fence would wait for
+    // every outstanding DMA (vmcnt(0)) and drain the pipeline.  This wave's
+    // tile-kt DMA is complete (the wait above) and its earlier LDS reads were
+    // consumed by MFMAs; the empty asm statements keep the compiler from
+    // moving memory operations across the barrier.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt + S - 1 < ktiles) issue(kt + S - 1, static_cast<int>((kt + S - 1) % S));
+    const uint8_t* As = smem + (kt % S) * STAGE;
+    const uint8_t* Bs = As + BM * RB;
+#pragma unroll
+    for (int ks = 0; ks < 8; ks += 4) {
+      vec av[TM], bv[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm * WTM + i * 16 + lrow;
+        av[i] = *reinterpret_cast<const vec*>(As + r * RB + (((ks + lchunk) ^ (r & 7)) << 4));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int r = wn * WTN + j * 16 + lrow;
+        bv[j] = *reinterpret_cast<const vec*>(Bs + r * RB + (((ks + lchunk) ^ (r & 7)) << 4));
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = Mma::mma(av[i], bv[j], acc[i][j]);
+    }
+  }
+
+  TO* outp = static_cast<TO*>(p.out);
+  const TO* resp = p.epi.residual ? static_cast<const TO*>(p.epi.residual) : nullptr;
+  const bool vec_ok = !p.out_nchw && (p.ldo % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(p.epi.residual) & 15) == 0);
+  __syncthreads();
+  float* stage = reinterpret_cast<float*>(smem) + wave * WTM * (WTN + 4);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float* dst = &stage[(i * 16 + (lane >> 4) * 4 + r) * (WTN + 4) + j * 16 + lrow];
+        if constexpr (Mma::kInt) *reinterpret_cast<int*>(dst) = acc[i][j][r];
+        else *dst = acc[i][j][r];
+      }
+  wave_sync_lds();
+#pragma nounroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t mrow0 = m0 + wm * WTM + i * 16, ncol0 = n0 + wn * WTN;
+    const float* strip = stage + i * 16 * (WTN + 4);
+    if constexpr (Mma::kInt) {
+      store_strip_q<TO, WTN>(strip, lane, mrow0, ncol0, outp, resp, vec_ok);
+    } else {
+      if (p.out_nchw) store_strip<TO, WTN>(p, strip, lane, mrow0, ncol0, outp, resp, 0);
+      else store_strip_vec<TO, WTN>(strip, lane, mrow0, ncol0, outp, resp, 0, vec_ok);
+    }
+  }
+}
+
+// =====================================================================
 // SIMT fp32 GEMM for operands the MFMA path cannot vector-load (odd K,
 // misaligned rows): one thread per output, same epilogue.
 // =====================================================================
@@ -935,10 +1162,36 @@ int launch_f32(Problem p, int64_t batch, hipStream_t s) {
   return launch_status("gemm_f32");
 }
 
+// The pipelined kernel needs byte offsets that fit the 32-bit buffer offset
+// with room for the out-of-range sentinel, and no batch strides.
+inline bool dma_eligible(const Problem& p, int64_t batch, int am) {
+  if (getenv("C3H_DISABLE_DMA")) return false;
+  // Implicit-GEMM convs stay on the register-prefetch kernel: their A tiles
+  // are L2-resident gathers, and two blocks per CU beat deeper prefetch.
+  if (am == kConvTap && !getenv("C3H_CONV_DMA")) return false;
+  return batch == 1 && (am == kDenseK || am == kConvTap) && p.a_bytes > 0 && p.b_bytes > 0 &&
+         p.a_bytes < (int64_t{1} << 31) && p.b_bytes < (int64_t{1} << 31);
+}
+
 template <typename Mma, typename TO, int AM>
 int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
   dim3 grid;
   const int64_t sms = 256;
+  if constexpr (AM == kDenseK || AM == kConvTap) {
+    if (dma_eligible(p, batch, AM)) {
+      if (p.n <= 64) {
+        grid_of<256, 64>(p, 1, grid);
+        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 64, 4, 1, AM, 3>), grid, dim3(kThreads), 0, s, p);
+      } else if (p.n <= 128 || ceil_div(p.m, 128) * ceil_div(p.n, 256) < 2 * sms) {
+        grid_of<128, 128>(p, 1, grid);
+        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 128, 128, 2, 2, AM, 4>), grid, dim3(kThreads), 0, s, p);
+      } else {
+        grid_of<128, 256>(p, 1, grid);
+        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 128, 256, 2, 2, AM, 3>), grid, dim3(kThreads), 0, s, p);
+      }
+      return launch_status(what);
+    }
+  }
   if (p.n <= 64) {
     grid_of<256, 64>(p, batch, grid);
     hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 256, 64, 4, 1, AM>), grid, dim3(kThreads), 0, s, p);
@@ -1008,6 +1261,11 @@ int c3h_gemm(const c3h_gemm_args* a, void* stream) {
   p.out_dtype = a->out_dtype;
   p.epi = a->epi;
   p.ho = 1; p.wo = 1;
+  {
+    const int es = dtype_size(a->in_dtype);
+    p.a_bytes = ((a->m - 1) * a->lda + a->k) * es;
+    p.b_bytes = ((a->n - 1) * a->ldb + a->k) * es;
+  }
   int64_t tiles = ceil_div(a->m, 64) * ceil_div(a->n, 64);
   C3H_REQUIRE(tiles < (1LL << 31), "gemm: too many tiles");
   hipStream_t s = as_stream(stream);
@@ -1061,6 +1319,12 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
   p.m = static_cast<int64_t>(a->n) * a->ho * a->wo;
   p.n = a->o;
   p.ldo = a->o;
+  p.a_bytes = static_cast<int64_t>(a->n) * a->h * a->w_ * a->c_stride * dtype_size(a->in_dtype);
+  C3H_REQUIRE(p.m < (int64_t{1} << 31), "conv2d: n*ho*wo must be below 2^31");
+  C3H_REQUIRE(static_cast<int64_t>(a->kh) * (a->kw + 8) * a->c_pack < (int64_t{1} << 31), "conv2d: K too large");
+  p.fd_hw = make_fastdiv(static_cast<uint32_t>(a->ho * a->wo));
+  p.fd_wo = make_fastdiv(static_cast<uint32_t>(a->wo));
+  p.fd_cpack = make_fastdiv(static_cast<uint32_t>(a->c_pack));
   hipStream_t s = as_stream(stream);
   if (a->in_dtype == C3H_F32) {
     // Packed K order (kh, kw, c_pack); 4-wide vectors must stay in one pixel.
@@ -1068,6 +1332,7 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
     C3H_REQUIRE(a->out_dtype == C3H_F32, "conv2d fp32: output must be fp32");
     C3H_REQUIRE(aligned(a->x, 16) && aligned(a->w, 16), "conv2d fp32: x and w must be 16-byte aligned");
     p.kw_pack = a->kw;
+    p.fd_kwpack = make_fastdiv(static_cast<uint32_t>(p.kw_pack));
     p.k = static_cast<int64_t>(a->kh) * a->kw * a->c_pack;
     p.ldb = p.k;
     return launch_f32<kConv, true>(p, 1, s);
@@ -1076,8 +1341,10 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
     C3H_REQUIRE(aligned(a->x, 16) && aligned(a->w, 16), "conv2d: x and w must be 16-byte aligned");
     if (a->c_pack % 8 == 0 && a->c_stride % 8 == 0) {
       p.kw_pack = a->kw;
+      p.fd_kwpack = make_fastdiv(static_cast<uint32_t>(p.kw_pack));
       p.k = static_cast<int64_t>(a->kh) * a->kw * a->c_pack;
       p.ldb = ceil_div(p.k, 32) * 32;  // weights padded to whole 32-wide K tiles
+      p.b_bytes = static_cast<int64_t>(a->o) * p.ldb * 2;
       // A 64-wide K tile stays inside one filter tap when c_pack % 64 == 0.
       if (a->c_pack % 64 == 0) return launch_h_any<kConvTap>(p, 1, s, a->in_dtype);
       return launch_h_any<kConv>(p, 1, s, a->in_dtype);
@@ -1086,6 +1353,7 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
     // 2 so each 32-wide K tile covers whole pixels (8-byte vectors).
     C3H_REQUIRE(a->c_pack == 4 && a->c_stride == 4, "conv2d: 16-bit path needs c_pack%8==0 or c_pack==c_stride==4");
     p.kw_pack = static_cast<int>(ceil_div(a->kw, 8) * 8);
+    p.fd_kwpack = make_fastdiv(static_cast<uint32_t>(p.kw_pack));
     p.k = static_cast<int64_t>(a->kh) * p.kw_pack * 4;
     p.ldb = p.k;
     return launch_h_any<kConvStem>(p, 1, s, a->in_dtype);
@@ -1115,6 +1383,8 @@ int c3h_qgemm(const c3h_qgemm_args* a, void* stream) {
   p.y_zero = a->y_zero; p.qmode = a->mode; p.out_dtype = a->out_dtype;
   p.epi = a->epi;
   p.ho = 1; p.wo = 1;
+  p.a_bytes = (a->m - 1) * a->lda + a->k;
+  p.b_bytes = (a->n - 1) * a->ldb + a->k;
   hipStream_t s = as_stream(stream);
   if (a->mode == 0) return launch_mfma<MmaI8, int32_t, kDenseK>(p, 1, s, "qgemm");
   if (a->mode == 1) return launch_mfma<MmaI8, int8_t, kDenseK>(p, 1, s, "qgemm");

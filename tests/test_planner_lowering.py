@@ -217,3 +217,23 @@ def test_dense_strides_and_broadcast():
     assert E.resolve_reshape_shape((2, 6, 8), [0, -1], 0) == (2, 48)
     with pytest.raises(ValueError):
         E.resolve_reshape_shape((2, 6, 8), [5, -1], 0)
+
+
+def test_invariant_division_multiplier_is_exact():
+    """The conv kernels' index division (mul = floor(2^32 (2^l - d) / d) + 1,
+    q = (mulhi(n, mul) + n) >> l) equals n // d for n < 2^31."""
+    rng = np.random.default_rng(0)
+    divisors = list(range(1, 600)) + [784, 3136, 12544, 50176, 200704, 802816, 3211264, 2 ** 20 + 7, 2 ** 30 - 3]
+    ns = np.concatenate([rng.integers(0, 2 ** 31, size=4000, dtype=np.int64), np.arange(0, 5000),
+                         np.array([2 ** 31 - 1, 2 ** 31 - 2])]).astype(np.uint64)
+    for d in divisors:
+        l = 0
+        while (1 << l) < d:
+            l += 1
+        mul = ((1 << 32) * ((1 << l) - d)) // d + 1
+        assert mul < 2 ** 32
+        q = ((ns * np.uint64(mul)) >> np.uint64(32)) + ns
+        q >>= np.uint64(l)
+        np.testing.assert_array_equal(q, ns // np.uint64(d))
+        for n in (d - 1, d, d + 1, 2 * d - 1, (2 ** 31 - 1) // d * d):
+            assert ((n * mul >> 32) + n) >> l == n // d
