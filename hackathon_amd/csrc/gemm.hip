@@ -154,6 +154,9 @@ struct FastDiv {
   uint32_t mul, shift;
 };
 
+// Buffer-load byte offset past every num_records used here: reads zeros.
+constexpr uint32_t kOobOffset = 0x80000000u;
+
 inline FastDiv make_fastdiv(uint32_t d) {
   uint32_t l = 0;
   while ((uint64_t{1} << l) < d) ++l;
@@ -683,7 +686,11 @@ __device__ __forceinline__ void store_strip_q(const float* stage, int lane, int6
   }
 }
 
-template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM>
+// BUF: operands read with buffer loads at 32-bit byte offsets (A and B below
+// 2^31 bytes, no batch): row bases are precomputed once, out-of-range lanes
+// use an offset past num_records and read zeros, so a K step costs a few
+// VALU per load instead of 64-bit address math and branches.
+template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, bool BUF = false>
 __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
   constexpr int ES = Mma::ES;
   constexpr int VE = 16 / ES;        // elements per 16-byte vector
@@ -724,6 +731,26 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
   int64_t rbase[AM == kDenseK ? 1 : A_V];
   int rhi[AM == kDenseK ? 1 : A_V], rwi[AM == kDenseK ? 1 : A_V];
   ConvRow crow[AM == kConv ? A_V : 1];
+  static_assert(!BUF || AM == kDenseK || AM == kConvTap, "buffer loads: dense or tap-uniform conv");
+  __amdgpu_buffer_rsrc_t rs_a, rs_b;
+  int32_t a_off[BUF ? A_V : 1];   // dense: row byte offset (-1: out of range); tap: pixel byte offset
+  int32_t b_off[BUF ? B_V : 1];
+  if constexpr (BUF) {
+    rs_a = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.a), 0, static_cast<int>(p.a_bytes), 0x00020000);
+    rs_b = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.b), 0, static_cast<int>(p.b_bytes), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < B_V; ++i) {
+      const int64_t n = n0 + trow + RSTEP * i;
+      b_off[i] = n < p.n ? static_cast<int32_t>(n * p.ldb * ES) : -1;
+    }
+    if (AM == kDenseK) {
+#pragma unroll
+      for (int i = 0; i < A_V; ++i) {
+        const int64_t m = m0 + trow + RSTEP * i;
+        a_off[i] = m < p.m ? static_cast<int32_t>(m * p.lda * ES) : -1;
+      }
+    }
+  }
   if (AM == kConvTap || AM == kConvStem) {
 #pragma unroll
     for (int i = 0; i < A_V; ++i) {
@@ -731,6 +758,9 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
       rbase[i] = r.base;
       rhi[i] = r.valid ? r.hi0 : -(1 << 28);  // invalid rows fail every bounds check
       rwi[i] = r.wi0;
+      if constexpr (BUF)
+        a_off[i] = static_cast<int32_t>(
+            (r.base + (static_cast<int64_t>(r.hi0) * p.cw + r.wi0) * p.c_stride) * ES);
     }
   } else if (AM == kConv) {
 #pragma unroll
@@ -740,6 +770,28 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
   int t_kh = 0, t_kw = 0, t_c0 = 0;
 
   auto load_a = [&](int64_t k0) {
+    if constexpr (BUF) {
+      if (AM == kDenseK) {
+        const bool kok = k0 + kc < p.k;
+        const int32_t koff = static_cast<int32_t>((k0 + kc) * ES);
+#pragma unroll
+        for (int i = 0; i < A_V; ++i) {
+          const uint32_t voff = (kok && a_off[i] >= 0) ? static_cast<uint32_t>(a_off[i] + koff) : kOobOffset;
+          ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs_a, voff, 0, 0));
+        }
+      } else {
+        const int dh = t_kh * p.dh, dw = t_kw * p.dw;
+        const int32_t tap = static_cast<int32_t>(((dh * p.cw + dw) * p.c_stride + t_c0 + kc) * ES);
+#pragma unroll
+        for (int i = 0; i < A_V; ++i) {
+          const bool ok = static_cast<unsigned>(rhi[i] + dh) < static_cast<unsigned>(p.ch) &&
+                          static_cast<unsigned>(rwi[i] + dw) < static_cast<unsigned>(p.cw);
+          const uint32_t voff = ok ? static_cast<uint32_t>(a_off[i] + tap) : kOobOffset;
+          ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs_a, voff, 0, 0));
+        }
+      }
+      return;
+    }
     if (AM == kDenseK) {
       const int64_t k = k0 + kc;
 #pragma unroll
@@ -808,6 +860,16 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
   };
   auto load_b = [&](int64_t k0) {
     const int64_t k = k0 + kc;
+    if constexpr (BUF) {
+      const bool kok = k < p.k;
+      const int32_t koff = static_cast<int32_t>(k * ES);
+#pragma unroll
+      for (int i = 0; i < B_V; ++i) {
+        const uint32_t voff = (kok && b_off[i] >= 0) ? static_cast<uint32_t>(b_off[i] + koff) : kOobOffset;
+        rb[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs_b, voff, 0, 0));
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < B_V; ++i) {
       const int64_t n = n0 + trow + RSTEP * i;
@@ -926,8 +988,6 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
 // kDenseK or kConvTap.
 // =====================================================================
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
-
-constexpr uint32_t kOobOffset = 0x80000000u;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
@@ -1188,6 +1248,22 @@ int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
       } else {
         grid_of<128, 256>(p, 1, grid);
         hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 128, 256, 2, 2, AM, 3>), grid, dim3(kThreads), 0, s, p);
+      }
+      return launch_status(what);
+    }
+  }
+  if constexpr (AM == kDenseK || AM == kConvTap) {
+    if (batch == 1 && p.a_bytes > 0 && p.b_bytes > 0 && p.a_bytes < (int64_t{1} << 31) &&
+        p.b_bytes < (int64_t{1} << 31) && !getenv("C3H_DISABLE_BUF")) {
+      if (p.n <= 64) {
+        grid_of<256, 64>(p, 1, grid);
+        hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 256, 64, 4, 1, AM, true>), grid, dim3(kThreads), 0, s, p);
+      } else if (p.n <= 128 || ceil_div(p.m, 128) * ceil_div(p.n, 256) < 2 * sms) {
+        grid_of<128, 128>(p, 1, grid);
+        hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 128, 128, 2, 2, AM, true>), grid, dim3(kThreads), 0, s, p);
+      } else {
+        grid_of<128, 256>(p, 1, grid);
+        hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 128, 256, 2, 2, AM, true>), grid, dim3(kThreads), 0, s, p);
       }
       return launch_status(what);
     }
