@@ -317,6 +317,78 @@ __global__ void __launch_bounds__(kBlock) layernorm_kernel(c3h_layernorm_args a)
   }
 }
 
+// Vectorized LayerNorm: one wave per row, 8 consecutive columns per lane per
+// vector (16-byte loads of 16-bit data), up to kLnVec vectors per lane kept
+// in registers (NV = vectors per lane, chosen per width); statistics in fp32 (mean, then biased variance of the
+// centred values), as layernorm_kernel.  cols % 8 == 0, cols <= 512 * kLnVec.
+constexpr int kLnVec = 8;
+
+template <typename TX, typename TO, int NV>
+__global__ void __launch_bounds__(kBlock) layernorm_vec_kernel(c3h_layernorm_args a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + wave;
+  if (row >= a.rows) return;
+  const int nvec = static_cast<int>(a.cols / 8);
+  const TX* x = static_cast<const TX*>(a.x) + row * a.cols;
+  const TX* res = a.residual ? static_cast<const TX*>(a.residual) + row * a.cols : nullptr;
+  float v[NV][8];
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int vi = lane + 64 * j;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[j][e] = 0.0f;
+    if (vi < nvec) {
+      Elem<TX>::load8(x + vi * 8, v[j]);
+      if (res) {
+        float r[8];
+        Elem<TX>::load8(res + vi * 8, r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[j][e] += r[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum += v[j][e];
+    }
+  }
+  const float mean = wave_sum(sum) / static_cast<float>(a.cols);
+  float sq = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    if (lane + 64 * j < nvec) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = v[j][e] - mean;
+        sq += d * d;
+      }
+    }
+  }
+  const float var = wave_sum(sq) / static_cast<float>(a.cols);
+  const float inv_std = 1.0f / sqrtf(var + a.epsilon);
+  const float* scale = static_cast<const float*>(a.scale);
+  const float* bias = static_cast<const float*>(a.bias);
+  TO* out = static_cast<TO*>(a.out) + row * a.cols;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int vi = lane + 64 * j;
+    if (vi < nvec) {
+      float g[8], y[8];
+      Elem<float>::load8(scale + vi * 8, g);
+      float b[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (bias) Elem<float>::load8(bias + vi * 8, b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        y[e] = (v[j][e] - mean) * inv_std * g[e];
+        if (bias) y[e] += b[e];
+      }
+      Elem<TO>::store8(out + vi * 8, y);
+    }
+  }
+  if (lane == 0) {
+    if (a.mean_out) static_cast<float*>(a.mean_out)[row] = mean;
+    if (a.invstd_out) static_cast<float*>(a.invstd_out)[row] = inv_std;
+  }
+}
+
 // ------------------------------------------------------------------ batchnorm / fold
 __global__ void batchnorm_kernel(c3h_batchnorm_args a) {
   int64_t total = a.n * a.c * a.hw;
@@ -584,6 +656,27 @@ __global__ void quantize_kernel(c3h_quantize_args a) {
   }
 }
 
+// 8 elements per thread: one 16-byte (16-bit input) or 32-byte (fp32) load,
+// one 8-byte int8 store; same rintf / saturate arithmetic as quantize_kernel.
+template <typename TX>
+__global__ void __launch_bounds__(kBlock) quantize_vec_kernel(c3h_quantize_args a) {
+  const int64_t nvec = a.count / 8;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const TX* x = static_cast<const TX*>(a.x);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec; i += stride) {
+    float v[8];
+    Elem<TX>::load8(x + i * 8, v);
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float q = rintf(v[e] / a.scale) + static_cast<float>(a.zero_point);
+      q = fminf(fmaxf(q, -128.0f), 127.0f);
+      w[e >> 2] |= (static_cast<uint32_t>(static_cast<int8_t>(q)) & 0xffu) << (8 * (e & 3));
+    }
+    *reinterpret_cast<uint2*>(a.out + i * 8) = uint2{w[0], w[1]};
+  }
+}
+
 __global__ void dequantize_kernel(c3h_dequantize_args a) {
   int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < a.count; i += stride)
@@ -639,6 +732,18 @@ __global__ void __launch_bounds__(kBlock) maxpool_nhwc_vec_kernel(c3h_pool_args 
     }
     T* dst = static_cast<T*>(a.out) + ((ni * a.ho + ho_i) * a.wo + wo_i) * a.c_stride + g * V;
     store_vec16(dst, m);
+  }
+}
+
+template <typename TX, typename TO>
+void launch_ln(const c3h_layernorm_args& a, int blocks, int nv, void* stream) {
+  const dim3 g(blocks), b(kBlock);
+  hipStream_t st = as_stream(stream);
+  switch (nv) {
+    case 1: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 1>), g, b, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 2>), g, b, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 4>), g, b, 0, st, a); break;
+    default: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 8>), g, b, 0, st, a); break;
   }
 }
 
@@ -784,6 +889,21 @@ int c3h_layernorm(const c3h_layernorm_args* a, void* stream) {
   C3H_REQUIRE(a && a->rows >= 0 && a->cols >= 1 && a->x && a->scale && a->out, "layernorm: bad args");
   if (a->rows == 0) return C3H_OK;
   int blocks = static_cast<int>(ceil_div(a->rows, kBlock / 64));
+  auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const bool vec = a->cols % 8 == 0 && a->cols <= 512 * kLnVec && al16(a->x) && al16(a->out) && al16(a->scale) &&
+                   (!a->bias || al16(a->bias)) && (!a->residual || al16(a->residual)) &&
+                   (a->x_dtype == C3H_F32 || a->x_dtype == C3H_BF16 || a->x_dtype == C3H_F16) &&
+                   (a->out_dtype == C3H_F32 || a->out_dtype == a->x_dtype);
+  if (vec) {
+    const int nv = static_cast<int>(ceil_div(a->cols / 8, 64));
+    const int NVsel = nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : 8;
+    if (a->x_dtype == C3H_F32) launch_ln<float, float>(*a, blocks, NVsel, stream);
+    else if (a->x_dtype == C3H_BF16 && a->out_dtype == C3H_F32) launch_ln<bf16_t, float>(*a, blocks, NVsel, stream);
+    else if (a->x_dtype == C3H_BF16) launch_ln<bf16_t, bf16_t>(*a, blocks, NVsel, stream);
+    else if (a->out_dtype == C3H_F32) launch_ln<f16_t, float>(*a, blocks, NVsel, stream);
+    else launch_ln<f16_t, f16_t>(*a, blocks, NVsel, stream);
+    return launch_status("layernorm_vec");
+  }
   hipLaunchKernelGGL(layernorm_kernel, dim3(blocks), dim3(kBlock), 0, as_stream(stream), *a);
   return launch_status("layernorm");
 }
@@ -907,6 +1027,16 @@ int c3h_pack_conv_weight(const c3h_pack_args* a, void* stream) {
 int c3h_quantize(const c3h_quantize_args* a, void* stream) {
   C3H_REQUIRE(a && a->count >= 0 && a->scale != 0.0f, "quantize: bad args");
   if (a->count == 0) return C3H_OK;
+  if (a->count % 8 == 0 && (reinterpret_cast<uintptr_t>(a->x) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(a->out) & 7) == 0 &&
+      (a->x_dtype == C3H_F32 || a->x_dtype == C3H_BF16 || a->x_dtype == C3H_F16)) {
+    const dim3 g(grid_for(a->count / 8)), b(kBlock);
+    hipStream_t st = as_stream(stream);
+    if (a->x_dtype == C3H_F32) hipLaunchKernelGGL(quantize_vec_kernel<float>, g, b, 0, st, *a);
+    else if (a->x_dtype == C3H_BF16) hipLaunchKernelGGL(quantize_vec_kernel<bf16_t>, g, b, 0, st, *a);
+    else hipLaunchKernelGGL(quantize_vec_kernel<f16_t>, g, b, 0, st, *a);
+    return launch_status("quantize_vec");
+  }
   hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(a->count)), dim3(kBlock), 0, as_stream(stream), *a);
   return launch_status("quantize");
 }
