@@ -83,6 +83,7 @@ constexpr int kD = 64;        // head dim
 constexpr int kBQ = 64;       // queries per workgroup (16 per wave)
 constexpr int kBK = 64;       // keys per tile
 constexpr int kPad = 8;       // 16-byte skew of LDS rows
+constexpr float kLog2e = 1.4426950408889634f;
 
 template <typename T> struct FlashMma;
 template <> struct FlashMma<bf16_t> {
@@ -120,6 +121,8 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
   // dims 32*ks + 8*g + [0..7].
   const int q = qt * kBQ + wave * 16 + l16;
   const bool q_valid = q < a.seq_q;
+  const int wave_q0 = qt * kBQ + wave * 16;  // this wave's first query
+  const float scale_log2 = a.scale * kLog2e;
   vec8 qf[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
@@ -144,20 +147,27 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
 
   for (int t = 0; t < ntiles; ++t) {
     const int k0 = t * kBK;
-    // Stage K [key][dim] and V^T [dim][key]: 64x64 each, 16-byte vectors.
+    // Stage K [key][dim] (16-byte rows) and V^T [dim][key]: each thread takes
+    // a key pair x 8 dims of V and writes 8 packed 4-byte (key, key+1) words.
+    {
+      const int key = tid >> 3, d0 = (tid & 7) * 8;  // K: keys 0..31 and 32..63
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      int e = tid + 256 * i;
-      int key = e >> 3, d0 = (e & 7) * 8;
-      uint4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-      if (k0 + key < a.seq_k) {
-        kv = *reinterpret_cast<const uint4*>(K + (k0 + key) * a.k_ss + d0);
-        vv = *reinterpret_cast<const uint4*>(V + (k0 + key) * a.v_ss + d0);
+      for (int i = 0; i < 2; ++i) {
+        const int kk = key + 32 * i;
+        uint4 kv = {0u, 0u, 0u, 0u};
+        if (k0 + kk < a.seq_k) kv = *reinterpret_cast<const uint4*>(K + (k0 + kk) * a.k_ss + d0);
+        *reinterpret_cast<uint4*>(&Ks[kk][d0]) = kv;
       }
-      *reinterpret_cast<uint4*>(&Ks[key][d0]) = kv;
-      const uint16_t* vs = reinterpret_cast<const uint16_t*>(&vv);
+      const int kp = (tid >> 3) * 2;  // V: key pair kp, kp + 1 (keys 0..63)
+      uint4 v0 = {0u, 0u, 0u, 0u}, v1 = {0u, 0u, 0u, 0u};
+      if (k0 + kp < a.seq_k) v0 = *reinterpret_cast<const uint4*>(V + (k0 + kp) * a.v_ss + d0);
+      if (k0 + kp + 1 < a.seq_k) v1 = *reinterpret_cast<const uint4*>(V + (k0 + kp + 1) * a.v_ss + d0);
+      const uint32_t w0[4] = {v0.x, v0.y, v0.z, v0.w}, w1[4] = {v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
-      for (int j = 0; j < 8; ++j) Vt[d0 + j][key] = vs[j];
+      for (int j = 0; j < 4; ++j) {
+        *reinterpret_cast<uint32_t*>(&Vt[d0 + 2 * j][kp]) = (w0[j] & 0xffffu) | (w1[j] << 16);
+        *reinterpret_cast<uint32_t*>(&Vt[d0 + 2 * j + 1][kp]) = (w0[j] >> 16) | (w1[j] & 0xffff0000u);
+      }
     }
     __syncthreads();
 
@@ -172,26 +182,41 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
         s_acc[kt4] = FlashMma<T>::mma(kf, qf[ks], s_acc[kt4]);
       }
     }
-    // Scale, mask, running max.
+    // Scores in log2 units (scale * log2 e), so p = exp2(s - m).  Key-range
+    // and causal checks run only on tiles that reach past seq_k or the
+    // wave's first query (a uniform branch); interior tiles skip them.
     float tmax = -INFINITY;
+    const bool edge = (k0 + kBK > a.seq_k) || (MASK == 1 && k0 + kBK - 1 > wave_q0) || MASK == 2;
+    if (edge) {
 #pragma unroll
-    for (int kt4 = 0; kt4 < 4; ++kt4) {
+      for (int kt4 = 0; kt4 < 4; ++kt4) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = k0 + 16 * kt4 + 4 * g + j;
-        float s = s_acc[kt4][j] * a.scale;
-        if (key >= a.seq_k) s = -INFINITY;
-        if (MASK == 1 && key > q) s = -INFINITY;
-        if (MASK == 2 && q_valid && key < a.seq_k) s += mask[static_cast<int64_t>(q) * a.mask_ld + key];
-        s_acc[kt4][j] = s;
-        tmax = fmaxf(tmax, s);
+        for (int j = 0; j < 4; ++j) {
+          const int key = k0 + 16 * kt4 + 4 * g + j;
+          float s = s_acc[kt4][j] * scale_log2;
+          if (key >= a.seq_k) s = -INFINITY;
+          if (MASK == 1 && key > q) s = -INFINITY;
+          if (MASK == 2 && q_valid && key < a.seq_k) s += mask[static_cast<int64_t>(q) * a.mask_ld + key] * kLog2e;
+          s_acc[kt4][j] = s;
+          tmax = fmaxf(tmax, s);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int kt4 = 0; kt4 < 4; ++kt4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float s = s_acc[kt4][j] * scale_log2;
+          s_acc[kt4][j] = s;
+          tmax = fmaxf(tmax, s);
+        }
       }
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float m_new = fmaxf(m_run, tmax);
     const float base = m_new == -INFINITY ? 0.0f : m_new;
-    const float corr = m_run == -INFINITY ? 0.0f : expf(m_run - base);
+    const float corr = m_run == -INFINITY ? 0.0f : exp2f(m_run - base);
     m_run = m_new;
     l_part *= corr;
 #pragma unroll
@@ -204,7 +229,7 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
       uint16_t bits[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        float p = expf(s_acc[2 * ks + i / 4][i % 4] - base);
+        float p = exp2f(s_acc[2 * ks + i / 4][i % 4] - base);
         l_part += p;
         bits[i] = Elem<T>::from_f32(p).bits;
       }
