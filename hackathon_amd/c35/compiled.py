@@ -570,7 +570,10 @@ class CompiledPlan:
 
     # -- metadata ops as views ---------------------------------------------------------------
     def _op_Constant(self, node):
-        raise NotImplementedError("Constant nodes are preloaded as weights")
+        """Constant outputs arrive with the initializers (c35/executor.py:23-88) and load lazily."""
+        for o in node.outputs:
+            if o and o not in self.weights_src:
+                raise KeyError(f"Constant node '{node.id}' output '{o}' not pre-loaded")
 
     def _view(self, v: Val, shape, strides, offset_delta=0) -> Val:
         return Val(tuple(shape), v.dtype, v.buf, v.offset + offset_delta, tuple(strides), "dense", 0, None)

@@ -608,9 +608,15 @@ def load_and_infer(model_path: str, input_dir: str, output_dir: str, batch_size:
     trace = pipeline.optimized_executor.last_execution_trace
     counts_by_kind = {k: sum(a["kind"] == k for a in trace)
                       for k in ("ALLOC", "H2D", "EVENT_WAIT", "KERNEL", "EVENT_RECORD", "FREE", "D2H")}
+    from ..device import device_props
+
+    props = device_props(0)
+    evidence = {"device_name": props.name.decode(errors="replace"), "arch": props.arch.decode(errors="replace"),
+                "compute_units": props.compute_units, "library": str(_lib.lib()._name),
+                "batch_count": (total + batch - 1) // batch, "engine": engine_kind, "precision": precision}
     return {
         "model_path": model_path, "input_dir": input_dir, "output_dir": output_dir, "batch_size": batch,
-        "backend": "libc3hip", "engine": engine_kind, "total_samples": total, "output_shape": list(result.shape),
+        "backend": "libc3hip", "backend_evidence": evidence, "engine": engine_kind, "total_samples": total, "output_shape": list(result.shape),
         "parse_time_s": tp_end - tp, "infer_time_s": ti_end - ti, "total_time_s": t_end - t0,
         "cross_stage_reference": True, "optimized_graph_nodes": len(pipeline.graph.nodes),
         "fusion_stats": pipeline.fusion_result["Fusion"]["stats"],

@@ -215,6 +215,8 @@ def run_graph(graph, weights: Dict[str, np.ndarray], feed: Dict[str, np.ndarray]
         node = graph.nodes[nid]
         ins = [values[i] if i else None for i in node.inputs]
         op = node.op_type
+        if op == "Constant":  # value supplied with the weights (c35/executor.py:23-88 extraction)
+            continue
         if bypass_qdq and op == "QuantizeLinear":
             if record is not None:
                 record[node.inputs[1]] = max(record.get(node.inputs[1], 0.0), float(np.max(np.abs(ins[0]))))

@@ -1,0 +1,97 @@
+"""`python -m hackathon_amd.c35.deploy` end to end on the GPU.
+
+ONNX files written by PyTorch's C++ serializer (dynamic batch axis) and by
+this build's writer go through the CLI: manifest + .npy inputs in, logits.npy
++ manifest.json out, ragged last batch included.  fp32 runs are checked
+against PyTorch's fp32 forward (rtol 1e-3); the fp16 policy against the
+workload gate (max |logit diff| 2e-2 after scaling by the logit range, top-1
+agreement); files from this build's writer must give exactly the logits of
+the same graph run in-process.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = [pytest.mark.gpu, pytest.mark.filterwarnings("ignore::DeprecationWarning")]
+
+
+def _write_inputs(d, name, arr):
+    os.makedirs(d, exist_ok=True)
+    np.save(os.path.join(d, f"{name}.npy"), arr)
+    with open(os.path.join(d, "manifest.json"), "w") as f:
+        json.dump({"tensors": [{"name": name, "file": f"{name}.npy", "dtype": str(arr.dtype),
+                                "shape": list(arr.shape)}]}, f)
+
+
+def _deploy(tmp_path, model_path, in_name, arr, *extra):
+    from hackathon_amd.c35 import deploy
+
+    inp, out = str(tmp_path / "in"), str(tmp_path / "out")
+    _write_inputs(inp, in_name, arr)
+    print(f"deploy {os.path.basename(model_path)} {arr.shape} {extra}", flush=True)
+    rc = deploy.main(["--onnx", model_path, "--input", inp, "--output", out, *extra])
+    assert rc == 0
+    with open(os.path.join(out, "manifest.json")) as f:
+        man = json.load(f)
+    logits = np.load(os.path.join(out, "logits.npy"))
+    assert man["tensors"][0]["name"] == "logits" and man["tensors"][0]["shape"] == list(logits.shape)
+    return logits
+
+
+@pytest.mark.parametrize("name", ["cnn", "decoder"])
+def test_deploy_torch_export_fp32(gpu, tmp_path, name):
+    import torch
+
+    from test_onnx_io import _torch_modules, torch_export
+
+    module, example, in_name = _torch_modules()[name]
+    path = str(tmp_path / f"{name}.onnx")
+    torch_export(module, example, path, in_name, dynamic_batch=True)
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn((5,) + tuple(example.shape[1:]), generator=gen) if name == "cnn" else \
+        torch.randint(0, 50, (5,) + tuple(example.shape[1:]), generator=gen)
+    with torch.no_grad():
+        expect = module(x).numpy()
+    got = _deploy(tmp_path, path, in_name, x.numpy(), "--batch-size", "2")  # batches 2, 2, 1
+    np.testing.assert_allclose(got, expect, rtol=1e-3, atol=1e-4)
+
+
+def test_deploy_torch_decoder_fp16(gpu, tmp_path):
+    import torch
+
+    from test_onnx_io import _torch_modules, torch_export
+
+    module, example, in_name = _torch_modules()["decoder"]
+    path = str(tmp_path / "dec.onnx")
+    torch_export(module, example, path, in_name, dynamic_batch=True)
+    x = torch.randint(0, 50, (4,) + tuple(example.shape[1:]), generator=torch.Generator().manual_seed(2))
+    with torch.no_grad():
+        expect = module(x).numpy()
+    got = _deploy(tmp_path, path, in_name, x.numpy(), "--precision", "fp16")
+    scale = max(1.0, float(np.abs(expect).max()))
+    assert float(np.abs(got - expect).max()) <= 2e-2 * scale
+    agree = np.mean(got.argmax(-1) == expect.argmax(-1))
+    assert agree >= 0.99, agree
+
+
+@pytest.mark.parametrize("name,policy", [("resnet18_cifar", "fp32"), ("resnet18_224", "bf16")])
+def test_deploy_writer_file_matches_in_process(gpu, tmp_path, name, policy):
+    """The CLI over an exported file is the in-process pipeline, bit for bit."""
+    from hackathon_amd import models, onnx_io
+    from hackathon_amd.c35.executor import CrossStageReferencePipeline
+
+    kw = {"resnet18_cifar": dict(batch=4, image=16, widths=(16, 32, 32, 64)),
+          "resnet18_224": dict(batch=2, image=64, widths=(16, 32, 32, 64), classes=100)}[name]
+    m = models.build(name, **kw)
+    path = str(tmp_path / f"{name}.onnx")
+    onnx_io.export_model(m.graph, m.weights, path)
+    (in_name, arr), = m.inputs.items()
+    got = _deploy(tmp_path, path, in_name, arr, "--precision", policy)
+    pipe = CrossStageReferencePipeline(onnx_io.import_onnx(path), path, engine_kind="compiled", precision=policy)
+    ref = pipe.run({in_name: arr})["logits"].get()
+    np.testing.assert_array_equal(got, ref)
