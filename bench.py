@@ -13,8 +13,11 @@ roofline: the dominant kernel family of the workload (conv for ResNet,
 16-bit GEMM for the fp16 decoder, int8 GEMM for W8A8, fp32 GEMM for the
 MLP) is replayed alone as a hipGraph of just those launches, timed with HIP
 events on the compiled stream; achieved = algorithmic flops of those
-launches / their time.  cpu_baseline: the NumPy oracle (a restatement of
-the reference decomposition) on a bounded sample, on this host's cores.
+launches / their time.  roofline.traffic: measured HBM bytes per dominant
+launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy) read
+from the committed summary that `--traffic-run` / `--traffic-summary` make.
+cpu_baseline: the NumPy oracle (a restatement of the reference
+decomposition) on a bounded sample, on this host's cores.
 """
 
 from __future__ import annotations
@@ -157,6 +160,122 @@ def _cpu_baseline(name: str) -> dict:
                       f"batch, median of {len(times)} runs ({t:.2f} s each)"}
 
 
+# -- HBM traffic of the dominant kernel (two rocprofv3 --pmc passes) -------------------------------
+COPY_BYTES = 1 << 30
+TRAFFIC_PROFILE = ROOT / "profiles" / f"{HEADLINE}_conv_traffic.md"
+
+
+def _traffic_run(meta_path: str, reps: int = 3) -> int:
+    """The dispatch stream the FETCH_SIZE and WRITE_SIZE passes count.
+
+    First a plain copy of COPY_BYTES (strided_copy_kernel, 8-byte elements,
+    dense): what the counters read for it against the bytes it must move is
+    the calibration factor.  Then the headline workload's dominant launches
+    (every conv of one step) replayed `reps` + 1 times as a hipGraph; the
+    per-launch algorithmic bytes go to `meta_path` for the summary."""
+    import numpy as np
+
+    from hackathon_amd.c35 import engine
+    from hackathon_amd.device import DeviceArray, init, synchronize
+
+    init(0)
+    n = COPY_BYTES // 8
+    src, dst = DeviceArray.empty((n,), np.int64), DeviceArray.empty((n,), np.int64)
+    for _ in range(3):
+        engine.strided_copy(src, dst, (n,), (1,))
+    synchronize()
+    del src, dst
+    m, plan, prog = _prepare(HEADLINE)
+    idx = prog.launches_of(DOMINANT[HEADLINE][0])
+    prog.time_subset(idx, reps=reps)
+    synchronize()
+    meta = {"workload": HEADLINE, "copy_bytes": COPY_BYTES, "copy_dispatches": 3, "replays": reps + 1,
+            "launches": [{k: prog.launch_meta[i][k] for k in ("kind", "flops", "bytes")} for i in idx]}
+    with open(meta_path, "w") as f:
+        json.dump(meta, f, indent=1)
+    _log(f"traffic run: {len(idx)} dominant launches x {reps + 1} replays, meta -> {meta_path}")
+    return 0
+
+
+def _pmc_rows(run_dir: str, counter: str):
+    """(kernel name, value in KiB) per dispatch, in dispatch order, from a rocprofv3 csv directory."""
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(run_dir, "**", "*counter_collection.csv"), recursive=True))
+    if not files:
+        raise FileNotFoundError(f"no *counter_collection.csv under {run_dir}")
+    rows = []
+    for path in files:
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r.get("Counter_Name") == counter:
+                    rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return [(k, v) for _, k, v in rows]
+
+
+def _traffic_summary(fetch_dir: str, write_dir: str, meta_path: str) -> int:
+    """Calibrated HBM bytes per dominant launch -> profiles/<headline>_conv_traffic.md."""
+    import numpy as np
+
+    with open(meta_path) as f:
+        meta = json.load(f)
+    launches = meta["launches"]
+    out = {}
+    for counter, run_dir in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = _pmc_rows(run_dir, counter)
+        copy = [v for k, v in rows if "strided_copy_kernel" in k]
+        conv = [v for k, v in rows if "mfma_gemm" in k]
+        if len(copy) != meta["copy_dispatches"] or len(conv) != len(launches) * meta["replays"]:
+            raise ValueError(f"{counter}: {len(copy)} copy / {len(conv)} conv dispatches, expected "
+                             f"{meta['copy_dispatches']} / {len(launches) * meta['replays']}")
+        factor = meta["copy_bytes"] / (float(np.median(copy)) * 1024.0)
+        per = np.asarray(conv).reshape(meta["replays"], len(launches)).mean(axis=0) * 1024.0 * factor
+        out[counter] = (factor, float(np.median(copy)), per)
+    f_fac, f_copy, fetch = out["FETCH_SIZE"]
+    w_fac, w_copy, write = out["WRITE_SIZE"]
+    alg = np.asarray([l["bytes"] for l in launches], float)
+    traffic = fetch + write
+    lines = [
+        f"# {meta['workload']}: HBM traffic of the implicit-GEMM conv launches (rocprofv3 --pmc)", "",
+        "Commands (repository root, MI355X box; one counter per pass):", "", "```",
+        "timeout -s KILL 180 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch -o run -- \\",
+        "    python3 bench.py --traffic-run gpurun_out/traffic_meta_fetch.json",
+        "timeout -s KILL 180 rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write -o run -- \\",
+        "    python3 bench.py --traffic-run gpurun_out/traffic_meta.json",
+        "python3 bench.py --traffic-summary gpurun_out/pmc_fetch gpurun_out/pmc_write gpurun_out/traffic_meta.json",
+        "```", "",
+        f"Calibration: a dense copy of {meta['copy_bytes'] / 2**20:.0f} MiB (strided_copy_kernel) reads "
+        f"FETCH_SIZE {f_copy:.0f} KiB and WRITE_SIZE {w_copy:.0f} KiB per dispatch; scale factors "
+        f"{f_fac:.4f} (fetch) and {w_fac:.4f} (write) turn counter KiB into bytes moved.", "",
+        "| launch | algorithmic MB | fetched MB | written MB | traffic / algorithmic |",
+        "|---:|---:|---:|---:|---:|",
+    ]
+    for i in range(len(launches)):
+        lines.append(f"| {i} | {alg[i] / 1e6:.1f} | {fetch[i] / 1e6:.1f} | {write[i] / 1e6:.1f} | "
+                     f"{traffic[i] / alg[i]:.2f} |")
+    lines += ["", f"Per step: algorithmic {alg.sum() / 1e9:.3f} GB, measured {traffic.sum() / 1e9:.3f} GB "
+              f"({traffic.sum() / alg.sum():.2f}x).", "",
+              f"traffic_bytes_per_launch = {traffic.mean():.0f}",
+              f"algorithmic_bytes_per_launch = {alg.mean():.0f}", ""]
+    TRAFFIC_PROFILE.write_text("\n".join(lines))
+    _log(f"wrote {TRAFFIC_PROFILE}: {traffic.mean() / 1e6:.1f} MB per launch "
+         f"({traffic.sum() / alg.sum():.2f}x algorithmic)")
+    return 0
+
+
+def _committed_traffic():
+    """HBM bytes per dominant launch from the committed pmc summary, or None."""
+    import re
+
+    try:
+        m = re.search(r"^traffic_bytes_per_launch = (\d+)$", TRAFFIC_PROFILE.read_text(), re.M)
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -165,11 +284,19 @@ def main() -> int:
     ap.add_argument("--configs", default="mlp,resnet18_cifar,resnet18_224,decoder_fp16,decoder_w8a8",
                     help="comma-separated workloads to measure (the headline is always included)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-run", metavar="META_JSON",
+                    help="dispatch stream for a rocprofv3 --pmc pass (copy calibration + dominant launches)")
+    ap.add_argument("--traffic-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "META_JSON"),
+                    help="turn the two pmc passes into the committed traffic summary (no GPU)")
     args = ap.parse_args()
+    if args.traffic_summary:
+        return _traffic_summary(*args.traffic_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
               "Run with --gpus 1.", file=sys.stderr)
         return 2
+    if args.traffic_run:
+        return _traffic_run(args.traffic_run)
     from hackathon_amd.device import device_props, init
 
     init(0)
@@ -182,6 +309,7 @@ def main() -> int:
     for n in names:
         per[n] = _measure(n, args.steps, args.warmup)
     head = per[HEADLINE]
+    head["roofline"]["traffic"] = _committed_traffic()
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.time()
