@@ -33,7 +33,7 @@ EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_RELU, EW_ERF, EW_ERF_AS, EW_SQRT, EW_EXP, EW_
 OP_NOP, OP_EVENT_RECORD, OP_EVENT_WAIT, OP_COPY = 0, 1, 2, 3
 OP_FILL, OP_CAST, OP_EW, OP_STRIDED_COPY, OP_REDUCE, OP_SOFTMAX, OP_LAYERNORM, OP_BATCHNORM, \
     OP_GATHER, OP_ARGMAX, OP_IM2COL, OP_LAYOUT, OP_MAXPOOL, OP_GEMM, OP_CONV, OP_ATTN_SCORES, \
-    OP_FLASH, OP_QUANTIZE, OP_QGEMM, OP_DEQUANTIZE, OP_BNFOLD, OP_PACK = range(10, 32)
+    OP_FLASH, OP_QUANTIZE, OP_QGEMM, OP_DEQUANTIZE, OP_BNFOLD, OP_PACK, OP_CONV_POOL = range(10, 33)
 
 vp = C.c_void_p
 i32 = C.c_int32
@@ -184,6 +184,12 @@ class PackArgs(C.Structure):
         ("k_stride", i64), ("in_dtype", i32), ("out_dtype", i32)]
 
 
+class ConvPoolArgs(C.Structure):
+    _fields_ = [("x", vp), ("w", vp), ("bias", vp), ("out", vp)] + [(n, i32) for n in (
+        "n", "c", "h", "w_", "o", "k_stride", "kh", "kw", "sh", "sw", "pad_top", "pad_left", "ho", "wo",
+        "pkh", "pkw", "psh", "psw", "ppad_top", "ppad_left", "po", "qo", "relu", "in_dtype", "mm_dtype", "pad_")]
+
+
 class Op(C.Structure):
     _fields_ = [("kind", i32), ("stream", i32), ("event", i32), ("pad_", i32), ("args", vp),
                 ("dst", vp), ("src", vp), ("bytes", C.c_uint64)]
@@ -192,7 +198,7 @@ class Op(C.Structure):
 ABI_ORDER = [Props, FillArgs, CastArgs, EwArgs, CopyArgs, ReduceArgs, SoftmaxArgs, LayerNormArgs,
              BatchNormArgs, BnFoldArgs, GatherArgs, ArgmaxArgs, Im2colArgs, LayoutArgs, PoolArgs,
              Epilogue, GemmArgs, ConvArgs, AttnScoresArgs, FlashArgs, QuantizeArgs, QGemmArgs,
-             DequantizeArgs, Op, PackArgs]
+             DequantizeArgs, Op, PackArgs, ConvPoolArgs]
 
 # Kernel entry points: name -> args struct (all take (const args*, void* stream)).
 KERNELS = {
@@ -203,7 +209,7 @@ KERNELS = {
     "c3h_maxpool2d": PoolArgs, "c3h_gemm": GemmArgs, "c3h_conv2d": ConvArgs,
     "c3h_attention_scores": AttnScoresArgs, "c3h_flash_attention": FlashArgs,
     "c3h_quantize": QuantizeArgs, "c3h_qgemm": QGemmArgs, "c3h_dequantize": DequantizeArgs,
-    "c3h_pack_conv_weight": PackArgs,
+    "c3h_pack_conv_weight": PackArgs, "c3h_conv_stem_pool": ConvPoolArgs,
 }
 
 OP_KIND = {
@@ -213,7 +219,7 @@ OP_KIND = {
     Im2colArgs: OP_IM2COL, LayoutArgs: OP_LAYOUT, PoolArgs: OP_MAXPOOL, GemmArgs: OP_GEMM,
     ConvArgs: OP_CONV, AttnScoresArgs: OP_ATTN_SCORES, FlashArgs: OP_FLASH,
     QuantizeArgs: OP_QUANTIZE, QGemmArgs: OP_QGEMM, DequantizeArgs: OP_DEQUANTIZE,
-    BnFoldArgs: OP_BNFOLD, PackArgs: OP_PACK,
+    BnFoldArgs: OP_BNFOLD, PackArgs: OP_PACK, ConvPoolArgs: OP_CONV_POOL,
 }
 
 KERNEL_OF_ARGS = {v: k for k, v in KERNELS.items()}

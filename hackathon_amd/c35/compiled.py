@@ -135,7 +135,7 @@ class CompiledPlan:
 
     def __init__(self, graph: Graph, plan: ExecutionPlan, host_weights: Dict[str, Any],
                  host_constants: Optional[Dict[str, Any]] = None, policy: str = "fp32",
-                 use_graph: bool = True) -> None:
+                 use_graph: bool = True, fuse_stem: bool = True) -> None:
         init()
         if policy not in _POLICY_ACT:
             raise ValueError(f"unknown precision policy {policy!r}")
@@ -157,6 +157,7 @@ class CompiledPlan:
         self.node_kinds: List[str] = []     # launch labels (for reporting)
         self.launch_meta: List[Dict[str, Any]] = []  # per launch: kind, algorithmic flops and bytes
         self.use_graph = use_graph
+        self.fuse_stem = fuse_stem
         self._graph_exec = None
         self._stream = Stream()
         self._consumers = self._consumer_map()
@@ -934,7 +935,6 @@ class CompiledPlan:
             c_pack = (cin + 7) // 8 * 8
             kw_pack = kw
             k_stride = (kh * kw * c_pack + 31) // 32 * 32
-        xin = self._nhwc_input(x, conv_dtype, c_pack)
         wkey = (w_name, c_pack, kw_pack, k_stride, str(conv_dtype))
         wcache = self.__dict__.setdefault("_convw", {})
         if wkey not in wcache:
@@ -943,6 +943,10 @@ class CompiledPlan:
             packed = E.pack_conv_weight(src_dev, c_pack, kw_pack, k_stride, out_dtype=conv_dtype)
             wcache[wkey] = Val(packed.shape, packed.dtype, self._persist(packed))
         wv = wcache[wkey]
+        if narrow and residual_name is None and self._stem_pool(node, x, wv, bias_name, act, cin, o, kh, kw, sh, sw,
+                                                                  dh, dw, pads, ho, wo, k_stride):
+            return
+        xin = self._nhwc_input(x, conv_dtype, c_pack)
         out_shape = (n, o, ho, wo)
         st = _Epi(bias=self._bias_val(bias_name), act=act)
         if residual_name is not None:
@@ -964,6 +968,56 @@ class CompiledPlan:
         self._emit("conv", build, [xin, wv] + self._epi_reads(st), [out],
                    flops=2.0 * n * ho * wo * o * cin * kh * kw)
         self.vals[st.final] = out
+
+    def _stem_pool(self, node, x: Val, wv: Val, bias_name, act, cin, o, kh, kw, sh, sw, dh, dw, pads, ho, wo,
+                   k_stride) -> bool:
+        """Conv 7x7/2 (c <= 3 -> 64) [+ ReLU] -> MaxPool 3x3/2 as one c3h_conv_stem_pool launch.
+
+        Taken when the conv reads an NCHW tensor and its only consumer is the
+        pool; the launch reads the NCHW input directly (no layout pass) and
+        keeps the conv output in LDS.  Results equal the unfused chain."""
+        if not self.fuse_stem or x.layout != "dense" or not x.dense or x.dtype not in (
+                np.float32, np.float16) and x.dtype != self.act_dtype:
+            return False
+        if (cin > 3 or o != 64 or (kh, kw, sh, sw, dh, dw) != (7, 7, 2, 2, 1, 1) or tuple(pads[:2]) != (3, 3)
+                or k_stride != 224 or act not in (0, 1)):
+            return False
+        pool, relu_node = self._single_consumer(node.outputs[0]), None
+        if pool is not None and pool.op_type == "Relu" and act == 0:  # an unfused Relu between conv and pool
+            relu_node, act = pool, 1
+            pool = self._single_consumer(relu_node.outputs[0])
+        if pool is None or pool.op_type != "MaxPool" or int(pool.attributes.get("ceil_mode", 0)):
+            return False
+        pk = list(pool.attributes.get("kernel_shape", []))
+        pst = list(pool.attributes.get("strides", [1, 1]))
+        pdl = list(pool.attributes.get("dilations", [1, 1]))
+        ppads = list(pool.attributes.get("pads", [0, 0, 0, 0]))
+        if pk != [3, 3] or pst != [2, 2] or pdl != [1, 1] or ppads[:2] != [1, 1] or pool.attributes.get("auto_pad",
+                                                                                                        "NOTSET") != "NOTSET":
+            return False
+        n, _, h, w = x.shape
+        _, _, _, _, _, _, _, po, qo = E.conv_geometry((n, o, ho, wo), (0, 0, 3, 3), pool.attributes)
+        if not (2 * (po - 1) - 1 < ho and 2 * (qo - 1) - 1 < wo):
+            return False
+        out = self._new((n, o, po, qo), self.act_dtype, "nhwc", o)
+        bias = self._bias_val(bias_name)
+
+        def build(r, x=x, wv=wv, bias=bias, out=out):
+            a = _lib.ConvPoolArgs()
+            a.x, a.w, a.out = self._ptr(x, r), self._ptr(wv, r), self._ptr(out, r)
+            a.bias = self._ptr(bias, r) if bias is not None else None
+            a.n, a.c, a.h, a.w_, a.o, a.k_stride = n, cin, h, w, o, k_stride
+            a.kh, a.kw, a.sh, a.sw, a.pad_top, a.pad_left, a.ho, a.wo = kh, kw, sh, sw, 3, 3, ho, wo
+            a.pkh, a.pkw, a.psh, a.psw, a.ppad_top, a.ppad_left, a.po, a.qo = 3, 3, 2, 2, 1, 1, po, qo
+            a.relu, a.in_dtype, a.mm_dtype = int(act == 1), dtype_code(x.dtype), self.mm_code
+            return a
+        self._emit("conv:stem_pool", build, [x, wv] + ([bias] if bias is not None else []), [out],
+                   flops=2.0 * n * ho * wo * o * cin * kh * kw)
+        self.consumed.add(pool.id)
+        if relu_node is not None:
+            self.consumed.add(relu_node.id)
+        self.vals[pool.outputs[0]] = out
+        return True
 
     def _op_Conv(self, node):
         self._conv(node, node.inputs[0], node.inputs[1], node.inputs[2] if len(node.inputs) > 2 else None, 0, None)

@@ -451,6 +451,33 @@ typedef struct {
 } c3h_conv_args;
 int c3h_conv2d(const c3h_conv_args* a, void* stream);
 
+/* Fused network stem: Conv 7x7 / stride 2 / pad 3 (c <= 3 input channels,
+ * 64 output channels) + per-channel bias (folded BatchNorm) + optional ReLU
+ * + MaxPool 3x3 / stride 2 / pad 1.  x is NCHW (F32, BF16 or F16, rounded to
+ * mm_dtype on load); w is the narrow-channel packing of c3h_conv2d
+ * ([64][kh][kw_pack = 8][c_pack = 4], k_stride 224); out is NHWC
+ * [n, po, qo, 64] in mm_dtype.  Bit-identical to layout -> c3h_conv2d
+ * (bias, relu) -> c3h_maxpool2d; replaces that chain for the Conv
+ * (+BatchNormalization) + Relu + MaxPool nodes of c32/decompositions.py
+ * :300-375 and the MaxPool that the reference registry lacks. */
+typedef struct {
+  const void* x;
+  const void* w;
+  const float* bias; /* [64] or NULL */
+  void* out;
+  int32_t n, c, h, w_;
+  int32_t o, k_stride;
+  int32_t kh, kw, sh, sw, pad_top, pad_left;
+  int32_t ho, wo;    /* conv output size */
+  int32_t pkh, pkw, psh, psw, ppad_top, ppad_left;
+  int32_t po, qo;    /* pooled output size */
+  int32_t relu;
+  int32_t in_dtype;
+  int32_t mm_dtype;  /* BF16 or F16: MFMA operands and output */
+  int32_t pad_;
+} c3h_conv_pool_args;
+int c3h_conv_stem_pool(const c3h_conv_pool_args* a, void* stream);
+
 /* Fused attention scores: softmax(Q K^T / divisor + mask) materialized, with
  * NumPy broadcast of batch/head dims and a rank<=4 mask
  * (c35/engine.py:1250-1380).  Q [q0,q1,rows,inner], Kt [k0,k1,inner,cols]. */
@@ -581,7 +608,8 @@ enum c3h_op_kind {
   C3H_OP_QGEMM = 28,
   C3H_OP_DEQUANTIZE = 29,
   C3H_OP_BNFOLD = 30,
-  C3H_OP_PACK = 31
+  C3H_OP_PACK = 31,
+  C3H_OP_CONV_POOL = 32
 };
 
 typedef struct {
@@ -614,7 +642,7 @@ int c3h_graph_destroy(void* graph_exec);
  * c3h_im2col_args, c3h_layout_args, c3h_pool_args, c3h_epilogue,
  * c3h_gemm_args, c3h_conv_args, c3h_attn_scores_args, c3h_flash_args,
  * c3h_quantize_args, c3h_qgemm_args, c3h_dequantize_args, c3h_op,
- * c3h_pack_args.
+ * c3h_pack_args, c3h_conv_pool_args.
  * Returns the number of sizes available (host-only; needs no GPU). */
 int32_t c3h_abi_sizes(int64_t* out, int32_t capacity);
 

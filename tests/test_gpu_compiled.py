@@ -29,7 +29,7 @@ SMALL = {
 }
 
 
-def _compiled(m, policy: str, use_graph: bool = True):
+def _compiled(m, policy: str, use_graph: bool = True, **kw):
     from hackathon_amd.c32.strategy import PrecisionPolicy
     from hackathon_amd.c33.pipeline import GraphPassPipeline
     from hackathon_amd.c34.scheduler import ExecutionScheduler
@@ -42,7 +42,8 @@ def _compiled(m, policy: str, use_graph: bool = True):
     batch = next(iter(m.inputs.values())).shape[0]
     plan = ExecutionScheduler(m.graph, batch_size=batch, precision_policy=PrecisionPolicy(policy)).build()
     assert plan.validate() == []
-    prog = CompiledPlan(m.graph, plan, ex.weight_sources(), ex.host_constants, policy=policy, use_graph=use_graph)
+    prog = CompiledPlan(m.graph, plan, ex.weight_sources(), ex.host_constants, policy=policy, use_graph=use_graph,
+                        **kw)
     return plan, prog, {**m.weights, **folded}
 
 
@@ -132,3 +133,21 @@ def test_compiled_graph_replay_matches_eager(gpu):
         a = _logits(graph_prog, feed)["logits"]
         b = _logits(eager_prog, feed)["logits"]
         np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("policy", ["bf16", "fp16"])
+def test_compiled_stem_pool_fusion_is_exact(gpu, policy):
+    """Conv 7x7/2 -> BN -> ReLU -> MaxPool as one fused launch gives the unfused logits exactly."""
+    from hackathon_amd import models
+
+    kw = dict(batch=3, image=72, widths=(64, 32, 32, 64), classes=10)
+    m1 = models.build("resnet18_224", **kw)
+    m2 = copy.deepcopy(m1)
+    _, fused, _ = _compiled(m1, policy)
+    _, plain, _ = _compiled(m2, policy, fuse_stem=False)
+    kinds = [k for k in fused.node_kinds]
+    assert "conv:stem_pool" in kinds and "maxpool" not in kinds and "layout" not in kinds
+    assert "maxpool" in plain.node_kinds
+    a = _logits(fused, m1.inputs)["logits"]
+    b = _logits(plain, m2.inputs)["logits"]
+    np.testing.assert_array_equal(a, b)

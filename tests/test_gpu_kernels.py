@@ -385,3 +385,70 @@ def test_quantize_vectorized_bit_exact(gpu, kind):
     a.x_dtype = {"fp32": _lib.F32, "bf16": _lib.BF16, "fp16": _lib.F16}[kind]
     _lib.launch(a, None)
     np.testing.assert_array_equal(out.get(), R.quantize(xr, np.float32(0.5), 0))
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+@pytest.mark.parametrize("n,h,w,relu,in_kind", [(2, 64, 64, 1, "fp32"), (3, 70, 57, 1, "fp32"), (1, 45, 83, 0, "fp32"),
+                                                (2, 38, 40, 1, "same")])
+def test_conv_stem_pool_matches_unfused_chain(gpu, kind, n, h, w, relu, in_kind):
+    """c3h_conv_stem_pool == layout -> c3h_conv2d (bias, relu) -> c3h_maxpool2d, bit for bit;
+    and within 16-bit rounding of a float64 conv + max pool of the rounded operands."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    rng = np.random.default_rng(h * w + n)
+    x, wt, b, attrs = _conv_case(rng, n, 3, h, w, 64, 7, 7, 2, 3)
+    code = {"bf16": _lib.BF16, "fp16": _lib.F16}[kind]
+    sdt = {"bf16": BF16, "fp16": np.float16}[kind]
+    ho, wo = (h + 6 - 7) // 2 + 1, (w + 6 - 7) // 2 + 1
+    po, qo = (ho + 2 - 3) // 2 + 1, (wo + 2 - 3) // 2 + 1
+    xd = _dev(x) if in_kind == "fp32" else _dev(_bits(x, kind)[0])
+    wp = E.pack_conv_weight(_dev(wt), 4, 8, 224, out_dtype=sdt)
+    bd = _dev(b)
+    # unfused chain through the C ABI
+    xn = E.to_nhwc(xd, 4, out_dtype=sdt)
+    conv = DeviceArray.empty((n, ho, wo, 64), sdt)
+    a = _lib.ConvArgs()
+    a.x, a.w, a.out = xn.ptr, wp.ptr, conv.ptr
+    a.n, a.c, a.h, a.w_, a.c_stride, a.c_pack, a.o = n, 3, h, w, 4, 4, 64
+    a.kh, a.kw, a.sh, a.sw, a.pad_top, a.pad_left, a.dh, a.dw, a.ho, a.wo = 7, 7, 2, 2, 3, 3, 1, 1, ho, wo
+    a.out_layout, a.in_dtype, a.out_dtype = 1, code, code
+    a.epi = E.epilogue(bias=bd, bias_mode=2, act=relu)
+    _lib.launch(a, None)
+    pooled = DeviceArray.empty((n, po, qo, 64), sdt)
+    pa = _lib.PoolArgs()
+    pa.x, pa.out, pa.n, pa.c, pa.h, pa.w = conv.ptr, pooled.ptr, n, 64, ho, wo
+    pa.kh, pa.kw, pa.sh, pa.sw, pa.pad_top, pa.pad_left, pa.dh, pa.dw = 3, 3, 2, 2, 1, 1, 1, 1
+    pa.ho, pa.wo, pa.layout, pa.c_stride, pa.dtype = po, qo, 1, 64, code
+    _lib.launch(pa, None)
+    # fused
+    fused = DeviceArray.empty((n, po, qo, 64), sdt)
+    f = _lib.ConvPoolArgs()
+    f.x, f.w, f.bias, f.out = xd.ptr, wp.ptr, bd.ptr, fused.ptr
+    f.n, f.c, f.h, f.w_, f.o, f.k_stride = n, 3, h, w, 64, 224
+    f.kh, f.kw, f.sh, f.sw, f.pad_top, f.pad_left, f.ho, f.wo = 7, 7, 2, 2, 3, 3, ho, wo
+    f.pkh, f.pkw, f.psh, f.psw, f.ppad_top, f.ppad_left, f.po, f.qo = 3, 3, 2, 2, 1, 1, po, qo
+    f.relu, f.in_dtype, f.mm_dtype = relu, _lib.F32 if in_kind == "fp32" else code, code
+    print(f"conv_stem_pool {kind} n={n} {h}x{w} relu={relu} in={in_kind}", flush=True)
+    _lib.launch(f, None)
+    got = fused.get()
+    np.testing.assert_array_equal(got.view(np.uint16), pooled.get().view(np.uint16))
+    xr, wr = G.round_to(x, kind), G.round_to(wt, kind)
+    ref = R.conv2d(xr.astype(np.float64), wr.astype(np.float64), attrs) + b.reshape(1, 64, 1, 1)
+    ref = np.maximum(ref, 0) if relu else ref
+    ref = R.maxpool2d(ref.astype(np.float32), {"kernel_shape": [3, 3], "strides": [2, 2], "pads": [1, 1, 1, 1]})
+    np.testing.assert_allclose(_from16(got, kind).transpose(0, 3, 1, 2), ref, rtol=1e-2, atol=1e-2)
+
+
+def test_conv_stem_pool_rejects_other_geometry(gpu):
+    from hackathon_amd import _lib
+
+    f = _lib.ConvPoolArgs()
+    f.x = f.w = f.out = 16
+    f.n, f.c, f.h, f.w_, f.o, f.k_stride = 1, 3, 32, 32, 64, 224
+    f.kh, f.kw, f.sh, f.sw, f.pad_top, f.pad_left, f.ho, f.wo = 5, 5, 2, 2, 2, 2, 16, 16
+    f.pkh, f.pkw, f.psh, f.psw, f.ppad_top, f.ppad_left, f.po, f.qo = 3, 3, 2, 2, 1, 1, 8, 8
+    f.mm_dtype, f.in_dtype = _lib.BF16, _lib.F32
+    with pytest.raises(_lib.C3HError, match="7x7"):
+        _lib.launch(f, None)

@@ -237,3 +237,25 @@ def test_invariant_division_multiplier_is_exact():
         np.testing.assert_array_equal(q, ns // np.uint64(d))
         for n in (d - 1, d, d + 1, 2 * d - 1, (2 ** 31 - 1) // d * d):
             assert ((n * mul >> 32) + n) >> l == n // d
+
+
+def test_compiled_fuses_stem_conv_relu_maxpool(fake_lib):
+    """A 7x7/2 stem to 64 channels followed by ReLU and a 3x3/2 max pool is one launch
+    that reads the NCHW input directly (no layout pass, no maxpool launch)."""
+    from hackathon_amd import models
+    from hackathon_amd.c35.compiled import CompiledPlan
+    from hackathon_amd.c35.executor import PlannedGraphExecutor
+
+    m = models.build("resnet18_224", batch=2, image=64, widths=(64, 32, 32, 64), classes=10)
+    plan = _plan(m, "bf16")
+    ex = PlannedGraphExecutor(m.graph, m.weights)
+    prog = CompiledPlan(m.graph, plan, ex.weight_sources(), ex.host_constants, policy="bf16")
+    assert prog.node_kinds[0] == "conv:stem_pool"
+    kinds = collections.Counter(k.split(":")[0] for k in prog.node_kinds)
+    assert dict(kinds) == {"conv": 20, "gap": 1, "gemm": 1}
+    a = prog._args[0]
+    assert (a.kh, a.sh, a.pad_top, a.o, a.relu, a.po, a.qo) == (7, 2, 3, 64, 1, 16, 16)
+    assert a.in_dtype == 0  # reads the fp32 NCHW graph input
+    plain = CompiledPlan(m.graph, plan, ex.weight_sources(), ex.host_constants, policy="bf16", fuse_stem=False)
+    assert collections.Counter(k.split(":")[0] for k in plain.node_kinds) == {
+        "layout": 1, "conv": 20, "maxpool": 1, "gap": 1, "gemm": 1}
