@@ -997,7 +997,7 @@ class CompiledPlan:
             return False
         n, _, h, w = x.shape
         _, _, _, _, _, _, _, po, qo = E.conv_geometry((n, o, ho, wo), (0, 0, 3, 3), pool.attributes)
-        if not (2 * (po - 1) - 1 < ho and 2 * (qo - 1) - 1 < wo):
+        if not (2 * (po - 1) < ho and 2 * (qo - 1) < wo):
             return False
         out = self._new((n, o, po, qo), self.act_dtype, "nhwc", o)
         bias = self._bias_val(bias_name)

@@ -53,11 +53,22 @@ __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + 
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
+// gfx950 converts in hardware (v_cvt_pk_bf16_f32): round to nearest even,
+// NaN quieted as (bits >> 16) | 0x40, denormals kept.  Checked equal to the
+// integer formulation (u + 0x7fff + lsb) >> 16 for all 2^32 inputs.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+// Two values -> one packed pair (lo in bits 0-15): a single v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
+  typedef __attribute__((ext_vector_type(2))) float f2;
+  typedef __attribute__((ext_vector_type(2))) __bf16 b2;
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{lo, hi}, b2));
+}
+__device__ __forceinline__ uint32_t f32x2_to_f16x2_bits(float lo, float hi) {
+  typedef __attribute__((ext_vector_type(2))) float f2;
+  typedef __attribute__((ext_vector_type(2))) _Float16 h2;
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{lo, hi}, h2));
 }
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
   _Float16 v;
@@ -116,7 +127,7 @@ template <> struct Elem<float> {
 struct bf16_t { uint16_t bits; };
 struct f16_t { uint16_t bits; };
 
-template <typename T, float (*ToF)(uint16_t), uint16_t (*FromF)(float)>
+template <typename T, float (*ToF)(uint16_t), uint16_t (*FromF)(float), uint32_t (*Pack2)(float, float)>
 struct Elem16 {
   static __device__ __forceinline__ float to_f32(T v) { return ToF(v.bits); }
   static __device__ __forceinline__ T from_f32(float v) { return T{FromF(v)}; }
@@ -132,13 +143,12 @@ struct Elem16 {
   static __device__ __forceinline__ void store8(T* p, const float* v) {
     uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = static_cast<uint32_t>(FromF(v[2 * i])) | (static_cast<uint32_t>(FromF(v[2 * i + 1])) << 16);
+    for (int i = 0; i < 4; ++i) w[i] = Pack2(v[2 * i], v[2 * i + 1]);
     *reinterpret_cast<uint4*>(p) = uint4{w[0], w[1], w[2], w[3]};
   }
 };
-template <> struct Elem<bf16_t> : Elem16<bf16_t, bf16_bits_to_f32, f32_to_bf16_bits> {};
-template <> struct Elem<f16_t> : Elem16<f16_t, f16_bits_to_f32, f32_to_f16_bits> {};
+template <> struct Elem<bf16_t> : Elem16<bf16_t, bf16_bits_to_f32, f32_to_bf16_bits, f32x2_to_bf16x2_bits> {};
+template <> struct Elem<f16_t> : Elem16<f16_t, f16_bits_to_f32, f32_to_f16_bits, f32x2_to_f16x2_bits> {};
 
 // 16 bytes of T <-> fp32 values (8 for 16-bit types, 4 for fp32).
 template <typename T>

@@ -1,5 +1,5 @@
 // Fused image-network stem for gfx950: Conv 7x7 / stride 2 / pad 3 over a
-// narrow (c <= 4) NCHW input, + per-channel bias, + optional ReLU, then
+// narrow (c <= 3) NCHW input, + per-channel bias, + optional ReLU, then
 // MaxPool 3x3 / stride 2 / pad 1, written channels-last in 16-bit.
 //
 // Unfused, this is three launches and four HBM passes over the conv output
@@ -7,17 +7,24 @@
 // fused, the conv output never leaves LDS.  Results are identical to the
 // unfused sequence: inputs are rounded to 16 bits exactly as the layout
 // kernel does, the conv uses the same MFMA (16x16x32, K chunk order and
-// accumulation order of c3h_conv2d's narrow-channel packing), and the
-// maximum of 16-bit-rounded values equals the rounding of the maximum.
+// accumulation order of c3h_conv2d's narrow-channel packing), the epilogue
+// performs the same float operations, and the maximum of 16-bit-rounded
+// values equals the rounding of the maximum.
 //
 // Work decomposition: a tile is 4 x 8 pooled pixels x 64 channels of one
-// image.  It needs a 9 x 17 conv-output tile (153 pixels, 10 MFMA row
+// image.  It needs a 9 x 17 conv-output tile (153 pixels, 10 MFMA column
 // tiles), which needs a 23 x 40 x 4 input patch.  A persistent workgroup
 // (4 waves) walks a contiguous range of tiles: the next tile's patch is
 // loaded into registers while the current tile's MFMAs run, so global
 // latency hides behind compute, and neighbouring tiles share their input
-// halo in the workgroup's L2.  Every wave keeps the whole packed weight
-// (64 x 224, as 28 MFMA B fragments) in registers for the kernel's life.
+// halo in L2.  Every wave keeps the whole packed weight (64 x 224, as 28
+// MFMA fragments) in registers for the kernel's life.
+//
+// The MFMA computes C^T = W . X^T, so a lane's four accumulators are four
+// consecutive channels of one conv pixel: bias, ReLU and the 16-bit
+// rounding run on them in registers and leave as one 8-byte LDS store.
+// After ReLU every value is +0 or positive, whose 16-bit patterns order like
+// the values, so the pool takes packed unsigned 16-bit maxima.
 #include "common.h"
 
 using namespace c3h;
@@ -27,6 +34,7 @@ namespace {
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(2))) unsigned short u16x2;
 
 constexpr int kThreads = 256;
 constexpr int KH = 7, KWP = 8, CP = 4;  // filter rows, packed filter columns, packed channels
@@ -36,28 +44,35 @@ constexpr int PH = 4, PW = 8;           // pooled tile (rows, columns)
 constexpr int CTH = 2 * PH + 1;         // 9 conv tile rows
 constexpr int CTW = 2 * PW + 1;         // 17 conv tile columns
 constexpr int CPIX = CTH * CTW;         // 153 conv pixels per tile
-constexpr int MT = (CPIX + 15) / 16;    // 10 MFMA row tiles
+constexpr int MT = (CPIX + 15) / 16;    // 10 MFMA pixel tiles
 constexpr int PR = 2 * (CTH - 1) + KH;  // 23 patch rows
 constexpr int PC = 2 * (CTW - 1) + KWP; // 40 patch columns
 constexpr int PROW = PC * CP * 2;       // 320 bytes per patch row
 constexpr int PATCH_BYTES = PR * PROW;  // 7360
-constexpr int CS = 192;                 // conv-tile row bytes (128 used): conflict-free pool reads
-constexpr int CT_BYTES = CPIX * CS;     // 29376
+constexpr int CS = 136;                 // conv-tile pixel stride (128 used): conflict-free 8-byte stores
+constexpr int CT_BYTES = CPIX * CS;     // 20808
 constexpr int SLOTS = (PR * PC + kThreads - 1) / kThreads;  // 4 patch pixels per thread
-constexpr int TPW = (MT + 3) / 4;       // 3 row tiles per wave (waves 2 and 3 have 2)
+constexpr int TPW = (MT + 3) / 4;       // 3 pixel tiles per wave (waves 2 and 3 have 2)
+constexpr uint32_t kOob = 0x80000000u;  // buffer offset past num_records: reads 0
 static_assert(PH * PW * 8 == kThreads, "one pooled item (8 channels) per thread");
 
 template <typename T> struct In;
 template <> struct In<float> {
-  static __device__ __forceinline__ uint32_t load(const float* p) { return __float_as_uint(*p); }
+  static __device__ __forceinline__ uint32_t load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  }
   static __device__ __forceinline__ float f32(uint32_t v) { return __uint_as_float(v); }
 };
 template <> struct In<bf16_t> {
-  static __device__ __forceinline__ uint32_t load(const bf16_t* p) { return p->bits; }
+  static __device__ __forceinline__ uint32_t load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  }
   static __device__ __forceinline__ float f32(uint32_t v) { return bf16_bits_to_f32(static_cast<uint16_t>(v)); }
 };
 template <> struct In<f16_t> {
-  static __device__ __forceinline__ uint32_t load(const f16_t* p) { return p->bits; }
+  static __device__ __forceinline__ uint32_t load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  }
   static __device__ __forceinline__ float f32(uint32_t v) { return f16_bits_to_f32(static_cast<uint16_t>(v)); }
 };
 
@@ -67,7 +82,7 @@ template <> struct Mm<bf16_t> {
   static __device__ __forceinline__ f32x4 mma(uint4 a, uint4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(vec, a), __builtin_bit_cast(vec, b), c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint32_t bits(float v) { return f32_to_bf16_bits(v); }
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return f32x2_to_bf16x2_bits(lo, hi); }
   static __device__ __forceinline__ float f32(uint32_t b) { return bf16_bits_to_f32(static_cast<uint16_t>(b)); }
 };
 template <> struct Mm<f16_t> {
@@ -75,7 +90,7 @@ template <> struct Mm<f16_t> {
   static __device__ __forceinline__ f32x4 mma(uint4 a, uint4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vec, a), __builtin_bit_cast(vec, b), c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint32_t bits(float v) { return f32_to_f16_bits(v); }
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return f32x2_to_f16x2_bits(lo, hi); }
   static __device__ __forceinline__ float f32(uint32_t b) { return f16_bits_to_f32(static_cast<uint16_t>(b)); }
 };
 
@@ -83,7 +98,13 @@ struct StemGeom {
   int64_t tiles;
   int n, c, h, w, ho, wo, po, qo, tq, tpi;
   int relu;
+  uint32_t image_bytes;  // c * h * w * sizeof(input element)
 };
+
+__device__ __forceinline__ uint32_t umax16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
+                                                                __builtin_bit_cast(u16x2, b)));
+}
 
 template <typename TI, typename T16>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -98,21 +119,24 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
 
-  // Whole weight as B fragments: lane (n = 16 j + l16, k = 32 kh + 8 lg .. + 7).
+  // Whole weight as MFMA A fragments: lane (channel 16 j + l16, k = 32 kh + 8 lg .. + 7).
   uint4 bw[KH][4];
 #pragma unroll
   for (int kh = 0; kh < KH; ++kh)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       bw[kh][j] = *reinterpret_cast<const uint4*>(wp + (16 * j + l16) * KSTRIDE + 32 * kh + 8 * lg);
-  float bv[4];
+  // Bias of the lane's accumulator channels 16 j + 4 lg + r.
+  float bv[4][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) bv[j] = bias ? bias[16 * j + l16] : 0.0f;
-  // Packed column kw = 7 only pads the filter: zero its half of the A operand so
-  // that non-finite inputs there cannot turn 0 * x into NaN.
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bv[j][r] = bias ? bias[16 * j + 4 * lg + r] : 0.0f;
+  // Packed column kw = 7 only pads the filter: zero its half of the patch
+  // operand so that non-finite inputs there cannot turn 0 * x into NaN.
   const uint32_t kw7_mask = lg == 3 ? 0u : 0xffffffffu;
 
-  // A-fragment byte offsets in the patch for this wave's row tiles (pixel m = 16 i + l16).
+  // Patch byte offsets of this lane's pixel (m = 16 i + l16) in each of the wave's pixel tiles.
   int aoff[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
@@ -121,28 +145,39 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
     const int r = m / CTW, c = m - r * CTW;
     aoff[t] = 2 * r * PROW + (2 * c + 2 * lg) * (CP * 2);
   }
+  // This thread's patch slots: fixed (row, col) inside every tile.
+  int s_row[SLOTS], s_col[SLOTS];
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    const int slot = tid + s * kThreads;
+    s_row[s] = slot / PC;
+    s_col[s] = slot - s_row[s] * PC;
+  }
+  const uint32_t plane_bytes = static_cast<uint32_t>(g.h) * g.w * sizeof(TI);
 
   const int64_t G = gridDim.x;
   const int64_t t_begin = g.tiles * blockIdx.x / G, t_end = g.tiles * (blockIdx.x + 1) / G;
-  const int64_t plane = static_cast<int64_t>(g.h) * g.w;
+  // Tile coordinates, advanced incrementally (no division in the loop).
+  int img = static_cast<int>(t_begin / g.tpi);
+  int rem = static_cast<int>(t_begin - static_cast<int64_t>(img) * g.tpi);
+  int pt = rem / g.tq, qt = rem - pt * g.tq;
 
   uint32_t pre[SLOTS][3];
-  auto fetch = [&](int64_t t) {
-    const int img = static_cast<int>(t / g.tpi);
-    const int rem = static_cast<int>(t - static_cast<int64_t>(img) * g.tpi);
-    const int pt = rem / g.tq, qt = rem - pt * g.tq;
-    const int hi0 = 4 * PH * pt - 5, wi0 = 4 * PW * qt - 5;
-    const TI* base = x + static_cast<int64_t>(img) * g.c * plane;
+  auto fetch = [&](int f_img, int f_pt, int f_qt) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<TI*>(x + static_cast<int64_t>(f_img) * g.c * g.h * g.w), 0, static_cast<int>(g.image_bytes),
+        0x00020000);
+    const int hi0 = 4 * PH * f_pt - 5, wi0 = 4 * PW * f_qt - 5;
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
-      const int slot = tid + s * kThreads;
-      const int row = slot / PC, col = slot - row * PC;
-      const int hi = hi0 + row, wi = wi0 + col;
-      const bool ok = slot < PR * PC && col < PC - 1 && static_cast<unsigned>(hi) < static_cast<unsigned>(g.h) &&
+      const int hi = hi0 + s_row[s], wi = wi0 + s_col[s];
+      const bool ok = tid + s * kThreads < PR * PC && s_col[s] < PC - 1 &&
+                      static_cast<unsigned>(hi) < static_cast<unsigned>(g.h) &&
                       static_cast<unsigned>(wi) < static_cast<unsigned>(g.w);
-      const TI* px = base + static_cast<int64_t>(hi) * g.w + wi;
+      const uint32_t off = ok ? static_cast<uint32_t>((hi * g.w + wi) * static_cast<int>(sizeof(TI))) : kOob;
 #pragma unroll
-      for (int ch = 0; ch < 3; ++ch) pre[s][ch] = (ok && ch < g.c) ? In<TI>::load(px + ch * plane) : 0u;
+      for (int ch = 0; ch < 3; ++ch)
+        pre[s][ch] = In<TI>::load(rs, (ok && ch < g.c) ? off + ch * plane_bytes : kOob);
     }
   };
   auto stash = [&]() {
@@ -150,20 +185,29 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
     for (int s = 0; s < SLOTS; ++s) {
       const int slot = tid + s * kThreads;
       if (slot < PR * PC) {
-        const uint32_t c0 = MM::bits(In<TI>::f32(pre[s][0])), c1 = MM::bits(In<TI>::f32(pre[s][1]));
-        const uint32_t c2 = MM::bits(In<TI>::f32(pre[s][2]));
-        *reinterpret_cast<uint2*>(patch + slot * (CP * 2)) = uint2{c0 | (c1 << 16), c2};
+        const uint32_t c01 = MM::pack(In<TI>::f32(pre[s][0]), In<TI>::f32(pre[s][1]));
+        const uint32_t c2 = MM::pack(In<TI>::f32(pre[s][2]), 0.0f);
+        *reinterpret_cast<uint2*>(patch + slot * (CP * 2)) = uint2{c01, c2};
       }
     }
   };
 
   if (t_begin < t_end) {
-    fetch(t_begin);
+    fetch(img, pt, qt);
     stash();
   }
   __syncthreads();
   for (int64_t t = t_begin; t < t_end; ++t) {
-    if (t + 1 < t_end) fetch(t + 1);
+    // coordinates of tile t + 1
+    int n_img = img, n_pt = pt, n_qt = qt + 1;
+    if (n_qt == g.tq) {
+      n_qt = 0;
+      if (++n_pt * g.tq == g.tpi) {
+        n_pt = 0;
+        ++n_img;
+      }
+    }
+    if (t + 1 < t_end) fetch(n_img, n_pt, n_qt);
 
     f32x4 acc[TPW][4];
 #pragma unroll
@@ -179,52 +223,66 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
           a.z &= kw7_mask;
           a.w &= kw7_mask;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = MM::mma(a, bw[kh][j], acc[i][j]);
+          for (int j = 0; j < 4; ++j) acc[i][j] = MM::mma(bw[kh][j], a, acc[i][j]);
         }
       }
     }
-    // bias + ReLU, rounded to 16 bits, into the conv tile [pixel][channel].
+    // bias (+ the absent residual's +0, as c3h_conv2d) + ReLU, rounded, into the conv tile [pixel][channel].
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
-      if (wave + 4 * i < MT) {
+      const int m = 16 * (wave + 4 * i) + l16;
+      if (wave + 4 * i < MT && m < CPIX) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = 16 * (wave + 4 * i) + 4 * lg + r;
-          if (m < CPIX) {
+        for (int j = 0; j < 4; ++j) {
+          float v[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              float v = acc[i][j][r] + bv[j];
-              v += 0.0f;  // as c3h_conv2d's epilogue (adds the absent residual): -0 becomes +0
-              if (g.relu) v = fmaxf(v, 0.0f);
-              *reinterpret_cast<uint16_t*>(ctile + m * CS + (16 * j + l16) * 2) = static_cast<uint16_t>(MM::bits(v));
-            }
+          for (int r = 0; r < 4; ++r) {
+            v[r] = (acc[i][j][r] + bv[j][r]) + 0.0f;
+            if (g.relu) v[r] = v[r] > 0.0f ? v[r] : 0.0f;
           }
+          *reinterpret_cast<uint2*>(ctile + m * CS + (16 * j + 4 * lg) * 2) =
+              uint2{MM::pack(v[0], v[1]), MM::pack(v[2], v[3])};
         }
       }
     }
     __syncthreads();
     if (t + 1 < t_end) stash();  // every wave is past its patch reads
-    // 3x3 / stride 2 max over valid conv pixels; 8 channels per item.
+    // 3x3 / stride 2 max over the valid conv pixels of each pooled pixel, 8 channels per thread.
     {
-      const int img = static_cast<int>(t / g.tpi);
-      const int rem = static_cast<int>(t - static_cast<int64_t>(img) * g.tpi);
-      const int pt = rem / g.tq, qt = rem - pt * g.tq;
-      {
-        const int px = tid >> 3, cg = tid & 7;
-        const int pr = px / PW, qc = px - pr * PW;
-        const int P = PH * pt + pr, Q = PW * qt + qc;
-        if (P < g.po && Q < g.qo) {
+      const int px = tid >> 3, cg = tid & 7;
+      const int pr = px / PW, qc = px - pr * PW;
+      const int P = PH * pt + pr, Q = PW * qt + qc;
+      if (P < g.po && Q < g.qo) {
+        uint4 res;
+        if (g.relu) {
+          // Every window holds the valid pixel (2 pr + 1, 2 qc + 1); invalid
+          // positions re-read it, which leaves the maximum unchanged.
+          uint32_t mx[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+          for (int dr = 0; dr < 3; ++dr) {
+            const bool rok = static_cast<unsigned>(2 * P - 1 + dr) < static_cast<unsigned>(g.ho);
+#pragma unroll
+            for (int dc = 0; dc < 3; ++dc) {
+              const bool ok = rok && static_cast<unsigned>(2 * Q - 1 + dc) < static_cast<unsigned>(g.wo);
+              const int m = ok ? (2 * pr + dr) * CTW + 2 * qc + dc : (2 * pr + 1) * CTW + 2 * qc + 1;
+              const uint4 v = *reinterpret_cast<const uint4*>(ctile + m * CS + cg * 16);
+              mx[0] = umax16x2(mx[0], v.x);
+              mx[1] = umax16x2(mx[1], v.y);
+              mx[2] = umax16x2(mx[2], v.z);
+              mx[3] = umax16x2(mx[3], v.w);
+            }
+          }
+          res = uint4{mx[0], mx[1], mx[2], mx[3]};
+        } else {
           float mx[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) mx[e] = -__builtin_huge_valf();
 #pragma unroll
           for (int dr = 0; dr < 3; ++dr) {
-            const int cr = 2 * P - 1 + dr;
-            if (static_cast<unsigned>(cr) >= static_cast<unsigned>(g.ho)) continue;
+            if (static_cast<unsigned>(2 * P - 1 + dr) >= static_cast<unsigned>(g.ho)) continue;
 #pragma unroll
             for (int dc = 0; dc < 3; ++dc) {
-              const int cc = 2 * Q - 1 + dc;
-              if (static_cast<unsigned>(cc) >= static_cast<unsigned>(g.wo)) continue;
+              if (static_cast<unsigned>(2 * Q - 1 + dc) >= static_cast<unsigned>(g.wo)) continue;
               const int m = (2 * pr + dr) * CTW + 2 * qc + dc;
               const uint4 v = *reinterpret_cast<const uint4*>(ctile + m * CS + cg * 16);
               const uint32_t wds[4] = {v.x, v.y, v.z, v.w};
@@ -235,15 +293,16 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
               }
             }
           }
-          uint32_t o4[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o4[e] = MM::bits(mx[2 * e]) | (MM::bits(mx[2 * e + 1]) << 16);
-          const int64_t o = ((static_cast<int64_t>(img) * g.po + P) * g.qo + Q) * O + cg * 8;
-          *reinterpret_cast<uint4*>(out + o) = uint4{o4[0], o4[1], o4[2], o4[3]};
+          res = uint4{MM::pack(mx[0], mx[1]), MM::pack(mx[2], mx[3]), MM::pack(mx[4], mx[5]), MM::pack(mx[6], mx[7])};
         }
+        const int64_t o = ((static_cast<int64_t>(img) * g.po + P) * g.qo + Q) * O + cg * 8;
+        *reinterpret_cast<uint4*>(out + o) = res;
       }
     }
     __syncthreads();
+    img = n_img;
+    pt = n_pt;
+    qt = n_qt;
   }
 }
 
@@ -270,14 +329,16 @@ int c3h_conv_stem_pool(const c3h_conv_pool_args* a, void* stream) {
               "conv_stem_pool: supports a 7x7 / stride 2 / pad 3 conv to 64 channels (packed K stride 224)");
   C3H_REQUIRE(a->pkh == 3 && a->pkw == 3 && a->psh == 2 && a->psw == 2 && a->ppad_top == 1 && a->ppad_left == 1,
               "conv_stem_pool: supports a 3x3 / stride 2 / pad 1 max pool");
-  C3H_REQUIRE(a->ho > 0 && a->wo > 0 && a->po > 0 && a->qo > 0 && 2 * (a->po - 1) - 1 < a->ho &&
-                  2 * (a->qo - 1) - 1 < a->wo,
+  // Every pooled window's centre conv pixel must exist (true for pool pads 1/1).
+  C3H_REQUIRE(a->ho > 0 && a->wo > 0 && a->po > 0 && a->qo > 0 && 2 * (a->po - 1) < a->ho && 2 * (a->qo - 1) < a->wo,
               "conv_stem_pool: inconsistent conv/pool output sizes");
   C3H_REQUIRE(a->mm_dtype == C3H_BF16 || a->mm_dtype == C3H_F16, "conv_stem_pool: compute dtype must be BF16 or F16");
   C3H_REQUIRE(a->in_dtype == C3H_F32 || a->in_dtype == C3H_BF16 || a->in_dtype == C3H_F16,
               "conv_stem_pool: input dtype must be F32, BF16 or F16");
   C3H_REQUIRE((reinterpret_cast<uintptr_t>(a->w) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 15) == 0,
               "conv_stem_pool: weight and output must be 16-byte aligned");
+  const int64_t image_bytes = static_cast<int64_t>(a->c) * a->h * a->w_ * dtype_size(a->in_dtype);
+  C3H_REQUIRE(image_bytes < (int64_t{1} << 31), "conv_stem_pool: one input image must be below 2 GiB");
   if (a->n == 0) return C3H_OK;
   StemGeom g;
   g.n = a->n; g.c = a->c; g.h = a->h; g.w = a->w_; g.ho = a->ho; g.wo = a->wo; g.po = a->po; g.qo = a->qo;
@@ -285,6 +346,7 @@ int c3h_conv_stem_pool(const c3h_conv_pool_args* a, void* stream) {
   g.tpi = ((a->po + PH - 1) / PH) * g.tq;
   g.tiles = static_cast<int64_t>(a->n) * g.tpi;
   g.relu = a->relu ? 1 : 0;
+  g.image_bytes = static_cast<uint32_t>(image_bytes);
   const int grid = static_cast<int>(g.tiles < stem_grid() ? g.tiles : stem_grid());
   hipStream_t s = as_stream(stream);
   const uint16_t* w = static_cast<const uint16_t*>(a->w);

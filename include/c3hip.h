@@ -456,7 +456,8 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream);
  * + MaxPool 3x3 / stride 2 / pad 1.  x is NCHW (F32, BF16 or F16, rounded to
  * mm_dtype on load); w is the narrow-channel packing of c3h_conv2d
  * ([64][kh][kw_pack = 8][c_pack = 4], k_stride 224); out is NHWC
- * [n, po, qo, 64] in mm_dtype.  Bit-identical to layout -> c3h_conv2d
+ * [n, po, qo, 64] in mm_dtype (each pooled window's centre conv pixel must
+ * lie inside [ho, wo]).  Bit-identical to layout -> c3h_conv2d
  * (bias, relu) -> c3h_maxpool2d; replaces that chain for the Conv
  * (+BatchNormalization) + Relu + MaxPool nodes of c32/decompositions.py
  * :300-375 and the MaxPool that the reference registry lacks. */

@@ -452,3 +452,20 @@ def test_conv_stem_pool_rejects_other_geometry(gpu):
     f.mm_dtype, f.in_dtype = _lib.BF16, _lib.F32
     with pytest.raises(_lib.C3HError, match="7x7"):
         _lib.launch(f, None)
+
+
+def test_bf16_narrowing_is_round_to_nearest_even_bit_exact(gpu):
+    """fp32 -> bf16 (the hardware conversion every 16-bit epilogue uses) equals the integer
+    round-to-nearest-even formula on ties, denormals, infinities, NaN payloads and random patterns."""
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray, f32_to_bf16
+
+    special = np.array([0x3F808000, 0x3F818000, 0x3F80FFFF, 0x00000001, 0x007FFFFF, 0x00008000, 0x00018000,
+                        0x7F800000, 0xFF800000, 0x7F7FFFFF, 0x7F7F8000, 0x80000000, 0x7F800001, 0xFFC00001,
+                        0x7FFFFFFF, 0x7FBFFFFF, 0x807F8000], np.uint32)
+    rnd = np.random.default_rng(11).integers(0, 2 ** 32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    bits = np.concatenate([special, rnd])
+    x = DeviceArray.from_host(bits.view(np.float32))
+    out = DeviceArray.empty(x.shape, BF16)
+    E.cast_into(x, out)
+    np.testing.assert_array_equal(out.get().view(np.uint16), f32_to_bf16(bits.view(np.float32)).view(np.uint16))
