@@ -122,6 +122,13 @@ template <> struct Elem<float> {
     reinterpret_cast<float4*>(p)[0] = float4{v[0], v[1], v[2], v[3]};
     reinterpret_cast<float4*>(p)[1] = float4{v[4], v[5], v[6], v[7]};
   }
+  static __device__ __forceinline__ void load4(const float* p, float* v) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  }
+  static __device__ __forceinline__ void store4(float* p, const float* v) {
+    *reinterpret_cast<float4*>(p) = float4{v[0], v[1], v[2], v[3]};
+  }
 };
 
 struct bf16_t { uint16_t bits; };
@@ -145,6 +152,17 @@ struct Elem16 {
 #pragma unroll
     for (int i = 0; i < 4; ++i) w[i] = Pack2(v[2 * i], v[2 * i + 1]);
     *reinterpret_cast<uint4*>(p) = uint4{w[0], w[1], w[2], w[3]};
+  }
+  // 4 consecutive elements, 8-byte aligned.
+  static __device__ __forceinline__ void load4(const T* p, float* v) {
+    const uint2 q = *reinterpret_cast<const uint2*>(p);
+    v[0] = ToF(static_cast<uint16_t>(q.x & 0xffffu));
+    v[1] = ToF(static_cast<uint16_t>(q.x >> 16));
+    v[2] = ToF(static_cast<uint16_t>(q.y & 0xffffu));
+    v[3] = ToF(static_cast<uint16_t>(q.y >> 16));
+  }
+  static __device__ __forceinline__ void store4(T* p, const float* v) {
+    *reinterpret_cast<uint2*>(p) = uint2{Pack2(v[0], v[1]), Pack2(v[2], v[3])};
   }
 };
 template <> struct Elem<bf16_t> : Elem16<bf16_t, bf16_bits_to_f32, f32_to_bf16_bits, f32x2_to_bf16x2_bits> {};

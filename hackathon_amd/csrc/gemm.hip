@@ -13,6 +13,7 @@
 // same XCD and hit its L2.
 #include <stdlib.h>
 #include <type_traits>
+#include <utility>
 
 #include "common.h"
 
@@ -686,6 +687,84 @@ __device__ __forceinline__ void store_strip_q(const float* stage, int lane, int6
   }
 }
 
+// Epilogue straight from C^T accumulators (16-bit and fp32 MFMA kernels,
+// which multiply with the operands swapped): acc[i][j][r] is output row
+// m = mbase + 16 i + l16, column n = nbase + 16 j + 4 lg + r, so a lane owns
+// 4 consecutive columns of a row and writes them as one 8-byte (16-bit) or
+// 16-byte (fp32) store after the epilogue, with no LDS round trip.
+// Calls f(std::integral_constant<int, 0>) ... f(<N - 1>): indices that are
+// constants before any loop unrolling, so register arrays indexed by them
+// never become addressable (scratch) memory.
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// The 16-bit and fp32 MFMA kernels multiply with the operands swapped, so
+// acc[i][j][r] is C^T: output row m = mbase + 16 i + l16, column
+// n = nbase + 16 j + 4 lg + r.  A lane owns 4 consecutive columns of a row.
+//
+// Common epilogue (row-major output, alpha = beta = 1, bias absent or per
+// column, optional residual, optional ReLU, no program) straight from the
+// accumulators: one 8-byte (16-bit) or 16-byte (fp32) store per 4 values, no
+// LDS round trip.  Same arithmetic as apply_epilogue: ((acc + b) + res), max 0.
+template <typename TO, int TM, int TN, typename Acc>
+__device__ __forceinline__ void epilogue_direct(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
+                                                TO* outp, const TO* resp, const float* bias, bool relu) {
+  const KArg<Problem>& p = kernel_arg<Problem>();
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
+  static_for<TN>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    const int64_t n = nbase + 16 * j + 4 * lg;
+    const bool nfull = n + 4 <= pn;
+    float b[4] = {0.f, 0.f, 0.f, 0.f};
+    if (bias && nfull) {
+      const float4 q = *reinterpret_cast<const float4*>(bias + n);
+      b[0] = q.x; b[1] = q.y; b[2] = q.z; b[3] = q.w;
+    }
+    static_for<TM>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      const int64_t m = mbase + 16 * i + l16;
+      if (m < pm && n < pn) {
+        float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+        if (nfull) {
+          const int64_t o = m * ldo + n;
+          float res[4] = {0.f, 0.f, 0.f, 0.f};
+          if (resp) Elem<TO>::load4(resp + o, res);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float t = (v[r] + b[r]) + res[r];
+            v[r] = relu ? fmaxf(t, 0.0f) : t;
+          }
+          Elem<TO>::store4(outp + o, v);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (n + r < pn) {
+              const int64_t o = m * ldo + n + r;
+              float t = (v[r] + (bias ? bias[n + r] : 0.0f)) + (resp ? Elem<TO>::to_f32(resp[o]) : 0.0f);
+              outp[o] = Elem<TO>::from_f32(relu ? fmaxf(t, 0.0f) : t);
+            }
+          }
+        }
+      }
+    });
+  });
+}
+
+// Whether epilogue_direct applies (uniform): see its comment.
+__device__ __forceinline__ bool epilogue_is_simple(const KArg<Problem>& p, bool vec4) {
+  const int bm = p.epi.bias_mode;
+  return vec4 && !p.out_nchw && p.epi.alpha == 1.0f && p.epi.beta == 1.0f && (bm == 0 || bm == 2) &&
+         p.epi.act <= 1 && p.epi.n_inst == 0 &&
+         (bm == 0 || (reinterpret_cast<uintptr_t>(p.epi.bias) & 15) == 0);
+}
+
 // BUF: operands read with buffer loads at 32-bit byte offsets (A and B below
 // 2^31 bytes, no batch): row bases are precomputed once, out-of-range lanes
 // use an offset past num_records and read zeros, so a K step costs a few
@@ -725,7 +804,9 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
   const int kchunk = tid & 7;        // 16-byte K chunk of all of this thread's vectors
   const int kc = kchunk * VE;        // ... as an element column
 
-  uint4 ra[A_V], rb[B_V];
+  // Two register sets: the loads of tile kt + 2 are issued while tile kt is
+  // multiplied and tile kt + 1 is still in flight.
+  uint4 ra0[A_V], rb0[B_V], ra1[A_V], rb1[B_V];
 
   // Per-row conv state (conv modes): pixel base offset, top-left input coords.
   int64_t rbase[AM == kDenseK ? 1 : A_V];
@@ -769,10 +850,13 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
   // kConvTap: the next tile's filter tap and channel base.
   int t_kh = 0, t_kw = 0, t_c0 = 0;
 
-  auto load_a = [&](int64_t k0) {
+  // `live` is false for the tiles past the end that the fixed-depth prefetch
+  // still issues: their loads read zeros, so every issue() is the same number
+  // of load instructions and the compiler's vmcnt waits stay exact.
+  auto load_a = [&](int64_t k0, uint4 (&ra)[A_V], bool live) {
     if constexpr (BUF) {
       if (AM == kDenseK) {
-        const bool kok = k0 + kc < p.k;
+        const bool kok = live && k0 + kc < p.k;
         const int32_t koff = static_cast<int32_t>((k0 + kc) * ES);
 #pragma unroll
         for (int i = 0; i < A_V; ++i) {
@@ -784,7 +868,7 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
         const int32_t tap = static_cast<int32_t>(((dh * p.cw + dw) * p.c_stride + t_c0 + kc) * ES);
 #pragma unroll
         for (int i = 0; i < A_V; ++i) {
-          const bool ok = static_cast<unsigned>(rhi[i] + dh) < static_cast<unsigned>(p.ch) &&
+          const bool ok = live && static_cast<unsigned>(rhi[i] + dh) < static_cast<unsigned>(p.ch) &&
                           static_cast<unsigned>(rwi[i] + dw) < static_cast<unsigned>(p.cw);
           const uint32_t voff = ok ? static_cast<uint32_t>(a_off[i] + tap) : kOobOffset;
           ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs_a, voff, 0, 0));
@@ -808,7 +892,7 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
       for (int i = 0; i < A_V; ++i) {
         const int hi = rhi[i] + dh, wi = rwi[i] + dw;
         uint4 v = {0u, 0u, 0u, 0u};
-        if (static_cast<unsigned>(hi) < static_cast<unsigned>(p.ch) &&
+        if (live && static_cast<unsigned>(hi) < static_cast<unsigned>(p.ch) &&
             static_cast<unsigned>(wi) < static_cast<unsigned>(p.cw))
           v = *reinterpret_cast<const uint4*>(
               A + (rbase[i] + (static_cast<int64_t>(rhi[i]) * p.cw + rwi[i]) * p.c_stride + tap_off) * ES);
@@ -858,10 +942,10 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
       }
     }
   };
-  auto load_b = [&](int64_t k0) {
+  auto load_b = [&](int64_t k0, uint4 (&rb)[B_V], bool live) {
     const int64_t k = k0 + kc;
     if constexpr (BUF) {
-      const bool kok = k < p.k;
+      const bool kok = live && k < p.k;
       const int32_t koff = static_cast<int32_t>(k * ES);
 #pragma unroll
       for (int i = 0; i < B_V; ++i) {
@@ -880,7 +964,7 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
   };
   // Byte offset of 16-byte chunk c of row r (XOR swizzle).
   auto swz = [](int r, int c) { return (c ^ (r & 7)) << 4; };
-  auto store_tiles = [&](int buf) {
+  auto store_tiles = [&](int buf, const uint4 (&ra)[A_V], const uint4 (&rb)[B_V]) {
 #pragma unroll
     for (int i = 0; i < A_V; ++i) {
       const int r = trow + RSTEP * i;
@@ -900,19 +984,8 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
     for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
 
   const int64_t ktiles = ceil_div(p.k, BK);
-  load_a(0);
-  load_b(0);
-  advance_tap();
-  store_tiles(0);
-  __syncthreads();
   const int lrow = lane & 15, lchunk = lane >> 4;
-  for (int64_t kt = 0; kt < ktiles; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < ktiles) {
-      load_a((kt + 1) * BK);
-      load_b((kt + 1) * BK);
-      advance_tap();
-    }
+  auto compute = [&](int cur) {
 #pragma unroll
     for (int ks = 0; ks < 8; ks += 4) {  // two MFMA K steps of 64 bytes
       vec av[TM], bv[TN];
@@ -929,13 +1002,47 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = Mma::mma(av[i], bv[j], acc[i][j]);
+        for (int j = 0; j < TN; ++j) {
+          if constexpr (Mma::kInt) acc[i][j] = Mma::mma(av[i], bv[j], acc[i][j]);
+          else acc[i][j] = Mma::mma(bv[j], av[i], acc[i][j]);  // C^T: see epilogue_direct
+        }
     }
-    if (kt + 1 < ktiles) {
-      store_tiles(cur ^ 1);
-      __syncthreads();
+  };
+  // LDS barrier that leaves global loads in flight: this wave's LDS stores
+  // are complete (lgkmcnt 0); __syncthreads would also wait for vmcnt(0).
+  auto lds_barrier = [&]() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  auto issue = [&](int64_t kt, uint4 (&ra)[A_V], uint4 (&rb)[B_V]) {
+    const bool live = kt < ktiles;
+    load_a(kt * BK, ra, live);
+    load_b(kt * BK, rb, live);
+    advance_tap();
+  };
+
+  issue(0, ra0, rb0);
+  issue(1, ra1, rb1);
+  store_tiles(0, ra0, rb0);
+  lds_barrier();
+  int64_t kt = 0;
+  for (; kt + 2 <= ktiles; kt += 2) {
+    // LDS buffer 0 holds tile kt; ra1/rb1 carry tile kt + 1.
+    issue(kt + 2, ra0, rb0);
+    compute(0);
+    store_tiles(1, ra1, rb1);
+    lds_barrier();
+    // LDS buffer 1 holds tile kt + 1; ra0/rb0 carry tile kt + 2.
+    issue(kt + 3, ra1, rb1);
+    compute(1);
+    if (kt + 2 < ktiles) {
+      store_tiles(0, ra0, rb0);
+      lds_barrier();
     }
   }
+  if (kt < ktiles) compute(0);  // odd tile count: the last tile sits in buffer 0
 
   // Epilogue: a lane holds (m = 4*(lane/16)+r, n = lane%16) of each 16x16
   // tile.  The whole wave tile is staged in LDS (accumulators only ever
@@ -944,6 +1051,17 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
   TO* outp = static_cast<TO*>(p.out) + bz * p.stride_out;
   const TO* resp = p.epi.residual ? static_cast<const TO*>(p.epi.residual) + bz * p.stride_res : nullptr;
   const int64_t bias_off = bz * p.stride_bias;
+  if constexpr (!Mma::kInt) {
+    constexpr uintptr_t kA = 4 * sizeof(TO) - 1;
+    const bool vec4 = (p.ldo % 4 == 0) && (p.stride_out % 4 == 0) && (p.stride_res % 4 == 0) &&
+                      (p.stride_bias % 4 == 0) && ((reinterpret_cast<uintptr_t>(outp) & kA) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(resp) & kA) == 0);
+    if (epilogue_is_simple(kernel_arg<Problem>(), vec4)) {
+      const float* bias = p.epi.bias_mode == 2 ? static_cast<const float*>(p.epi.bias) + bias_off : nullptr;
+      epilogue_direct<TO, TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act == 1);
+      return;
+    }
+  }
   const bool vec_ok = !p.out_nchw && (p.ldo % 8 == 0) && (p.stride_out % 8 == 0) && (p.stride_res % 8 == 0) &&
                       ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0) &&
                       ((reinterpret_cast<uintptr_t>(p.epi.residual) & 15) == 0);
@@ -955,9 +1073,11 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float* dst = &stage[(i * 16 + (lane >> 4) * 4 + r) * (WTN + 4) + j * 16 + lrow];
-        if constexpr (Mma::kInt) *reinterpret_cast<int*>(dst) = acc[i][j][r];
-        else *dst = acc[i][j][r];
+        if constexpr (Mma::kInt) {
+          *reinterpret_cast<int*>(&stage[(i * 16 + (lane >> 4) * 4 + r) * (WTN + 4) + j * 16 + lrow]) = acc[i][j][r];
+        } else {  // C^T accumulators (swapped MFMA operands)
+          stage[(i * 16 + lrow) * (WTN + 4) + j * 16 + (lane >> 4) * 4 + r] = acc[i][j][r];
+        }
       }
   wave_sync_lds();
 #pragma nounroll
@@ -1141,12 +1261,25 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = Mma::mma(av[i], bv[j], acc[i][j]);
+        for (int j = 0; j < TN; ++j) {
+          if constexpr (Mma::kInt) acc[i][j] = Mma::mma(av[i], bv[j], acc[i][j]);
+          else acc[i][j] = Mma::mma(bv[j], av[i], acc[i][j]);  // C^T: see epilogue_direct
+        }
     }
   }
 
   TO* outp = static_cast<TO*>(p.out);
   const TO* resp = p.epi.residual ? static_cast<const TO*>(p.epi.residual) : nullptr;
+  if constexpr (!Mma::kInt) {
+    constexpr uintptr_t kA = 4 * sizeof(TO) - 1;
+    const bool vec4 = (p.ldo % 4 == 0) && ((reinterpret_cast<uintptr_t>(outp) & kA) == 0) &&
+                      ((reinterpret_cast<uintptr_t>(resp) & kA) == 0);
+    if (epilogue_is_simple(kernel_arg<Problem>(), vec4)) {
+      const float* bias = p.epi.bias_mode == 2 ? static_cast<const float*>(p.epi.bias) : nullptr;
+      epilogue_direct<TO, TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act == 1);
+      return;
+    }
+  }
   const bool vec_ok = !p.out_nchw && (p.ldo % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0) &&
                       ((reinterpret_cast<uintptr_t>(p.epi.residual) & 15) == 0);
   __syncthreads();
@@ -1157,9 +1290,11 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float* dst = &stage[(i * 16 + (lane >> 4) * 4 + r) * (WTN + 4) + j * 16 + lrow];
-        if constexpr (Mma::kInt) *reinterpret_cast<int*>(dst) = acc[i][j][r];
-        else *dst = acc[i][j][r];
+        if constexpr (Mma::kInt) {
+          *reinterpret_cast<int*>(&stage[(i * 16 + (lane >> 4) * 4 + r) * (WTN + 4) + j * 16 + lrow]) = acc[i][j][r];
+        } else {  // C^T accumulators (swapped MFMA operands)
+          stage[(i * 16 + lrow) * (WTN + 4) + j * 16 + (lane >> 4) * 4 + r] = acc[i][j][r];
+        }
       }
   wave_sync_lds();
 #pragma nounroll
@@ -1258,12 +1393,9 @@ int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
       if (p.n <= 64) {
         grid_of<256, 64>(p, 1, grid);
         hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 256, 64, 4, 1, AM, true>), grid, dim3(kThreads), 0, s, p);
-      } else if (p.n <= 128 || ceil_div(p.m, 128) * ceil_div(p.n, 256) < 2 * sms) {
+      } else {
         grid_of<128, 128>(p, 1, grid);
         hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 128, 128, 2, 2, AM, true>), grid, dim3(kThreads), 0, s, p);
-      } else {
-        grid_of<128, 256>(p, 1, grid);
-        hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 128, 256, 2, 2, AM, true>), grid, dim3(kThreads), 0, s, p);
       }
       return launch_status(what);
     }
@@ -1271,12 +1403,9 @@ int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
   if (p.n <= 64) {
     grid_of<256, 64>(p, batch, grid);
     hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 256, 64, 4, 1, AM>), grid, dim3(kThreads), 0, s, p);
-  } else if (p.n <= 128 || ceil_div(p.m, 128) * ceil_div(p.n, 256) * batch < 2 * sms) {
+  } else {
     grid_of<128, 128>(p, batch, grid);
     hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 128, 128, 2, 2, AM>), grid, dim3(kThreads), 0, s, p);
-  } else {
-    grid_of<128, 256>(p, batch, grid);
-    hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 128, 256, 2, 2, AM>), grid, dim3(kThreads), 0, s, p);
   }
   return launch_status(what);
 }
