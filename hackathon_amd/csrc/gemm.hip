@@ -1361,9 +1361,9 @@ int launch_f32(Problem p, int64_t batch, hipStream_t s) {
 // with room for the out-of-range sentinel, and no batch strides.
 inline bool dma_eligible(const Problem& p, int64_t batch, int am) {
   if (getenv("C3H_DISABLE_DMA")) return false;
-  // Implicit-GEMM convs stay on the register-prefetch kernel: their A tiles
-  // are L2-resident gathers, and two blocks per CU beat deeper prefetch.
-  if (am == kConvTap && !getenv("C3H_CONV_DMA")) return false;
+  // Narrow implicit-GEMM convs (N <= 64) stay on the register-prefetch
+  // kernel, which measured faster there; wider ones use the DMA kernel.
+  if (am == kConvTap && p.n <= 64) return false;
   return batch == 1 && (am == kDenseK || am == kConvTap) && p.a_bytes > 0 && p.b_bytes > 0 &&
          p.a_bytes < (int64_t{1} << 31) && p.b_bytes < (int64_t{1} << 31);
 }
@@ -1371,18 +1371,17 @@ inline bool dma_eligible(const Problem& p, int64_t batch, int am) {
 template <typename Mma, typename TO, int AM>
 int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
   dim3 grid;
-  const int64_t sms = 256;
   if constexpr (AM == kDenseK || AM == kConvTap) {
     if (dma_eligible(p, batch, AM)) {
+      // Two stages (one tile in flight): 64-80 KB of LDS, so two blocks share
+      // a CU and one's fill and epilogue overlap the other's MFMAs -- this
+      // measured faster than deeper pipelines at one block per CU.
       if (p.n <= 64) {
         grid_of<256, 64>(p, 1, grid);
-        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 64, 4, 1, AM, 3>), grid, dim3(kThreads), 0, s, p);
-      } else if (p.n <= 128 || ceil_div(p.m, 128) * ceil_div(p.n, 256) < 2 * sms) {
-        grid_of<128, 128>(p, 1, grid);
-        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 128, 128, 2, 2, AM, 4>), grid, dim3(kThreads), 0, s, p);
+        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 64, 4, 1, AM, 2>), grid, dim3(kThreads), 0, s, p);
       } else {
-        grid_of<128, 256>(p, 1, grid);
-        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 128, 256, 2, 2, AM, 3>), grid, dim3(kThreads), 0, s, p);
+        grid_of<128, 128>(p, 1, grid);
+        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 128, 128, 2, 2, AM, 2>), grid, dim3(kThreads), 0, s, p);
       }
       return launch_status(what);
     }
