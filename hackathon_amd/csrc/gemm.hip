@@ -549,12 +549,12 @@ enum AMode16 { kConvTap = 3, kConvStem = 4 };
 // Grouped tile order: each XCD (blockIdx % 8) owns a contiguous range of tile
 // ids, walked in column-major groups of 8 tile rows so blocks resident at
 // the same time share both A and B panels in that XCD's L2.
-__device__ __forceinline__ void tile_coords_grouped(const Problem& p, int& tm, int& tn) {
+__device__ __forceinline__ void tile_coords_of(const Problem& p, int id, int& tm, int& tn) {
   const int total = p.tiles_m * p.tiles_n;
-  int tile = blockIdx.x;
+  int tile = id;
   if ((total & 7) == 0) {
     const int per = total >> 3;
-    tile = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    tile = (id & 7) * per + (id >> 3);
   }
   constexpr int G = 8;
   const int group = tile / (G * p.tiles_n);
@@ -563,6 +563,9 @@ __device__ __forceinline__ void tile_coords_grouped(const Problem& p, int& tm, i
   const int in_group = tile - group * G * p.tiles_n;
   tm = first_m + in_group % gsize;
   tn = in_group / gsize;
+}
+__device__ __forceinline__ void tile_coords_grouped(const Problem& p, int& tm, int& tn) {
+  tile_coords_of(p, blockIdx.x, tm, tn);
 }
 
 // Vectorized epilogue of one 16-row strip (row-major [m, n] output): each
@@ -757,12 +760,104 @@ __device__ __forceinline__ void epilogue_direct(const Acc (&acc)[TM][TN], int64_
   });
 }
 
+// int8 GEMM (c3h_qgemm) counterpart of epilogue_direct for C^T int32
+// accumulators: qmode 0 stores int32, 1 requantizes to int8 (4 bytes per
+// lane), 2 dequantizes and 3 requantizes then dequantizes, both followed by
+// the common float epilogue (simple_epi).  Arithmetic as store_strip_q.
+template <typename TO, int TM, int TN, typename Acc>
+__device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
+                                                  TO* outp, const TO* resp, const float* bias, bool relu) {
+  const KArg<Problem>& p = kernel_arg<Problem>();
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
+  const int mode = p.qmode;
+  const float sa = p.a_scale, sy = p.y_scale, zy = static_cast<float>(p.y_zero);
+  static_for<TN>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    const int64_t n = nbase + 16 * j + 4 * lg;
+    const bool nfull = n + 4 <= pn;
+    float sb[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (n + r < pn) {
+        sb[r] = p.b_scale[n + r];
+        if (bias) b[r] = bias[n + r];
+      }
+    }
+    static_for<TM>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      const int64_t m = mbase + 16 * i + l16;
+      if (m < pm && n < pn) {
+        const int64_t o = m * ldo + n;
+        if constexpr (std::is_same<TO, int32_t>::value) {
+          if (nfull) {
+            *reinterpret_cast<int4*>(outp + o) = int4{acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (n + r < pn) outp[o + r] = acc[i][j][r];
+          }
+        } else {
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float a = static_cast<float>(acc[i][j][r]);
+            if (mode == 1 || mode == 3) {
+              const float mult = (sa * sb[r]) / sy;
+              float y = rintf(a * mult) + zy;
+              y = fminf(fmaxf(y, -128.0f), 127.0f);
+              v[r] = mode == 1 ? y : (y - zy) * sy;
+            } else {
+              v[r] = a * (sa * sb[r]);
+            }
+          }
+          if constexpr (std::is_same<TO, int8_t>::value) {
+            if (nfull) {
+              uint32_t w = 0u;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) w |= (static_cast<uint32_t>(static_cast<int8_t>(v[r])) & 0xffu) << (8 * r);
+              *reinterpret_cast<uint32_t*>(outp + o) = w;
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (n + r < pn) outp[o + r] = static_cast<int8_t>(v[r]);
+            }
+          } else {
+            float res[4] = {0.f, 0.f, 0.f, 0.f};
+            if (resp && nfull) Elem<TO>::load4(resp + o, res);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              if (resp && !nfull && n + r < pn) res[r] = Elem<TO>::to_f32(resp[o + r]);
+              const float t = (v[r] + b[r]) + res[r];
+              v[r] = relu ? fmaxf(t, 0.0f) : t;
+            }
+            if (nfull) {
+              Elem<TO>::store4(outp + o, v);
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (n + r < pn) outp[o + r] = Elem<TO>::from_f32(v[r]);
+            }
+          }
+        }
+      }
+    });
+  });
+}
+
+// Whether epilogue_direct_q applies: int32 / int8 outputs need only aligned
+// row-major stores; dequantized ones also need the common float epilogue.
+__device__ __forceinline__ bool epilogue_q_direct_ok(const KArg<Problem>& p, bool vec4);
+
 // Whether epilogue_direct applies (uniform): see its comment.
 __device__ __forceinline__ bool epilogue_is_simple(const KArg<Problem>& p, bool vec4) {
   const int bm = p.epi.bias_mode;
   return vec4 && !p.out_nchw && p.epi.alpha == 1.0f && p.epi.beta == 1.0f && (bm == 0 || bm == 2) &&
          p.epi.act <= 1 && p.epi.n_inst == 0 &&
          (bm == 0 || (reinterpret_cast<uintptr_t>(p.epi.bias) & 15) == 0);
+}
+__device__ __forceinline__ bool epilogue_q_direct_ok(const KArg<Problem>& p, bool vec4) {
+  return p.qmode <= 1 ? (vec4 && !p.out_nchw) : epilogue_is_simple(p, vec4);
 }
 
 // BUF: operands read with buffer loads at 32-bit byte offsets (A and B below
@@ -1003,8 +1098,7 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          if constexpr (Mma::kInt) acc[i][j] = Mma::mma(av[i], bv[j], acc[i][j]);
-          else acc[i][j] = Mma::mma(bv[j], av[i], acc[i][j]);  // C^T: see epilogue_direct
+          acc[i][j] = Mma::mma(bv[j], av[i], acc[i][j]);  // C^T: see epilogue_direct
         }
     }
   };
@@ -1051,12 +1145,18 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
   TO* outp = static_cast<TO*>(p.out) + bz * p.stride_out;
   const TO* resp = p.epi.residual ? static_cast<const TO*>(p.epi.residual) + bz * p.stride_res : nullptr;
   const int64_t bias_off = bz * p.stride_bias;
-  if constexpr (!Mma::kInt) {
+  {
     constexpr uintptr_t kA = 4 * sizeof(TO) - 1;
     const bool vec4 = (p.ldo % 4 == 0) && (p.stride_out % 4 == 0) && (p.stride_res % 4 == 0) &&
                       (p.stride_bias % 4 == 0) && ((reinterpret_cast<uintptr_t>(outp) & kA) == 0) &&
                       ((reinterpret_cast<uintptr_t>(resp) & kA) == 0);
-    if (epilogue_is_simple(kernel_arg<Problem>(), vec4)) {
+    if constexpr (Mma::kInt) {
+      if (bz == 0 && epilogue_q_direct_ok(kernel_arg<Problem>(), vec4)) {
+        const float* bias = p.epi.bias_mode == 2 ? static_cast<const float*>(p.epi.bias) : nullptr;
+        epilogue_direct_q<TO, TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act == 1);
+        return;
+      }
+    } else if (epilogue_is_simple(kernel_arg<Problem>(), vec4)) {
       const float* bias = p.epi.bias_mode == 2 ? static_cast<const float*>(p.epi.bias) + bias_off : nullptr;
       epilogue_direct<TO, TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act == 1);
       return;
@@ -1073,11 +1173,9 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        if constexpr (Mma::kInt) {
-          *reinterpret_cast<int*>(&stage[(i * 16 + (lane >> 4) * 4 + r) * (WTN + 4) + j * 16 + lrow]) = acc[i][j][r];
-        } else {  // C^T accumulators (swapped MFMA operands)
-          stage[(i * 16 + lrow) * (WTN + 4) + j * 16 + (lane >> 4) * 4 + r] = acc[i][j][r];
-        }
+        float* dst = &stage[(i * 16 + lrow) * (WTN + 4) + j * 16 + (lane >> 4) * 4 + r];  // C^T accumulators
+        if constexpr (Mma::kInt) *reinterpret_cast<int*>(dst) = acc[i][j][r];
+        else *dst = acc[i][j][r];
       }
   wave_sync_lds();
 #pragma nounroll
@@ -1262,20 +1360,24 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          if constexpr (Mma::kInt) acc[i][j] = Mma::mma(av[i], bv[j], acc[i][j]);
-          else acc[i][j] = Mma::mma(bv[j], av[i], acc[i][j]);  // C^T: see epilogue_direct
+          acc[i][j] = Mma::mma(bv[j], av[i], acc[i][j]);  // C^T: see epilogue_direct
         }
     }
   }
 
   TO* outp = static_cast<TO*>(p.out);
   const TO* resp = p.epi.residual ? static_cast<const TO*>(p.epi.residual) : nullptr;
-  if constexpr (!Mma::kInt) {
+  {
     constexpr uintptr_t kA = 4 * sizeof(TO) - 1;
     const bool vec4 = (p.ldo % 4 == 0) && ((reinterpret_cast<uintptr_t>(outp) & kA) == 0) &&
                       ((reinterpret_cast<uintptr_t>(resp) & kA) == 0);
-    if (epilogue_is_simple(kernel_arg<Problem>(), vec4)) {
-      const float* bias = p.epi.bias_mode == 2 ? static_cast<const float*>(p.epi.bias) : nullptr;
+    const float* bias = p.epi.bias_mode == 2 ? static_cast<const float*>(p.epi.bias) : nullptr;
+    if constexpr (Mma::kInt) {
+      if (epilogue_q_direct_ok(kernel_arg<Problem>(), vec4)) {
+        epilogue_direct_q<TO, TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act == 1);
+        return;
+      }
+    } else if (epilogue_is_simple(kernel_arg<Problem>(), vec4)) {
       epilogue_direct<TO, TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act == 1);
       return;
     }
@@ -1290,11 +1392,9 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        if constexpr (Mma::kInt) {
-          *reinterpret_cast<int*>(&stage[(i * 16 + (lane >> 4) * 4 + r) * (WTN + 4) + j * 16 + lrow]) = acc[i][j][r];
-        } else {  // C^T accumulators (swapped MFMA operands)
-          stage[(i * 16 + lrow) * (WTN + 4) + j * 16 + (lane >> 4) * 4 + r] = acc[i][j][r];
-        }
+        float* dst = &stage[(i * 16 + lrow) * (WTN + 4) + j * 16 + (lane >> 4) * 4 + r];  // C^T accumulators
+        if constexpr (Mma::kInt) *reinterpret_cast<int*>(dst) = acc[i][j][r];
+        else *dst = acc[i][j][r];
       }
   wave_sync_lds();
 #pragma nounroll
