@@ -45,7 +45,7 @@ DOMINANT = {
     "decoder_w8a8": (["qgemm"], "int8", "int8 GEMM + requant/dequant epilogue (MFMA i32 16x16x64)"),
 }
 BASELINE_INDEX = {"mlp": 0, "resnet18_cifar": 1, "resnet18_224": 2, "decoder_fp16": 3, "decoder_w8a8": 4}
-CPU_SAMPLE = {"mlp": 256, "resnet18_cifar": 16, "resnet18_224": 8, "decoder_fp16": 8, "decoder_w8a8": 1}
+CPU_SAMPLE = {"mlp": 4096, "resnet18_cifar": 128, "resnet18_224": 48, "decoder_fp16": 16, "decoder_w8a8": 2}
 
 
 def _log(msg: str) -> None:
@@ -226,7 +226,7 @@ def _traffic_summary(fetch_dir: str, write_dir: str, meta_path: str) -> int:
     for counter, run_dir in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         rows = _pmc_rows(run_dir, counter)
         copy = [v for k, v in rows if "strided_copy_kernel" in k]
-        conv = [v for k, v in rows if "mfma_gemm" in k]
+        conv = [v for k, v in rows if "mfma_gemm" in k or "conv_stem_pool" in k]
         if len(copy) != meta["copy_dispatches"] or len(conv) != len(launches) * meta["replays"]:
             raise ValueError(f"{counter}: {len(copy)} copy / {len(conv)} conv dispatches, expected "
                              f"{meta['copy_dispatches']} / {len(launches) * meta['replays']}")

@@ -721,30 +721,44 @@ __device__ __forceinline__ void epilogue_direct(const Acc (&acc)[TM][TN], int64_
   const KArg<Problem>& p = kernel_arg<Problem>();
   const int l16 = lane & 15, lg = lane >> 4;
   const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
+  // Bias of this lane's columns, for every column tile.
+  float b[TN][4];
   static_for<TN>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
     const int64_t n = nbase + 16 * j + 4 * lg;
-    const bool nfull = n + 4 <= pn;
-    float b[4] = {0.f, 0.f, 0.f, 0.f};
-    if (bias && nfull) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) b[j][r] = 0.0f;
+    if (bias && n + 4 <= pn) {
       const float4 q = *reinterpret_cast<const float4*>(bias + n);
-      b[0] = q.x; b[1] = q.y; b[2] = q.z; b[3] = q.w;
+      b[j][0] = q.x; b[j][1] = q.y; b[j][2] = q.z; b[j][3] = q.w;
     }
-    static_for<TM>([&](auto ic) {
-      constexpr int i = decltype(ic)::value;
-      const int64_t m = mbase + 16 * i + l16;
-      if (m < pm && n < pn) {
+  });
+  // Row by row: a row's column tiles share cache lines, so its residual
+  // loads and its stores go out back to back (interleaving rows makes L2
+  // write partial lines back more than once).
+  static_for<TM>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    const int64_t m = mbase + 16 * i + l16;
+    if (m < pm) {
+      float res[TN][4];
+      static_for<TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const int64_t n = nbase + 16 * j + 4 * lg;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) res[j][r] = 0.0f;
+        if (resp && n + 4 <= pn) Elem<TO>::load4(resp + m * ldo + n, res[j]);
+      });
+      static_for<TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const int64_t n = nbase + 16 * j + 4 * lg;
         float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-        if (nfull) {
-          const int64_t o = m * ldo + n;
-          float res[4] = {0.f, 0.f, 0.f, 0.f};
-          if (resp) Elem<TO>::load4(resp + o, res);
+        if (n + 4 <= pn) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            float t = (v[r] + b[r]) + res[r];
+            float t = (v[r] + b[j][r]) + res[j][r];
             v[r] = relu ? fmaxf(t, 0.0f) : t;
           }
-          Elem<TO>::store4(outp + o, v);
+          Elem<TO>::store4(outp + m * ldo + n, v);
         } else {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
@@ -755,8 +769,8 @@ __device__ __forceinline__ void epilogue_direct(const Acc (&acc)[TM][TN], int64_
             }
           }
         }
-      }
-    });
+      });
+    }
   });
 }
 
@@ -772,76 +786,94 @@ __device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int6
   const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
   const int mode = p.qmode;
   const float sa = p.a_scale, sy = p.y_scale, zy = static_cast<float>(p.y_zero);
+  float sb[TN][4], b[TN][4];
   static_for<TN>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
     const int64_t n = nbase + 16 * j + 4 * lg;
-    const bool nfull = n + 4 <= pn;
-    float sb[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
+      sb[j][r] = 0.0f;
+      b[j][r] = 0.0f;
       if (n + r < pn) {
-        sb[r] = p.b_scale[n + r];
-        if (bias) b[r] = bias[n + r];
+        if (mode != 0) sb[j][r] = p.b_scale[n + r];
+        if (bias) b[j][r] = bias[n + r];
       }
     }
-    static_for<TM>([&](auto ic) {
-      constexpr int i = decltype(ic)::value;
-      const int64_t m = mbase + 16 * i + l16;
-      if (m < pm && n < pn) {
+  });
+  // Row by row, as epilogue_direct: a row's stores go out back to back.
+  static_for<TM>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    const int64_t m = mbase + 16 * i + l16;
+    if (m < pm) {
+      float res[TN][4];
+      static_for<TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const int64_t n = nbase + 16 * j + 4 * lg;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) res[j][r] = 0.0f;
+        if constexpr (!std::is_same<TO, int32_t>::value && !std::is_same<TO, int8_t>::value) {
+          if (resp && n + 4 <= pn) Elem<TO>::load4(resp + m * ldo + n, res[j]);
+        }
+      });
+      static_for<TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const int64_t n = nbase + 16 * j + 4 * lg;
+        const bool nfull = n + 4 <= pn;
         const int64_t o = m * ldo + n;
-        if constexpr (std::is_same<TO, int32_t>::value) {
-          if (nfull) {
-            *reinterpret_cast<int4*>(outp + o) = int4{acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-          } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              if (n + r < pn) outp[o + r] = acc[i][j][r];
-          }
-        } else {
-          float v[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float a = static_cast<float>(acc[i][j][r]);
-            if (mode == 1 || mode == 3) {
-              const float mult = (sa * sb[r]) / sy;
-              float y = rintf(a * mult) + zy;
-              y = fminf(fmaxf(y, -128.0f), 127.0f);
-              v[r] = mode == 1 ? y : (y - zy) * sy;
-            } else {
-              v[r] = a * (sa * sb[r]);
-            }
-          }
-          if constexpr (std::is_same<TO, int8_t>::value) {
+        if (n < pn) {
+          if constexpr (std::is_same<TO, int32_t>::value) {
             if (nfull) {
-              uint32_t w = 0u;
-#pragma unroll
-              for (int r = 0; r < 4; ++r) w |= (static_cast<uint32_t>(static_cast<int8_t>(v[r])) & 0xffu) << (8 * r);
-              *reinterpret_cast<uint32_t*>(outp + o) = w;
+              *reinterpret_cast<int4*>(outp + o) = int4{acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
             } else {
 #pragma unroll
               for (int r = 0; r < 4; ++r)
-                if (n + r < pn) outp[o + r] = static_cast<int8_t>(v[r]);
+                if (n + r < pn) outp[o + r] = acc[i][j][r];
             }
           } else {
-            float res[4] = {0.f, 0.f, 0.f, 0.f};
-            if (resp && nfull) Elem<TO>::load4(resp + o, res);
+            float v[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              if (resp && !nfull && n + r < pn) res[r] = Elem<TO>::to_f32(resp[o + r]);
-              const float t = (v[r] + b[r]) + res[r];
-              v[r] = relu ? fmaxf(t, 0.0f) : t;
+              const float a = static_cast<float>(acc[i][j][r]);
+              if (mode == 1 || mode == 3) {
+                const float mult = (sa * sb[j][r]) / sy;
+                float y = rintf(a * mult) + zy;
+                y = fminf(fmaxf(y, -128.0f), 127.0f);
+                v[r] = mode == 1 ? y : (y - zy) * sy;
+              } else {
+                v[r] = a * (sa * sb[j][r]);
+              }
             }
-            if (nfull) {
-              Elem<TO>::store4(outp + o, v);
+            if constexpr (std::is_same<TO, int8_t>::value) {
+              if (nfull) {
+                uint32_t w = 0u;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) w |= (static_cast<uint32_t>(static_cast<int8_t>(v[r])) & 0xffu) << (8 * r);
+                *reinterpret_cast<uint32_t*>(outp + o) = w;
+              } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                  if (n + r < pn) outp[o + r] = static_cast<int8_t>(v[r]);
+              }
             } else {
 #pragma unroll
-              for (int r = 0; r < 4; ++r)
-                if (n + r < pn) outp[o + r] = Elem<TO>::from_f32(v[r]);
+              for (int r = 0; r < 4; ++r) {
+                float rr = res[j][r];
+                if (resp && !nfull && n + r < pn) rr = Elem<TO>::to_f32(resp[o + r]);
+                const float t = (v[r] + b[j][r]) + rr;
+                v[r] = relu ? fmaxf(t, 0.0f) : t;
+              }
+              if (nfull) {
+                Elem<TO>::store4(outp + o, v);
+              } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                  if (n + r < pn) outp[o + r] = Elem<TO>::from_f32(v[r]);
+              }
             }
           }
         }
-      }
-    });
+      });
+    }
   });
 }
 
