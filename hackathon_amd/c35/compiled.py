@@ -43,7 +43,7 @@ from .. import _lib
 from ..c3common.ir.graph import Graph, Node
 from ..c34.execution_plan import ExecutionPlan
 from ..c34.memory_pool import DeviceMemoryPool
-from ..device import BF16, Buffer, DeviceArray, Stream, dtype_code, init
+from ..device import BF16, Buffer, DeviceArray, PinnedArray, Stream, dtype_code, init
 from . import engine as E
 
 _POLICY_ACT = {"fp32": np.dtype(np.float32), "bf16": BF16, "fp16": np.dtype(np.float16), "w8a8": BF16}
@@ -420,6 +420,12 @@ class CompiledPlan:
                 if src.nbytes != dst.nbytes:
                     raise ValueError(f"input '{name}' has {src.nbytes} bytes, plan expects {dst.nbytes}")
                 _lib.check(_lib.lib().c3h_memcpy_d2d_async(dst.ptr, src.ptr, src.nbytes, self._stream.handle), "d2d")
+            elif isinstance(src, tuple) and len(src) == 2 and isinstance(src[0], PinnedArray):
+                # (pinned buffer, byte count): asynchronous on the compiled stream
+                pinned, nbytes = src
+                if nbytes != dst.nbytes:
+                    raise ValueError(f"input '{name}' has {nbytes} bytes, plan expects {dst.nbytes}")
+                _lib.check(_lib.lib().c3h_memcpy_h2d_async(dst.ptr, pinned.ptr, nbytes, self._stream.handle), "h2d")
             else:
                 host = np.ascontiguousarray(np.asarray(src), dtype=dst.dtype)
                 dst.copy_from_host(host, self._stream.handle)

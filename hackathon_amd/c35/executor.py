@@ -512,6 +512,120 @@ class CrossStageReferencePipeline:
         return optimized
 
 
+def _check_output(out: DeviceArray, out_name: str, tail: Optional[Tuple[int, ...]]) -> Tuple[int, ...]:
+    if out.dtype != np.float32:
+        raise ValueError(f"Output '{out_name}' must be float32, got {out.dtype}")
+    if tail is not None and out.shape[1:] != tail:
+        raise ValueError(f"Output '{out_name}' changed non-batch shape from {tail} to {out.shape[1:]}")
+    return out.shape[1:]
+
+
+def _run_planned_batches(pipeline, arrays, total, batch, out_name, out_path) -> Tuple[int, ...]:
+    """Strict path: one batch at a time, logits gathered on the device (X:1137-1201)."""
+    final: Optional[DeviceArray] = None
+    for start in range(0, total, batch):
+        end = min(start + batch, total)
+        out = pipeline.run({name: DeviceArray.from_host(arr[start:end]) for name, arr in arrays.items()})[out_name]
+        tail = _check_output(out, out_name, final.shape[1:] if final is not None else None)
+        if final is None:
+            final = DeviceArray.empty((total,) + tail, np.float32)
+        engine.copy_into(out, final.split_axis0(start, end))
+    if final is None:
+        raise RuntimeError("Inference produced no output batches")
+    result = final.get()
+    if not np.all(np.isfinite(result)):
+        raise ValueError("Output contains non-finite values (NaN or Inf)")
+    np.save(out_path, result)
+    return result.shape
+
+
+_CHUNK_BYTES = 64 << 20
+
+
+def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path) -> Tuple[int, ...]:
+    """Compiled path with host I/O overlapped with the GPU.
+
+    Per batch: the input slice goes through a pinned buffer (two, used in
+    turn) as an asynchronous H2D on the program's stream; the program runs;
+    its logits are copied on the device into one of two staging buffers.
+    While the GPU runs batch i, the host drains batch i - 1: a copy stream
+    moves its staging buffer to the host in 64 MB pinned chunks (two, used in
+    turn), and each chunk is checked for non-finite values and written into
+    the memory-mapped logits.npy.  No whole-output device or host copy is
+    ever built, so C5's 2.1 GB of logits cost one staging buffer per slot.
+    """
+    from ..device import Event, PinnedArray, Stream
+
+    names = list(arrays)
+    pin_in = [{n: PinnedArray((batch,) + arrays[n].shape[1:], arrays[n].dtype) for n in names} for _ in range(2)]
+    copy_stream = Stream()
+    stage: list = [None, None]
+    ready = [Event(), Event()]
+    chunks = [PinnedArray((_CHUNK_BYTES // 4,), np.float32) for _ in range(2)]
+    chunk_done = [Event(), Event()]
+    mm = None
+    tail: Optional[Tuple[int, ...]] = None
+    pending = None  # (slot, start, end) of the batch still on the device
+
+    def drain(slot, start, end):
+        copy_stream.wait_event(ready[slot])
+        src = stage[slot]
+        row = math.prod(tail)
+        flat = mm.reshape(-1)
+        first, last = start * row, end * row
+        step = _CHUNK_BYTES // 4
+        spans = [(o, min(o + step, last)) for o in range(first, last, step)]
+
+        def issue(k):
+            o0, o1 = spans[k]
+            _lib.check(_lib.lib().c3h_memcpy_d2h_async(chunks[k % 2].ptr, src.ptr + (o0 - first) * 4, (o1 - o0) * 4,
+                                                       copy_stream.handle), "d2h")
+            chunk_done[k % 2].record(copy_stream)
+
+        if spans:
+            issue(0)
+        for k, (o0, o1) in enumerate(spans):
+            if k + 1 < len(spans):
+                issue(k + 1)
+            chunk_done[k % 2].synchronize()
+            host = chunks[k % 2].array[: o1 - o0]
+            if not np.all(np.isfinite(host)):
+                raise ValueError("Output contains non-finite values (NaN or Inf)")
+            flat[o0:o1] = host
+
+    for i, start in enumerate(range(0, total, batch)):
+        end = min(start + batch, total)
+        nb = end - start
+        slot = i % 2
+        prog = pipeline.compiled_for_batch(nb)
+        pipeline.last_plan = pipeline._plan_for_batch(nb)
+        feed = {}
+        for n in names:
+            view = pin_in[slot][n].array[:nb]
+            view[...] = arrays[n][start:end]
+            feed[n] = (pin_in[slot][n], view.nbytes)
+        prog.stage_inputs(feed)
+        prog.launch()
+        out = prog.output_arrays[out_name]
+        tail = _check_output(out, out_name, tail)
+        if mm is None:
+            mm = np.lib.format.open_memmap(out_path, mode="w+", dtype=np.float32, shape=(total,) + tail)
+        if stage[slot] is None:
+            stage[slot] = DeviceArray.empty((batch,) + tail, np.float32)
+        _lib.check(_lib.lib().c3h_memcpy_d2d_async(stage[slot].ptr, out.ptr, out.nbytes, prog.stream.handle), "d2d")
+        ready[slot].record(prog.stream)
+        if pending is not None:
+            drain(*pending)
+        pending = (slot, start, end)
+    if pending is None:
+        raise RuntimeError("Inference produced no output batches")
+    drain(*pending)
+    mm.flush()
+    shape = mm.shape
+    del mm
+    return shape
+
+
 def load_and_infer(model_path: str, input_dir: str, output_dir: str, batch_size: Optional[int] = None,
                    qualify_optimizations: bool = False, engine_kind: str = "compiled",
                    precision: Optional[str] = None, weights: Optional[Dict[str, Any]] = None,
@@ -578,32 +692,19 @@ def load_and_infer(model_path: str, input_dir: str, output_dir: str, batch_size:
                                            qualify_optimizations=qualify_optimizations, engine_kind=engine_kind,
                                            precision=precision)
     out_name = graph.outputs[0].name if graph.outputs else "logits"
-    final: Optional[DeviceArray] = None
-    ti = time.perf_counter()
-    for start in range(0, total, batch):
-        end = min(start + batch, total)
-        feed = {name: DeviceArray.from_host(arr[start:end]) for name, arr in arrays.items()}
-        out = pipeline.run(feed)[out_name]
-        if out.dtype != np.float32:
-            raise ValueError(f"Output '{out_name}' must be float32, got {out.dtype}")
-        if final is None:
-            final = DeviceArray.empty((total,) + out.shape[1:], np.float32)
-        if out.shape[1:] != final.shape[1:]:
-            raise ValueError(f"Output '{out_name}' changed non-batch shape from {final.shape[1:]} to {out.shape[1:]}")
-        engine.copy_into(out, final.split_axis0(start, end))
-    from ..device import synchronize
-    synchronize()
-    ti_end = time.perf_counter()
-    if final is None:
-        raise RuntimeError("Inference produced no output batches")
-    result = final.get()
-    if not np.all(np.isfinite(result)):
-        raise ValueError("Output contains non-finite values (NaN or Inf)")
     os.makedirs(output_dir, exist_ok=True)
-    np.save(os.path.join(output_dir, "logits.npy"), result)
+    out_path = os.path.join(output_dir, "logits.npy")
+    ti = time.perf_counter()
+    if engine_kind == "compiled":
+        if qualify_optimizations:  # C3.3 check on the first batch (X:955-994), then the streamed run
+            pipeline.run({name: DeviceArray.from_host(arr[:batch]) for name, arr in arrays.items()})
+        out_shape = _stream_compiled(pipeline, arrays, total, batch, out_name, out_path)
+    else:
+        out_shape = _run_planned_batches(pipeline, arrays, total, batch, out_name, out_path)
+    ti_end = time.perf_counter()
     with open(os.path.join(output_dir, "manifest.json"), "w") as f:
         json.dump({"tensors": [{"name": out_name, "file": "logits.npy", "dtype": "float32",
-                                "shape": list(result.shape)}]}, f, indent=2)
+                                "shape": list(out_shape)}]}, f, indent=2)
     t_end = time.perf_counter()
     trace = pipeline.optimized_executor.last_execution_trace
     counts_by_kind = {k: sum(a["kind"] == k for a in trace)
@@ -616,7 +717,7 @@ def load_and_infer(model_path: str, input_dir: str, output_dir: str, batch_size:
                 "batch_count": (total + batch - 1) // batch, "engine": engine_kind, "precision": precision}
     return {
         "model_path": model_path, "input_dir": input_dir, "output_dir": output_dir, "batch_size": batch,
-        "backend": "libc3hip", "backend_evidence": evidence, "engine": engine_kind, "total_samples": total, "output_shape": list(result.shape),
+        "backend": "libc3hip", "backend_evidence": evidence, "engine": engine_kind, "total_samples": total, "output_shape": list(out_shape),
         "parse_time_s": tp_end - tp, "infer_time_s": ti_end - ti, "total_time_s": t_end - t0,
         "cross_stage_reference": True, "optimized_graph_nodes": len(pipeline.graph.nodes),
         "fusion_stats": pipeline.fusion_result["Fusion"]["stats"],

@@ -209,6 +209,32 @@ class DeviceArray:
                                                   current_stream() if stream is None else stream), "d2d")
 
 
+class PinnedArray:
+    """Page-locked host memory (hipHostMalloc) viewed as a NumPy array.
+
+    Async H2D/D2H copies from or into it do not stage through a bounce
+    buffer, so they overlap with kernels and with host work."""
+
+    __slots__ = ("ptr", "nbytes", "array", "__weakref__")
+
+    def __init__(self, shape: Sequence[int], dtype=np.float32) -> None:
+        init()
+        shape = tuple(int(d) for d in shape)
+        dtype = np.dtype(dtype)
+        self.nbytes = math.prod(shape) * dtype.itemsize
+        ptr = C.c_void_p()
+        _lib.check(_lib.lib().c3h_host_alloc(C.byref(ptr), max(self.nbytes, 1)), "c3h_host_alloc")
+        self.ptr = int(ptr.value or 0)
+        raw = (C.c_uint8 * max(self.nbytes, 1)).from_address(self.ptr)
+        self.array = np.frombuffer(raw, dtype=np.uint8, count=self.nbytes).view(dtype).reshape(shape)
+
+    def __del__(self) -> None:
+        if getattr(self, "ptr", 0) and _lib._LIB is not None:
+            self.array = None
+            _lib._LIB.c3h_host_free(self.ptr)
+            self.ptr = 0
+
+
 def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
     """Decode bfloat16 bit patterns (uint16 or BF16-tagged) to float32."""
     u = np.asarray(bits).view(np.uint16).astype(np.uint32) << 16

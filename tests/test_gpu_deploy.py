@@ -95,3 +95,19 @@ def test_deploy_writer_file_matches_in_process(gpu, tmp_path, name, policy):
     pipe = CrossStageReferencePipeline(onnx_io.import_onnx(path), path, engine_kind="compiled", precision=policy)
     ref = pipe.run({in_name: arr})["logits"].get()
     np.testing.assert_array_equal(got, ref)
+
+
+def test_deploy_planned_engine_matches_torch(gpu, tmp_path):
+    """The strict timeline engine (`--engine planned`, fp32) behind the same CLI."""
+    import torch
+
+    from test_onnx_io import _torch_modules, torch_export
+
+    module, example, in_name = _torch_modules()["cnn"]
+    path = str(tmp_path / "cnn.onnx")
+    torch_export(module, example, path, in_name, dynamic_batch=True)
+    x = torch.randn((3,) + tuple(example.shape[1:]), generator=torch.Generator().manual_seed(4))
+    with torch.no_grad():
+        expect = module(x).numpy()
+    got = _deploy(tmp_path, path, in_name, x.numpy(), "--engine", "planned", "--batch-size", "2")
+    np.testing.assert_allclose(got, expect, rtol=1e-3, atol=1e-4)
