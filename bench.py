@@ -35,7 +35,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "samples/s (tokens/s) @1 GPU per config; % of MFMA or HBM roofline per kernel"
 HEADLINE = "resnet18_224"
 # MI355X published dense peaks (TFLOP/s or TOP/s) and HBM bandwidth (GB/s).
-PEAK = {"bf16": 2500.0, "fp16": 2500.0, "int8": 5000.0, "fp32": 157.3, "hbm": 8000.0}
+PEAK = {"bf16": 2500.0, "fp16": 2500.0, "fp8": 5000.0, "int8": 5000.0, "fp32": 157.3, "hbm": 8000.0}
 # Dominant kernel family and its roofline per workload.
 DOMINANT = {
     "mlp": (["gemm"], "fp32", "fp32 GEMM (MFMA 16x16x4 f32)"),
@@ -43,9 +43,11 @@ DOMINANT = {
     "resnet18_224": (["conv"], "bf16", "implicit-GEMM conv (bf16 MFMA 16x16x32)"),
     "decoder_fp16": (["gemm"], "fp16", "GEMM + fused epilogues (fp16 MFMA 16x16x32)"),
     "decoder_w8a8": (["qgemm"], "int8", "int8 GEMM + requant/dequant epilogue (MFMA i32 16x16x64)"),
+    "decoder_fp8": (["gemm_fp8"], "fp8", "E4M3 GEMM + scale/epilogue (MFMA f32 16x16x128 f8f6f4)"),
 }
 BASELINE_INDEX = {"mlp": 0, "resnet18_cifar": 1, "resnet18_224": 2, "decoder_fp16": 3, "decoder_w8a8": 4}
 CPU_SAMPLE = {"mlp": 4096, "resnet18_cifar": 128, "resnet18_224": 48, "decoder_fp16": 16, "decoder_w8a8": 2}
+# decoder_fp8 is no BASELINE config: the decoder_fp16 model under the "fp8" policy (E4M3 GEMMs).
 
 
 def _log(msg: str) -> None:

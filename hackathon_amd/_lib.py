@@ -33,7 +33,8 @@ EW_ADD, EW_SUB, EW_MUL, EW_DIV, EW_RELU, EW_ERF, EW_ERF_AS, EW_SQRT, EW_EXP, EW_
 OP_NOP, OP_EVENT_RECORD, OP_EVENT_WAIT, OP_COPY = 0, 1, 2, 3
 OP_FILL, OP_CAST, OP_EW, OP_STRIDED_COPY, OP_REDUCE, OP_SOFTMAX, OP_LAYERNORM, OP_BATCHNORM, \
     OP_GATHER, OP_ARGMAX, OP_IM2COL, OP_LAYOUT, OP_MAXPOOL, OP_GEMM, OP_CONV, OP_ATTN_SCORES, \
-    OP_FLASH, OP_QUANTIZE, OP_QGEMM, OP_DEQUANTIZE, OP_BNFOLD, OP_PACK, OP_CONV_POOL = range(10, 33)
+    OP_FLASH, OP_QUANTIZE, OP_QGEMM, OP_DEQUANTIZE, OP_BNFOLD, OP_PACK, OP_CONV_POOL, OP_QUANT_FP8, \
+    OP_GEMM_FP8 = range(10, 35)
 
 vp = C.c_void_p
 i32 = C.c_int32
@@ -184,6 +185,17 @@ class PackArgs(C.Structure):
         ("k_stride", i64), ("in_dtype", i32), ("out_dtype", i32)]
 
 
+class Fp8QuantArgs(C.Structure):
+    _fields_ = [("x", vp), ("out", vp), ("scale", vp), ("rows", i64), ("cols", i64), ("ldx", i64),
+                ("ldo", i64), ("x_dtype", i32), ("pad_", i32)]
+
+
+class Fp8GemmArgs(C.Structure):
+    _fields_ = [("a", vp), ("b", vp), ("a_scale", vp), ("b_scale", vp), ("out", vp), ("m", i64),
+                ("n", i64), ("k", i64), ("lda", i64), ("ldb", i64), ("ldo", i64), ("out_dtype", i32),
+                ("pad_", i32), ("epi", Epilogue)]
+
+
 class ConvPoolArgs(C.Structure):
     _fields_ = [("x", vp), ("w", vp), ("bias", vp), ("out", vp)] + [(n, i32) for n in (
         "n", "c", "h", "w_", "o", "k_stride", "kh", "kw", "sh", "sw", "pad_top", "pad_left", "ho", "wo",
@@ -198,7 +210,7 @@ class Op(C.Structure):
 ABI_ORDER = [Props, FillArgs, CastArgs, EwArgs, CopyArgs, ReduceArgs, SoftmaxArgs, LayerNormArgs,
              BatchNormArgs, BnFoldArgs, GatherArgs, ArgmaxArgs, Im2colArgs, LayoutArgs, PoolArgs,
              Epilogue, GemmArgs, ConvArgs, AttnScoresArgs, FlashArgs, QuantizeArgs, QGemmArgs,
-             DequantizeArgs, Op, PackArgs, ConvPoolArgs]
+             DequantizeArgs, Op, PackArgs, ConvPoolArgs, Fp8QuantArgs, Fp8GemmArgs]
 
 # Kernel entry points: name -> args struct (all take (const args*, void* stream)).
 KERNELS = {
@@ -210,6 +222,7 @@ KERNELS = {
     "c3h_attention_scores": AttnScoresArgs, "c3h_flash_attention": FlashArgs,
     "c3h_quantize": QuantizeArgs, "c3h_qgemm": QGemmArgs, "c3h_dequantize": DequantizeArgs,
     "c3h_pack_conv_weight": PackArgs, "c3h_conv_stem_pool": ConvPoolArgs,
+    "c3h_quantize_fp8_rows": Fp8QuantArgs, "c3h_gemm_fp8": Fp8GemmArgs,
 }
 
 OP_KIND = {
@@ -220,6 +233,7 @@ OP_KIND = {
     ConvArgs: OP_CONV, AttnScoresArgs: OP_ATTN_SCORES, FlashArgs: OP_FLASH,
     QuantizeArgs: OP_QUANTIZE, QGemmArgs: OP_QGEMM, DequantizeArgs: OP_DEQUANTIZE,
     BnFoldArgs: OP_BNFOLD, PackArgs: OP_PACK, ConvPoolArgs: OP_CONV_POOL,
+    Fp8QuantArgs: OP_QUANT_FP8, Fp8GemmArgs: OP_GEMM_FP8,
 }
 
 KERNEL_OF_ARGS = {v: k for k, v in KERNELS.items()}

@@ -14,7 +14,15 @@ the planner passes through to `KernelStep.precision_profile`:
     Softmax, attention) compute in fp32 from 16-bit storage; graph outputs
     are fp32;
   * "w8a8" - QLinearMatMul computes int8 x int8 -> int32; float activations
-    are stored in bf16 as in "bf16".
+    are stored in bf16 as in "bf16";
+  * "fp8"  - the executable form of the reference's mixed-precision choice
+    (c32/strategy.py:124-160): a constant-weight GEMM that the reference's
+    rule gives fp8 (or fp4, which falls back to fp8 on a profile without
+    fp4, c32/strategy.py:113-122) computes OCP E4M3 x E4M3 with fp32
+    accumulation (row-wise dynamic activation scales, per-output-channel
+    weight scales); every other contraction, and every activation in
+    storage, is fp16.  The reference also picks fp8 for aligned 1x1 convs;
+    no fp8 conv kernel exists here, so those run fp16.
 """
 
 from __future__ import annotations
@@ -62,21 +70,22 @@ METADATA_KERNELS: Set[str] = {"constant", "flatten", "reshape", "transpose", "sp
 
 @dataclass(frozen=True)
 class PrecisionPolicy:
-    """Executable precision policy (name in {"fp32", "bf16", "fp16", "w8a8"})."""
+    """Executable precision policy (name in {"fp32", "bf16", "fp16", "w8a8", "fp8"})."""
 
     name: str = "fp32"
 
     def __post_init__(self) -> None:
-        if self.name not in ("fp32", "bf16", "fp16", "w8a8"):
+        if self.name not in ("fp32", "bf16", "fp16", "w8a8", "fp8"):
             raise ValueError(f"unknown precision policy {self.name!r}")
 
     @property
     def activation_dtype(self) -> str:
-        return {"fp32": "fp32", "bf16": "bf16", "fp16": "fp16", "w8a8": "bf16"}[self.name]
+        return {"fp32": "fp32", "bf16": "bf16", "fp16": "fp16", "w8a8": "bf16", "fp8": "fp16"}[self.name]
 
     @property
     def contraction_dtype(self) -> str:
-        return {"fp32": "fp32", "bf16": "bf16", "fp16": "fp16", "w8a8": "bf16"}[self.name]
+        """Contraction type of nodes the policy does not single out (fp8: the fp16 fallback)."""
+        return {"fp32": "fp32", "bf16": "bf16", "fp16": "fp16", "w8a8": "bf16", "fp8": "fp16"}[self.name]
 
 
 FP32_POLICY = PrecisionPolicy("fp32")
@@ -120,6 +129,9 @@ class Strategy:
         if node.op_type == "DequantizeLinear":
             return PrecisionProfile(compute_dtype="fp32", input_dtype="int8", output_dtype=out)
         if node.op_type in CONTRACTION_OPS:
+            if self.policy.name == "fp8" and self.executable_fp8(node, graph):
+                return PrecisionProfile(compute_dtype="fp8", accumulator_dtype="fp32", input_dtype="fp8",
+                                        weight_dtype="fp8", output_dtype=out)
             c = self.policy.contraction_dtype
             return PrecisionProfile(compute_dtype=c, accumulator_dtype="fp32", input_dtype=act,
                                     weight_dtype=c, output_dtype=out)
@@ -135,15 +147,32 @@ class Strategy:
                 return prec
         return "fp32"
 
-    def _preferred_tunable_precision(self, node: Node, graph: Graph) -> str:
-        if node.op_type in {"Conv", "Conv2d"}:
+    # GEMM-shaped fused forms judged by the reference's MatMul/Gemm rule.
+    _GEMM_FORMS = {"MatMul": "MatMul", "Linear": "Linear", "Gemm": "Gemm", "FusedMatMulBias": "MatMul",
+                   "FusedGemmEpilogue": "Gemm"}
+
+    def executable_fp8(self, node: Node, graph: Graph) -> bool:
+        """Whether the "fp8" policy runs `node` on the E4M3 GEMM: a GEMM-shaped
+        node with a constant rank-2 weight that the reference's rule sends to
+        fp8 (directly, or fp4 falling back to fp8 on this profile)."""
+        form = self._GEMM_FORMS.get(node.op_type)
+        if form is None or len(node.inputs) < 2:
+            return False
+        w = graph.get_tensor(node.inputs[1])
+        if w is None or not (w.is_initializer or w.is_constant) or len(w.shape) != 2:
+            return False
+        return self._supported_fallback(self._preferred_tunable_precision(node, graph, form)) == "fp8"
+
+    def _preferred_tunable_precision(self, node: Node, graph: Graph, op_type: Optional[str] = None) -> str:
+        op_type = op_type or node.op_type
+        if op_type in {"Conv", "Conv2d"}:
             ks = list(node.attributes.get("kernel_shape", []))
             w = graph.get_tensor(node.inputs[1]) if len(node.inputs) > 1 else None
             o = _concrete_dim(w.shape[0]) if w and w.shape else None
             c = _concrete_dim(w.shape[1]) if w and len(w.shape) > 1 else None
             aligned = o is not None and c is not None and o % 16 == 0 and c % 16 == 0
             return "fp8" if ks in ([1, 1], [1]) and aligned else "fp16"
-        if node.op_type in {"MatMul", "Linear", "Gemm"}:
+        if op_type in {"MatMul", "Linear", "Gemm"}:
             k, n = _gemm_k_n(node, graph)
             w = graph.get_tensor(node.inputs[1]) if len(node.inputs) > 1 else None
             const_w = bool(w and (w.is_initializer or w.is_constant))

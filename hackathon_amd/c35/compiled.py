@@ -13,6 +13,9 @@ the MI355X instead:
   GEMM, FusedAttentionScores + its P.V MatMul into one flash-attention launch
   writing straight into the FusedTransposeReshape layout, and
   QLinearMatMul -> DequantizeLinear -> bias (-> GELU) into one int8 GEMM.
+  Under the "fp8" policy a GEMM the plan marks fp8 becomes a row-wise E4M3
+  quantization of its activation plus one E4M3 GEMM (weights quantized per
+  output channel once at compile time) with the same absorbed epilogue.
 * Views: Reshape / Flatten / Split / Transpose produce strided views (no
   copies, no host syncs: shape tensors are read at compile time); a consumer
   that needs dense data materializes once.
@@ -20,7 +23,7 @@ the MI355X instead:
   padded to a vector multiple) between convolutions; graph inputs are
   converted once, and channel-last data feeds GlobalAveragePool / MaxPool /
   elementwise chains directly.
-* Precision: the plan's policy ("fp32" | "bf16" | "fp16" | "w8a8") picks the
+* Precision: the plan's policy ("fp32" | "bf16" | "fp16" | "w8a8" | "fp8") picks the
   storage dtype of every activation and the MFMA input type of every
   contraction; weights are packed and converted once at compile time.
 * Memory: activation buffers are re-planned over the grouped launch order
@@ -43,11 +46,12 @@ from .. import _lib
 from ..c3common.ir.graph import Graph, Node
 from ..c34.execution_plan import ExecutionPlan
 from ..c34.memory_pool import DeviceMemoryPool
-from ..device import BF16, Buffer, DeviceArray, PinnedArray, Stream, dtype_code, init
+from ..device import BF16, Buffer, DeviceArray, PinnedArray, Stream, dtype_code, init, synchronize
 from . import engine as E
 
-_POLICY_ACT = {"fp32": np.dtype(np.float32), "bf16": BF16, "fp16": np.dtype(np.float16), "w8a8": BF16}
-_MM_CODE = {"fp32": _lib.F32, "bf16": _lib.BF16, "fp16": _lib.F16, "w8a8": _lib.BF16}
+_POLICY_ACT = {"fp32": np.dtype(np.float32), "bf16": BF16, "fp16": np.dtype(np.float16), "w8a8": BF16,
+               "fp8": np.dtype(np.float16)}
+_MM_CODE = {"fp32": _lib.F32, "bf16": _lib.BF16, "fp16": _lib.F16, "w8a8": _lib.BF16, "fp8": _lib.F16}
 
 
 # ---------------------------------------------------------------- values and buffers
@@ -161,7 +165,11 @@ class CompiledPlan:
         self._graph_exec = None
         self._stream = Stream()
         self._consumers = self._consumer_map()
+        # per node: the contraction type the plan's precision profile chose
+        self._node_compute = {k.node_id: (k.precision_profile or {}).get("compute_dtype")
+                              for k in plan.kernel_steps}
         self._lower()
+        synchronize()  # compile-time weight conversions (null stream) before the plan's stream runs
         self._finalize()
 
     # ---------------------------------------------------------------- analysis helpers
@@ -811,16 +819,57 @@ class CompiledPlan:
         elif res.dtype != out.dtype or not res.dense:
             st.residual = self._dense(res, out.dtype)
 
-    def _gemm_node(self, node, a: Val, w_name: str, trans_b: int, bias_name: Optional[str], alpha: float,
-                   beta: float, act: int, lead: Tuple[int, ...]) -> None:
-        """out[lead..., n] = epilogue(alpha * A @ W + beta * bias) with absorbed tails."""
+    def _fp8_weight(self, name: str, trans_b: int) -> Tuple[Val, Val, int, int]:
+        """Weight as E4M3 codes B^T [n][k] + per-output-channel scales [n] (quantized on the GPU)."""
+        cache = self.__dict__.setdefault("_f8cache", {})
+        key = (name, trans_b)
+        if key not in cache:
+            w32, n, k = self._packed_weight_nk(name, trans_b, np.float32)
+            codes = DeviceArray.empty((n, k), np.uint8)
+            scales = DeviceArray.empty((n,), np.float32)
+            q = _lib.Fp8QuantArgs()
+            q.x, q.out, q.scale = w32.buf.array.ptr, codes.ptr, scales.ptr
+            q.rows, q.cols, q.ldx, q.ldo, q.x_dtype = n, k, k, k, _lib.F32
+            _lib.launch(q, None)
+            cache[key] = (Val((n, k), np.dtype(np.uint8), self._persist(codes)),
+                          Val((n,), np.dtype(np.float32), self._persist(scales)), n, k)
+        return cache[key]
+
+    def _gemm_fp8(self, node, a: Val, w_name: str, trans_b: int, st: "_Epi", alpha: float, beta: float,
+                  bmode, out_shape: Tuple[int, ...]) -> Val:
+        """Row-wise E4M3 quantization of A, then the E4M3 GEMM with the epilogue `st`."""
         m, k = math.prod(a.shape[:-1]), a.shape[-1]
-        code = self.mm_code
-        in_dtype = np.dtype(np.float32) if code == _lib.F32 else self.act_dtype
-        w, n, kw = self._packed_weight_nk(w_name, trans_b, in_dtype)
-        if kw != k or w.shape[1] != k:
-            raise NotImplementedError(f"GEMM {node.id}: K={k} (weight K={kw}) needs padding for 16-bit MFMA")
-        out_shape = tuple(lead) + (n,)
+        wq, ws, n, kw = self._fp8_weight(w_name, trans_b)
+        if kw != k:
+            raise NotImplementedError(f"GEMM {node.id}: K={k} vs weight K={kw}")
+        a2 = a if (a.dense and a.dtype == self.act_dtype) else self._dense(a, self.act_dtype)
+        qa = self._new((m, k), np.uint8)
+        sa = self._new((m,), np.float32)
+        xcode = dtype_code(a2.dtype)
+
+        def qbuild(r, a2=a2, qa=qa, sa=sa):
+            q = _lib.Fp8QuantArgs()
+            q.x, q.out, q.scale = self._ptr(a2, r), self._ptr(qa, r), self._ptr(sa, r)
+            q.rows, q.cols, q.ldx, q.ldo, q.x_dtype = m, k, k, k, xcode
+            return q
+        self._emit("quantize_fp8", qbuild, [a2], [qa, sa])
+        out = self._new(out_shape, self._out_dtype(st.final))
+        self._finish_residual(st, out)
+
+        def build(r, out=out, st=st):
+            g = _lib.Fp8GemmArgs()
+            g.a, g.b, g.a_scale, g.b_scale = self._ptr(qa, r), self._ptr(wq, r), self._ptr(sa, r), self._ptr(ws, r)
+            g.out = self._ptr(out, r)
+            g.m, g.n, g.k, g.lda, g.ldb, g.ldo, g.out_dtype = m, n, k, k, k, n, dtype_code(out.dtype)
+            self._fill_epi(g.epi, st, r, alpha, beta, bmode)
+            return g
+        self._emit(f"gemm_fp8:{node.op_type}", build, [qa, sa, wq, ws] + self._epi_reads(st), [out],
+                   flops=2.0 * m * n * k)
+        return out
+
+    def _gemm_epi_state(self, node, bias_name: Optional[str], act: int, m: int, n: int,
+                        out_shape: Tuple[int, ...]) -> Tuple["_Epi", Optional[int]]:
+        """Bias mode + the epilogue state with single-consumer tails absorbed."""
         bmode = None
         st = _Epi(act=act)
         if bias_name:
@@ -833,6 +882,27 @@ class CompiledPlan:
             st = self._absorb_tail(node.outputs[0], out_shape, st)
         else:
             st.final = node.outputs[0]
+        return st, bmode
+
+    def _gemm_node(self, node, a: Val, w_name: str, trans_b: int, bias_name: Optional[str], alpha: float,
+                   beta: float, act: int, lead: Tuple[int, ...]) -> None:
+        """out[lead..., n] = epilogue(alpha * A @ W + beta * bias) with absorbed tails."""
+        m, k = math.prod(a.shape[:-1]), a.shape[-1]
+        if self._node_compute.get(node.id) == "fp8":
+            if self.policy != "fp8":
+                raise ValueError(f"GEMM {node.id}: plan computes fp8 but the engine policy is {self.policy!r}")
+            n = self._fp8_weight(w_name, trans_b)[2]
+            st, bmode = self._gemm_epi_state(node, bias_name, act, m, n, tuple(lead) + (n,))
+            self.vals[st.final] = self._gemm_fp8(node, a, w_name, trans_b, st, alpha, beta, bmode,
+                                                 tuple(lead) + (n,))
+            return
+        code = self.mm_code
+        in_dtype = np.dtype(np.float32) if code == _lib.F32 else self.act_dtype
+        w, n, kw = self._packed_weight_nk(w_name, trans_b, in_dtype)
+        if kw != k or w.shape[1] != k:
+            raise NotImplementedError(f"GEMM {node.id}: K={k} (weight K={kw}) needs padding for 16-bit MFMA")
+        out_shape = tuple(lead) + (n,)
+        st, bmode = self._gemm_epi_state(node, bias_name, act, m, n, out_shape)
         a2 = a if (a.dense and a.dtype == in_dtype) else self._dense(a, in_dtype)
         out = self._new(out_shape, self._out_dtype(st.final))
         self._finish_residual(st, out)

@@ -187,6 +187,7 @@ struct Problem {
   int qmode, y_zero;
   float a_scale, y_scale;
   const float* b_scale;
+  const float* a_rows;  // fp8 GEMM (c3h_gemm_fp8): per-row A scale
   c3h_epilogue epi;
 };
 
@@ -516,11 +517,16 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(Problem p) {
 // =====================================================================
 typedef __attribute__((ext_vector_type(4))) int i32x4;
 
+// kStep: 16-byte K chunks of a tile row one MFMA consumes per lane group
+// (4: two MFMA steps per 128-byte row; 8: one step).  kScaled: accumulators
+// are multiplied by a_rows[m] * b_scale[n] before the epilogue.
 struct MmaBF16 {
   typedef bf16x8 vec;
   typedef f32x4 acc_t;
   static constexpr int ES = 2;
   static constexpr bool kInt = false;
+  static constexpr int kStep = 4;
+  static constexpr bool kScaled = false;
   static __device__ __forceinline__ acc_t mma(vec a, vec b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
@@ -530,6 +536,8 @@ struct MmaF16 {
   typedef f32x4 acc_t;
   static constexpr int ES = 2;
   static constexpr bool kInt = false;
+  static constexpr int kStep = 4;
+  static constexpr bool kScaled = false;
   static __device__ __forceinline__ acc_t mma(vec a, vec b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
@@ -539,10 +547,42 @@ struct MmaI8 {
   typedef i32x4 acc_t;
   static constexpr int ES = 1;
   static constexpr bool kInt = true;
+  static constexpr int kStep = 4;
+  static constexpr bool kScaled = false;
   static __device__ __forceinline__ acc_t mma(vec a, vec b, acc_t c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
   }
 };
+// OCP E4M3 x E4M3 -> fp32 (v_mfma_f32_16x16x128_f8f6f4, format code 0 on
+// both operands, no block scales).  A lane supplies 32 K bytes: lane group g
+// (lane >> 4) takes tile-row chunks g and g + 4.  A and B use the same
+// lane/byte -> k assignment, so the dot product covers each k exactly once
+// whatever order the instruction walks K in.
+typedef __attribute__((ext_vector_type(8))) int i32x8;
+struct MmaF8 {
+  typedef i32x8 vec;
+  typedef f32x4 acc_t;
+  static constexpr int ES = 1;
+  static constexpr bool kInt = false;
+  static constexpr int kStep = 8;
+  static constexpr bool kScaled = true;
+  static __device__ __forceinline__ acc_t mma(vec a, vec b, acc_t c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+  }
+};
+
+// MFMA operand of tile row `r` (row base `row`, XOR-swizzled 16-byte chunks)
+// for the K step starting at chunk ks.
+template <typename Mma>
+__device__ __forceinline__ typename Mma::vec read_operand(const uint8_t* row, int r, int ks, int lchunk) {
+  if constexpr (Mma::kStep == 8) {
+    const i32x4 lo = *reinterpret_cast<const i32x4*>(row + ((lchunk ^ (r & 7)) << 4));
+    const i32x4 hi = *reinterpret_cast<const i32x4*>(row + (((lchunk + 4) ^ (r & 7)) << 4));
+    return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  } else {
+    return *reinterpret_cast<const typename Mma::vec*>(row + (((ks + lchunk) ^ (r & 7)) << 4));
+  }
+}
 
 enum AMode16 { kConvTap = 3, kConvStem = 4 };
 
@@ -877,6 +917,38 @@ __device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int6
   });
 }
 
+// fp8 GEMM: C^T accumulators (row m = mbase + 16 i + l16, column
+// n = nbase + 16 j + 4 lg + r) times a_rows[m] * b_scale[n], in registers,
+// before either epilogue.  Rows / columns past the edge get scale 0 (never
+// stored).
+template <int TM, int TN>
+__device__ __forceinline__ void scale_acc(f32x4 (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane) {
+  const KArg<Problem>& p = kernel_arg<Problem>();
+  const int l16 = lane & 15, lg = lane >> 4;
+  float sb[TN][4];
+  static_for<TN>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    const int64_t n = nbase + 16 * j + 4 * lg;
+    if (n + 4 <= p.n) {
+      const float4 q = *reinterpret_cast<const float4*>(p.b_scale + n);
+      sb[j][0] = q.x; sb[j][1] = q.y; sb[j][2] = q.z; sb[j][3] = q.w;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sb[j][r] = n + r < p.n ? p.b_scale[n + r] : 0.0f;
+    }
+  });
+  static_for<TM>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    const int64_t m = mbase + 16 * i + l16;
+    const float sa = m < p.m ? p.a_rows[m] : 0.0f;
+    static_for<TN>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = (acc[i][j][r] * sa) * sb[j][r];
+    });
+  });
+}
+
 // Whether epilogue_direct_q applies: int32 / int8 outputs need only aligned
 // row-major stores; dequantized ones also need the common float epilogue.
 __device__ __forceinline__ bool epilogue_q_direct_ok(const KArg<Problem>& p, bool vec4);
@@ -1114,17 +1186,17 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
   const int lrow = lane & 15, lchunk = lane >> 4;
   auto compute = [&](int cur) {
 #pragma unroll
-    for (int ks = 0; ks < 8; ks += 4) {  // two MFMA K steps of 64 bytes
+    for (int ks = 0; ks < 8; ks += Mma::kStep) {  // MFMA K steps of 16 * kStep bytes
       vec av[TM], bv[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = wm * WTM + i * 16 + lrow;
-        av[i] = *reinterpret_cast<const vec*>(&As[cur][r][swz(r, ks + lchunk)]);
+        av[i] = read_operand<Mma>(&As[cur][r][0], r, ks, lchunk);
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int r = wn * WTN + j * 16 + lrow;
-        bv[j] = *reinterpret_cast<const vec*>(&Bs[cur][r][swz(r, ks + lchunk)]);
+        bv[j] = read_operand<Mma>(&Bs[cur][r][0], r, ks, lchunk);
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
@@ -1169,6 +1241,7 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
     }
   }
   if (kt < ktiles) compute(0);  // odd tile count: the last tile sits in buffer 0
+  if constexpr (Mma::kScaled) scale_acc<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane);
 
   // Epilogue: a lane holds (m = 4*(lane/16)+r, n = lane%16) of each 16x16
   // tile.  The whole wave tile is staged in LDS (accumulators only ever
@@ -1376,17 +1449,17 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
     const uint8_t* As = smem + (kt % S) * STAGE;
     const uint8_t* Bs = As + BM * RB;
 #pragma unroll
-    for (int ks = 0; ks < 8; ks += 4) {
+    for (int ks = 0; ks < 8; ks += Mma::kStep) {
       vec av[TM], bv[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = wm * WTM + i * 16 + lrow;
-        av[i] = *reinterpret_cast<const vec*>(As + r * RB + (((ks + lchunk) ^ (r & 7)) << 4));
+        av[i] = read_operand<Mma>(As + r * RB, r, ks, lchunk);
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int r = wn * WTN + j * 16 + lrow;
-        bv[j] = *reinterpret_cast<const vec*>(Bs + r * RB + (((ks + lchunk) ^ (r & 7)) << 4));
+        bv[j] = read_operand<Mma>(Bs + r * RB, r, ks, lchunk);
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
@@ -1397,6 +1470,7 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
     }
   }
 
+  if constexpr (Mma::kScaled) scale_acc<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane);
   TO* outp = static_cast<TO*>(p.out);
   const TO* resp = p.epi.residual ? static_cast<const TO*>(p.epi.residual) : nullptr;
   {
@@ -1555,6 +1629,29 @@ int launch_h_any(Problem p, int64_t batch, hipStream_t s, int in_dtype) {
                               : launch_h<MmaF16, f16_t, AM>(p, batch, s, in_dtype);
 }
 
+// fp8 GEMM: the two-stage DMA kernel where its 32-bit buffer offsets reach,
+// else the register-prefetch kernel.
+template <typename TO>
+int launch_fp8(Problem p, hipStream_t s) {
+  dim3 grid;
+  if (dma_eligible(p, 1, kDenseK)) {
+    if (p.n <= 64) {
+      grid_of<256, 64>(p, 1, grid);
+      hipLaunchKernelGGL((mfma_gemm_dma_kernel<MmaF8, TO, 256, 64, 4, 1, kDenseK, 2>), grid, dim3(kThreads), 0, s, p);
+    } else {
+      grid_of<128, 128>(p, 1, grid);
+      hipLaunchKernelGGL((mfma_gemm_dma_kernel<MmaF8, TO, 128, 128, 2, 2, kDenseK, 2>), grid, dim3(kThreads), 0, s, p);
+    }
+  } else if (p.n <= 64) {
+    grid_of<256, 64>(p, 1, grid);
+    hipLaunchKernelGGL((mfma_gemm_kernel<MmaF8, TO, 256, 64, 4, 1, kDenseK>), grid, dim3(kThreads), 0, s, p);
+  } else {
+    grid_of<128, 128>(p, 1, grid);
+    hipLaunchKernelGGL((mfma_gemm_kernel<MmaF8, TO, 128, 128, 2, 2, kDenseK>), grid, dim3(kThreads), 0, s, p);
+  }
+  return launch_status("gemm_fp8");
+}
+
 int check_epilogue(const c3h_epilogue& e) {
   C3H_REQUIRE(e.bias_mode >= 0 && e.bias_mode <= 4, "epilogue: bad bias_mode %d", e.bias_mode);
   C3H_REQUIRE(e.bias_mode == 0 || e.bias != nullptr, "epilogue: bias_mode %d needs a bias pointer", e.bias_mode);
@@ -1695,6 +1792,37 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
     return launch_h_any<kConvStem>(p, 1, s, a->in_dtype);
   }
   return fail(C3H_EUNSUPPORTED, "conv2d: input dtype %d unsupported", a->in_dtype);
+}
+
+int c3h_gemm_fp8(const c3h_fp8_gemm_args* a, void* stream) {
+  C3H_REQUIRE(a != nullptr, "gemm_fp8: null args");
+  C3H_REQUIRE(a->m >= 0 && a->n >= 0 && a->k >= 1, "gemm_fp8: bad sizes");
+  C3H_REQUIRE(a->k % 16 == 0 && a->lda % 16 == 0 && a->ldb % 16 == 0, "gemm_fp8: k, lda, ldb must be multiples of 16");
+  C3H_REQUIRE(a->lda >= a->k && a->ldb >= a->k && a->ldo >= a->n, "gemm_fp8: leading dimension too small");
+  C3H_REQUIRE(aligned(a->a, 16) && aligned(a->b, 16), "gemm_fp8: operands must be 16-byte aligned");
+  C3H_REQUIRE(a->a_scale != nullptr && a->b_scale != nullptr && aligned(a->b_scale, 16),
+              "gemm_fp8: a_scale and a 16-byte aligned b_scale are required");
+  C3H_REQUIRE(a->out_dtype == C3H_F32 || a->out_dtype == C3H_BF16 || a->out_dtype == C3H_F16,
+              "gemm_fp8: output dtype must be fp32, bf16 or fp16");
+  C3H_REQUIRE(a->m < (int64_t{1} << 31) && a->n < (int64_t{1} << 31), "gemm_fp8: m and n must be below 2^31");
+  int rc = check_epilogue(a->epi);
+  if (rc) return rc;
+  if (a->m == 0 || a->n == 0) return C3H_OK;
+  C3H_REQUIRE(ceil_div(a->m, 64) * ceil_div(a->n, 64) < (int64_t{1} << 31), "gemm_fp8: too many tiles");
+  Problem p;
+  memset(&p, 0, sizeof(p));
+  p.a = a->a; p.b = a->b; p.out = a->out;
+  p.m = a->m; p.n = a->n; p.k = a->k; p.lda = a->lda; p.ldb = a->ldb; p.ldo = a->ldo;
+  p.a_rows = a->a_scale; p.b_scale = a->b_scale;
+  p.out_dtype = a->out_dtype;
+  p.epi = a->epi;
+  p.ho = 1; p.wo = 1;
+  p.a_bytes = (a->m - 1) * a->lda + a->k;
+  p.b_bytes = (a->n - 1) * a->ldb + a->k;
+  hipStream_t s = as_stream(stream);
+  if (a->out_dtype == C3H_F32) return launch_fp8<float>(p, s);
+  if (a->out_dtype == C3H_BF16) return launch_fp8<bf16_t>(p, s);
+  return launch_fp8<f16_t>(p, s);
 }
 
 int c3h_qgemm(const c3h_qgemm_args* a, void* stream) {

@@ -677,6 +677,91 @@ __global__ void __launch_bounds__(kBlock) quantize_vec_kernel(c3h_quantize_args 
   }
 }
 
+// Row-wise E4M3 quantization (c3h_quantize_fp8_rows): one wave per row.
+// NV > 0: the row (cols <= 512 NV) stays in registers between the amax pass
+// and the encode pass; NV == 0: any width, the encode pass re-reads the row
+// (from L2).  Encoding: v_cvt_pk_fp8_f32 (round to nearest even) of values
+// clamped to +-448 first, four codes packed little-endian per 32-bit word.
+__device__ __forceinline__ uint2 fp8_encode8(const float* v, float inv) {
+  float q[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) q[e] = fminf(fmaxf(v[e] * inv, -448.0f), 448.0f);
+  int w0 = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+  w0 = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], w0, true);
+  int w1 = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
+  w1 = __builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], w1, true);
+  return uint2{static_cast<uint32_t>(w0), static_cast<uint32_t>(w1)};
+}
+
+template <typename TX, int NV>
+__global__ void __launch_bounds__(kBlock) quantize_fp8_rows_kernel(c3h_fp8_quant_args a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + wave;
+  if (row >= a.rows) return;
+  const int64_t nvec = a.cols / 8;
+  const TX* x = static_cast<const TX*>(a.x) + row * a.ldx;
+  uint8_t* out = a.out + row * a.ldo;
+  constexpr int R = NV > 0 ? NV : 1;
+  float v[R][8];
+  float amax = 0.0f;
+  bool bad = false;
+  auto scan = [&](const float* t) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float m = fabsf(t[e]);
+      bad |= !(m <= 3.402823466e38f);  // Inf or NaN
+      amax = fmaxf(amax, m);
+    }
+  };
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t vi = lane + 64 * j;
+      if (vi < nvec) {
+        load_vec16(x + vi * 8, v[j]);
+        if constexpr (sizeof(TX) == 4) load_vec16(x + vi * 8 + 4, v[j] + 4);
+        scan(v[j]);
+      }
+    }
+  } else {
+    for (int64_t vi = lane; vi < nvec; vi += 64) {
+      load_vec16(x + vi * 8, v[0]);
+      if constexpr (sizeof(TX) == 4) load_vec16(x + vi * 8 + 4, v[0] + 4);
+      scan(v[0]);
+    }
+  }
+  amax = wave_max(amax);
+  bad = __any(bad);
+  const float inv = amax > 0.0f ? fminf(448.0f / amax, 3.402823466e38f) : 0.0f;
+  const uint2 nan8 = uint2{0x7f7f7f7fu, 0x7f7f7f7fu};
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t vi = lane + 64 * j;
+      if (vi < nvec) *reinterpret_cast<uint2*>(out + vi * 8) = bad ? nan8 : fp8_encode8(v[j], inv);
+    }
+  } else {
+    for (int64_t vi = lane; vi < nvec; vi += 64) {
+      load_vec16(x + vi * 8, v[0]);
+      if constexpr (sizeof(TX) == 4) load_vec16(x + vi * 8 + 4, v[0] + 4);
+      *reinterpret_cast<uint2*>(out + vi * 8) = bad ? nan8 : fp8_encode8(v[0], inv);
+    }
+  }
+  if (lane == 0) a.scale[row] = bad ? __builtin_nanf("") : amax / 448.0f;
+}
+
+template <typename TX>
+int launch_fp8_rows(const c3h_fp8_quant_args& a, hipStream_t s) {
+  const dim3 g(static_cast<unsigned>(ceil_div(a.rows, kBlock / 64))), b(kBlock);
+  const int64_t nvec = a.cols / 8;
+  if (nvec <= 64) hipLaunchKernelGGL((quantize_fp8_rows_kernel<TX, 1>), g, b, 0, s, a);
+  else if (nvec <= 128) hipLaunchKernelGGL((quantize_fp8_rows_kernel<TX, 2>), g, b, 0, s, a);
+  else if (nvec <= 256) hipLaunchKernelGGL((quantize_fp8_rows_kernel<TX, 4>), g, b, 0, s, a);
+  else if (nvec <= 512) hipLaunchKernelGGL((quantize_fp8_rows_kernel<TX, 8>), g, b, 0, s, a);
+  else hipLaunchKernelGGL((quantize_fp8_rows_kernel<TX, 0>), g, b, 0, s, a);
+  return launch_status("quantize_fp8_rows");
+}
+
 __global__ void dequantize_kernel(c3h_dequantize_args a) {
   int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < a.count; i += stride)
@@ -1039,6 +1124,23 @@ int c3h_quantize(const c3h_quantize_args* a, void* stream) {
   }
   hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(a->count)), dim3(kBlock), 0, as_stream(stream), *a);
   return launch_status("quantize");
+}
+
+int c3h_quantize_fp8_rows(const c3h_fp8_quant_args* a, void* stream) {
+  C3H_REQUIRE(a && a->rows >= 0 && a->cols >= 0, "quantize_fp8_rows: bad args");
+  C3H_REQUIRE(a->cols % 8 == 0 && a->ldx % 8 == 0 && a->ldo % 8 == 0 && a->ldx >= a->cols && a->ldo >= a->cols,
+              "quantize_fp8_rows: cols, ldx, ldo must be multiples of 8 with ldx, ldo >= cols");
+  C3H_REQUIRE((reinterpret_cast<uintptr_t>(a->x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 7) == 0,
+              "quantize_fp8_rows: x must be 16-byte and out 8-byte aligned");
+  C3H_REQUIRE(a->x_dtype == C3H_F32 || a->x_dtype == C3H_BF16 || a->x_dtype == C3H_F16,
+              "quantize_fp8_rows: x dtype must be fp32, bf16 or fp16");
+  C3H_REQUIRE(a->scale != nullptr, "quantize_fp8_rows: scale output required");
+  C3H_REQUIRE(ceil_div(a->rows, kBlock / 64) < (int64_t{1} << 31), "quantize_fp8_rows: too many rows");
+  if (a->rows == 0) return C3H_OK;
+  hipStream_t st = as_stream(stream);
+  if (a->x_dtype == C3H_F32) return launch_fp8_rows<float>(*a, st);
+  if (a->x_dtype == C3H_BF16) return launch_fp8_rows<bf16_t>(*a, st);
+  return launch_fp8_rows<f16_t>(*a, st);
 }
 
 int c3h_dequantize(const c3h_dequantize_args* a, void* stream) {

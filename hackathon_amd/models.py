@@ -14,6 +14,9 @@ Configs (BASELINE.json:7-11):
   3 resnet18_224   ResNet-18 (7x7/2 stem + max-pool), bf16 policy, B=256, 224x224
   4 decoder_fp16   6 layers, d=512, 8 heads, FFN 2048 GELU, pre-LN, vocab 8192, S=256, B=64
   5 decoder_w8a8   12 layers, d=768, 12 heads, FFN 3072, vocab 32000, S=1024, B=16, W8A8 Linear
+Extra workload (not a BASELINE config):
+    decoder_fp8    config 4's model under the "fp8" policy (E4M3 GEMMs for every
+                   aligned constant-weight Linear, fp16 elsewhere)
 """
 
 from __future__ import annotations
@@ -355,6 +358,7 @@ CONFIGS: Dict[str, Callable[..., Model]] = {
     "resnet18_cifar": build_resnet18_cifar,
     "resnet18_224": build_resnet18_224,
     "decoder_fp16": lambda **kw: build_decoder(**{"precision": "fp16", **kw}),
+    "decoder_fp8": lambda **kw: build_decoder(**{"precision": "fp8", "name": "decoder_fp8", **kw}),
     "decoder_w8a8": lambda **kw: build_decoder(**{"batch": 16, "seq": 1024, "d_model": 768, "heads": 12,
                                                   "ffn": 3072, "layers": 12, "vocab": 32000,
                                                   "quantized": True, **kw}),

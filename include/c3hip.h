@@ -577,6 +577,48 @@ typedef struct {
 int c3h_dequantize(const c3h_dequantize_args* a, void* stream);
 
 /* ------------------------------------------------------------------ */
+/* fp8 (OCP E4M3) GEMM: the executable form of the reference's         */
+/* structural `matmul_f8` (c32/hardware.py:80-81), chosen by the mixed  */
+/* policy for aligned GEMMs (c32/strategy.py:150-157) with fp32         */
+/* accumulation (c32/strategy.py:103-108).                              */
+/* ------------------------------------------------------------------ */
+
+/* Row-wise dynamic quantization to E4M3: per row r, amax = max |x[r,:]|,
+ * scale[r] = amax / 448, out[r,k] = E4M3(x[r,k] * min(448 / amax, FLT_MAX))
+ * (round to nearest even, saturating at +-448).  A zero row gives scale 0
+ * and zero codes; a row holding Inf/NaN gives scale NaN and NaN codes
+ * (0x7F).  Used for activations (rows = tokens) and for weights packed as
+ * B^T [n][k] (rows = output channels).  cols % 8 == 0, ldx % 8 == 0,
+ * ldo % 8 == 0, x 16-byte and out 8-byte aligned. */
+typedef struct {
+  const void* x;    /* [rows][ldx] fp32 / fp16 / bf16 */
+  uint8_t* out;     /* [rows][ldo] E4M3 codes */
+  float* scale;     /* [rows] */
+  int64_t rows, cols, ldx, ldo;
+  int32_t x_dtype;
+  int32_t pad_;
+} c3h_fp8_quant_args;
+int c3h_quantize_fp8_rows(const c3h_fp8_quant_args* a, void* stream);
+
+/* out[m,n] = epilogue((sum_k A[m,k] * B[n,k]) * a_scale[m] * b_scale[n])
+ * with E4M3 operands (B packed [n][k]), fp32 accumulation on the MFMA, and
+ * the common epilogue (bias, residual, activation/program) into fp32, bf16
+ * or fp16.  k, lda, ldb multiples of 16; b_scale 16-byte aligned. */
+typedef struct {
+  const uint8_t* a;
+  const uint8_t* b;
+  const float* a_scale; /* [m] */
+  const float* b_scale; /* [n] */
+  void* out;
+  int64_t m, n, k;
+  int64_t lda, ldb, ldo;
+  int32_t out_dtype;
+  int32_t pad_;
+  c3h_epilogue epi;
+} c3h_fp8_gemm_args;
+int c3h_gemm_fp8(const c3h_fp8_gemm_args* a, void* stream);
+
+/* ------------------------------------------------------------------ */
 /* Native timeline interpreter and graph capture                        */
 /* ------------------------------------------------------------------ */
 
@@ -610,7 +652,9 @@ enum c3h_op_kind {
   C3H_OP_DEQUANTIZE = 29,
   C3H_OP_BNFOLD = 30,
   C3H_OP_PACK = 31,
-  C3H_OP_CONV_POOL = 32
+  C3H_OP_CONV_POOL = 32,
+  C3H_OP_QUANT_FP8 = 33,
+  C3H_OP_GEMM_FP8 = 34
 };
 
 typedef struct {
@@ -643,7 +687,7 @@ int c3h_graph_destroy(void* graph_exec);
  * c3h_im2col_args, c3h_layout_args, c3h_pool_args, c3h_epilogue,
  * c3h_gemm_args, c3h_conv_args, c3h_attn_scores_args, c3h_flash_args,
  * c3h_quantize_args, c3h_qgemm_args, c3h_dequantize_args, c3h_op,
- * c3h_pack_args, c3h_conv_pool_args.
+ * c3h_pack_args, c3h_conv_pool_args, c3h_fp8_quant_args, c3h_fp8_gemm_args.
  * Returns the number of sizes available (host-only; needs no GPU). */
 int32_t c3h_abi_sizes(int64_t* out, int32_t capacity);
 

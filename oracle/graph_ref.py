@@ -9,7 +9,10 @@ TEST INFRASTRUCTURE ONLY (see oracle/registry_ref.py).
   the registry oracle: the reference's own decomposition evaluated on the host
   (c35/executor.py:514-604 without streams).  With a 16-bit policy it rounds
   where the executable policy rounds: contraction inputs and weights, and
-  every node output stored in the activation type.
+  every node output stored in the activation type.  Under the "fp8" policy a
+  step whose profile computes fp8 sees its activation quantized row-wise and
+  its weight per output channel to E4M3 and back (oracle.fp8_ref), then the
+  fp32 kernel.
 * `run_graph` evaluates the unfused graph node by node with ONNX opset-17
   semantics (the reference's GraphExecutor, c35/executor.py:221-321).
 * `calibration_ranges` runs `run_graph` with every QDQ pair bypassed and
@@ -23,6 +26,7 @@ from typing import Any, Dict, List, Optional, Tuple
 
 import numpy as np
 
+from . import fp8_ref as F8
 from . import registry_ref as R
 
 F32 = np.float32
@@ -83,7 +87,7 @@ def _lookup_policy_kernel(name: str):
     renames (`matmul_bf16`, `fused_ew_fp16`, ...) are evaluated with the fp32
     kernel, and run_plan applies the policy's rounding at node boundaries.
     """
-    for suffix in ("_bf16", "_fp16", "_f16", "_fp8", "_fp4", "_int8"):
+    for suffix in ("_bf16", "_fp16", "_f16", "_fp8", "_f8", "_fp4", "_int8"):
         if name.endswith(suffix):
             return R.lookup(name[: -len(suffix)] + "_f32")
     return R.lookup(name)
@@ -101,8 +105,8 @@ def run_plan(plan, graph, weights: Dict[str, np.ndarray], feed: Dict[str, np.nda
     node_last_step: Dict[str, int] = {}
     for k in plan.kernel_steps:
         node_last_step[k.node_id] = k.step_index
-    round_inputs = policy in ("bf16", "fp16", "w8a8")
-    act = {"bf16": "bf16", "fp16": "fp16", "w8a8": "bf16"}.get(policy, "fp32")
+    round_inputs = policy in ("bf16", "fp16", "w8a8", "fp8")
+    act = {"bf16": "bf16", "fp16": "fp16", "w8a8": "bf16", "fp8": "fp16"}.get(policy, "fp32")
     if round_inputs:
         for name in feed:
             if np.asarray(feed[name]).dtype == np.float32:
@@ -119,6 +123,8 @@ def run_plan(plan, graph, weights: Dict[str, np.ndarray], feed: Dict[str, np.nda
                     and np.asarray(v).dtype == F32 and np.asarray(v).ndim >= 2:
                 v = round_to(v, prof["weight_dtype"])
             ins.append(v)
+        if prof.get("compute_dtype") == "fp8":
+            ins = _fp8_operands(ins, k.operator_params)
         outs = []
         for n in k.logical_outputs:
             count = max(_elements(plan, n, graph, plan.batch_size), 1)
@@ -132,6 +138,21 @@ def run_plan(plan, graph, weights: Dict[str, np.ndarray], feed: Dict[str, np.nda
                 o = round_to(o, prof["output_dtype"])
             values[n] = o
     return {t.name: values[t.name] for t in graph.outputs}
+
+
+def _fp8_operands(ins: List[np.ndarray], params: Dict[str, Any]) -> List[np.ndarray]:
+    """E4M3 round trip of a GEMM step's activation (per row) and weight (per output channel)."""
+    a = np.asarray(ins[0], F32)
+    w = np.asarray(ins[1], F32)
+    qa, sa = F8.quantize_rows(a.reshape(-1, a.shape[-1]))
+    a8 = F8.dequantize_rows(qa, sa).reshape(a.shape)
+    if int(params.get("transB", 0)):
+        qw, sw = F8.quantize_rows(w)
+        w8 = F8.dequantize_rows(qw, sw)
+    else:
+        qw, sw = F8.quantize_rows(np.ascontiguousarray(w.T))
+        w8 = np.ascontiguousarray(F8.dequantize_rows(qw, sw).T)
+    return [a8, w8] + list(ins[2:])
 
 
 # -- unfused graph evaluation (ONNX semantics) --------------------------------------------------

@@ -109,6 +109,65 @@ def test_compiled_w8a8_decoder(gpu):
     assert _agree(got, ref) >= 0.9
 
 
+def _rms(x) -> float:
+    return float(np.sqrt(np.mean(np.square(np.asarray(x, np.float64)))))
+
+
+def test_compiled_fp8_mlp_matches_fp8_oracle(gpu):
+    """The "fp8" policy on the MLP: 784->512 and 512->256 run E4M3 (the 256->10
+    head is not 16-aligned and stays fp16).  The graph input feeds the first
+    quantization directly, so the engine tracks the oracle's E4M3 emulation
+    of the plan closely: the 16-bit workload gate (2e-2 of the logit range)."""
+    from hackathon_amd import models
+
+    m = models.build("mlp", batch=64)
+    plan, prog, weights = _compiled(m, "fp8")
+    assert sum(k.startswith("gemm_fp8:") for k in prog.node_kinds) == 2
+    got = _logits(prog, m.inputs)["logits"]
+    ref = G.run_plan(plan, m.graph, weights, m.inputs, policy="fp8")["logits"]
+    ref32 = G.run_plan(plan, m.graph, weights, m.inputs)["logits"]
+    got = got.reshape(ref.shape)
+    scale = max(1.0, float(np.max(np.abs(ref32))))
+    diff = float(np.max(np.abs(got - ref)))
+    print(f"mlp/fp8: max|diff| vs fp8 oracle {diff:.3e}, vs fp32 {float(np.max(np.abs(got - ref32))):.3e} "
+          f"(logit range {scale:.2f}), argmax agree vs oracle {_agree(got, ref):.4f}")
+    assert diff <= 2e-2 * scale
+    assert _agree(got, ref) >= 0.95
+
+
+def test_compiled_fp8_decoder(gpu):
+    """The "fp8" policy on a decoder: every aligned constant-weight Linear (the
+    LM head included) runs as E4M3 quantize + E4M3 GEMM.  The engine rounds
+    activations at fewer places than the oracle's node-by-node emulation, and
+    a one-ulp fp16 difference can move an E4M3 code by a whole step (2^-4
+    relative), so after nine chained E4M3 GEMMs the engine and the emulation
+    differ by as much as either differs from fp32.  The gate is therefore
+    accuracy against fp32: the engine's RMS logit error may exceed the E4M3
+    definition's own (the oracle emulation's) by at most 25 %, its largest
+    error stays within 0.1 of the logit range, and its argmax agreement with
+    fp32 is within 0.05 of the emulation's."""
+    from hackathon_amd import models
+
+    m = models.build("decoder_fp8", **{**SMALL["decoder_fp16"], "vocab": 320})
+    plan, prog, weights = _compiled(m, "fp8")
+    fp8_nodes = {k.node_id for k in plan.kernel_steps if (k.precision_profile or {}).get("compute_dtype") == "fp8"}
+    assert len(fp8_nodes) == 2 * 4 + 1
+    assert sum(k.startswith("gemm_fp8:") for k in prog.node_kinds) == len(fp8_nodes)
+    assert sum(k == "quantize_fp8" for k in prog.node_kinds) == len(fp8_nodes)
+    got = _logits(prog, m.inputs)["logits"]
+    ref8 = G.run_plan(plan, m.graph, weights, m.inputs, policy="fp8")["logits"]
+    ref32 = G.run_plan(plan, m.graph, weights, m.inputs)["logits"]
+    got = got.reshape(ref8.shape)
+    scale = max(1.0, float(np.max(np.abs(ref32))))
+    e_gpu, e_def = _rms(got - ref32), _rms(ref8 - ref32)
+    print(f"decoder_fp8: RMS error vs fp32 {e_gpu:.3e} (E4M3 emulation {e_def:.3e}), max "
+          f"{float(np.max(np.abs(got - ref32))):.3e} (logit range {scale:.2f}), argmax agree vs fp32 "
+          f"{_agree(got, ref32):.4f} (emulation {_agree(ref8, ref32):.4f})")
+    assert e_gpu <= 1.25 * e_def
+    assert float(np.max(np.abs(got - ref32))) <= 0.1 * scale
+    assert _agree(got, ref32) >= _agree(ref8, ref32) - 0.05
+
+
 class _AllOnes(dict):
     """Unit scales for every name (the calibration forward bypasses QDQ)."""
 
