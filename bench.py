@@ -38,7 +38,7 @@ HEADLINE = "resnet18_224"
 PEAK = {"bf16": 2500.0, "fp16": 2500.0, "fp8": 5000.0, "int8": 5000.0, "fp32": 157.3, "hbm": 8000.0}
 # Dominant kernel family and its roofline per workload.
 DOMINANT = {
-    "mlp": (["gemm"], "fp32", "fp32 GEMM (MFMA 16x16x4 f32)"),
+    "mlp": (["gemm", "splitk_reduce"], "fp32", "fp32 GEMM, split-K partials + ordered reduce (MFMA 16x16x4 f32)"),
     "resnet18_cifar": (["conv"], "fp32", "implicit-GEMM conv (fp32 MFMA)"),
     "resnet18_224": (["conv"], "bf16", "implicit-GEMM conv (bf16 MFMA 16x16x32)"),
     "decoder_fp16": (["gemm"], "fp16", "GEMM + fused epilogues (fp16 MFMA 16x16x32)"),

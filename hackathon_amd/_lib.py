@@ -34,7 +34,7 @@ OP_NOP, OP_EVENT_RECORD, OP_EVENT_WAIT, OP_COPY = 0, 1, 2, 3
 OP_FILL, OP_CAST, OP_EW, OP_STRIDED_COPY, OP_REDUCE, OP_SOFTMAX, OP_LAYERNORM, OP_BATCHNORM, \
     OP_GATHER, OP_ARGMAX, OP_IM2COL, OP_LAYOUT, OP_MAXPOOL, OP_GEMM, OP_CONV, OP_ATTN_SCORES, \
     OP_FLASH, OP_QUANTIZE, OP_QGEMM, OP_DEQUANTIZE, OP_BNFOLD, OP_PACK, OP_CONV_POOL, OP_QUANT_FP8, \
-    OP_GEMM_FP8 = range(10, 35)
+    OP_GEMM_FP8, OP_SPLITK = range(10, 36)
 
 vp = C.c_void_p
 i32 = C.c_int32
@@ -196,6 +196,11 @@ class Fp8GemmArgs(C.Structure):
                 ("pad_", i32), ("epi", Epilogue)]
 
 
+class SplitKArgs(C.Structure):
+    _fields_ = [("partial", vp), ("out", vp), ("m", i64), ("n", i64), ("ldo", i64), ("splits", i32),
+                ("out_dtype", i32), ("epi", Epilogue)]
+
+
 class ConvPoolArgs(C.Structure):
     _fields_ = [("x", vp), ("w", vp), ("bias", vp), ("out", vp)] + [(n, i32) for n in (
         "n", "c", "h", "w_", "o", "k_stride", "kh", "kw", "sh", "sw", "pad_top", "pad_left", "ho", "wo",
@@ -210,7 +215,8 @@ class Op(C.Structure):
 ABI_ORDER = [Props, FillArgs, CastArgs, EwArgs, CopyArgs, ReduceArgs, SoftmaxArgs, LayerNormArgs,
              BatchNormArgs, BnFoldArgs, GatherArgs, ArgmaxArgs, Im2colArgs, LayoutArgs, PoolArgs,
              Epilogue, GemmArgs, ConvArgs, AttnScoresArgs, FlashArgs, QuantizeArgs, QGemmArgs,
-             DequantizeArgs, Op, PackArgs, ConvPoolArgs, Fp8QuantArgs, Fp8GemmArgs]
+             DequantizeArgs, Op, PackArgs, ConvPoolArgs, Fp8QuantArgs, Fp8GemmArgs,
+             SplitKArgs]
 
 # Kernel entry points: name -> args struct (all take (const args*, void* stream)).
 KERNELS = {
@@ -223,6 +229,7 @@ KERNELS = {
     "c3h_quantize": QuantizeArgs, "c3h_qgemm": QGemmArgs, "c3h_dequantize": DequantizeArgs,
     "c3h_pack_conv_weight": PackArgs, "c3h_conv_stem_pool": ConvPoolArgs,
     "c3h_quantize_fp8_rows": Fp8QuantArgs, "c3h_gemm_fp8": Fp8GemmArgs,
+    "c3h_gemm_splitk_reduce": SplitKArgs,
 }
 
 OP_KIND = {
@@ -233,7 +240,7 @@ OP_KIND = {
     ConvArgs: OP_CONV, AttnScoresArgs: OP_ATTN_SCORES, FlashArgs: OP_FLASH,
     QuantizeArgs: OP_QUANTIZE, QGemmArgs: OP_QGEMM, DequantizeArgs: OP_DEQUANTIZE,
     BnFoldArgs: OP_BNFOLD, PackArgs: OP_PACK, ConvPoolArgs: OP_CONV_POOL,
-    Fp8QuantArgs: OP_QUANT_FP8, Fp8GemmArgs: OP_GEMM_FP8,
+    Fp8QuantArgs: OP_QUANT_FP8, Fp8GemmArgs: OP_GEMM_FP8, SplitKArgs: OP_SPLITK,
 }
 
 KERNEL_OF_ARGS = {v: k for k, v in KERNELS.items()}

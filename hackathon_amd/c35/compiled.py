@@ -46,7 +46,7 @@ from .. import _lib
 from ..c3common.ir.graph import Graph, Node
 from ..c34.execution_plan import ExecutionPlan
 from ..c34.memory_pool import DeviceMemoryPool
-from ..device import BF16, Buffer, DeviceArray, PinnedArray, Stream, dtype_code, init, synchronize
+from ..device import BF16, Buffer, DeviceArray, PinnedArray, Stream, device_props, dtype_code, init, synchronize
 from . import engine as E
 
 _POLICY_ACT = {"fp32": np.dtype(np.float32), "bf16": BF16, "fp16": np.dtype(np.float16), "w8a8": BF16,
@@ -162,6 +162,7 @@ class CompiledPlan:
         self.launch_meta: List[Dict[str, Any]] = []  # per launch: kind, algorithmic flops and bytes
         self.use_graph = use_graph
         self.fuse_stem = fuse_stem
+        self._cus = int(device_props().compute_units)
         self._graph_exec = None
         self._stream = Stream()
         self._consumers = self._consumer_map()
@@ -907,6 +908,10 @@ class CompiledPlan:
         out = self._new(out_shape, self._out_dtype(st.final))
         self._finish_residual(st, out)
         mm = code
+        splits = self._splitk(m, n, k) if code == _lib.F32 else 1
+        if splits > 1:
+            self._gemm_splitk(node, a2, w, out, st, m, n, k, splits, alpha, beta, bmode)
+            return
 
         def build(r, a2=a2, w=w, out=out, st=st, m=m, n=n, k=k):
             g = _lib.GemmArgs()
@@ -916,6 +921,48 @@ class CompiledPlan:
             self._fill_epi(g.epi, st, r, alpha, beta, bmode)
             return g
         self._emit(f"gemm:{node.op_type}", build, [a2, w] + self._epi_reads(st), [out], flops=2.0 * m * n * k)
+        self.vals[st.final] = out
+
+    def _splitk(self, m: int, n: int, k: int, vec: int = 4) -> int:
+        """K splits for an fp32 GEMM whose 64x64 output tiles cannot fill two
+        blocks per CU: the largest split with K/split a multiple of `vec`, at
+        least 32 deep, and at most two blocks per CU in total (1 = no split)."""
+        tiles = -(-m // 64) * -(-n // 64)
+        target = 2 * self._cus
+        if 2 * tiles > target or k < 128:
+            return 1
+        best = 1
+        for s in range(2, 65):
+            if tiles * s > target:
+                break
+            if k % s == 0 and (k // s) % vec == 0 and k // s >= 32:
+                best = s
+        return best
+
+    def _gemm_splitk(self, node, a2: Val, w: Val, out: Val, st: "_Epi", m: int, n: int, k: int, splits: int,
+                     alpha: float, beta: float, bmode) -> None:
+        """Split-K: `splits` batched partial GEMMs over K/splits each into an fp32
+        workspace, then c3h_gemm_splitk_reduce (fixed summation order + epilogue)."""
+        ks = k // splits
+        part = self._new((splits, m, n), np.float32)
+
+        def gbuild(r, a2=a2, w=w, part=part):
+            g = _lib.GemmArgs()
+            g.a, g.b, g.out = self._ptr(a2, r), self._ptr(w, r), self._ptr(part, r)
+            g.m, g.n, g.k, g.lda, g.ldb, g.ldo, g.batch = m, n, ks, k, k, n, splits
+            g.stride_a, g.stride_b, g.stride_out = ks, ks, m * n
+            g.trans_a, g.trans_b, g.in_dtype, g.out_dtype = 0, 1, _lib.F32, _lib.F32
+            g.epi.alpha, g.epi.beta = 1.0, 1.0
+            return g
+        self._emit(f"gemm:{node.op_type}", gbuild, [a2, w], [part], flops=2.0 * m * n * k)
+
+        def rbuild(r, part=part, out=out, st=st):
+            g = _lib.SplitKArgs()
+            g.partial, g.out = self._ptr(part, r), self._ptr(out, r)
+            g.m, g.n, g.ldo, g.splits, g.out_dtype = m, n, n, splits, dtype_code(out.dtype)
+            self._fill_epi(g.epi, st, r, alpha, beta, bmode)
+            return g
+        self._emit("splitk_reduce", rbuild, [part] + self._epi_reads(st), [out])
         self.vals[st.final] = out
 
     def _op_FusedGemmEpilogue(self, node):

@@ -1517,6 +1517,24 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
 }
 
 // =====================================================================
+// Split-K finish (c3h_gemm_splitk_reduce): one thread per output, the
+// partial products summed in split order, then the common epilogue.
+// =====================================================================
+template <typename TO>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(c3h_splitk_args a) {
+  const KArg<c3h_splitk_args>& p = kernel_arg<c3h_splitk_args>();
+  const int64_t mn = p.m * p.n;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= mn) return;
+  const int64_t row = i / p.n, col = i - row * p.n;
+  float v = p.partial[i];
+  for (int s = 1; s < p.splits; ++s) v += p.partial[s * mn + i];
+  const int64_t o = row * p.ldo + col;
+  const float res = p.epi.residual ? Elem<TO>::to_f32(static_cast<const TO*>(p.epi.residual)[o]) : 0.0f;
+  static_cast<TO*>(a.out)[o] = Elem<TO>::from_f32(apply_epilogue(p.epi, v, row, col, p.n, res, 0));
+}
+
+// =====================================================================
 // SIMT fp32 GEMM for operands the MFMA path cannot vector-load (odd K,
 // misaligned rows): one thread per output, same epilogue.
 // =====================================================================
@@ -1553,7 +1571,8 @@ int launch_f32(Problem p, int64_t batch, hipStream_t s) {
   if (p.n <= 64 && p.m >= 4096) {
     grid_of<256, 64>(p, batch, grid);
     hipLaunchKernelGGL((gemm_f32_kernel<256, 64, 4, 1, AM, BK_>), grid, dim3(kThreads), 0, s, p);
-  } else if (p.m <= 64 || p.n <= 64) {
+  } else if (p.m <= 64 || p.n <= 64 || ceil_div(p.m, 128) * ceil_div(p.n, 128) * batch < 256) {
+    // narrow operands, or too few 128x128 tiles to fill the chip
     grid_of<64, 64>(p, batch, grid);
     hipLaunchKernelGGL((gemm_f32_kernel<64, 64, 2, 2, AM, BK_>), grid, dim3(kThreads), 0, s, p);
   } else {
@@ -1792,6 +1811,24 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
     return launch_h_any<kConvStem>(p, 1, s, a->in_dtype);
   }
   return fail(C3H_EUNSUPPORTED, "conv2d: input dtype %d unsupported", a->in_dtype);
+}
+
+int c3h_gemm_splitk_reduce(const c3h_splitk_args* a, void* stream) {
+  C3H_REQUIRE(a != nullptr && a->partial != nullptr && a->out != nullptr, "splitk_reduce: null args");
+  C3H_REQUIRE(a->m >= 0 && a->n >= 0 && a->splits >= 1 && a->ldo >= a->n, "splitk_reduce: bad sizes");
+  C3H_REQUIRE(a->out_dtype == C3H_F32 || a->out_dtype == C3H_BF16 || a->out_dtype == C3H_F16,
+              "splitk_reduce: output dtype must be fp32, bf16 or fp16");
+  int rc = check_epilogue(a->epi);
+  if (rc) return rc;
+  const int64_t mn = a->m * a->n;
+  if (mn == 0) return C3H_OK;
+  C3H_REQUIRE(ceil_div(mn, 256) < (int64_t{1} << 31), "splitk_reduce: too many outputs");
+  const dim3 g(static_cast<unsigned>(ceil_div(mn, 256))), b(256);
+  hipStream_t s = as_stream(stream);
+  if (a->out_dtype == C3H_F32) hipLaunchKernelGGL(splitk_reduce_kernel<float>, g, b, 0, s, *a);
+  else if (a->out_dtype == C3H_BF16) hipLaunchKernelGGL(splitk_reduce_kernel<bf16_t>, g, b, 0, s, *a);
+  else hipLaunchKernelGGL(splitk_reduce_kernel<f16_t>, g, b, 0, s, *a);
+  return launch_status("splitk_reduce");
 }
 
 int c3h_gemm_fp8(const c3h_fp8_gemm_args* a, void* stream) {

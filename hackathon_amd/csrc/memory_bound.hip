@@ -202,6 +202,61 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(c3h_reduce_args a) 
   }
 }
 
+// inner % 8 == 0, 16-byte aligned (channels-last GlobalAveragePool): a block
+// covers one outer index and 64 vectors of 8 inner elements; its four waves
+// split the reduce axis (positions w, w + 4, ...), each thread keeping 8
+// running values with four positions in flight, and the four partials are
+// combined through LDS in wave order.
+template <typename T>
+__global__ void __launch_bounds__(kBlock) reduce_cols_vec_kernel(c3h_reduce_args a) {
+  __shared__ float part[kBlock / 64][64][9];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t o = blockIdx.x;
+  const int64_t c8 = static_cast<int64_t>(blockIdx.y) * 64 + lane;
+  const bool live = c8 * 8 < a.inner;
+  const T* in = static_cast<const T*>(a.in) + o * a.reduce * a.inner + c8 * 8;
+  const float init = a.kind == 0 ? -INFINITY : 0.0f;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = init;
+  if (live) {
+    int64_t i = wave;
+    for (; i + 12 < a.reduce; i += 16) {
+      float v[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) load_vec16(in + (i + 4 * u) * a.inner, v[u]);
+      if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) load_vec16(in + (i + 4 * u) * a.inner + 4, v[u] + 4);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = a.kind == 0 ? fmaxf(acc[e], v[u][e]) : acc[e] + v[u][e];
+    }
+    for (; i < a.reduce; i += 4) {
+      float v[8];
+      load_vec16(in + i * a.inner, v);
+      if constexpr (sizeof(T) == 4) load_vec16(in + i * a.inner + 4, v + 4);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = a.kind == 0 ? fmaxf(acc[e], v[e]) : acc[e] + v[e];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) part[wave][lane][e] = acc[e];
+  __syncthreads();
+  if (wave == 0 && live) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float r = part[0][lane][e];
+#pragma unroll
+      for (int w = 1; w < kBlock / 64; ++w) r = a.kind == 0 ? fmaxf(r, part[w][lane][e]) : r + part[w][lane][e];
+      if (a.kind == 2) r = r / static_cast<float>(a.reduce);
+      store_from_f32(a.out, a.out_dtype, o * a.inner + c8 * 8 + e, r);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ softmax
 __global__ void __launch_bounds__(kBlock) softmax_rows_kernel(c3h_softmax_args a) {
   // one block per row (inner == 1)
@@ -952,6 +1007,14 @@ int c3h_reduce(const c3h_reduce_args* a, void* stream) {
   if (a->inner == 1) {
     int blocks = static_cast<int>(ceil_div(a->outer, kBlock / 64));
     hipLaunchKernelGGL(reduce_rows_kernel, dim3(blocks), dim3(kBlock), 0, as_stream(stream), *a);
+  } else if (a->inner % 8 == 0 && (reinterpret_cast<uintptr_t>(a->in) & 15) == 0 && a->outer < (int64_t{1} << 31) &&
+             (a->in_dtype == C3H_F32 || a->in_dtype == C3H_BF16 || a->in_dtype == C3H_F16)) {
+    const dim3 g(static_cast<unsigned>(a->outer), static_cast<unsigned>(ceil_div(a->inner / 8, 64)));
+    hipStream_t st = as_stream(stream);
+    C3H_REQUIRE(g.y <= 65535, "reduce: inner too large");
+    if (a->in_dtype == C3H_F32) hipLaunchKernelGGL(reduce_cols_vec_kernel<float>, g, dim3(kBlock), 0, st, *a);
+    else if (a->in_dtype == C3H_BF16) hipLaunchKernelGGL(reduce_cols_vec_kernel<bf16_t>, g, dim3(kBlock), 0, st, *a);
+    else hipLaunchKernelGGL(reduce_cols_vec_kernel<f16_t>, g, dim3(kBlock), 0, st, *a);
   } else {
     hipLaunchKernelGGL(reduce_cols_kernel, dim3(grid_for(a->outer * a->inner)), dim3(kBlock), 0, as_stream(stream), *a);
   }

@@ -576,6 +576,23 @@ typedef struct {
 } c3h_dequantize_args;
 int c3h_dequantize(const c3h_dequantize_args* a, void* stream);
 
+/* Split-K finish of a GEMM whose K range was cut into `splits` batched
+ * partial products (c3h_gemm with batch = splits, K/splits per batch, fp32
+ * output [splits][m][n]): out = epilogue(sum_s partial[s]) summed in s
+ * order, then the common epilogue into fp32 / bf16 / fp16 (residual in the
+ * output dtype, row stride ldo).  Lets the compiled engine spread a GEMM
+ * with few output tiles (the MLP's 256-row layers, fused_gemm_epilogue_f32,
+ * R:606-633) over every CU; deterministic for a given split. */
+typedef struct {
+  const float* partial; /* [splits][m][n] */
+  void* out;
+  int64_t m, n, ldo;
+  int32_t splits;
+  int32_t out_dtype;
+  c3h_epilogue epi;
+} c3h_splitk_args;
+int c3h_gemm_splitk_reduce(const c3h_splitk_args* a, void* stream);
+
 /* ------------------------------------------------------------------ */
 /* fp8 (OCP E4M3) GEMM: the executable form of the reference's         */
 /* structural `matmul_f8` (c32/hardware.py:80-81), chosen by the mixed  */
@@ -654,7 +671,8 @@ enum c3h_op_kind {
   C3H_OP_PACK = 31,
   C3H_OP_CONV_POOL = 32,
   C3H_OP_QUANT_FP8 = 33,
-  C3H_OP_GEMM_FP8 = 34
+  C3H_OP_GEMM_FP8 = 34,
+  C3H_OP_SPLITK = 35
 };
 
 typedef struct {
@@ -687,7 +705,8 @@ int c3h_graph_destroy(void* graph_exec);
  * c3h_im2col_args, c3h_layout_args, c3h_pool_args, c3h_epilogue,
  * c3h_gemm_args, c3h_conv_args, c3h_attn_scores_args, c3h_flash_args,
  * c3h_quantize_args, c3h_qgemm_args, c3h_dequantize_args, c3h_op,
- * c3h_pack_args, c3h_conv_pool_args, c3h_fp8_quant_args, c3h_fp8_gemm_args.
+ * c3h_pack_args, c3h_conv_pool_args, c3h_fp8_quant_args, c3h_fp8_gemm_args,
+ * c3h_splitk_args.
  * Returns the number of sizes available (host-only; needs no GPU). */
 int32_t c3h_abi_sizes(int64_t* out, int32_t capacity);
 

@@ -61,7 +61,8 @@ def test_compiled_fp32_matches_oracle(gpu, name):
     ref = G.run_plan(plan, m.graph, weights, m.inputs)
     for k in ref:
         np.testing.assert_allclose(got[k].reshape(ref[k].shape), ref[k], rtol=1e-3, atol=1e-3)
-    assert prog.num_launches <= len(plan.kernel_steps)
+    # launch groups never add launches, except the finishing reduce of a split-K GEMM
+    assert prog.num_launches - prog.node_kinds.count("splitk_reduce") <= len(plan.kernel_steps)
 
 
 def _agree(got: np.ndarray, ref: np.ndarray) -> float:

@@ -469,3 +469,112 @@ def test_bf16_narrowing_is_round_to_nearest_even_bit_exact(gpu):
     out = DeviceArray.empty(x.shape, BF16)
     E.cast_into(x, out)
     np.testing.assert_array_equal(out.get().view(np.uint16), f32_to_bf16(bits.view(np.float32)).view(np.uint16))
+
+
+@pytest.mark.parametrize("out_kind", ["fp32", "bf16", "fp16"])
+def test_splitk_reduce_fixed_order_bit_exact(gpu, out_kind):
+    """c3h_gemm_splitk_reduce: partials summed in split order, then alpha,
+    beta * bias, residual and ReLU in the common epilogue's float32 order."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    rng = np.random.default_rng(7)
+    splits, m, n = 7, 130, 70
+    part = rng.standard_normal((splits, m, n)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    r32 = rng.standard_normal((m, n)).astype(np.float32)
+    code, sdt = {"fp32": (_lib.F32, np.float32), "bf16": (_lib.BF16, BF16), "fp16": (_lib.F16, np.float16)}[out_kind]
+    if out_kind == "fp32":
+        res_dev, res_val = _dev(r32), r32
+    else:
+        bits, res_val = _bits(r32, out_kind)
+        res_dev = _dev(bits)
+    acc = part[0].copy()
+    for s_ in range(1, splits):
+        acc = (acc + part[s_]).astype(np.float32)
+    want = np.maximum(((np.float32(0.5) * acc) + np.float32(2.0) * bias[None, :]) + res_val, 0).astype(np.float32)
+    out = DeviceArray.empty((m, n), sdt)
+    pd, bd = _dev(part), _dev(bias)
+    g = _lib.SplitKArgs()
+    g.partial, g.out, g.m, g.n, g.ldo, g.splits, g.out_dtype = pd.ptr, out.ptr, m, n, n, splits, code
+    g.epi = E.epilogue(bias=bd, bias_mode=2, alpha=0.5, beta=2.0, act=1, residual=res_dev)
+    _lib.launch(g, None)
+    got = out.get()
+    if out_kind == "fp32":
+        np.testing.assert_array_equal(got, want)
+    else:
+        np.testing.assert_array_equal(_from16(got, out_kind), G.round_to(want, out_kind))
+
+
+@pytest.mark.parametrize("kind_name,dt", [("fp32", "fp32"), ("bf16", "bf16"), ("fp16", "fp16")])
+@pytest.mark.parametrize("outer,red,inner", [(3, 49, 512), (2, 13, 8), (5, 3, 1024), (1, 64, 136)])
+def test_reduce_channels_last_vec(gpu, kind_name, dt, outer, red, inner):
+    """Channels-last reductions (inner % 8 == 0: GlobalAveragePool over NHWC):
+    max exact, sum / mean within float32 summation error of float64."""
+    from hackathon_amd import _lib
+    from hackathon_amd.device import DeviceArray
+
+    rng = np.random.default_rng(outer * 100 + red + inner)
+    x32 = rng.standard_normal((outer, red, inner)).astype(np.float32)
+    if dt == "fp32":
+        xd, xv, code = _dev(x32), x32, _lib.F32
+    else:
+        bits, xv = _bits(x32, dt)
+        xd, code = _dev(bits), (_lib.BF16 if dt == "bf16" else _lib.F16)
+    for kind in (0, 1, 2):
+        out = DeviceArray.empty((outer, inner), np.float32)
+        a = _lib.ReduceArgs()
+        a.in_, a.out, a.outer, a.reduce, a.inner = xd.ptr, out.ptr, outer, red, inner
+        a.kind, a.in_dtype, a.out_dtype = kind, code, _lib.F32
+        _lib.launch(a, None)
+        got = out.get()
+        x64 = xv.astype(np.float64)
+        if kind == 0:
+            np.testing.assert_array_equal(got, xv.max(axis=1))
+        else:
+            want = x64.sum(axis=1) / (red if kind == 2 else 1)
+            bound = np.abs(x64).sum(axis=1) / (red if kind == 2 else 1) * red * 2.0 ** -23
+            assert np.all(np.abs(got - want) <= bound + 1e-7)
+
+
+@pytest.mark.parametrize("rows,cols,res,bias,dt", [(37, 512, False, True, "fp16"), (16384 // 64, 512, True, True, "fp16"),
+                                                  (5, 1024, True, False, "bf16"), (7, 2048, False, True, "fp32"),
+                                                  (3, 4096, True, True, "fp16"), (1, 8, False, False, "fp32")])
+def test_layernorm_vec_against_float64(gpu, rows, cols, res, bias, dt):
+    """Vectorized LayerNorm (one wave per row, 1-8 vectors per lane): mean,
+    centred variance and the affine map against float64 of the same inputs."""
+    from hackathon_amd import _lib
+    from hackathon_amd.device import BF16, DeviceArray
+
+    rng = np.random.default_rng(rows + cols)
+    x32 = (rng.standard_normal((rows, cols)) * 3 + 1).astype(np.float32)
+    r32 = rng.standard_normal((rows, cols)).astype(np.float32)
+    g = rng.standard_normal(cols).astype(np.float32)
+    b = rng.standard_normal(cols).astype(np.float32)
+    if dt == "fp32":
+        xd, xv, rd, rv, code, sdt = _dev(x32), x32, _dev(r32), r32, _lib.F32, np.float32
+    else:
+        xb, xv = _bits(x32, dt)
+        rb, rv = _bits(r32, dt)
+        xd, rd = _dev(xb), _dev(rb)
+        code, sdt = (_lib.BF16, BF16) if dt == "bf16" else (_lib.F16, np.float16)
+    out = DeviceArray.empty((rows, cols), sdt)
+    mean_d, inv_d = DeviceArray.empty((rows,), np.float32), DeviceArray.empty((rows,), np.float32)
+    gd, bd = _dev(g), _dev(b)
+    a = _lib.LayerNormArgs()
+    a.x, a.residual, a.scale, a.bias, a.out = xd.ptr, rd.ptr if res else None, gd.ptr, bd.ptr if bias else None, out.ptr
+    a.mean_out, a.invstd_out, a.rows, a.cols, a.epsilon = mean_d.ptr, inv_d.ptr, rows, cols, 1e-5
+    a.x_dtype, a.out_dtype = code, code
+    print(f"layernorm rows={rows} cols={cols} res={res} bias={bias} {dt}", flush=True)
+    _lib.launch(a, None)
+    s = (xv.astype(np.float64) + (rv if res else 0))
+    mu = s.mean(axis=1, keepdims=True)
+    inv = 1.0 / np.sqrt(((s - mu) ** 2).mean(axis=1, keepdims=True) + 1e-5)
+    want = (s - mu) * inv * g + (b if bias else 0)
+    got = out.get()
+    got = got.astype(np.float32) if dt != "bf16" else _from16(got, "bf16")
+    tol = {"fp32": 1e-4, "fp16": 2e-3, "bf16": 1.6e-2}[dt]
+    np.testing.assert_allclose(got, want, rtol=tol, atol=tol * 4)
+    np.testing.assert_allclose(mean_d.get(), mu[:, 0], rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(inv_d.get(), inv[:, 0], rtol=1e-4)
