@@ -1323,8 +1323,12 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, int S>
-__global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
+// NW waves per block.  NW = 8 is the large-tile form (256 x 256, wave tiles
+// 64 x 128, one block per CU): half the operand bytes per flop of 128 x 128,
+// direct epilogues only (its LDS cannot also hold a staged epilogue).
+template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, int S, int NW = 4>
+__global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
+  constexpr bool DIRECT = NW > 4;
   constexpr int ES = Mma::ES;
   constexpr int VE = 16 / ES;
   constexpr int BK = 128 / ES;
@@ -1332,12 +1336,12 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
   constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int GROUPS = (BM + BN) / 8;   // 8-row wave loads per stage
-  constexpr int LPW = GROUPS / 4;         // wave loads per wave per stage
+  constexpr int LPW = GROUPS / NW;        // wave loads per wave per stage
   constexpr int STAGE = (BM + BN) * RB;
-  static_assert(WM * WN == 4 && GROUPS % 4 == 0 && BM % 8 == 0, "shape");
+  static_assert(WM * WN == NW && GROUPS % NW == 0 && BM % 8 == 0, "shape");
   static_assert(AM == kDenseK || AM == kConvTap, "dma kernel: dense or tap-uniform conv only");
   static_assert(S >= 2 && S <= 4 && LPW * (S - 2) < 64, "stages");
-  constexpr int kStageBytes = 4 * WTM * (WTN + 4) * 4;
+  constexpr int kStageBytes = DIRECT ? 0 : NW * WTM * (WTN + 4) * 4;
   constexpr int kSmem = S * STAGE > kStageBytes ? S * STAGE : kStageBytes;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
   typedef typename Mma::vec vec;
@@ -1361,7 +1365,7 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
   int slot_hi[LPW], slot_wi[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
-    const int g = wave + 4 * j;
+    const int g = wave + NW * j;
     const int r = g * 8 + (lane >> 3);
     slot_hi[j] = 0;
     slot_wi[j] = 0;
@@ -1388,7 +1392,7 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
     const int dh = t_kh * p.dh, dw = t_kw * p.dw;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      const int g = wave + 4 * j;
+      const int g = wave + NW * j;
       uint32_t voff = kOobOffset;
       if (g < BM / 8) {
         if (AM == kConvTap) {
@@ -1483,11 +1487,12 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
         epilogue_direct_q<TO, TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act == 1);
         return;
       }
-    } else if (epilogue_is_simple(kernel_arg<Problem>(), vec4)) {
+    } else if (DIRECT || epilogue_is_simple(kernel_arg<Problem>(), vec4)) {
       epilogue_direct<TO, TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act == 1);
       return;
     }
   }
+  if constexpr (!DIRECT) {
   const bool vec_ok = !p.out_nchw && (p.ldo % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0) &&
                       ((reinterpret_cast<uintptr_t>(p.epi.residual) & 15) == 0);
   __syncthreads();
@@ -1513,6 +1518,7 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_dma_kernel(Problem p) {
       if (p.out_nchw) store_strip<TO, WTN>(p, strip, lane, mrow0, ncol0, outp, resp, 0);
       else store_strip_vec<TO, WTN>(strip, lane, mrow0, ncol0, outp, resp, 0, vec_ok);
     }
+  }
   }
 }
 
@@ -1593,10 +1599,44 @@ inline bool dma_eligible(const Problem& p, int64_t batch, int am) {
          p.a_bytes < (int64_t{1} << 31) && p.b_bytes < (int64_t{1} << 31);
 }
 
+// Whether the 256 x 256 eight-wave DMA kernel beats 128 x 128 at two blocks
+// per CU: rounds of resident tiles, a 256-tile round costing 1.66 rounds of
+// 128-tiles (measured: 8192^3 GEMM, 1195 vs 994 us), and an epilogue that
+// epilogue_direct handles (host-side restatement of epilogue_is_simple).
+bool big_tile_wins(const Problem& p, int cus, size_t out_size) {
+  if (getenv("C3H_DISABLE_BIGTILE") || p.n <= 128) return false;
+  const c3h_epilogue& e = p.epi;
+  const uintptr_t al = 4 * out_size - 1;
+  const bool simple = !p.out_nchw && e.alpha == 1.0f && e.beta == 1.0f && (e.bias_mode == 0 || e.bias_mode == 2) &&
+                      e.act <= 1 && e.n_inst == 0 && (e.bias_mode == 0 || (reinterpret_cast<uintptr_t>(e.bias) & 15) == 0) &&
+                      p.ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(p.out) & al) == 0 &&
+                      (reinterpret_cast<uintptr_t>(e.residual) & al) == 0;
+  if (!simple) return false;
+  const int64_t t128 = ceil_div(p.m, 128) * ceil_div(p.n, 128), t256 = ceil_div(p.m, 256) * ceil_div(p.n, 256);
+  const double r128 = static_cast<double>(ceil_div(t128, 2 * cus));
+  const double r256 = static_cast<double>(ceil_div(t256, cus)) * 1.66;
+  return r256 < r128;
+}
+
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
 template <typename Mma, typename TO, int AM>
 int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
   dim3 grid;
   if constexpr (AM == kDenseK || AM == kConvTap) {
+    if constexpr (!Mma::kInt && !Mma::kScaled) {
+      if (dma_eligible(p, batch, AM) && big_tile_wins(p, device_cus(), sizeof(TO))) {
+        grid_of<256, 256>(p, 1, grid);
+        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 256, 4, 2, AM, 2, 8>), grid, dim3(512), 0, s, p);
+        return launch_status(what);
+      }
+    }
     if (dma_eligible(p, batch, AM)) {
       // Two stages (one tile in flight): 64-80 KB of LDS, so two blocks share
       // a CU and one's fill and epilogue overlap the other's MFMAs -- this

@@ -578,3 +578,102 @@ def test_layernorm_vec_against_float64(gpu, rows, cols, res, bias, dt):
     np.testing.assert_allclose(got, want, rtol=tol, atol=tol * 4)
     np.testing.assert_allclose(mean_d.get(), mu[:, 0], rtol=1e-5, atol=1e-5)
     np.testing.assert_allclose(inv_d.get(), inv[:, 0], rtol=1e-4)
+
+
+def _bigtile_pair(launch):
+    """Run `launch` with the 256x256 eight-wave kernel allowed, then with it disabled."""
+    import os
+
+    os.environ.pop("C3H_DISABLE_BIGTILE", None)
+    a = launch()
+    os.environ["C3H_DISABLE_BIGTILE"] = "1"
+    try:
+        b = launch()
+    finally:
+        os.environ.pop("C3H_DISABLE_BIGTILE", None)
+    return a, b
+
+
+@pytest.mark.parametrize("kind,out_kind", [("bf16", "bf16"), ("fp16", "fp32")])
+def test_gemm_big_tile_matches_128_tiles(gpu, kind, out_kind):
+    """4096x4096x192 (enough tiles that the 256x256 eight-wave kernel is
+    chosen) with bias + residual + ReLU: bit-identical to the 128x128 kernel
+    (same K order per output) and within the 16-bit GEMM tolerance of float64
+    on sampled rows."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    rng = np.random.default_rng(11)
+    m = n = 4096
+    k = 192
+    a32 = (rng.standard_normal((m, k)) * 0.5).astype(np.float32)
+    b32 = (rng.standard_normal((n, k)) * 0.5).astype(np.float32)
+    ab, av = _bits(a32, kind)
+    bb, bv = _bits(b32, kind)
+    bias = rng.standard_normal(n).astype(np.float32)
+    r32 = rng.standard_normal((m, n)).astype(np.float32)
+    code = _lib.BF16 if kind == "bf16" else _lib.F16
+    ocode, sdt = {"fp32": (_lib.F32, np.float32), "bf16": (_lib.BF16, BF16)}[out_kind]
+    if out_kind == "fp32":
+        rd, rv = _dev(r32), r32
+    else:
+        rb, rv = _bits(r32, out_kind)
+        rd = _dev(rb)
+    ad, bd, biasd = _dev(ab), _dev(bb), _dev(bias)
+    out = DeviceArray.empty((m, n), sdt)
+
+    def launch():
+        g = _lib.GemmArgs()
+        g.a, g.b, g.out = ad.ptr, bd.ptr, out.ptr
+        g.m, g.n, g.k, g.lda, g.ldb, g.ldo, g.batch = m, n, k, k, k, n, 1
+        g.trans_a, g.trans_b, g.in_dtype, g.out_dtype = 0, 1, code, ocode
+        g.epi = E.epilogue(bias=biasd, bias_mode=2, act=1, residual=rd)
+        print(f"gemm {m}x{n}x{k} {kind}->{out_kind}", flush=True)
+        _lib.launch(g, None)
+        return out.get().copy()
+    big, small = _bigtile_pair(launch)
+    np.testing.assert_array_equal(big.view(np.uint8), small.view(np.uint8))
+    rows = np.arange(0, m, 97)
+    want = np.maximum(av[rows].astype(np.float64) @ bv.astype(np.float64).T + bias + rv[rows], 0)
+    got = big[rows] if out_kind == "fp32" else _from16(big[rows], out_kind)
+    tol = 1e-4 if out_kind == "fp32" else 1e-2
+    np.testing.assert_allclose(got, want, rtol=tol, atol=tol * 4)
+
+
+def test_conv_big_tile_matches_128_tiles(gpu):
+    """The ResNet layer-3 conv (256 x 14 x 14 x 256, 3x3) takes the 256x256
+    kernel; bit-identical to the 128x128 one, and a float64 spot check."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    rng = np.random.default_rng(12)
+    n, c, h, w, o = 256, 256, 14, 14, 256
+    x32 = rng.standard_normal((n, h, w, c)).astype(np.float32)
+    w32 = (rng.standard_normal((o, 3, 3, c)) * 0.05).astype(np.float32)
+    xb, xv = _bits(x32, "bf16")
+    wb, wv = _bits(w32.reshape(o, -1), "bf16")
+    bias = rng.standard_normal(o).astype(np.float32)
+    xd, wd, bd = _dev(xb), _dev(wb), _dev(bias)
+    out = DeviceArray.empty((n, h, w, o), BF16)
+
+    def launch():
+        a = _lib.ConvArgs()
+        a.x, a.w, a.out = xd.ptr, wd.ptr, out.ptr
+        a.n, a.c, a.h, a.w_, a.c_stride, a.c_pack, a.o = n, c, h, w, c, c, o
+        a.kh, a.kw, a.sh, a.sw, a.pad_top, a.pad_left, a.dh, a.dw, a.ho, a.wo = 3, 3, 1, 1, 1, 1, 1, 1, h, w
+        a.out_layout, a.in_dtype, a.out_dtype = 1, _lib.BF16, _lib.BF16
+        a.epi = E.epilogue(bias=bd, bias_mode=2, act=1)
+        print("conv 256x14x14x256 3x3 bf16", flush=True)
+        _lib.launch(a, None)
+        return out.get().copy()
+    big, small = _bigtile_pair(launch)
+    np.testing.assert_array_equal(big.view(np.uint16), small.view(np.uint16))
+    got = _from16(big, "bf16")
+    xp = np.pad(xv.astype(np.float64), ((0, 0), (1, 1), (1, 1), (0, 0)))
+    wv4 = wv.astype(np.float64).reshape(o, 3, 3, c)
+    for (b_, y, x_) in [(0, 0, 0), (7, 5, 13), (255, 13, 6), (100, 7, 7)]:
+        patch = xp[b_, y:y + 3, x_:x_ + 3, :]
+        want = np.maximum(np.einsum("hwc,ohwc->o", patch, wv4) + bias, 0)
+        np.testing.assert_allclose(got[b_, y, x_], want, rtol=1e-2, atol=4e-2)
