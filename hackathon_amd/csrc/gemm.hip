@@ -1603,15 +1603,17 @@ inline bool dma_eligible(const Problem& p, int64_t batch, int am) {
 // per CU: rounds of resident tiles, a 256-tile round costing 1.66 rounds of
 // 128-tiles (measured: 8192^3 GEMM, 1195 vs 994 us), and an epilogue that
 // epilogue_direct handles (host-side restatement of epilogue_is_simple).
-bool big_tile_wins(const Problem& p, int cus, size_t out_size) {
+// int8 GEMMs writing int32 / int8 (qmode 0 / 1) need only aligned row-major
+// stores (epilogue_q_direct_ok).
+bool big_tile_wins(const Problem& p, int cus, size_t out_size, bool int_mma) {
   if (getenv("C3H_DISABLE_BIGTILE") || p.n <= 128) return false;
   const c3h_epilogue& e = p.epi;
   const uintptr_t al = 4 * out_size - 1;
-  const bool simple = !p.out_nchw && e.alpha == 1.0f && e.beta == 1.0f && (e.bias_mode == 0 || e.bias_mode == 2) &&
+  const bool stores = !p.out_nchw && p.ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(p.out) & al) == 0;
+  const bool simple = stores && e.alpha == 1.0f && e.beta == 1.0f && (e.bias_mode == 0 || e.bias_mode == 2) &&
                       e.act <= 1 && e.n_inst == 0 && (e.bias_mode == 0 || (reinterpret_cast<uintptr_t>(e.bias) & 15) == 0) &&
-                      p.ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(p.out) & al) == 0 &&
                       (reinterpret_cast<uintptr_t>(e.residual) & al) == 0;
-  if (!simple) return false;
+  if (!(int_mma && p.qmode <= 1 ? stores : simple)) return false;
   const int64_t t128 = ceil_div(p.m, 128) * ceil_div(p.n, 128), t256 = ceil_div(p.m, 256) * ceil_div(p.n, 256);
   const double r128 = static_cast<double>(ceil_div(t128, 2 * cus));
   const double r256 = static_cast<double>(ceil_div(t256, cus)) * 1.66;
@@ -1630,12 +1632,10 @@ template <typename Mma, typename TO, int AM>
 int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
   dim3 grid;
   if constexpr (AM == kDenseK || AM == kConvTap) {
-    if constexpr (!Mma::kInt && !Mma::kScaled) {
-      if (dma_eligible(p, batch, AM) && big_tile_wins(p, device_cus(), sizeof(TO))) {
-        grid_of<256, 256>(p, 1, grid);
-        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 256, 4, 2, AM, 2, 8>), grid, dim3(512), 0, s, p);
-        return launch_status(what);
-      }
+    if (dma_eligible(p, batch, AM) && big_tile_wins(p, device_cus(), sizeof(TO), Mma::kInt)) {
+      grid_of<256, 256>(p, 1, grid);
+      hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 256, 4, 2, AM, 2, 8>), grid, dim3(512), 0, s, p);
+      return launch_status(what);
     }
     if (dma_eligible(p, batch, AM)) {
       // Two stages (one tile in flight): 64-80 KB of LDS, so two blocks share
@@ -1693,7 +1693,10 @@ int launch_h_any(Problem p, int64_t batch, hipStream_t s, int in_dtype) {
 template <typename TO>
 int launch_fp8(Problem p, hipStream_t s) {
   dim3 grid;
-  if (dma_eligible(p, 1, kDenseK)) {
+  if (dma_eligible(p, 1, kDenseK) && big_tile_wins(p, device_cus(), sizeof(TO), false)) {
+    grid_of<256, 256>(p, 1, grid);
+    hipLaunchKernelGGL((mfma_gemm_dma_kernel<MmaF8, TO, 256, 256, 4, 2, kDenseK, 2, 8>), grid, dim3(512), 0, s, p);
+  } else if (dma_eligible(p, 1, kDenseK)) {
     if (p.n <= 64) {
       grid_of<256, 64>(p, 1, grid);
       hipLaunchKernelGGL((mfma_gemm_dma_kernel<MmaF8, TO, 256, 64, 4, 1, kDenseK, 2>), grid, dim3(kThreads), 0, s, p);

@@ -677,3 +677,74 @@ def test_conv_big_tile_matches_128_tiles(gpu):
         patch = xp[b_, y:y + 3, x_:x_ + 3, :]
         want = np.maximum(np.einsum("hwc,ohwc->o", patch, wv4) + bias, 0)
         np.testing.assert_allclose(got[b_, y, x_], want, rtol=1e-2, atol=4e-2)
+
+
+@pytest.mark.parametrize("mode", [0, 2])
+def test_qgemm_big_tile_matches_128_tiles(gpu, mode):
+    """int8 GEMM 4096x4096x256 on the 256x256 kernel: int32 accumulators
+    (mode 0) equal the exact integer product; the dequantized bf16 output with
+    bias + residual (mode 2) is bit-identical to the 128x128 kernel."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    rng = np.random.default_rng(13 + mode)
+    m = n = 4096
+    k = 256
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    bt = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    sb = (rng.random(n) * 0.01 + 0.001).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    rb, _ = _bits(rng.standard_normal((m, n)).astype(np.float32), "bf16")
+    ad, bd, sbd, biasd, rd = _dev(a), _dev(bt), _dev(sb), _dev(bias), _dev(rb)
+    out = DeviceArray.empty((m, n), np.int32 if mode == 0 else BF16)
+
+    def launch():
+        g = _lib.QGemmArgs()
+        g.a, g.b, g.out, g.m, g.n, g.k, g.lda, g.ldb, g.ldo = ad.ptr, bd.ptr, out.ptr, m, n, k, k, k, n
+        g.a_scale, g.y_scale, g.b_scale, g.mode = 0.02, 1.0, sbd.ptr, mode
+        g.out_dtype = _lib.I32 if mode == 0 else _lib.BF16
+        if mode == 2:
+            g.epi = E.epilogue(bias=biasd, bias_mode=2, residual=rd)
+        else:
+            g.epi = E.epilogue()
+        print(f"qgemm {m}x{n}x{k} mode {mode}", flush=True)
+        _lib.launch(g, None)
+        return out.get().copy()
+    big, small = _bigtile_pair(launch)
+    np.testing.assert_array_equal(big.view(np.uint8), small.view(np.uint8))
+    if mode == 0:
+        rows = np.arange(0, m, 61)
+        np.testing.assert_array_equal(big[rows], a[rows].astype(np.int64) @ bt.T.astype(np.int64))
+
+
+def test_gemm_fp8_big_tile_matches_128_tiles(gpu):
+    """E4M3 GEMM 4096x4096x512 on the 256x256 kernel: bit-identical to the
+    128x128 kernel (same K order), integer operands exact."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import DeviceArray
+
+    from oracle import fp8_ref as F8
+
+    rng = np.random.default_rng(14)
+    m = n = 4096
+    k = 512
+    vals = np.arange(-8, 9, dtype=np.float32)
+    qa, qb = F8.encode(rng.choice(vals, (m, k))), F8.encode(rng.choice(vals, (n, k)))
+    sa, sb = np.ones(m, np.float32), np.ones(n, np.float32)
+    keep = [_dev(qa), _dev(qb), _dev(sa), _dev(sb)]
+    out = DeviceArray.empty((m, n), np.float32)
+
+    def launch():
+        g = _lib.Fp8GemmArgs()
+        g.a, g.b, g.a_scale, g.b_scale, g.out = keep[0].ptr, keep[1].ptr, keep[2].ptr, keep[3].ptr, out.ptr
+        g.m, g.n, g.k, g.lda, g.ldb, g.ldo, g.out_dtype = m, n, k, k, k, n, _lib.F32
+        g.epi = E.epilogue()
+        print(f"gemm_fp8 {m}x{n}x{k}", flush=True)
+        _lib.launch(g, None)
+        return out.get().copy()
+    big, small = _bigtile_pair(launch)
+    np.testing.assert_array_equal(big, small)
+    rows = np.arange(0, m, 61)
+    np.testing.assert_array_equal(big[rows], (F8.decode(qa[rows]).astype(np.float64) @ F8.decode(qb).astype(np.float64).T).astype(np.float32))
