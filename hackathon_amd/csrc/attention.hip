@@ -82,7 +82,6 @@ __global__ void __launch_bounds__(kScoreThreads) attention_scores_kernel(c3h_att
 constexpr int kD = 64;        // head dim
 constexpr int kBQ = 64;       // queries per workgroup (16 per wave)
 constexpr int kBK = 64;       // keys per tile
-constexpr int kPad = 8;       // 16-byte skew of LDS rows
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <typename T> struct FlashMma;
@@ -99,11 +98,28 @@ template <> struct FlashMma<f16_t> {
   }
 };
 
+// LDS tiles (128-byte rows, 16-byte chunks XOR-swizzled so every MFMA
+// operand is one conflict-free ds_read_b128, as in the GEMM kernels):
+//   Ks[key][dim]:  chunk c of row `key` at slot c ^ (key & 7);
+//   Vt[dim][pos]:  V transposed, keys permuted by vt_pos so that the eight
+//                  keys a lane holds in a P^T fragment (32 ks + 16 (i / 4) +
+//                  4 g + i % 4, the S^T accumulator layout) are one chunk
+//                  (4 ks + g); chunk slot c ^ vt_swz(dim).
+__device__ __forceinline__ int vt_pos(int key) {
+  const int r = key & 31;
+  return (key & 32) + 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3);
+}
+__device__ __forceinline__ int vt_swz(int dim) { return (dim ^ (dim >> 1)) & 7; }
+
+template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <> __device__ __forceinline__ uint32_t pack2<bf16_t>(float lo, float hi) { return f32x2_to_bf16x2_bits(lo, hi); }
+template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float lo, float hi) { return f32x2_to_f16x2_bits(lo, hi); }
+
 template <typename T, int MASK>
 __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
   typedef typename FlashMma<T>::vec vec8;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBK][kD + kPad];   // [key][dim]
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[kD][kBK + kPad];   // [dim][key]
+  __shared__ __attribute__((aligned(16))) uint8_t Ks[kBK * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t Vt[kD * 128];
 
   const int qtiles = (a.seq_q + kBQ - 1) / kBQ;
   const int qt = blockIdx.x % qtiles;
@@ -122,7 +138,6 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
   const int q = qt * kBQ + wave * 16 + l16;
   const bool q_valid = q < a.seq_q;
   const int wave_q0 = qt * kBQ + wave * 16;  // this wave's first query
-  const float scale_log2 = a.scale * kLog2e;
   vec8 qf[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
@@ -134,7 +149,10 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
   f32x4 o_acc[4];  // O^T tiles: dims 16*d + 4*g + j, query l16
 #pragma unroll
   for (int d = 0; d < 4; ++d) o_acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;  // running max of this lane's query
+  // Softmax state in raw score units: p = exp2(s * c - m * c), c = scale * log2 e.
+  const float c = a.scale * kLog2e;
+  const float inv_scale = 1.0f / a.scale;
+  float m_run = -INFINITY;  // running max (raw) of this lane's query
   float l_part = 0.0f;      // this lane's partial row sum (its keys only)
 
   const float* mask = static_cast<const float*>(a.mask);
@@ -145,46 +163,69 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
   }
   const int ntiles = (kend + kBK - 1) / kBK;
 
+  // Staging: K rows (tid >> 3) and (tid >> 3) + 32, chunk tid & 7; V keys
+  // kq .. kq + 3 x dims d0 .. d0 + 3, transposed in registers.
+  const int k_row = tid >> 3, k_chunk = tid & 7;
+  const int kq = 4 * (tid & 15), d0 = 4 * (tid >> 4);
+  uint4 kreg[2];
+  uint2 vreg[4];
+  auto load_tile = [&](int t) {
+    const int k0 = t * kBK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = k0 + k_row + 32 * i;
+      kreg[i] = uint4{0u, 0u, 0u, 0u};
+      if (key < a.seq_k) kreg[i] = *reinterpret_cast<const uint4*>(K + key * a.k_ss + 8 * k_chunk);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = k0 + kq + i;
+      vreg[i] = uint2{0u, 0u};
+      if (key < a.seq_k) vreg[i] = *reinterpret_cast<const uint2*>(V + key * a.v_ss + d0);
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = k_row + 32 * i;
+      *reinterpret_cast<uint4*>(Ks + key * 128 + ((k_chunk ^ (key & 7)) << 4)) = kreg[i];
+    }
+    const int p = vt_pos(kq);  // multiple of 4: keys kq .. kq + 3 land at p .. p + 3
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int dim = d0 + jj;
+      uint32_t e[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = (jj < 2) ? vreg[i].x : vreg[i].y;
+        e[i] = (jj & 1) ? (w >> 16) : (w & 0xffffu);
+      }
+      const uint2 word = uint2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+      *reinterpret_cast<uint2*>(Vt + dim * 128 + (((p >> 3) ^ vt_swz(dim)) << 4) + (p & 7) * 2) = word;
+    }
+  };
+
+  if (ntiles > 0) load_tile(0);
   for (int t = 0; t < ntiles; ++t) {
     const int k0 = t * kBK;
-    // Stage K [key][dim] (16-byte rows) and V^T [dim][key]: each thread takes
-    // a key pair x 8 dims of V and writes 8 packed 4-byte (key, key+1) words.
-    {
-      const int key = tid >> 3, d0 = (tid & 7) * 8;  // K: keys 0..31 and 32..63
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int kk = key + 32 * i;
-        uint4 kv = {0u, 0u, 0u, 0u};
-        if (k0 + kk < a.seq_k) kv = *reinterpret_cast<const uint4*>(K + (k0 + kk) * a.k_ss + d0);
-        *reinterpret_cast<uint4*>(&Ks[kk][d0]) = kv;
-      }
-      const int kp = (tid >> 3) * 2;  // V: key pair kp, kp + 1 (keys 0..63)
-      uint4 v0 = {0u, 0u, 0u, 0u}, v1 = {0u, 0u, 0u, 0u};
-      if (k0 + kp < a.seq_k) v0 = *reinterpret_cast<const uint4*>(V + (k0 + kp) * a.v_ss + d0);
-      if (k0 + kp + 1 < a.seq_k) v1 = *reinterpret_cast<const uint4*>(V + (k0 + kp + 1) * a.v_ss + d0);
-      const uint32_t w0[4] = {v0.x, v0.y, v0.z, v0.w}, w1[4] = {v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        *reinterpret_cast<uint32_t*>(&Vt[d0 + 2 * j][kp]) = (w0[j] & 0xffffu) | (w1[j] << 16);
-        *reinterpret_cast<uint32_t*>(&Vt[d0 + 2 * j + 1][kp]) = (w0[j] >> 16) | (w1[j] & 0xffff0000u);
-      }
-    }
+    store_tile();
     __syncthreads();
+    if (t + 1 < ntiles) load_tile(t + 1);  // in flight while this tile is multiplied
 
     // S^T tiles: keys 16*kt4 + 4*g + j (j = 0..3), query l16.
     f32x4 s_acc[4];
 #pragma unroll
     for (int kt4 = 0; kt4 < 4; ++kt4) {
       s_acc[kt4] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int key = 16 * kt4 + l16;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        vec8 kf = *reinterpret_cast<const vec8*>(&Ks[16 * kt4 + l16][32 * ks + 8 * g]);
+        const vec8 kf = *reinterpret_cast<const vec8*>(Ks + key * 128 + (((4 * ks + g) ^ (key & 7)) << 4));
         s_acc[kt4] = FlashMma<T>::mma(kf, qf[ks], s_acc[kt4]);
       }
     }
-    // Scores in log2 units (scale * log2 e), so p = exp2(s - m).  Key-range
-    // and causal checks run only on tiles that reach past seq_k or the
-    // wave's first query (a uniform branch); interior tiles skip them.
+    // Key-range and causal checks run only on tiles that reach past seq_k or
+    // the wave's first query (a uniform branch); interior tiles skip them.
     float tmax = -INFINITY;
     const bool edge = (k0 + kBK > a.seq_k) || (MASK == 1 && k0 + kBK - 1 > wave_q0) || MASK == 2;
     if (edge) {
@@ -193,30 +234,25 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int key = k0 + 16 * kt4 + 4 * g + j;
-          float s = s_acc[kt4][j] * scale_log2;
-          if (key >= a.seq_k) s = -INFINITY;
-          if (MASK == 1 && key > q) s = -INFINITY;
-          if (MASK == 2 && q_valid && key < a.seq_k) s += mask[static_cast<int64_t>(q) * a.mask_ld + key] * kLog2e;
-          s_acc[kt4][j] = s;
-          tmax = fmaxf(tmax, s);
+          float sv = s_acc[kt4][j];
+          if (key >= a.seq_k) sv = -INFINITY;
+          if (MASK == 1 && key > q) sv = -INFINITY;
+          if (MASK == 2 && q_valid && key < a.seq_k) sv += mask[static_cast<int64_t>(q) * a.mask_ld + key] * inv_scale;
+          s_acc[kt4][j] = sv;
+          tmax = fmaxf(tmax, sv);
         }
       }
     } else {
 #pragma unroll
-      for (int kt4 = 0; kt4 < 4; ++kt4) {
+      for (int kt4 = 0; kt4 < 4; ++kt4)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float s = s_acc[kt4][j] * scale_log2;
-          s_acc[kt4][j] = s;
-          tmax = fmaxf(tmax, s);
-        }
-      }
+        for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, s_acc[kt4][j]);
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float m_new = fmaxf(m_run, tmax);
-    const float base = m_new == -INFINITY ? 0.0f : m_new;
-    const float corr = m_run == -INFINITY ? 0.0f : exp2f(m_run - base);
+    const float base = m_new == -INFINITY ? 0.0f : m_new * c;
+    const float corr = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, c, -base));
     m_run = m_new;
     l_part *= corr;
 #pragma unroll
@@ -226,26 +262,25 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
     vec8 pf[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      uint16_t bits[8];
+      float pv[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        float p = exp2f(s_acc[2 * ks + i / 4][i % 4] - base);
-        l_part += p;
-        bits[i] = Elem<T>::from_f32(p).bits;
+        pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[2 * ks + i / 4][i % 4], c, -base));
+        l_part += pv[i];
       }
-      pf[ks] = __builtin_bit_cast(vec8, *reinterpret_cast<const uint4*>(bits));
+      const uint4 packed = {pack2<T>(pv[0], pv[1]), pack2<T>(pv[2], pv[3]), pack2<T>(pv[4], pv[5]),
+                            pack2<T>(pv[6], pv[7])};
+      pf[ks] = __builtin_bit_cast(vec8, packed);
     }
-    // O^T += V^T P^T: A operand = V^T rows (dims 16*d + l16), keys in the
-    // same order as P^T: two runs of 4 consecutive keys.
+    // O^T += V^T P^T: A operand = V^T row (dim 16*d + l16), chunk 4*ks + g
+    // holds the same eight keys as the lane's P^T fragment.
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
+      const int dim = 16 * d + l16;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const uint16_t* row = &Vt[16 * d + l16][32 * ks + 4 * g];
-        uint2 lo = *reinterpret_cast<const uint2*>(row);
-        uint2 hi = *reinterpret_cast<const uint2*>(row + 16);
-        uint4 packed = {lo.x, lo.y, hi.x, hi.y};
-        o_acc[d] = FlashMma<T>::mma(__builtin_bit_cast(vec8, packed), pf[ks], o_acc[d]);
+        const vec8 vf = *reinterpret_cast<const vec8*>(Vt + dim * 128 + (((4 * ks + g) ^ vt_swz(dim)) << 4));
+        o_acc[d] = FlashMma<T>::mma(vf, pf[ks], o_acc[d]);
       }
     }
     __syncthreads();
@@ -257,10 +292,8 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
   if (q_valid) {
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      uint16_t bits[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bits[j] = Elem<T>::from_f32(o_acc[d][j] * inv).bits;
-      *reinterpret_cast<uint2*>(O + q * a.o_ss + 16 * d + 4 * g) = *reinterpret_cast<const uint2*>(bits);
+      const uint2 w = {pack2<T>(o_acc[d][0] * inv, o_acc[d][1] * inv), pack2<T>(o_acc[d][2] * inv, o_acc[d][3] * inv)};
+      *reinterpret_cast<uint2*>(O + q * a.o_ss + 16 * d + 4 * g) = w;
     }
   }
 }
@@ -297,6 +330,7 @@ int c3h_flash_attention(const c3h_flash_args* a, void* stream) {
   C3H_REQUIRE(a->batch >= 0 && a->heads >= 1 && a->seq_q >= 0 && a->seq_k >= 1, "flash: bad sizes");
   C3H_REQUIRE(a->mask_kind >= 0 && a->mask_kind <= 2, "flash: bad mask_kind");
   C3H_REQUIRE(a->mask_kind != 2 || a->mask != nullptr, "flash: additive mask pointer missing");
+  C3H_REQUIRE(a->scale > 0.0f, "flash: scale must be positive");
   C3H_REQUIRE(a->q_ss % 8 == 0 && a->k_ss % 8 == 0 && a->v_ss % 8 == 0 && a->q_sh % 8 == 0 && a->k_sh % 8 == 0 &&
                   a->v_sh % 8 == 0 && a->q_sb % 8 == 0 && a->k_sb % 8 == 0 && a->v_sb % 8 == 0,
               "flash: Q/K/V strides must be multiples of 8 elements");
