@@ -43,9 +43,15 @@ def _hipcc() -> str:
     return path
 
 
+# Per-source additions.  attention.hip: MFMA accumulators in ordinary VGPRs
+# (the flash kernel's softmax reads and rescales them every K tile; in AGPRs
+# each access costs a v_accvgpr_read / write pair).
+EXTRA_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr[-6000:]}")

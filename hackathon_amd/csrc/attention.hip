@@ -7,8 +7,9 @@
 //   recomputes each three times).
 //
 // flash_attention: the launch-grouped FusedAttentionScores + P.V MatMul.  A
-//   workgroup owns 64 queries of one (batch, head) (16 per wave); K and V
-//   tiles of 64 keys are staged in LDS.  Each wave computes S^T = K Q^T with
+//   workgroup owns 128 queries of one (batch, head) (two groups of 16 per
+//   wave); K and V tiles of 64 keys are staged in LDS, the next tile's loads
+//   in flight while the current one is multiplied.  Each wave computes S^T = K Q^T with
 //   v_mfma_f32_16x16x32_{f16,bf16} so that a lane holds one query's scores;
 //   the online-softmax state is then per lane and P^T feeds the O^T = V^T P^T
 //   MFMA straight from registers (both operands use the same key order, so
@@ -80,7 +81,8 @@ __global__ void __launch_bounds__(kScoreThreads) attention_scores_kernel(c3h_att
 
 // ------------------------------------------------------------ flash attention
 constexpr int kD = 64;        // head dim
-constexpr int kBQ = 64;       // queries per workgroup (16 per wave)
+constexpr int QG = 2;         // 16-query groups per wave
+constexpr int kBQ = 64 * QG;  // queries per workgroup
 constexpr int kBK = 64;       // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -115,6 +117,9 @@ template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float 
 template <> __device__ __forceinline__ uint32_t pack2<bf16_t>(float lo, float hi) { return f32x2_to_bf16x2_bits(lo, hi); }
 template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float lo, float hi) { return f32x2_to_f16x2_bits(lo, hi); }
 
+// Each wave owns QG groups of 16 queries (kBQ = 64 * QG per workgroup): every
+// K / V^T fragment read from LDS feeds QG MFMAs, and the tile staging is
+// shared by 4 * 16 * QG queries.
 template <typename T, int MASK>
 __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
   typedef typename FlashMma<T>::vec vec8;
@@ -133,27 +138,39 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
   const uint16_t* V = static_cast<const uint16_t*>(a.v) + batch * a.v_sb + head * a.v_sh;
   uint16_t* O = static_cast<uint16_t*>(a.out) + batch * a.o_sb + head * a.o_sh;
 
-  // This lane's query (B operand column of S^T = K Q^T) and its Q fragment:
-  // dims 32*ks + 8*g + [0..7].
-  const int q = qt * kBQ + wave * 16 + l16;
-  const bool q_valid = q < a.seq_q;
-  const int wave_q0 = qt * kBQ + wave * 16;  // this wave's first query
-  vec8 qf[2];
+  // This lane's queries (B operand column of S^T = K Q^T), one per group,
+  // and their Q fragments: dims 32*ks + 8*g + [0..7].
+  const int wave_q0 = qt * kBQ + wave * 16 * QG;  // this wave's first query
+  const int wave_q1 = wave_q0 + 16 * QG - 1;      // ... and last
+  int q[QG];
+  bool q_valid[QG];
+  vec8 qf[QG][2];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    uint4 raw = {0u, 0u, 0u, 0u};
-    if (q_valid) raw = *reinterpret_cast<const uint4*>(Q + q * a.q_ss + 32 * ks + 8 * g);
-    qf[ks] = __builtin_bit_cast(vec8, raw);
+  for (int u = 0; u < QG; ++u) {
+    q[u] = wave_q0 + 16 * u + l16;
+    q_valid[u] = q[u] < a.seq_q;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      uint4 raw = {0u, 0u, 0u, 0u};
+      if (q_valid[u]) raw = *reinterpret_cast<const uint4*>(Q + q[u] * a.q_ss + 32 * ks + 8 * g);
+      qf[u][ks] = __builtin_bit_cast(vec8, raw);
+    }
   }
 
-  f32x4 o_acc[4];  // O^T tiles: dims 16*d + 4*g + j, query l16
+  f32x4 o_acc[QG][4];  // O^T tiles: dims 16*d + 4*g + j, query q[u]
 #pragma unroll
-  for (int d = 0; d < 4; ++d) o_acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int u = 0; u < QG; ++u)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o_acc[u][d] = f32x4{0.f, 0.f, 0.f, 0.f};
   // Softmax state in raw score units: p = exp2(s * c - m * c), c = scale * log2 e.
   const float c = a.scale * kLog2e;
   const float inv_scale = 1.0f / a.scale;
-  float m_run = -INFINITY;  // running max (raw) of this lane's query
-  float l_part = 0.0f;      // this lane's partial row sum (its keys only)
+  float m_run[QG], l_part[QG];  // running max (raw) and this lane's partial row sum
+#pragma unroll
+  for (int u = 0; u < QG; ++u) {
+    m_run[u] = -INFINITY;
+    l_part[u] = 0.0f;
+  }
 
   const float* mask = static_cast<const float*>(a.mask);
   int kend = a.seq_k;
@@ -212,88 +229,103 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
     __syncthreads();
     if (t + 1 < ntiles) load_tile(t + 1);  // in flight while this tile is multiplied
 
-    // S^T tiles: keys 16*kt4 + 4*g + j (j = 0..3), query l16.
-    f32x4 s_acc[4];
-#pragma unroll
-    for (int kt4 = 0; kt4 < 4; ++kt4) {
-      s_acc[kt4] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int key = 16 * kt4 + l16;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const vec8 kf = *reinterpret_cast<const vec8*>(Ks + key * 128 + (((4 * ks + g) ^ (key & 7)) << 4));
-        s_acc[kt4] = FlashMma<T>::mma(kf, qf[ks], s_acc[kt4]);
-      }
-    }
-    // Key-range and causal checks run only on tiles that reach past seq_k or
-    // the wave's first query (a uniform branch); interior tiles skip them.
-    float tmax = -INFINITY;
-    const bool edge = (k0 + kBK > a.seq_k) || (MASK == 1 && k0 + kBK - 1 > wave_q0) || MASK == 2;
-    if (edge) {
+    // Causal: a tile wholly after this wave's last query contributes nothing.
+    if (MASK != 1 || k0 <= wave_q1) {
+      // S^T tiles: keys 16*kt4 + 4*g + j (j = 0..3), query q[u].
+      f32x4 s_acc[QG][4];
 #pragma unroll
       for (int kt4 = 0; kt4 < 4; ++kt4) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int key = k0 + 16 * kt4 + 4 * g + j;
-          float sv = s_acc[kt4][j];
-          if (key >= a.seq_k) sv = -INFINITY;
-          if (MASK == 1 && key > q) sv = -INFINITY;
-          if (MASK == 2 && q_valid && key < a.seq_k) sv += mask[static_cast<int64_t>(q) * a.mask_ld + key] * inv_scale;
-          s_acc[kt4][j] = sv;
-          tmax = fmaxf(tmax, sv);
+        for (int u = 0; u < QG; ++u) s_acc[u][kt4] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int key = 16 * kt4 + l16;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const vec8 kf = *reinterpret_cast<const vec8*>(Ks + key * 128 + (((4 * ks + g) ^ (key & 7)) << 4));
+#pragma unroll
+          for (int u = 0; u < QG; ++u) s_acc[u][kt4] = FlashMma<T>::mma(kf, qf[u][ks], s_acc[u][kt4]);
         }
       }
-    } else {
+      // Key-range and causal checks run only on tiles that reach past seq_k
+      // or the wave's first query (a uniform branch).
+      const bool edge = (k0 + kBK > a.seq_k) || (MASK == 1 && k0 + kBK - 1 > wave_q0) || MASK == 2;
+      vec8 pf[QG][2];
 #pragma unroll
-      for (int kt4 = 0; kt4 < 4; ++kt4)
+      for (int u = 0; u < QG; ++u) {
+        float tmax = -INFINITY;
+        if (edge) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, s_acc[kt4][j]);
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const float base = m_new == -INFINITY ? 0.0f : m_new * c;
-    const float corr = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, c, -base));
-    m_run = m_new;
-    l_part *= corr;
+          for (int kt4 = 0; kt4 < 4; ++kt4) {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) o_acc[d] *= corr;
-    // P^T fragments for the two 32-key halves: element i of half ks is key
-    // 32*ks + 16*(i/4) + 4*g + (i%4), i.e. s_acc[2*ks + i/4][i%4].
-    vec8 pf[2];
+            for (int j = 0; j < 4; ++j) {
+              const int key = k0 + 16 * kt4 + 4 * g + j;
+              float sv = s_acc[u][kt4][j];
+              if (key >= a.seq_k) sv = -INFINITY;
+              if (MASK == 1 && key > q[u]) sv = -INFINITY;
+              if (MASK == 2 && q_valid[u] && key < a.seq_k)
+                sv += mask[static_cast<int64_t>(q[u]) * a.mask_ld + key] * inv_scale;
+              s_acc[u][kt4][j] = sv;
+              tmax = fmaxf(tmax, sv);
+            }
+          }
+        } else {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      float pv[8];
+          for (int kt4 = 0; kt4 < 4; ++kt4)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[2 * ks + i / 4][i % 4], c, -base));
-        l_part += pv[i];
+            for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, s_acc[u][kt4][j]);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_new = fmaxf(m_run[u], tmax);
+        const float base = m_new == -INFINITY ? 0.0f : m_new * c;
+        const float corr =
+            m_run[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(m_run[u], c, -base));
+        m_run[u] = m_new;
+        l_part[u] *= corr;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) o_acc[u][d] *= corr;
+        // P^T fragments for the two 32-key halves: element i of half ks is
+        // key 32*ks + 16*(i/4) + 4*g + (i%4), i.e. s_acc[2*ks + i/4][i%4].
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          float pv[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[u][2 * ks + i / 4][i % 4], c, -base));
+            l_part[u] += pv[i];
+          }
+          const uint4 packed = {pack2<T>(pv[0], pv[1]), pack2<T>(pv[2], pv[3]), pack2<T>(pv[4], pv[5]),
+                                pack2<T>(pv[6], pv[7])};
+          pf[u][ks] = __builtin_bit_cast(vec8, packed);
+        }
       }
-      const uint4 packed = {pack2<T>(pv[0], pv[1]), pack2<T>(pv[2], pv[3]), pack2<T>(pv[4], pv[5]),
-                            pack2<T>(pv[6], pv[7])};
-      pf[ks] = __builtin_bit_cast(vec8, packed);
-    }
-    // O^T += V^T P^T: A operand = V^T row (dim 16*d + l16), chunk 4*ks + g
-    // holds the same eight keys as the lane's P^T fragment.
+      // O^T += V^T P^T: A operand = V^T row (dim 16*d + l16), chunk 4*ks + g
+      // holds the same eight keys as the lane's P^T fragment.
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const int dim = 16 * d + l16;
+      for (int d = 0; d < 4; ++d) {
+        const int dim = 16 * d + l16;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const vec8 vf = *reinterpret_cast<const vec8*>(Vt + dim * 128 + (((4 * ks + g) ^ vt_swz(dim)) << 4));
-        o_acc[d] = FlashMma<T>::mma(vf, pf[ks], o_acc[d]);
+        for (int ks = 0; ks < 2; ++ks) {
+          const vec8 vf = *reinterpret_cast<const vec8*>(Vt + dim * 128 + (((4 * ks + g) ^ vt_swz(dim)) << 4));
+#pragma unroll
+          for (int u = 0; u < QG; ++u) o_acc[u][d] = FlashMma<T>::mma(vf, pf[u][ks], o_acc[u][d]);
+        }
       }
     }
     __syncthreads();
   }
 
-  float l_tot = l_part + __shfl_xor(l_part, 16, 64);
-  l_tot += __shfl_xor(l_tot, 32, 64);
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (q_valid) {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint2 w = {pack2<T>(o_acc[d][0] * inv, o_acc[d][1] * inv), pack2<T>(o_acc[d][2] * inv, o_acc[d][3] * inv)};
-      *reinterpret_cast<uint2*>(O + q * a.o_ss + 16 * d + 4 * g) = w;
+  for (int u = 0; u < QG; ++u) {
+    float l_tot = l_part[u] + __shfl_xor(l_part[u], 16, 64);
+    l_tot += __shfl_xor(l_tot, 32, 64);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (q_valid[u]) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint2 w = {pack2<T>(o_acc[u][d][0] * inv, o_acc[u][d][1] * inv),
+                         pack2<T>(o_acc[u][d][2] * inv, o_acc[u][d][3] * inv)};
+        *reinterpret_cast<uint2*>(O + q[u] * a.o_ss + 16 * d + 4 * g) = w;
+      }
     }
   }
 }
