@@ -755,10 +755,15 @@ __device__ __forceinline__ void static_for(F&& f) {
 // column, optional residual, optional ReLU, no program) straight from the
 // accumulators: one 8-byte (16-bit) or 16-byte (fp32) store per 4 values, no
 // LDS round trip.  Same arithmetic as apply_epilogue: ((acc + b) + res), max 0.
-template <typename TO, int TM, int TN, typename Acc>
-__device__ __forceinline__ void epilogue_direct(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
-                                                TO* outp, const TO* resp, const float* bias, bool relu) {
+// G: the GELU form (act 2, gelu_erf with imm[0..2]), a separate
+// instantiation so the plain form carries no per-element GELU code.
+template <typename TO, int TM, int TN, bool G, typename Acc>
+__device__ __forceinline__ void epilogue_direct_impl(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase,
+                                                     int lane, TO* outp, const TO* resp, const float* bias, int act) {
   const KArg<Problem>& p = kernel_arg<Problem>();
+  const bool relu = !G && act == 1;
+  constexpr bool gelu = G;
+  const float g0 = G ? p.epi.imm[0] : 0.0f, g1 = G ? p.epi.imm[1] : 0.0f, g2 = G ? p.epi.imm[2] : 0.0f;
   const int l16 = lane & 15, lg = lane >> 4;
   const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
   // Bias of this lane's columns, for every column tile.
@@ -796,7 +801,7 @@ __device__ __forceinline__ void epilogue_direct(const Acc (&acc)[TM][TN], int64_
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             float t = (v[r] + b[j][r]) + res[j][r];
-            v[r] = relu ? fmaxf(t, 0.0f) : t;
+            v[r] = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t);
           }
           Elem<TO>::store4(outp + m * ldo + n, v);
         } else {
@@ -805,7 +810,7 @@ __device__ __forceinline__ void epilogue_direct(const Acc (&acc)[TM][TN], int64_
             if (n + r < pn) {
               const int64_t o = m * ldo + n + r;
               float t = (v[r] + (bias ? bias[n + r] : 0.0f)) + (resp ? Elem<TO>::to_f32(resp[o]) : 0.0f);
-              outp[o] = Elem<TO>::from_f32(relu ? fmaxf(t, 0.0f) : t);
+              outp[o] = Elem<TO>::from_f32(relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t));
             }
           }
         }
@@ -814,14 +819,26 @@ __device__ __forceinline__ void epilogue_direct(const Acc (&acc)[TM][TN], int64_
   });
 }
 
+// GELU: act 2 is computed in registers only by the instantiations that ask
+// for it (the large-tile kernel, which has no staged epilogue).
+template <typename TO, int TM, int TN, bool GELU = false, typename Acc>
+__device__ __forceinline__ void epilogue_direct(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
+                                                TO* outp, const TO* resp, const float* bias, int act) {
+  if (GELU && act == 2) epilogue_direct_impl<TO, TM, TN, true>(acc, mbase, nbase, lane, outp, resp, bias, act);
+  else epilogue_direct_impl<TO, TM, TN, false>(acc, mbase, nbase, lane, outp, resp, bias, act);
+}
+
 // int8 GEMM (c3h_qgemm) counterpart of epilogue_direct for C^T int32
 // accumulators: qmode 0 stores int32, 1 requantizes to int8 (4 bytes per
 // lane), 2 dequantizes and 3 requantizes then dequantizes, both followed by
 // the common float epilogue (simple_epi).  Arithmetic as store_strip_q.
-template <typename TO, int TM, int TN, typename Acc>
-__device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
-                                                  TO* outp, const TO* resp, const float* bias, bool relu) {
+template <typename TO, int TM, int TN, bool G, typename Acc>
+__device__ __forceinline__ void epilogue_direct_q_impl(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase,
+                                                       int lane, TO* outp, const TO* resp, const float* bias, int act) {
   const KArg<Problem>& p = kernel_arg<Problem>();
+  const bool relu = !G && act == 1;
+  constexpr bool gelu = G;
+  const float g0 = G ? p.epi.imm[0] : 0.0f, g1 = G ? p.epi.imm[1] : 0.0f, g2 = G ? p.epi.imm[2] : 0.0f;
   const int l16 = lane & 15, lg = lane >> 4;
   const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
   const int mode = p.qmode;
@@ -900,7 +917,7 @@ __device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int6
                 float rr = res[j][r];
                 if (resp && !nfull && n + r < pn) rr = Elem<TO>::to_f32(resp[o + r]);
                 const float t = (v[r] + b[j][r]) + rr;
-                v[r] = relu ? fmaxf(t, 0.0f) : t;
+                v[r] = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t);
               }
               if (nfull) {
                 Elem<TO>::store4(outp + o, v);
@@ -949,6 +966,13 @@ __device__ __forceinline__ void scale_acc(f32x4 (&acc)[TM][TN], int64_t mbase, i
   });
 }
 
+template <typename TO, int TM, int TN, bool GELU = false, typename Acc>
+__device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
+                                                  TO* outp, const TO* resp, const float* bias, int act) {
+  if (GELU && act == 2) epilogue_direct_q_impl<TO, TM, TN, true>(acc, mbase, nbase, lane, outp, resp, bias, act);
+  else epilogue_direct_q_impl<TO, TM, TN, false>(acc, mbase, nbase, lane, outp, resp, bias, act);
+}
+
 // Whether epilogue_direct_q applies: int32 / int8 outputs need only aligned
 // row-major stores; dequantized ones also need the common float epilogue.
 __device__ __forceinline__ bool epilogue_q_direct_ok(const KArg<Problem>& p, bool vec4);
@@ -970,6 +994,7 @@ __device__ __forceinline__ bool epilogue_q_direct_ok(const KArg<Problem>& p, boo
 // VALU per load instead of 64-bit address math and branches.
 template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, bool BUF = false>
 __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
+  constexpr bool DIRECT_GELU = false;  // GELU epilogues take the staged path here
   constexpr int ES = Mma::ES;
   constexpr int VE = 16 / ES;        // elements per 16-byte vector
   constexpr int BK = 128 / ES;       // elements per 128-byte tile row
@@ -1258,12 +1283,12 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
     if constexpr (Mma::kInt) {
       if (bz == 0 && epilogue_q_direct_ok(kernel_arg<Problem>(), vec4)) {
         const float* bias = p.epi.bias_mode == 2 ? static_cast<const float*>(p.epi.bias) : nullptr;
-        epilogue_direct_q<TO, TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act == 1);
+        epilogue_direct_q<TO, TM, TN, DIRECT_GELU>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act);
         return;
       }
     } else if (epilogue_is_simple(kernel_arg<Problem>(), vec4)) {
       const float* bias = p.epi.bias_mode == 2 ? static_cast<const float*>(p.epi.bias) + bias_off : nullptr;
-      epilogue_direct<TO, TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act == 1);
+      epilogue_direct<TO, TM, TN, DIRECT_GELU>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act);
       return;
     }
   }
@@ -1329,6 +1354,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, int S, int NW = 4>
 __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
   constexpr bool DIRECT = NW > 4;
+  constexpr bool DIRECT_GELU = DIRECT;
   constexpr int ES = Mma::ES;
   constexpr int VE = 16 / ES;
   constexpr int BK = 128 / ES;
@@ -1483,12 +1509,14 @@ __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
                       ((reinterpret_cast<uintptr_t>(resp) & kA) == 0);
     const float* bias = p.epi.bias_mode == 2 ? static_cast<const float*>(p.epi.bias) : nullptr;
     if constexpr (Mma::kInt) {
-      if (epilogue_q_direct_ok(kernel_arg<Problem>(), vec4)) {
-        epilogue_direct_q<TO, TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act == 1);
+      // DIRECT: the host admitted only epilogues epilogue_direct_q computes
+      // (big_tile_wins), GELU included; there is no staged path to fall to.
+      if (DIRECT || epilogue_q_direct_ok(kernel_arg<Problem>(), vec4)) {
+        epilogue_direct_q<TO, TM, TN, DIRECT_GELU>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act);
         return;
       }
     } else if (DIRECT || epilogue_is_simple(kernel_arg<Problem>(), vec4)) {
-      epilogue_direct<TO, TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act == 1);
+      epilogue_direct<TO, TM, TN, DIRECT_GELU>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act);
       return;
     }
   }
@@ -1602,7 +1630,9 @@ inline bool dma_eligible(const Problem& p, int64_t batch, int am) {
 // Whether the 256 x 256 eight-wave DMA kernel beats 128 x 128 at two blocks
 // per CU: rounds of resident tiles, a 256-tile round costing 1.66 rounds of
 // 128-tiles (measured: 8192^3 GEMM, 1195 vs 994 us), and an epilogue that
-// epilogue_direct handles (host-side restatement of epilogue_is_simple).
+// epilogue_direct(_q) handles (host-side restatement of epilogue_is_simple;
+// plus GELU for int8, which the large-tile instantiation computes in
+// registers).
 // int8 GEMMs writing int32 / int8 (qmode 0 / 1) need only aligned row-major
 // stores (epilogue_q_direct_ok).
 bool big_tile_wins(const Problem& p, int cus, size_t out_size, bool int_mma) {
@@ -1610,14 +1640,18 @@ bool big_tile_wins(const Problem& p, int cus, size_t out_size, bool int_mma) {
   const c3h_epilogue& e = p.epi;
   const uintptr_t al = 4 * out_size - 1;
   const bool stores = !p.out_nchw && p.ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(p.out) & al) == 0;
+  // GELU in registers measured slower than the staged 128 x 128 epilogue for
+  // 16-bit GEMMs (16384x2048x512: 101 vs 95 us) and faster for int8 ones.
+  const int max_act = int_mma ? 2 : 1;
   const bool simple = stores && e.alpha == 1.0f && e.beta == 1.0f && (e.bias_mode == 0 || e.bias_mode == 2) &&
-                      e.act <= 1 && e.n_inst == 0 && (e.bias_mode == 0 || (reinterpret_cast<uintptr_t>(e.bias) & 15) == 0) &&
+                      e.act <= max_act && e.n_inst == 0 &&
+                      (e.bias_mode == 0 || (reinterpret_cast<uintptr_t>(e.bias) & 15) == 0) &&
                       (reinterpret_cast<uintptr_t>(e.residual) & al) == 0;
   if (!(int_mma && p.qmode <= 1 ? stores : simple)) return false;
   const int64_t t128 = ceil_div(p.m, 128) * ceil_div(p.n, 128), t256 = ceil_div(p.m, 256) * ceil_div(p.n, 256);
   const double r128 = static_cast<double>(ceil_div(t128, 2 * cus));
   const double r256 = static_cast<double>(ceil_div(t256, cus)) * 1.66;
-  return r256 < r128;
+  return r256 < 0.9 * r128;  // a clear margin: near-ties measured slower (16384x2304x768 int8)
 }
 
 int device_cus() {

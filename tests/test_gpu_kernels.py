@@ -594,12 +594,13 @@ def _bigtile_pair(launch):
     return a, b
 
 
-@pytest.mark.parametrize("kind,out_kind", [("bf16", "bf16"), ("fp16", "fp32")])
-def test_gemm_big_tile_matches_128_tiles(gpu, kind, out_kind):
+@pytest.mark.parametrize("kind,out_kind,act", [("bf16", "bf16", 1), ("fp16", "fp32", 1), ("fp16", "fp16", 2)])
+def test_gemm_big_tile_matches_128_tiles(gpu, kind, out_kind, act):
     """4096x4096x192 (enough tiles that the 256x256 eight-wave kernel is
-    chosen) with bias + residual + ReLU: bit-identical to the 128x128 kernel
-    (same K order per output) and within the 16-bit GEMM tolerance of float64
-    on sampled rows."""
+    chosen) with bias + residual + ReLU or GELU (computed in registers there,
+    through the staged epilogue by the 128x128 kernel): bit-identical to the
+    128x128 kernel (same K order per output and the same epilogue arithmetic)
+    and within the 16-bit GEMM tolerance of float64 on sampled rows."""
     from hackathon_amd import _lib
     from hackathon_amd.c35 import engine as E
     from hackathon_amd.device import BF16, DeviceArray
@@ -614,7 +615,7 @@ def test_gemm_big_tile_matches_128_tiles(gpu, kind, out_kind):
     bias = rng.standard_normal(n).astype(np.float32)
     r32 = rng.standard_normal((m, n)).astype(np.float32)
     code = _lib.BF16 if kind == "bf16" else _lib.F16
-    ocode, sdt = {"fp32": (_lib.F32, np.float32), "bf16": (_lib.BF16, BF16)}[out_kind]
+    ocode, sdt = {"fp32": (_lib.F32, np.float32), "bf16": (_lib.BF16, BF16), "fp16": (_lib.F16, np.float16)}[out_kind]
     if out_kind == "fp32":
         rd, rv = _dev(r32), r32
     else:
@@ -628,14 +629,21 @@ def test_gemm_big_tile_matches_128_tiles(gpu, kind, out_kind):
         g.a, g.b, g.out = ad.ptr, bd.ptr, out.ptr
         g.m, g.n, g.k, g.lda, g.ldb, g.ldo, g.batch = m, n, k, k, k, n, 1
         g.trans_a, g.trans_b, g.in_dtype, g.out_dtype = 0, 1, code, ocode
-        g.epi = E.epilogue(bias=biasd, bias_mode=2, act=1, residual=rd)
-        print(f"gemm {m}x{n}x{k} {kind}->{out_kind}", flush=True)
+        g.epi = E.epilogue(bias=biasd, bias_mode=2, act=act, residual=rd,
+                           imm=[math.sqrt(2.0), 1.0, 0.5] if act == 2 else [])
+        print(f"gemm {m}x{n}x{k} {kind}->{out_kind} act={act}", flush=True)
         _lib.launch(g, None)
         return out.get().copy()
     big, small = _bigtile_pair(launch)
     np.testing.assert_array_equal(big.view(np.uint8), small.view(np.uint8))
     rows = np.arange(0, m, 97)
-    want = np.maximum(av[rows].astype(np.float64) @ bv.astype(np.float64).T + bias + rv[rows], 0)
+    t = av[rows].astype(np.float64) @ bv.astype(np.float64).T + bias + rv[rows]
+    if act == 1:
+        want = np.maximum(t, 0)
+    else:
+        from scipy.special import erf
+
+        want = t * (erf(t / math.sqrt(2.0)) + 1.0) * 0.5
     got = big[rows] if out_kind == "fp32" else _from16(big[rows], out_kind)
     tol = 1e-4 if out_kind == "fp32" else 1e-2
     np.testing.assert_allclose(got, want, rtol=tol, atol=tol * 4)
@@ -679,11 +687,13 @@ def test_conv_big_tile_matches_128_tiles(gpu):
         np.testing.assert_allclose(got[b_, y, x_], want, rtol=1e-2, atol=4e-2)
 
 
-@pytest.mark.parametrize("mode", [0, 2])
-def test_qgemm_big_tile_matches_128_tiles(gpu, mode):
+@pytest.mark.parametrize("mode,act", [(0, 0), (2, 0), (3, 2)])
+def test_qgemm_big_tile_matches_128_tiles(gpu, mode, act):
     """int8 GEMM 4096x4096x256 on the 256x256 kernel: int32 accumulators
     (mode 0) equal the exact integer product; the dequantized bf16 output with
-    bias + residual (mode 2) is bit-identical to the 128x128 kernel."""
+    bias + residual (mode 2), and requantize -> dequantize + bias + GELU (mode
+    3, computed in registers there and through the staged epilogue by the
+    128x128 kernel) are bit-identical to the 128x128 kernel."""
     from hackathon_amd import _lib
     from hackathon_amd.c35 import engine as E
     from hackathon_amd.device import BF16, DeviceArray
@@ -702,17 +712,21 @@ def test_qgemm_big_tile_matches_128_tiles(gpu, mode):
     def launch():
         g = _lib.QGemmArgs()
         g.a, g.b, g.out, g.m, g.n, g.k, g.lda, g.ldb, g.ldo = ad.ptr, bd.ptr, out.ptr, m, n, k, k, k, n
-        g.a_scale, g.y_scale, g.b_scale, g.mode = 0.02, 1.0, sbd.ptr, mode
+        g.a_scale, g.y_scale, g.b_scale, g.mode = 0.02, 0.37, sbd.ptr, mode
         g.out_dtype = _lib.I32 if mode == 0 else _lib.BF16
         if mode == 2:
             g.epi = E.epilogue(bias=biasd, bias_mode=2, residual=rd)
+        elif mode == 3:
+            g.epi = E.epilogue(bias=biasd, bias_mode=2, act=act, imm=[math.sqrt(2.0), 1.0, 0.5])
         else:
             g.epi = E.epilogue()
-        print(f"qgemm {m}x{n}x{k} mode {mode}", flush=True)
+        out.copy_from_host(np.zeros(out.nbytes, np.uint8))  # a launch that writes nothing cannot pass
+        print(f"qgemm {m}x{n}x{k} mode {mode} act {act}", flush=True)
         _lib.launch(g, None)
         return out.get().copy()
     big, small = _bigtile_pair(launch)
     np.testing.assert_array_equal(big.view(np.uint8), small.view(np.uint8))
+    assert np.any(big.view(np.uint8) != 0)
     if mode == 0:
         rows = np.arange(0, m, 61)
         np.testing.assert_array_equal(big[rows], a[rows].astype(np.int64) @ bt.T.astype(np.int64))
