@@ -590,12 +590,12 @@ enum AMode16 { kConvTap = 3, kConvStem = 4 };
 // ids, walked in column-major groups of 8 tile rows so blocks resident at
 // the same time share both A and B panels in that XCD's L2.
 __device__ __forceinline__ void tile_coords_of(const Problem& p, int id, int& tm, int& tn) {
+  // XCD x = id % 8 receives ids x, x + 8, ...: count q + (x < r) of them for
+  // total = 8 q + r; its j-th one takes tile x q + min(x, r) + j, so every
+  // XCD walks a contiguous tile range (a bijection for any total).
   const int total = p.tiles_m * p.tiles_n;
-  int tile = id;
-  if ((total & 7) == 0) {
-    const int per = total >> 3;
-    tile = (id & 7) * per + (id >> 3);
-  }
+  const int x = id & 7, q = total >> 3, r = total & 7;
+  const int tile = x * q + min(x, r) + (id >> 3);
   constexpr int G = 8;
   const int group = tile / (G * p.tiles_n);
   const int first_m = group * G;
