@@ -229,4 +229,8 @@ struct EwRegs {
   float r[24];
 };
 
+// conv3x3.hip: the banded 3x3 / 64-channel convolution.  Sets *handled when
+// it launched (the return value is then the launch status).
+int conv3x3_c64_launch(const c3h_conv_args* a, hipStream_t s, bool* handled);
+
 }  // namespace c3h

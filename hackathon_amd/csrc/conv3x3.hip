@@ -1,0 +1,354 @@
+// Spatially tiled 3x3 convolution for 64 -> 64 channels (gfx950), the
+// 56x56 layer-1 convolutions of ResNet-18 224: Conv 3x3 / stride 1 / pad 1
+// + per-channel bias (folded BatchNorm) + optional residual + optional ReLU,
+// NHWC 16-bit activations, fp32 accumulation on v_mfma_f32_16x16x32_{bf16,f16}.
+//
+// The implicit-GEMM kernels (gemm.hip) gather each input pixel once per
+// filter tap, so the 3x3 layer moves 9x its input through L2 -> LDS, and
+// with N = 64 output channels every LDS byte feeds few MFMAs.  Here:
+//   * a tile is a band of R full output rows of one image (R * W <= 448
+//     pixels); its (R + 2) x (W + 2) input patch, halo and zero padding
+//     included, is brought into LDS once by buffer_load ... lds (out-of-image
+//     pixels read zeros) and all nine taps read it from there;
+//   * the block is persistent (one per CU, 148 KB of LDS: two patch stages),
+//     and the next band's patch is in flight while the current one is
+//     multiplied;
+//   * each of the 4 waves (one per SIMD, so the accumulators can live in
+//     AGPRs beside 144 VGPRs of weights) keeps its 32 output channels'
+//     weights (all K = 576) in registers as 36 MFMA fragments, loaded once
+//     per block; waves are 2 (pixels) x 2 (channels), 224 pixels x 32
+//     channels each, so every A fragment read from LDS feeds two MFMAs.
+// The K order (tap-major, then channel chunks 0-31 and 32-63 with lane group
+// g supplying chunk g) and the epilogue arithmetic ((acc + bias) + residual,
+// then max 0) are those of the tap-uniform implicit-GEMM kernel, so the
+// outputs are bit-identical to c3h_conv2d's generic path.
+#include <type_traits>
+#include <utility>
+
+#include "common.h"
+
+namespace c3h {
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(2))) int i32x2;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+constexpr int kC = 64;                 // input channels: one tap = one 128-byte pixel row
+constexpr int kO = 64;                 // output channels
+constexpr int kK = 9 * kC;             // 576
+constexpr int kTilePix = 448;          // output pixels per band (28 MFMA row tiles)
+constexpr int kWaves = 4;              // 2 (pixels) x 2 (channels)
+constexpr int kWavePix = kTilePix / 2; // 224 = 14 row tiles
+constexpr int kTM = kWavePix / 16;     // 14
+constexpr int kTN = 2;                 // 32 channels per wave
+constexpr int kGroups = 73;            // DMA groups of 8 patch pixels per stage
+constexpr int kMaxPatch = kGroups * 8; // 584 patch pixels
+constexpr int kSlots = (kGroups + kWaves - 1) / kWaves;  // 19 DMA slots per wave
+constexpr int kStage = kGroups * 1024;
+constexpr uint32_t kOob = 0x80000000u;  // buffer offset past num_records: reads zeros
+
+struct Conv3x3Args {
+  const void* x;
+  const void* w;  // [64][576] packed (kh, kw, c)
+  void* out;      // NHWC [n, h, w, 64]
+  const float* bias;
+  const void* residual;
+  int n, h, wd, rows;  // wd: width; rows: output rows per band
+  int bands, tiles;   // bands per image, n * bands
+  int pw, npix;       // patch width w + 2, patch pixels (rows + 2) * pw
+  uint32_t pw_magic;  // pix / pw == (pix * pw_magic) >> 20 for pix < kMaxPatch (checked on the host)
+  int relu;
+  int x_bytes;
+};
+
+// Calls f(integral_constant<0>) ... f(<N - 1>): indices that are constants
+// before unrolling, so register arrays indexed by them stay in registers.
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <bool F16>
+struct Frag {
+  typedef typename std::conditional<F16, f16x8, bf16x8>::type vec;
+  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+    if constexpr (F16) return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+// s_waitcnt vmcnt(N), lgkmcnt/expcnt unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <bool F16>
+__device__ __forceinline__ float to_f32(uint32_t bits) {
+  if constexpr (F16) return f16_bits_to_f32(static_cast<uint16_t>(bits));
+  else return bf16_bits_to_f32(static_cast<uint16_t>(bits));
+}
+template <bool F16>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  if constexpr (F16) return f32x2_to_f16x2_bits(lo, hi);
+  else return f32x2_to_bf16x2_bits(lo, hi);
+}
+
+template <typename T, bool F16>
+__global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p) {
+  typedef typename Frag<F16>::vec vec;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStage];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int W = p.wd, H = p.h, pw = p.pw;
+
+  // This wave's weights: output channel nb + 16 j + l16, K chunk 4 s + lg.
+  vec bw[kTN][18];
+  {
+    const T* w = static_cast<const T*>(p.w);
+#pragma unroll
+    for (int j = 0; j < kTN; ++j)
+#pragma unroll
+      for (int s = 0; s < 18; ++s)
+        bw[j][s] = *reinterpret_cast<const vec*>(w + (wn * 32 + 16 * j + l16) * kK + s * 32 + lg * 8);
+  }
+
+  // DMA slot j of this wave moves patch pixels 8 g .. 8 g + 7, g = wave + 4 j;
+  // a lane moves one 16-byte chunk of pixel 8 g + (lane >> 3).
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.x), 0, p.x_bytes, 0x00020000);
+  const int chunk = (lane & 7) ^ (lane >> 3);  // logical 16-byte chunk stored at physical chunk lane & 7
+  auto issue = [&](int t, int buf) {
+    const int img = t / p.bands, h0 = (t - img * p.bands) * p.rows;
+    const int img_base = img * H;
+    // Opaque per call: keeps the compiler from hoisting 19 slots' worth of
+    // loop-invariant address math out of the tile loop (it would spill it).
+    int lsub = lane >> 3, lchunk = chunk;
+    asm volatile("" : "+v"(lsub), "+v"(lchunk));
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+      const int g = wave + kWaves * j;
+      if (g < kGroups) {
+        const int pix = g * 8 + lsub;
+        const int pr = static_cast<int>((static_cast<uint32_t>(pix) * p.pw_magic) >> 20);
+        const int hi = h0 - 1 + pr, wi = pix - pr * pw - 1;
+        uint32_t voff = kOob;
+        if (pix < p.npix && static_cast<unsigned>(hi) < static_cast<unsigned>(H) &&
+            static_cast<unsigned>(wi) < static_cast<unsigned>(W))
+          voff = static_cast<uint32_t>(((img_base + hi) * W + wi) * (kC * 2) + lchunk * 16);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(smem + buf * kStage + g * 1024), 16, voff, 0, 0, 0);
+      }
+    }
+  };
+
+  // Patch index of output pixel q = wm * 224 + 16 i + l16 of the band at tap
+  // (0, 0); pixels past the band (a band shorter than 448 pixels) read the
+  // band's last pixel and are never stored.
+  int p0[kTM];
+  const int band_pix = p.rows * W;
+#pragma unroll
+  for (int i = 0; i < kTM; ++i) {
+    const int q = min(wm * kWavePix + 16 * i + l16, band_pix - 1);
+    const int r = q / W;
+    p0[i] = r * pw + (q - r * W);
+  }
+
+  // out and residual have x's extent (NHWC, 64 channels): below 2^31 bytes.
+  const __amdgpu_buffer_rsrc_t rs_out = __builtin_amdgcn_make_buffer_rsrc(p.out, 0, p.x_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_res =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.residual), 0, p.x_bytes, 0x00020000);
+  float bias[kTN][4];
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    const int n = wn * 32 + 16 * j + 4 * lg;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bias[j][r] = p.bias ? p.bias[n + r] : 0.0f;
+  }
+  // Retire the weight and bias loads before the band loop.  Left pending,
+  // the compiler's wait insertion merges them into the loop header's state
+  // and emits a vmcnt wait before every weight use in every band, which
+  // also waits for the next band's patch DMA and serializes it with the MFMAs.
+  wait_vm<0>();
+
+  int t = blockIdx.x;
+  if (t < p.tiles) issue(t, 0);
+  int buf = 0;
+
+  for (bool first = true; t < p.tiles; t += gridDim.x, first = false) {
+    // This wave's DMAs of band t are complete (vector-memory operations
+    // retire in issue order; the only later ones are the previous band's
+    // kTM * kTN stores, which may stay in flight); the barrier makes every
+    // wave's complete and retires all reads of the other stage.
+    if (first) wait_vm<0>();
+    else wait_vm<kTM * kTN>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (t + static_cast<int>(gridDim.x) < p.tiles) issue(t + gridDim.x, buf ^ 1);
+
+    const uint8_t* base = smem + buf * kStage;
+    // Likewise for the 252 LDS addresses derived from p0 (14 fragments x 18
+    // K steps): recomputed per tile, a few VALU per read.
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) asm volatile("" : "+v"(p0[i]));
+    f32x4 acc[kTM][kTN];
+#pragma unroll
+    for (int i = 0; i < kTM; ++i)
+#pragma unroll
+      for (int j = 0; j < kTN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // 36 sub-steps u = (tap, ks, half): tap u / 4, K chunks 4 ks .. 4 ks + 3
+    // with ks = (u / 2) & 1, pixel row tiles 7 half .. 7 half + 6.  Each
+    // sub-step's 7 A fragments are read from LDS one sub-step ahead, and a
+    // scheduling barrier between sub-steps keeps the compiler from hoisting
+    // more reads (the weights already hold 144 VGPRs).
+    vec av[2][kTM / 2];
+    auto load_a = [&](auto uc, vec (&dst)[kTM / 2]) {
+      constexpr int u = decltype(uc)::value;
+      constexpr int tap = u / 4, ks = (u / 2) & 1, half = u & 1;
+      const int toff = (tap / 3) * pw + (tap % 3);
+#pragma unroll
+      for (int i = 0; i < kTM / 2; ++i) {
+        const int pp = p0[half * (kTM / 2) + i] + toff;
+        dst[i] = *reinterpret_cast<const vec*>(base + pp * 128 + ((((ks << 2) + lg) ^ (pp & 7)) << 4));
+      }
+    };
+    load_a(std::integral_constant<int, 0>{}, av[0]);
+    static_for<36>([&](auto uc) {
+      constexpr int u = decltype(uc)::value;
+      constexpr int tap = u / 4, ks = (u / 2) & 1, half = u & 1;
+      if constexpr (u + 1 < 36) load_a(std::integral_constant<int, u + 1>{}, av[(u + 1) & 1]);
+#pragma unroll
+      for (int i = 0; i < kTM / 2; ++i)
+#pragma unroll
+        for (int j = 0; j < kTN; ++j)
+          acc[half * (kTM / 2) + i][j] = Frag<F16>::mma(bw[j][tap * 2 + ks], av[u & 1][i], acc[half * (kTM / 2) + i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+
+    // Epilogue from the C^T accumulators: acc[i][j][r] is output pixel
+    // q = wm * 224 + 16 i + l16 of the band, channel wn * 32 + 16 j + 4 lg + r.
+    // Buffer loads and stores at 32-bit byte offsets: rows past the band get
+    // an offset past num_records (loads read zeros, stores are dropped), so
+    // every wave issues exactly kTM * kTN stores per band (the wait at the
+    // top of the loop counts them).  All residual loads are issued before
+    // the first store: out and residual may alias, so loads placed after a
+    // store would each wait for a full memory round trip.
+    const int img = t / p.bands, h0 = (t - img * p.bands) * p.rows;
+    const int valid = min(p.rows, H - h0) * W;
+    const uint32_t band_off = static_cast<uint32_t>((img * H + h0) * W) * (kO * 2);
+    const uint32_t col_off = static_cast<uint32_t>(wn * 32 + 4 * lg) * 2;
+    uint32_t roff[kTM];
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+      const int q = wm * kWavePix + 16 * i + l16;
+      roff[i] = q < valid ? band_off + static_cast<uint32_t>(q) * (kO * 2) + col_off : kOob;
+    }
+    i32x2 rraw[kTM][kTN];
+    if (p.residual) {
+#pragma unroll
+      for (int i = 0; i < kTM; ++i)
+#pragma unroll
+        for (int j = 0; j < kTN; ++j) rraw[i][j] = __builtin_amdgcn_raw_buffer_load_b64(rs_res, roff[i] + 32 * j, 0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kTM; ++i)
+#pragma unroll
+        for (int j = 0; j < kTN; ++j) rraw[i][j] = i32x2{0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < kTM; ++i)
+#pragma unroll
+      for (int j = 0; j < kTN; ++j) {
+        const uint32_t r01 = static_cast<uint32_t>(rraw[i][j][0]), r23 = static_cast<uint32_t>(rraw[i][j][1]);
+        const float res[4] = {to_f32<F16>(r01 & 0xffffu), to_f32<F16>(r01 >> 16), to_f32<F16>(r23 & 0xffffu),
+                              to_f32<F16>(r23 >> 16)};
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float s = (acc[i][j][r] + bias[j][r]) + res[r];
+          v[r] = p.relu ? fmaxf(s, 0.0f) : s;
+        }
+        const i32x2 packed{static_cast<int>(pack2<F16>(v[0], v[1])), static_cast<int>(pack2<F16>(v[2], v[3]))};
+        __builtin_amdgcn_raw_buffer_store_b64(packed, rs_out, roff[i] + 32 * j, 0, 0);
+      }
+    buf ^= 1;
+  }
+}
+
+// Output rows per band: as many full rows as fit 448 pixels, fewer when the
+// halo patch would exceed the 584 pixels of a stage.
+int band_rows(int h, int w) {
+  int r = kTilePix / w;
+  if (r > h) r = h;
+  while (r > 0 && (r + 2) * (w + 2) > kMaxPatch) --r;
+  return r;
+}
+
+int device_cu_count() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
+}  // namespace
+
+// Launches the band kernel when the convolution is one it covers and sets
+// *handled; otherwise leaves *handled false and launches nothing.
+int conv3x3_c64_launch(const c3h_conv_args* a, hipStream_t s, bool* handled) {
+  *handled = false;
+  if (getenv("C3H_DISABLE_CONV3X3")) return C3H_OK;
+  const c3h_epilogue& e = a->epi;
+  const bool shape = (a->in_dtype == C3H_BF16 || a->in_dtype == C3H_F16) && a->out_dtype == a->in_dtype &&
+                     a->kh == 3 && a->kw == 3 && a->sh == 1 && a->sw == 1 && a->dh == 1 && a->dw == 1 &&
+                     a->pad_top == 1 && a->pad_left == 1 && a->ho == a->h && a->wo == a->w_ && a->c == kC &&
+                     a->c_pack == kC && a->c_stride == kC && a->o == kO && a->out_layout == 1 && a->n >= 1;
+  const bool epi = e.alpha == 1.0f && e.beta == 1.0f && (e.bias_mode == 0 || e.bias_mode == 2) && e.act <= 1 &&
+                   e.n_inst == 0 && (e.bias_mode == 0 || (reinterpret_cast<uintptr_t>(e.bias) & 15) == 0) &&
+                   (reinterpret_cast<uintptr_t>(e.residual) & 7) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 7) == 0 &&
+                   (reinterpret_cast<uintptr_t>(a->x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->w) & 15) == 0;
+  if (!shape || !epi) return C3H_OK;
+  const int64_t x_bytes = static_cast<int64_t>(a->n) * a->h * a->w_ * kC * 2;
+  if (x_bytes >= (int64_t{1} << 31) - 16) return C3H_OK;
+  const int rows = band_rows(a->h, a->w_);
+  if (rows < 1) return C3H_OK;
+  Conv3x3Args p;
+  p.x = a->x;
+  p.w = a->w;
+  p.out = a->out;
+  p.bias = e.bias_mode == 2 ? static_cast<const float*>(e.bias) : nullptr;
+  p.residual = e.residual;
+  p.n = a->n;
+  p.h = a->h;
+  p.wd = a->w_;
+  p.rows = rows;
+  p.bands = static_cast<int>(ceil_div(a->h, rows));
+  p.tiles = a->n * p.bands;
+  p.pw = a->w_ + 2;
+  p.npix = (rows + 2) * p.pw;
+  p.pw_magic = static_cast<uint32_t>(((1u << 20) + p.pw - 1) / p.pw);
+  for (int pix = 0; pix < kMaxPatch; ++pix)
+    C3H_REQUIRE(static_cast<int>((static_cast<uint32_t>(pix) * p.pw_magic) >> 20) == pix / p.pw,
+                "conv3x3: patch-width reciprocal inexact for width %d", a->w_);
+  p.relu = e.act == 1;
+  p.x_bytes = static_cast<int>(x_bytes);
+  const int grid = p.tiles < device_cu_count() ? p.tiles : device_cu_count();
+  if (a->in_dtype == C3H_BF16)
+    hipLaunchKernelGGL((conv3x3_c64_kernel<bf16_t, false>), dim3(grid), dim3(kWaves * 64), 0, s, p);
+  else
+    hipLaunchKernelGGL((conv3x3_c64_kernel<f16_t, true>), dim3(grid), dim3(kWaves * 64), 0, s, p);
+  *handled = true;
+  return launch_status("conv3x3_c64");
+}
+
+}  // namespace c3h

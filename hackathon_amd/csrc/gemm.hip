@@ -1874,6 +1874,9 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
       p.k = static_cast<int64_t>(a->kh) * a->kw * a->c_pack;
       p.ldb = ceil_div(p.k, 32) * 32;  // weights padded to whole 32-wide K tiles
       p.b_bytes = static_cast<int64_t>(a->o) * p.ldb * 2;
+      bool handled = false;
+      rc = conv3x3_c64_launch(a, s, &handled);
+      if (handled || rc) return rc;
       // A 64-wide K tile stays inside one filter tap when c_pack % 64 == 0.
       if (a->c_pack % 64 == 0) return launch_h_any<kConvTap>(p, 1, s, a->in_dtype);
       return launch_h_any<kConv>(p, 1, s, a->in_dtype);

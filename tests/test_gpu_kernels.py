@@ -762,3 +762,67 @@ def test_gemm_fp8_big_tile_matches_128_tiles(gpu):
     np.testing.assert_array_equal(big, small)
     rows = np.arange(0, m, 61)
     np.testing.assert_array_equal(big[rows], (F8.decode(qa[rows]).astype(np.float64) @ F8.decode(qb).astype(np.float64).T).astype(np.float32))
+
+
+@pytest.mark.parametrize("kind,n,h,w,resid,act,bias", [
+    ("bf16", 256, 56, 56, True, 1, True),    # ResNet-18 224 layer 1, second conv of a block
+    ("bf16", 256, 56, 56, False, 1, True),   # first conv of a block
+    ("fp16", 3, 13, 10, True, 1, True),      # ragged last band (13 rows, 44 per band)
+    ("bf16", 2, 9, 62, False, 0, False),     # wide rows, no bias, no ReLU
+    ("fp16", 1, 1, 5, True, 0, True),        # one output row
+    ("bf16", 5, 20, 100, True, 1, True),     # halo-limited band (3 rows of 100)
+])
+def test_conv3x3_band_kernel_matches_implicit_gemm(gpu, kind, n, h, w, resid, act, bias):
+    """The banded 3x3 / 64-channel kernel (conv3x3.hip) against the generic
+    implicit-GEMM path (C3H_DISABLE_CONV3X3) on the same inputs: bit-identical
+    (same K order and epilogue arithmetic), output zero-filled before each
+    run; plus a float64 spot check of the rounded operands."""
+    import os
+
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    rng = np.random.default_rng(n * 1000 + h * 10 + w)
+    c = o = 64
+    x32 = rng.standard_normal((n, h, w, c)).astype(np.float32)
+    w32 = (rng.standard_normal((o, 3, 3, c)) * 0.06).astype(np.float32)
+    xb, xv = _bits(x32, kind)
+    wb, wv = _bits(w32.reshape(o, -1), kind)
+    b32 = rng.standard_normal(o).astype(np.float32)
+    r32 = rng.standard_normal((n, h, w, o)).astype(np.float32)
+    rb, rv = _bits(r32, kind)
+    code, sdt = (_lib.BF16, BF16) if kind == "bf16" else (_lib.F16, np.float16)
+    xd, wd, bd, rd = _dev(xb), _dev(wb), _dev(b32), _dev(rb)
+    out = DeviceArray.empty((n, h, w, o), sdt)
+    zeros = np.zeros((n, h, w, o), dtype=np.uint16)
+
+    def launch(disable):
+        out.copy_from_host(zeros)
+        a = _lib.ConvArgs()
+        a.x, a.w, a.out = xd.ptr, wd.ptr, out.ptr
+        a.n, a.c, a.h, a.w_, a.c_stride, a.c_pack, a.o = n, c, h, w, c, c, o
+        a.kh, a.kw, a.sh, a.sw, a.pad_top, a.pad_left, a.dh, a.dw, a.ho, a.wo = 3, 3, 1, 1, 1, 1, 1, 1, h, w
+        a.out_layout, a.in_dtype, a.out_dtype = 1, code, code
+        a.epi = E.epilogue(bias=bd if bias else None, bias_mode=2 if bias else 0, act=act,
+                           residual=rd if resid else None)
+        if disable:
+            os.environ["C3H_DISABLE_CONV3X3"] = "1"
+        try:
+            print(f"conv3x3 {kind} n={n} h={h} w={w} resid={resid} act={act} bias={bias} generic={disable}", flush=True)
+            _lib.launch(a, None)
+            return out.get().copy()
+        finally:
+            os.environ.pop("C3H_DISABLE_CONV3X3", None)
+
+    band = launch(False)
+    generic = launch(True)
+    np.testing.assert_array_equal(band.view(np.uint16), generic.view(np.uint16))
+    got = _from16(band, kind)
+    xp = np.pad(xv.astype(np.float64), ((0, 0), (1, 1), (1, 1), (0, 0)))
+    wv4 = wv.astype(np.float64).reshape(o, 3, 3, c)
+    for (b_, y, x_) in [(0, 0, 0), (n - 1, h - 1, w - 1), (n // 2, h // 2, w // 3), (0, h - 1, 0)]:
+        t = np.einsum("hwc,ohwc->o", xp[b_, y:y + 3, x_:x_ + 3, :], wv4)
+        t = t + (b32 if bias else 0) + (rv[b_, y, x_] if resid else 0)
+        want = np.maximum(t, 0) if act == 1 else t
+        np.testing.assert_allclose(got[b_, y, x_], want, rtol=1e-2, atol=4e-2)
