@@ -6,18 +6,23 @@
 // The implicit-GEMM kernels (gemm.hip) gather each input pixel once per
 // filter tap, so the 3x3 layer moves 9x its input through L2 -> LDS, and
 // with N = 64 output channels every LDS byte feeds few MFMAs.  Here:
-//   * a tile is a band of R full output rows of one image (R * W <= 448
+//   * a tile is a band of R full output rows of one image (R * W <= 224
 //     pixels); its (R + 2) x (W + 2) input patch, halo and zero padding
 //     included, is brought into LDS once by buffer_load ... lds (out-of-image
 //     pixels read zeros) and all nine taps read it from there;
-//   * the block is persistent (one per CU, 148 KB of LDS: two patch stages),
-//     and the next band's patch is in flight while the current one is
-//     multiplied;
+//   * the band's residual (one contiguous NHWC range) rides in the same
+//     stage, so the epilogue reads it from LDS;
+//   * the block is persistent (one per CU, 148 KB of LDS: two stages) and
+//     walks a contiguous range of bands, so the next band's patch and
+//     residual are in flight while the current one is multiplied, and the
+//     two halo rows bands share were just fetched into this XCD's L2;
 //   * each of the 4 waves (one per SIMD, so the accumulators can live in
 //     AGPRs beside 144 VGPRs of weights) keeps its 32 output channels'
 //     weights (all K = 576) in registers as 36 MFMA fragments, loaded once
-//     per block; waves are 2 (pixels) x 2 (channels), 224 pixels x 32
-//     channels each, so every A fragment read from LDS feeds two MFMAs.
+//     per block; waves are 2 (pixels) x 2 (channels), 112 pixels x 32
+//     channels each, so every A fragment read from LDS feeds two MFMAs;
+//   * a band's kTM * kTN output stores per wave stay in flight while the
+//     next band is multiplied.
 // The K order (tap-major, then channel chunks 0-31 and 32-63 with lane group
 // g supplying chunk g) and the epilogue arithmetic ((acc + bias) + residual,
 // then max 0) are those of the tap-uniform implicit-GEMM kernel, so the
@@ -39,13 +44,15 @@ typedef __attribute__((address_space(3))) void* lds_void_ptr;
 constexpr int kC = 64;                 // input channels: one tap = one 128-byte pixel row
 constexpr int kO = 64;                 // output channels
 constexpr int kK = 9 * kC;             // 576
-constexpr int kTilePix = 448;          // output pixels per band (28 MFMA row tiles)
+constexpr int kTilePix = 224;          // output pixels per band (14 MFMA row tiles)
 constexpr int kWaves = 4;              // 2 (pixels) x 2 (channels)
-constexpr int kWavePix = kTilePix / 2; // 224 = 14 row tiles
-constexpr int kTM = kWavePix / 16;     // 14
+constexpr int kWavePix = kTilePix / 2; // 112 = 7 row tiles
+constexpr int kTM = kWavePix / 16;     // 7
 constexpr int kTN = 2;                 // 32 channels per wave
-constexpr int kGroups = 73;            // DMA groups of 8 patch pixels per stage
-constexpr int kMaxPatch = kGroups * 8; // 584 patch pixels
+constexpr int kPatchGroups = 46;                         // DMA groups of 8 patch pixels
+constexpr int kMaxPatch = kPatchGroups * 8;              // 368 patch pixels
+constexpr int kResGroups = kTilePix / 8;                 // 28 groups of 8 residual pixels
+constexpr int kGroups = kPatchGroups + kResGroups;       // 74 KB per stage
 constexpr int kSlots = (kGroups + kWaves - 1) / kWaves;  // 19 DMA slots per wave
 constexpr int kStage = kGroups * 1024;
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset past num_records: reads zeros
@@ -60,6 +67,7 @@ struct Conv3x3Args {
   int bands, tiles;   // bands per image, n * bands
   int pw, npix;       // patch width w + 2, patch pixels (rows + 2) * pw
   uint32_t pw_magic;  // pix / pw == (pix * pw_magic) >> 20 for pix < kMaxPatch (checked on the host)
+  int band_pix;       // rows * w
   int relu;
   int x_bytes;
 };
@@ -127,9 +135,15 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
   // a lane moves one 16-byte chunk of pixel 8 g + (lane >> 3).
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.x), 0, p.x_bytes, 0x00020000);
   const int chunk = (lane & 7) ^ (lane >> 3);  // logical 16-byte chunk stored at physical chunk lane & 7
+  // out and residual have x's extent (NHWC, 64 channels): below 2^31 bytes.
+  const __amdgpu_buffer_rsrc_t rs_out = __builtin_amdgcn_make_buffer_rsrc(p.out, 0, p.x_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_res =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.residual), 0, p.x_bytes, 0x00020000);
   auto issue = [&](int t, int buf) {
     const int img = t / p.bands, h0 = (t - img * p.bands) * p.rows;
     const int img_base = img * H;
+    const int valid = min(p.rows, H - h0) * W;
+    const uint32_t band_off = static_cast<uint32_t>((img_base + h0) * W) * (kO * 2);
     // Opaque per call: keeps the compiler from hoisting 19 slots' worth of
     // loop-invariant address math out of the tile loop (it would spill it).
     int lsub = lane >> 3, lchunk = chunk;
@@ -137,7 +151,8 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
 #pragma unroll
     for (int j = 0; j < kSlots; ++j) {
       const int g = wave + kWaves * j;
-      if (g < kGroups) {
+      uint8_t* dst = smem + buf * kStage + g * 1024;
+      if (g < kPatchGroups) {
         const int pix = g * 8 + lsub;
         const int pr = static_cast<int>((static_cast<uint32_t>(pix) * p.pw_magic) >> 20);
         const int hi = h0 - 1 + pr, wi = pix - pr * pw - 1;
@@ -145,16 +160,21 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
         if (pix < p.npix && static_cast<unsigned>(hi) < static_cast<unsigned>(H) &&
             static_cast<unsigned>(wi) < static_cast<unsigned>(W))
           voff = static_cast<uint32_t>(((img_base + hi) * W + wi) * (kC * 2) + lchunk * 16);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)(smem + buf * kStage + g * 1024), 16, voff, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)dst, 16, voff, 0, 0, 0);
+      } else if (g < kGroups && p.residual) {
+        // residual pixel q of the band, chunks swizzled as in the patch
+        const int q = (g - kPatchGroups) * 8 + lsub;
+        const uint32_t voff = q < valid ? band_off + static_cast<uint32_t>(q) * (kO * 2) + lchunk * 16 : kOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_res, (lds_void_ptr)dst, 16, voff, 0, 0, 0);
       }
     }
   };
 
-  // Patch index of output pixel q = wm * 224 + 16 i + l16 of the band at tap
-  // (0, 0); pixels past the band (a band shorter than 448 pixels) read the
+  // Patch index of output pixel q = wm * 112 + 16 i + l16 of the band at tap
+  // (0, 0); pixels past the band (a band shorter than 224 pixels) read the
   // band's last pixel and are never stored.
   int p0[kTM];
-  const int band_pix = p.rows * W;
+  const int band_pix = p.band_pix;
 #pragma unroll
   for (int i = 0; i < kTM; ++i) {
     const int q = min(wm * kWavePix + 16 * i + l16, band_pix - 1);
@@ -162,10 +182,6 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
     p0[i] = r * pw + (q - r * W);
   }
 
-  // out and residual have x's extent (NHWC, 64 channels): below 2^31 bytes.
-  const __amdgpu_buffer_rsrc_t rs_out = __builtin_amdgcn_make_buffer_rsrc(p.out, 0, p.x_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rs_res =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.residual), 0, p.x_bytes, 0x00020000);
   float bias[kTN][4];
 #pragma unroll
   for (int j = 0; j < kTN; ++j) {
@@ -179,11 +195,14 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
   // also waits for the next band's patch DMA and serializes it with the MFMAs.
   wait_vm<0>();
 
-  int t = blockIdx.x;
-  if (t < p.tiles) issue(t, 0);
+  // Bands [t_begin, t_end) of this block: a contiguous, balanced range.
+  const int t_begin = static_cast<int>(static_cast<int64_t>(blockIdx.x) * p.tiles / gridDim.x);
+  const int t_end = static_cast<int>(static_cast<int64_t>(blockIdx.x + 1) * p.tiles / gridDim.x);
+  int t = t_begin;
+  if (t < t_end) issue(t, 0);
   int buf = 0;
 
-  for (bool first = true; t < p.tiles; t += gridDim.x, first = false) {
+  for (bool first = true; t < t_end; ++t, first = false) {
     // This wave's DMAs of band t are complete (vector-memory operations
     // retire in issue order; the only later ones are the previous band's
     // kTM * kTN stores, which may stay in flight); the barrier makes every
@@ -193,10 +212,10 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (t + static_cast<int>(gridDim.x) < p.tiles) issue(t + gridDim.x, buf ^ 1);
+    if (t + 1 < t_end) issue(t + 1, buf ^ 1);
 
     const uint8_t* base = smem + buf * kStage;
-    // Likewise for the 252 LDS addresses derived from p0 (14 fragments x 18
+    // Likewise for the 126 LDS addresses derived from p0 (7 fragments x 18
     // K steps): recomputed per tile, a few VALU per read.
 #pragma unroll
     for (int i = 0; i < kTM; ++i) asm volatile("" : "+v"(p0[i]));
@@ -205,43 +224,39 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
     for (int i = 0; i < kTM; ++i)
 #pragma unroll
       for (int j = 0; j < kTN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // 36 sub-steps u = (tap, ks, half): tap u / 4, K chunks 4 ks .. 4 ks + 3
-    // with ks = (u / 2) & 1, pixel row tiles 7 half .. 7 half + 6.  Each
-    // sub-step's 7 A fragments are read from LDS one sub-step ahead, and a
-    // scheduling barrier between sub-steps keeps the compiler from hoisting
-    // more reads (the weights already hold 144 VGPRs).
-    vec av[2][kTM / 2];
-    auto load_a = [&](auto uc, vec (&dst)[kTM / 2]) {
+    // 18 sub-steps u = (tap, ks): tap u / 2, K chunks 4 ks .. 4 ks + 3 with
+    // ks = u & 1.  Each sub-step's 7 A fragments are read from LDS one
+    // sub-step ahead, and a scheduling barrier between sub-steps keeps the
+    // compiler from hoisting more reads (the weights hold 144 registers).
+    vec av[2][kTM];
+    auto load_a = [&](auto uc, vec (&dst)[kTM]) {
       constexpr int u = decltype(uc)::value;
-      constexpr int tap = u / 4, ks = (u / 2) & 1, half = u & 1;
+      constexpr int tap = u / 2, ks = u & 1;
       const int toff = (tap / 3) * pw + (tap % 3);
 #pragma unroll
-      for (int i = 0; i < kTM / 2; ++i) {
-        const int pp = p0[half * (kTM / 2) + i] + toff;
+      for (int i = 0; i < kTM; ++i) {
+        const int pp = p0[i] + toff;
         dst[i] = *reinterpret_cast<const vec*>(base + pp * 128 + ((((ks << 2) + lg) ^ (pp & 7)) << 4));
       }
     };
     load_a(std::integral_constant<int, 0>{}, av[0]);
-    static_for<36>([&](auto uc) {
+    static_for<18>([&](auto uc) {
       constexpr int u = decltype(uc)::value;
-      constexpr int tap = u / 4, ks = (u / 2) & 1, half = u & 1;
-      if constexpr (u + 1 < 36) load_a(std::integral_constant<int, u + 1>{}, av[(u + 1) & 1]);
+      if constexpr (u + 1 < 18) load_a(std::integral_constant<int, u + 1>{}, av[(u + 1) & 1]);
 #pragma unroll
-      for (int i = 0; i < kTM / 2; ++i)
+      for (int i = 0; i < kTM; ++i)
 #pragma unroll
-        for (int j = 0; j < kTN; ++j)
-          acc[half * (kTM / 2) + i][j] = Frag<F16>::mma(bw[j][tap * 2 + ks], av[u & 1][i], acc[half * (kTM / 2) + i][j]);
+        for (int j = 0; j < kTN; ++j) acc[i][j] = Frag<F16>::mma(bw[j][u], av[u & 1][i], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
     });
 
     // Epilogue from the C^T accumulators: acc[i][j][r] is output pixel
-    // q = wm * 224 + 16 i + l16 of the band, channel wn * 32 + 16 j + 4 lg + r.
-    // Buffer loads and stores at 32-bit byte offsets: rows past the band get
-    // an offset past num_records (loads read zeros, stores are dropped), so
-    // every wave issues exactly kTM * kTN stores per band (the wait at the
-    // top of the loop counts them).  All residual loads are issued before
-    // the first store: out and residual may alias, so loads placed after a
-    // store would each wait for a full memory round trip.
+    // q = wm * 112 + 16 i + l16 of the band, channel wn * 32 + 16 j + 4 lg + r.
+    // The residual comes from this stage's LDS copy (zeros past the band).
+    // Stores are buffer stores at 32-bit byte offsets: rows past the band get
+    // an offset past num_records and are dropped, so every wave issues
+    // exactly kTM * kTN stores per band (the wait at the top of the loop
+    // counts them).
     const int img = t / p.bands, h0 = (t - img * p.bands) * p.rows;
     const int valid = min(p.rows, H - h0) * W;
     const uint32_t band_off = static_cast<uint32_t>((img * H + h0) * W) * (kO * 2);
@@ -254,10 +269,16 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
     }
     i32x2 rraw[kTM][kTN];
     if (p.residual) {
+      const uint8_t* rbase = base + kPatchGroups * 1024;
 #pragma unroll
-      for (int i = 0; i < kTM; ++i)
+      for (int i = 0; i < kTM; ++i) {
+        const int q = wm * kWavePix + 16 * i + l16;
 #pragma unroll
-        for (int j = 0; j < kTN; ++j) rraw[i][j] = __builtin_amdgcn_raw_buffer_load_b64(rs_res, roff[i] + 32 * j, 0, 0);
+        for (int j = 0; j < kTN; ++j) {
+          const int c = wn * 4 + 2 * j + (lg >> 1);  // logical 16-byte chunk of channels wn*32+16j+4lg..+3
+          rraw[i][j] = *reinterpret_cast<const i32x2*>(rbase + q * 128 + ((c ^ (q & 7)) << 4) + (lg & 1) * 8);
+        }
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < kTM; ++i)
@@ -284,8 +305,8 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
   }
 }
 
-// Output rows per band: as many full rows as fit 448 pixels, fewer when the
-// halo patch would exceed the 584 pixels of a stage.
+// Output rows per band: as many full rows as fit 224 pixels, fewer when the
+// halo patch would exceed the 368 pixels of a stage.
 int band_rows(int h, int w) {
   int r = kTilePix / w;
   if (r > h) r = h;
@@ -337,6 +358,7 @@ int conv3x3_c64_launch(const c3h_conv_args* a, hipStream_t s, bool* handled) {
   p.pw = a->w_ + 2;
   p.npix = (rows + 2) * p.pw;
   p.pw_magic = static_cast<uint32_t>(((1u << 20) + p.pw - 1) / p.pw);
+  p.band_pix = rows * a->w_;
   for (int pix = 0; pix < kMaxPatch; ++pix)
     C3H_REQUIRE(static_cast<int>((static_cast<uint32_t>(pix) * p.pw_magic) >> 20) == pix / p.pw,
                 "conv3x3: patch-width reciprocal inexact for width %d", a->w_);
