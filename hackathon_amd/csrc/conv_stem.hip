@@ -132,6 +132,11 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int r = 0; r < 4; ++r) bv[j][r] = bias ? bias[16 * j + 4 * lg + r] : 0.0f;
+  // Retire the weight and bias loads here (s_waitcnt vmcnt(0)).  Left
+  // pending, the compiler's wait insertion carries them into the tile loop's
+  // header state and waits on vmcnt before the MFMAs of every tile, which
+  // also waits for the next tile's prefetch and serializes it with the MFMAs.
+  __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));
   // Packed column kw = 7 only pads the filter: zero its half of the patch
   // operand so that non-finite inputs there cannot turn 0 * x into NaN.
   const uint32_t kw7_mask = lg == 3 ? 0u : 0xffffffffu;
@@ -177,7 +182,10 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
       const uint32_t off = ok ? static_cast<uint32_t>((hi * g.w + wi) * static_cast<int>(sizeof(TI))) : kOob;
 #pragma unroll
       for (int ch = 0; ch < 3; ++ch)
-        pre[s][ch] = In<TI>::load(rs, (ok && ch < g.c) ? off + ch * plane_bytes : kOob);
+        // Out-of-range loads get distinct offsets past the buffer (each reads
+        // zero): identical ones are merged by the compiler into one load plus
+        // copies that must wait for it, a vmcnt(0) stall in every fetch.
+        pre[s][ch] = In<TI>::load(rs, (ok && ch < g.c) ? off + ch * plane_bytes : kOob + 4 * ch);
     }
   };
   auto stash = [&]() {
