@@ -228,7 +228,7 @@ def _traffic_summary(fetch_dir: str, write_dir: str, meta_path: str) -> int:
     for counter, run_dir in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         rows = _pmc_rows(run_dir, counter)
         copy = [v for k, v in rows if "strided_copy_kernel" in k]
-        conv = [v for k, v in rows if "mfma_gemm" in k or "conv_stem_pool" in k]
+        conv = [v for k, v in rows if "mfma_gemm" in k or "conv_stem_pool" in k or "conv3x3_c64" in k]
         if len(copy) != meta["copy_dispatches"] or len(conv) != len(launches) * meta["replays"]:
             raise ValueError(f"{counter}: {len(copy)} copy / {len(conv)} conv dispatches, expected "
                              f"{meta['copy_dispatches']} / {len(launches) * meta['replays']}")
