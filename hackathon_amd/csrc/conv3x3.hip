@@ -6,23 +6,23 @@
 // The implicit-GEMM kernels (gemm.hip) gather each input pixel once per
 // filter tap, so the 3x3 layer moves 9x its input through L2 -> LDS, and
 // with N = 64 output channels every LDS byte feeds few MFMAs.  Here:
-//   * a tile is a band of R full output rows of one image (R * W <= 224
-//     pixels); its (R + 2) x (W + 2) input patch, halo and zero padding
-//     included, is brought into LDS once by buffer_load ... lds (out-of-image
-//     pixels read zeros) and all nine taps read it from there;
-//   * the band's residual (one contiguous NHWC range) rides in the same
-//     stage, so the epilogue reads it from LDS;
-//   * the block is persistent (one per CU, 148 KB of LDS: two stages) and
-//     walks a contiguous range of bands, so the next band's patch and
-//     residual are in flight while the current one is multiplied, and the
-//     two halo rows bands share were just fetched into this XCD's L2;
-//   * each of the 4 waves (one per SIMD, so the accumulators can live in
-//     AGPRs beside 144 VGPRs of weights) keeps its 32 output channels'
-//     weights (all K = 576) in registers as 36 MFMA fragments, loaded once
-//     per block; waves are 2 (pixels) x 2 (channels), 112 pixels x 32
-//     channels each, so every A fragment read from LDS feeds two MFMAs;
-//   * a band's kTM * kTN output stores per wave stay in flight while the
-//     next band is multiplied.
+//   * a tile is a band of R full output rows of one image (R * W <= 112
+//     pixels, 2 rows at W = 56); its (R + 2) x (W + 2) input patch, halo and
+//     zero padding included, is brought into LDS once by buffer_load ... lds
+//     (out-of-image pixels read zeros) and all nine taps read it from there;
+//   * blocks are persistent, two per CU (60 KB of LDS each: two patch
+//     stages; at most 256 registers per wave), and walk contiguous ranges
+//     of bands: the next band's patch is in flight while the current one is
+//     multiplied, one block's waits and epilogue overlap the other's MFMAs,
+//     and the halo rows bands share were just fetched into this XCD's L2;
+//   * each of the 4 waves keeps its 32 output channels' weights (all
+//     K = 576) in registers as 36 MFMA fragments, loaded once per block;
+//     waves are 2 (pixels) x 2 (channels), 64 pixels (the band padded to
+//     128) x 32 channels each, so every A fragment read from LDS feeds two
+//     MFMAs;
+//   * the band's residual is loaded into registers before the MFMAs, and a
+//     band's kTM * kTN output stores per wave stay in flight while the next
+//     band is multiplied.
 // The K order (tap-major, then channel chunks 0-31 and 32-63 with lane group
 // g supplying chunk g) and the epilogue arithmetic ((acc + bias) + residual,
 // then max 0) are those of the tap-uniform implicit-GEMM kernel, so the
@@ -44,15 +44,14 @@ typedef __attribute__((address_space(3))) void* lds_void_ptr;
 constexpr int kC = 64;                 // input channels: one tap = one 128-byte pixel row
 constexpr int kO = 64;                 // output channels
 constexpr int kK = 9 * kC;             // 576
-constexpr int kTilePix = 224;          // output pixels per band (14 MFMA row tiles)
+constexpr int kTilePix = 112;          // output pixels per band (7 MFMA row tiles, padded to 8)
 constexpr int kWaves = 4;              // 2 (pixels) x 2 (channels)
-constexpr int kWavePix = kTilePix / 2; // 112 = 7 row tiles
-constexpr int kTM = kWavePix / 16;     // 7
+constexpr int kWavePix = 64;           // 4 row tiles per wave (the band padded to 128 pixels)
+constexpr int kTM = kWavePix / 16;     // 4
 constexpr int kTN = 2;                 // 32 channels per wave
-constexpr int kPatchGroups = 46;                         // DMA groups of 8 patch pixels
-constexpr int kMaxPatch = kPatchGroups * 8;              // 368 patch pixels
-constexpr int kResGroups = kTilePix / 8;                 // 28 groups of 8 residual pixels
-constexpr int kGroups = kPatchGroups + kResGroups;       // 74 KB per stage
+constexpr int kPatchGroups = 30;                         // DMA groups of 8 patch pixels
+constexpr int kMaxPatch = kPatchGroups * 8;              // 240 patch pixels
+constexpr int kGroups = kPatchGroups;                    // 30 KB per stage
 constexpr int kSlots = (kGroups + kWaves - 1) / kWaves;  // 19 DMA slots per wave
 constexpr int kStage = kGroups * 1024;
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset past num_records: reads zeros
@@ -111,7 +110,7 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 }
 
 template <typename T, bool F16>
-__global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p) {
+__global__ void __launch_bounds__(kWaves * 64, 2) conv3x3_c64_kernel(Conv3x3Args p) {
   typedef typename Frag<F16>::vec vec;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kStage];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -142,8 +141,6 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
   auto issue = [&](int t, int buf) {
     const int img = t / p.bands, h0 = (t - img * p.bands) * p.rows;
     const int img_base = img * H;
-    const int valid = min(p.rows, H - h0) * W;
-    const uint32_t band_off = static_cast<uint32_t>((img_base + h0) * W) * (kO * 2);
     // Opaque per call: keeps the compiler from hoisting 19 slots' worth of
     // loop-invariant address math out of the tile loop (it would spill it).
     int lsub = lane >> 3, lchunk = chunk;
@@ -161,18 +158,13 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
             static_cast<unsigned>(wi) < static_cast<unsigned>(W))
           voff = static_cast<uint32_t>(((img_base + hi) * W + wi) * (kC * 2) + lchunk * 16);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)dst, 16, voff, 0, 0, 0);
-      } else if (g < kGroups && p.residual) {
-        // residual pixel q of the band, chunks swizzled as in the patch
-        const int q = (g - kPatchGroups) * 8 + lsub;
-        const uint32_t voff = q < valid ? band_off + static_cast<uint32_t>(q) * (kO * 2) + lchunk * 16 : kOob;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_res, (lds_void_ptr)dst, 16, voff, 0, 0, 0);
       }
     }
   };
 
-  // Patch index of output pixel q = wm * 112 + 16 i + l16 of the band at tap
-  // (0, 0); pixels past the band (a band shorter than 224 pixels) read the
-  // band's last pixel and are never stored.
+  // Patch index of output pixel q = wm * 64 + 16 i + l16 of the band at tap
+  // (0, 0); pixels past the band (the padding to 128, or a band shorter than
+  // 112 pixels) read the band's last pixel and are never stored.
   int p0[kTM];
   const int band_pix = p.band_pix;
 #pragma unroll
@@ -212,6 +204,29 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    // This band's residual, into registers now; used by the epilogue.
+    const int img = t / p.bands, h0 = (t - img * p.bands) * p.rows;
+    const int valid = min(p.rows, H - h0) * W;
+    const uint32_t band_off = static_cast<uint32_t>((img * H + h0) * W) * (kO * 2);
+    const uint32_t col_off = static_cast<uint32_t>(wn * 32 + 4 * lg) * 2;
+    uint32_t roff[kTM];
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+      const int q = wm * kWavePix + 16 * i + l16;
+      roff[i] = q < valid ? band_off + static_cast<uint32_t>(q) * (kO * 2) + col_off : kOob;
+    }
+    i32x2 rraw[kTM][kTN];
+    if (p.residual) {
+#pragma unroll
+      for (int i = 0; i < kTM; ++i)
+#pragma unroll
+        for (int j = 0; j < kTN; ++j) rraw[i][j] = __builtin_amdgcn_raw_buffer_load_b64(rs_res, roff[i] + 32 * j, 0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kTM; ++i)
+#pragma unroll
+        for (int j = 0; j < kTN; ++j) rraw[i][j] = i32x2{0, 0};
+    }
     if (t + 1 < t_end) issue(t + 1, buf ^ 1);
 
     const uint8_t* base = smem + buf * kStage;
@@ -229,15 +244,24 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
     // sub-step ahead, and a scheduling barrier between sub-steps keeps the
     // compiler from hoisting more reads (the weights hold 144 registers).
     vec av[2][kTM];
+    // Byte address of a fragment row's K chunks 4 ks + lg: pp * 128 +
+    // ((4 ks + lg) ^ (pp & 7)) * 16; the ks = 1 address is the ks = 0 one
+    // with bit 6 flipped, so each (tap, fragment) costs one address.
+    uint32_t aaddr[kTM];
     auto load_a = [&](auto uc, vec (&dst)[kTM]) {
       constexpr int u = decltype(uc)::value;
       constexpr int tap = u / 2, ks = u & 1;
-      const int toff = (tap / 3) * pw + (tap % 3);
+      if constexpr (ks == 0) {
+        const int toff = (tap / 3) * pw + (tap % 3);
 #pragma unroll
-      for (int i = 0; i < kTM; ++i) {
-        const int pp = p0[i] + toff;
-        dst[i] = *reinterpret_cast<const vec*>(base + pp * 128 + ((((ks << 2) + lg) ^ (pp & 7)) << 4));
+        for (int i = 0; i < kTM; ++i) {
+          const int pp = p0[i] + toff;
+          aaddr[i] = static_cast<uint32_t>(pp * 128 + ((lg ^ (pp & 7)) << 4));
+        }
       }
+#pragma unroll
+      for (int i = 0; i < kTM; ++i)
+        dst[i] = *reinterpret_cast<const vec*>(base + (ks ? (aaddr[i] ^ 64u) : aaddr[i]));
     };
     load_a(std::integral_constant<int, 0>{}, av[0]);
     static_for<18>([&](auto uc) {
@@ -251,40 +275,12 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
     });
 
     // Epilogue from the C^T accumulators: acc[i][j][r] is output pixel
-    // q = wm * 112 + 16 i + l16 of the band, channel wn * 32 + 16 j + 4 lg + r.
-    // The residual comes from this stage's LDS copy (zeros past the band).
+    // q = wm * 64 + 16 i + l16 of the band, channel wn * 32 + 16 j + 4 lg + r.
+    // The residual was loaded into rraw at the top of the band (zeros past it).
     // Stores are buffer stores at 32-bit byte offsets: rows past the band get
     // an offset past num_records and are dropped, so every wave issues
     // exactly kTM * kTN stores per band (the wait at the top of the loop
     // counts them).
-    const int img = t / p.bands, h0 = (t - img * p.bands) * p.rows;
-    const int valid = min(p.rows, H - h0) * W;
-    const uint32_t band_off = static_cast<uint32_t>((img * H + h0) * W) * (kO * 2);
-    const uint32_t col_off = static_cast<uint32_t>(wn * 32 + 4 * lg) * 2;
-    uint32_t roff[kTM];
-#pragma unroll
-    for (int i = 0; i < kTM; ++i) {
-      const int q = wm * kWavePix + 16 * i + l16;
-      roff[i] = q < valid ? band_off + static_cast<uint32_t>(q) * (kO * 2) + col_off : kOob;
-    }
-    i32x2 rraw[kTM][kTN];
-    if (p.residual) {
-      const uint8_t* rbase = base + kPatchGroups * 1024;
-#pragma unroll
-      for (int i = 0; i < kTM; ++i) {
-        const int q = wm * kWavePix + 16 * i + l16;
-#pragma unroll
-        for (int j = 0; j < kTN; ++j) {
-          const int c = wn * 4 + 2 * j + (lg >> 1);  // logical 16-byte chunk of channels wn*32+16j+4lg..+3
-          rraw[i][j] = *reinterpret_cast<const i32x2*>(rbase + q * 128 + ((c ^ (q & 7)) << 4) + (lg & 1) * 8);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kTM; ++i)
-#pragma unroll
-        for (int j = 0; j < kTN; ++j) rraw[i][j] = i32x2{0, 0};
-    }
 #pragma unroll
     for (int i = 0; i < kTM; ++i)
 #pragma unroll
@@ -305,8 +301,8 @@ __global__ void __launch_bounds__(kWaves * 64) conv3x3_c64_kernel(Conv3x3Args p)
   }
 }
 
-// Output rows per band: as many full rows as fit 224 pixels, fewer when the
-// halo patch would exceed the 368 pixels of a stage.
+// Output rows per band: as many full rows as fit 112 pixels, fewer when the
+// halo patch would exceed the 240 pixels of a stage (0: not covered).
 int band_rows(int h, int w) {
   int r = kTilePix / w;
   if (r > h) r = h;
@@ -364,7 +360,7 @@ int conv3x3_c64_launch(const c3h_conv_args* a, hipStream_t s, bool* handled) {
                 "conv3x3: patch-width reciprocal inexact for width %d", a->w_);
   p.relu = e.act == 1;
   p.x_bytes = static_cast<int>(x_bytes);
-  const int grid = p.tiles < device_cu_count() ? p.tiles : device_cu_count();
+  const int grid = p.tiles < 2 * device_cu_count() ? p.tiles : 2 * device_cu_count();
   if (a->in_dtype == C3H_BF16)
     hipLaunchKernelGGL((conv3x3_c64_kernel<bf16_t, false>), dim3(grid), dim3(kWaves * 64), 0, s, p);
   else

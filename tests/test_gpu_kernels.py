@@ -767,10 +767,11 @@ def test_gemm_fp8_big_tile_matches_128_tiles(gpu):
 @pytest.mark.parametrize("kind,n,h,w,resid,act,bias", [
     ("bf16", 256, 56, 56, True, 1, True),    # ResNet-18 224 layer 1, second conv of a block
     ("bf16", 256, 56, 56, False, 1, True),   # first conv of a block
-    ("fp16", 3, 13, 10, True, 1, True),      # ragged last band (13 rows, 44 per band)
+    ("fp16", 3, 13, 10, True, 1, True),      # ragged last band (13 rows, 11 per band)
     ("bf16", 2, 9, 62, False, 0, False),     # wide rows, no bias, no ReLU
     ("fp16", 1, 1, 5, True, 0, True),        # one output row
-    ("bf16", 5, 20, 100, True, 1, True),     # halo-limited band (1 row of 100)
+    ("bf16", 5, 20, 70, True, 1, True),      # one-row bands (70 wide)
+    ("bf16", 2, 6, 100, True, 1, False),     # too wide for a band: generic path on both sides
 ])
 def test_conv3x3_band_kernel_matches_implicit_gemm(gpu, kind, n, h, w, resid, act, bias):
     """The banded 3x3 / 64-channel kernel (conv3x3.hip) against the generic
