@@ -1386,8 +1386,16 @@ __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
   const int lchunk_ld = (lane & 7) ^ (lane >> 3);  // logical K chunk this lane fetches
   const int kc = lchunk_ld * VE;
 
-  // Per load slot j (group g = wave + 4 j): row base byte offset (or -1), conv coords.
-  int64_t slot_base[LPW];
+  // Per load slot j (group g = wave + NW j): the byte offset of this lane's
+  // chunk at K tile 0 (conv: at tap (0, 0), which may lie in the padding, so
+  // it can be negative), or -1 for a row past M / N; conv rows also keep
+  // their top-left input coordinates (rows past M get hi0 far out of range,
+  // so every tap's bounds check fails).  A and B byte extents are below 2^31
+  // (dma_eligible), so 32-bit offsets cover them.  Slots j < A_SLOTS hold A
+  // rows for every wave (BM / 8 is a multiple of NW), a compile-time split.
+  constexpr int A_SLOTS = BM / 8 / NW;
+  static_assert((BM / 8) % NW == 0, "A/B slot split");
+  int32_t slot_off[LPW];
   int slot_hi[LPW], slot_wi[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
@@ -1395,45 +1403,47 @@ __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
     const int r = g * 8 + (lane >> 3);
     slot_hi[j] = 0;
     slot_wi[j] = 0;
-    if (g < BM / 8) {
+    if (j < A_SLOTS) {
       const int64_t m = m0 + r;
       if (AM == kConvTap) {
         const ConvRow cr = conv_row(p, m);
-        slot_base[j] = cr.valid ? cr.base : -1;
-        slot_hi[j] = cr.hi0;
+        slot_off[j] = static_cast<int32_t>(
+            (cr.base + (static_cast<int64_t>(cr.hi0) * p.cw + cr.wi0) * p.c_stride + kc) * ES);
+        slot_hi[j] = cr.valid ? cr.hi0 : -0x40000000;
         slot_wi[j] = cr.wi0;
       } else {
-        slot_base[j] = m < p.m ? m * p.lda : -1;
+        slot_off[j] = m < p.m ? static_cast<int32_t>((m * p.lda + kc) * ES) : -1;
       }
     } else {
       const int64_t n = n0 + (r - BM);
-      slot_base[j] = n < p.n ? n * p.ldb : -1;
+      slot_off[j] = n < p.n ? static_cast<int32_t>((n * p.ldb + kc) * ES) : -1;
     }
   }
   int t_kh = 0, t_kw = 0, t_c0 = 0;  // kConvTap: tap of the next tile to issue
 
   auto issue = [&](int64_t kt, int buf) {
-    const int64_t k = kt * BK + kc;
-    const bool k_ok = k < p.k;
+    const bool k_ok = kt * BK + kc < p.k;
+    const int32_t k_bytes = static_cast<int32_t>(kt * BK * ES);  // dense operands: uniform
     const int dh = t_kh * p.dh, dw = t_kw * p.dw;
+    // conv: the tap's uniform byte offset from tap (0, 0)
+    const int32_t tap_bytes = ((dh * p.cw + dw) * p.c_stride + t_c0) * ES;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
       const int g = wave + NW * j;
       uint32_t voff = kOobOffset;
-      if (g < BM / 8) {
+      if (j < A_SLOTS) {
         if (AM == kConvTap) {
           const int hi = slot_hi[j] + dh, wi = slot_wi[j] + dw;
-          if (slot_base[j] >= 0 && static_cast<unsigned>(hi) < static_cast<unsigned>(p.ch) &&
+          if (static_cast<unsigned>(hi) < static_cast<unsigned>(p.ch) &&
               static_cast<unsigned>(wi) < static_cast<unsigned>(p.cw))
-            voff = static_cast<uint32_t>(
-                (slot_base[j] + (static_cast<int64_t>(hi) * p.cw + wi) * p.c_stride + t_c0 + kc) * ES);
-        } else if (slot_base[j] >= 0 && k_ok) {
-          voff = static_cast<uint32_t>((slot_base[j] + k) * ES);
+            voff = static_cast<uint32_t>(slot_off[j] + tap_bytes);
+        } else if (slot_off[j] >= 0 && k_ok) {
+          voff = static_cast<uint32_t>(slot_off[j] + k_bytes);
         }
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, (lds_void_ptr)(smem + buf * STAGE + g * 1024), 16, voff, 0,
                                                  0, 0);
       } else {
-        if (slot_base[j] >= 0 && k_ok) voff = static_cast<uint32_t>((slot_base[j] + k) * ES);
+        if (slot_off[j] >= 0 && k_ok) voff = static_cast<uint32_t>(slot_off[j] + k_bytes);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, (lds_void_ptr)(smem + buf * STAGE + g * 1024), 16, voff, 0,
                                                  0, 0);
       }
