@@ -245,8 +245,11 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
           float v[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            v[r] = (acc[i][j][r] + bv[j][r]) + 0.0f;
-            if (g.relu) v[r] = v[r] > 0.0f ? v[r] : 0.0f;
+            // With ReLU the zero residual's "+ 0" changes nothing (it only
+            // turns -0 into +0, and the select maps both zeros and NaN to
+            // +0), so it is added only without ReLU.
+            const float t = acc[i][j][r] + bv[j][r];
+            v[r] = g.relu ? (t > 0.0f ? t : 0.0f) : t + 0.0f;
           }
           *reinterpret_cast<uint2*>(ctile + m * CS + (16 * j + 4 * lg) * 2) =
               uint2{MM::pack(v[0], v[1]), MM::pack(v[2], v[3])};
