@@ -138,25 +138,33 @@ __global__ void __launch_bounds__(kWaves * 64, 2) conv3x3_c64_kernel(Conv3x3Args
   const __amdgpu_buffer_rsrc_t rs_out = __builtin_amdgcn_make_buffer_rsrc(p.out, 0, p.x_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs_res =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.residual), 0, p.x_bytes, 0x00020000);
+  // DMA slot j of this wave: patch pixel pix = g * 8 + (lane >> 3),
+  // g = wave + 4 j, at patch row pr = pix / pw, column pix - pr * pw.  Its
+  // input pixel, relative to (h0 - 1, -1), is pr * W + (pix - pr * pw) =
+  // pix - 2 pr (pw = W + 2).  Only the row is kept per slot (far out of
+  // range for pixels past the patch or in its padding columns, so the row
+  // check fails); a band then costs a few adds, a compare and a select.
+  int spr[kSlots];
+#pragma unroll
+  for (int j = 0; j < kSlots; ++j) {
+    const int pix = (wave + kWaves * j) * 8 + (lane >> 3);
+    const int pr = static_cast<int>((static_cast<uint32_t>(pix) * p.pw_magic) >> 20);
+    const int wi = pix - pr * pw - 1;
+    const bool ok = pix < p.npix && static_cast<unsigned>(wi) < static_cast<unsigned>(W);
+    spr[j] = ok ? pr : -0x10000000;  // 2 * spr stays within int
+  }
   auto issue = [&](int t, int buf) {
     const int img = t / p.bands, h0 = (t - img * p.bands) * p.rows;
-    const int img_base = img * H;
-    // Opaque per call: keeps the compiler from hoisting 19 slots' worth of
-    // loop-invariant address math out of the tile loop (it would spill it).
-    int lsub = lane >> 3, lchunk = chunk;
-    asm volatile("" : "+v"(lsub), "+v"(lchunk));
+    // byte offset of input pixel (h0 - 1, -1) of image img, plus this lane's pixel and chunk
+    const int lane_base = ((img * H + h0 - 1) * W - 1) * (kC * 2) + (lane >> 3) * (kC * 2) + chunk * 16;
 #pragma unroll
     for (int j = 0; j < kSlots; ++j) {
       const int g = wave + kWaves * j;
       uint8_t* dst = smem + buf * kStage + g * 1024;
       if (g < kPatchGroups) {
-        const int pix = g * 8 + lsub;
-        const int pr = static_cast<int>((static_cast<uint32_t>(pix) * p.pw_magic) >> 20);
-        const int hi = h0 - 1 + pr, wi = pix - pr * pw - 1;
-        uint32_t voff = kOob;
-        if (pix < p.npix && static_cast<unsigned>(hi) < static_cast<unsigned>(H) &&
-            static_cast<unsigned>(wi) < static_cast<unsigned>(W))
-          voff = static_cast<uint32_t>(((img_base + hi) * W + wi) * (kC * 2) + lchunk * 16);
+        const int hi = h0 - 1 + spr[j];
+        const int off = lane_base + (g * 8 - 2 * spr[j]) * (kC * 2);
+        const uint32_t voff = static_cast<unsigned>(hi) < static_cast<unsigned>(H) ? static_cast<uint32_t>(off) : kOob;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)dst, 16, voff, 0, 0, 0);
       }
     }
