@@ -1488,26 +1488,35 @@ __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
     if (kt + S - 1 < ktiles) issue(kt + S - 1, static_cast<int>((kt + S - 1) % S));
     const uint8_t* As = smem + (kt % S) * STAGE;
     const uint8_t* Bs = As + BM * RB;
+    // Every K step's operand fragments are read from LDS before the first
+    // MFMA (a scheduling barrier keeps them there), so the later steps'
+    // reads complete under the earlier steps' MFMAs.  Left to itself the
+    // scheduler issues each step's reads just before its MFMAs and waits on
+    // them (lgkmcnt(0) several times per K tile).
+    constexpr int KS = 8 / Mma::kStep;
+    vec av[KS][TM], bv[KS][TN];
 #pragma unroll
-    for (int ks = 0; ks < 8; ks += Mma::kStep) {
-      vec av[TM], bv[TN];
+    for (int q = 0; q < KS; ++q) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = wm * WTM + i * 16 + lrow;
-        av[i] = read_operand<Mma>(As + r * RB, r, ks, lchunk);
+        av[q][i] = read_operand<Mma>(As + r * RB, r, q * Mma::kStep, lchunk);
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int r = wn * WTN + j * 16 + lrow;
-        bv[j] = read_operand<Mma>(Bs + r * RB, r, ks, lchunk);
+        bv[q][j] = read_operand<Mma>(Bs + r * RB, r, q * Mma::kStep, lchunk);
       }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < KS; ++q)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          acc[i][j] = Mma::mma(bv[j], av[i], acc[i][j]);  // C^T: see epilogue_direct
+          acc[i][j] = Mma::mma(bv[q][j], av[q][i], acc[i][j]);  // C^T: see epilogue_direct
         }
-    }
   }
 
   if constexpr (Mma::kScaled) scale_acc<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane);
