@@ -36,6 +36,7 @@ the MI355X instead:
 from __future__ import annotations
 
 import ctypes as C
+import os
 import math
 from dataclasses import dataclass, field
 from typing import Any, Callable, Dict, List, Optional, Sequence, Tuple
@@ -139,7 +140,7 @@ class CompiledPlan:
 
     def __init__(self, graph: Graph, plan: ExecutionPlan, host_weights: Dict[str, Any],
                  host_constants: Optional[Dict[str, Any]] = None, policy: str = "fp32",
-                 use_graph: bool = True, fuse_stem: bool = True) -> None:
+                 use_graph: bool = True, fuse_stem: bool = True, concurrent: bool = True) -> None:
         init()
         if policy not in _POLICY_ACT:
             raise ValueError(f"unknown precision policy {policy!r}")
@@ -160,6 +161,9 @@ class CompiledPlan:
         self.consumed: set = set()         # node ids already lowered into an earlier launch
         self.node_kinds: List[str] = []     # launch labels (for reporting)
         self.launch_meta: List[Dict[str, Any]] = []  # per launch: kind, algorithmic flops and bytes
+        self.launch_rw: List[Tuple[List[Buf], List[Buf]]] = []  # per launch: buffers read, buffers written
+        self.concurrent = concurrent and not os.environ.get("C3H_SERIAL_PLAN")
+        self.pairs: List[int] = []         # launch p and p + 1 run concurrently (p + 1 on the side stream)
         self.use_graph = use_graph
         self.fuse_stem = fuse_stem
         self._cus = int(device_props().compute_units)
@@ -278,6 +282,8 @@ class CompiledPlan:
                 seen.add(key)
                 nbytes += v.size * v.dtype.itemsize
         self.launches.append(_Launch(build))
+        self.launch_rw.append(([v.buf for v in reads if v is not None and v.buf is not None],
+                               [v.buf for v in writes if v is not None and v.buf is not None]))
         self.node_kinds.append(kind)
         self.launch_meta.append({"kind": kind, "flops": float(flops), "bytes": int(nbytes)})
 
@@ -370,7 +376,35 @@ class CompiledPlan:
         return tuple(self._dim(d) for d in t.shape) if t is not None and t.shape else ()
 
     # ---------------------------------------------------------------- finalize / run
+    def _pair_independent_convs(self) -> None:
+        """Let consecutive convolutions that do not depend on each other run
+        concurrently: a residual block's downsample 1x1 conv and its first 3x3
+        conv both read only the block input.  Independent means neither
+        launch writes a buffer the other reads or writes (views count as
+        their whole buffer).  Both launches' buffers get their slab lifetimes
+        widened over the pair, so the best-fit pool cannot give one launch's
+        output the memory of a buffer the other is still reading."""
+        if not self.concurrent:
+            return
+        n, p = len(self.launches), 0
+        while p + 1 < n:
+            kinds = (self.node_kinds[p].split(":")[0], self.node_kinds[p + 1].split(":")[0])
+            (r0, w0), (r1, w1) = self.launch_rw[p], self.launch_rw[p + 1]
+            ids_w0, ids_w1 = {id(b) for b in w0}, {id(b) for b in w1}
+            independent = not (ids_w0 & ({id(b) for b in r1} | ids_w1)) and not (ids_w1 & {id(b) for b in r0})
+            if kinds == ("conv", "conv") and independent:
+                self.pairs.append(p)
+                for b in r0 + w0 + r1 + w1:
+                    if b.first in (p, p + 1):
+                        b.first = p
+                    if b.last in (p, p + 1):
+                        b.last = p + 1
+                p += 2
+            else:
+                p += 1
+
     def _finalize(self) -> None:
+        self._pair_independent_convs()
         pool = DeviceMemoryPool(alignment=256)
         slab_bufs = [b for b in self.bufs if b.kind == "slab" and b.first >= 0]
         by_first: Dict[int, List[Buf]] = {}
@@ -397,7 +431,7 @@ class CompiledPlan:
             return b.array.ptr
 
         self._args = []
-        ops = (_lib.Op * len(self.launches))()
+        ops = (_lib.Op * len(self.launches))()  # one per launch, stream 0 (subset timing uses these)
         for i, launch in enumerate(self.launches):
             args = launch.build(resolve)
             self._args.append(args)
@@ -407,13 +441,45 @@ class CompiledPlan:
             ops[i].args = C.cast(C.pointer(args), C.c_void_p)
         self._ops = ops
         self._streams = (C.c_void_p * 1)(self._stream.handle)
+        # The program: launches in order; each pair (p, p + 1) forks p + 1 onto
+        # the side stream after everything before p and joins it before p + 2.
+        firsts = set(self.pairs)
+        seq: List[Tuple[int, int, int, int]] = []  # (kind, stream, event, launch index or -1)
+        ev = 0
+        for i in range(len(self.launches)):
+            if i - 1 in firsts:
+                continue
+            if i in firsts:
+                seq += [(_lib.OP_EVENT_RECORD, 0, ev, -1), (_lib.OP_EVENT_WAIT, 1, ev, -1),
+                        (ops[i].kind, 0, 0, i), (ops[i + 1].kind, 1, 0, i + 1),
+                        (_lib.OP_EVENT_RECORD, 1, ev + 1, -1), (_lib.OP_EVENT_WAIT, 0, ev + 1, -1)]
+                ev += 2
+            else:
+                seq.append((ops[i].kind, 0, 0, i))
+        prog = (_lib.Op * len(seq))()
+        for j, (kind, stream, event, li) in enumerate(seq):
+            if li >= 0:
+                C.memmove(C.byref(prog[j]), C.byref(ops[li]), C.sizeof(_lib.Op))
+            prog[j].kind, prog[j].stream, prog[j].event = kind, stream, event
+        self._prog, self._n_prog = prog, len(seq)
+        if self.pairs:
+            from ..device import Event, Stream as _Stream
+
+            self._side = _Stream()
+            self._events = [Event(timing=False) for _ in range(ev)]
+            self._prog_streams = (C.c_void_p * 2)(self._stream.handle, self._side.handle)
+            self._prog_events = (C.c_void_p * ev)(*[e.handle for e in self._events])
+        else:
+            self._prog_streams, self._prog_events = self._streams, None
         self._resolve = resolve
         self.output_arrays = {name: DeviceArray(resolve(v.buf) + v.offset * v.dtype.itemsize, v.shape, v.dtype,
                                                 self.slab) for name, v in self.outputs.items()}
         if self.use_graph and self.launches:
             g = C.c_void_p()
-            _lib.check(_lib.lib().c3h_program_capture(self._ops, len(self.launches), self._streams, 1, None, 0,
-                                                      C.byref(g)), "c3h_program_capture")
+            _lib.check(_lib.lib().c3h_program_capture(self._prog, self._n_prog, self._prog_streams,
+                                                      len(self._prog_streams), self._prog_events,
+                                                      len(self._events) if self.pairs else 0, C.byref(g)),
+                       "c3h_program_capture")
             self._graph_exec = g.value
 
     @property
@@ -445,8 +511,9 @@ class CompiledPlan:
         if self._graph_exec is not None:
             _lib.check(_lib.lib().c3h_graph_launch(self._graph_exec, self._stream.handle), "c3h_graph_launch")
         else:
-            _lib.check(_lib.lib().c3h_program_run(self._ops, len(self.launches), self._streams, 1, None, 0),
-                       "c3h_program_run")
+            _lib.check(_lib.lib().c3h_program_run(self._prog, self._n_prog, self._prog_streams,
+                                                  len(self._prog_streams), self._prog_events,
+                                                  len(self._events) if self.pairs else 0), "c3h_program_run")
 
     def launches_of(self, kinds: Sequence[str]) -> List[int]:
         """Indices of launches whose kind (before any ':') is in `kinds`."""

@@ -211,3 +211,25 @@ def test_compiled_stem_pool_fusion_is_exact(gpu, policy):
     a = _logits(fused, m1.inputs)["logits"]
     b = _logits(plain, m2.inputs)["logits"]
     np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("name,policy,use_graph", [("resnet18_224", "bf16", True), ("resnet18_224", "bf16", False),
+                                                   ("resnet18_cifar", "fp32", True)])
+def test_compiled_concurrent_pairs_match_serial(gpu, name, policy, use_graph):
+    """Downsample and first 3x3 convs of each block on two streams (hipGraph
+    replays, several, with eager work between; and the native timeline)
+    give the serial program's logits bit for bit."""
+    from hackathon_amd import models
+
+    rng = np.random.default_rng(7)
+    m1 = models.build(name, **SMALL[name])
+    m2 = copy.deepcopy(m1)
+    _, conc, _ = _compiled(m1, policy, use_graph=use_graph, concurrent=True)
+    _, serial, _ = _compiled(m2, policy, use_graph=use_graph, concurrent=False)
+    assert len(conc.pairs) == 3 and not serial.pairs
+    for rep in range(3):
+        feed = {k: rng.standard_normal(v.shape, dtype=np.float32) for k, v in m1.inputs.items()}
+        print(f"concurrent pairs {name} {policy} graph={use_graph} replay {rep}", flush=True)
+        a = _logits(conc, feed)["logits"]
+        b = _logits(serial, feed)["logits"]
+        np.testing.assert_array_equal(a, b)

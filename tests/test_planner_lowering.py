@@ -259,3 +259,40 @@ def test_compiled_fuses_stem_conv_relu_maxpool(fake_lib):
     plain = CompiledPlan(m.graph, plan, ex.weight_sources(), ex.host_constants, policy="bf16", fuse_stem=False)
     assert collections.Counter(k.split(":")[0] for k in plain.node_kinds) == {
         "layout": 1, "conv": 20, "maxpool": 1, "gap": 1, "gemm": 1}
+
+
+@pytest.mark.parametrize("name,policy,npairs", [("resnet18_224", "bf16", 3), ("resnet18_cifar", "fp32", 3),
+                                                ("decoder_fp16", "fp16", 0), ("mlp", "fp32", 0)])
+def test_compiled_concurrent_conv_pairs(fake_lib, name, policy, npairs):
+    """Each downsample block's 1x1 conv and first 3x3 conv (both read only the
+    block input) form a concurrent pair: neither writes what the other reads,
+    no slab memory is shared between the two launches' buffers, and the
+    program forks the second launch onto the side stream after everything
+    before the pair and joins it before the next launch."""
+    from hackathon_amd import _lib
+
+    _, prog = _lower(name, policy)
+    assert len(prog.pairs) == npairs
+    for p in prog.pairs:
+        (r0, w0), (r1, w1) = prog.launch_rw[p], prog.launch_rw[p + 1]
+        assert {prog.node_kinds[p], prog.node_kinds[p + 1]} == {"conv"}
+        assert {prog._args[p].kh, prog._args[p + 1].kh} == {1, 3}  # the downsample conv and its sibling
+        assert not ({id(b) for b in w0} & {id(b) for b in r1 + w1}) and not ({id(b) for b in w1} & {id(b) for b in r0})
+        shared = {id(b) for b in r0} & {id(b) for b in r1}
+        assert shared  # the block input
+        a_bufs = [b for b in r0 + w0 if b.kind == "slab"]
+        b_bufs = [b for b in r1 + w1 if b.kind == "slab" and id(b) not in shared]
+        for a in a_bufs:
+            for b in b_bufs:
+                if a is not b:
+                    assert a.offset + a.nbytes <= b.offset or b.offset + b.nbytes <= a.offset
+    seq = [(prog._prog[j].kind, prog._prog[j].stream, prog._prog[j].event) for j in range(prog._n_prog)]
+    assert sum(1 for k, s, e in seq if k not in (_lib.OP_EVENT_RECORD, _lib.OP_EVENT_WAIT)) == prog.num_launches
+    for j, (k, s, e) in enumerate(seq):
+        if k not in (_lib.OP_EVENT_RECORD, _lib.OP_EVENT_WAIT) and s == 1:
+            # fork: record on 0, wait on 1 just before; join: record on 1, wait on 0 right after
+            assert seq[j - 3][:2] == (_lib.OP_EVENT_RECORD, 0) and seq[j - 2][:2] == (_lib.OP_EVENT_WAIT, 1)
+            assert seq[j - 3][2] == seq[j - 2][2]
+            assert seq[j + 1][:2] == (_lib.OP_EVENT_RECORD, 1) and seq[j + 2][:2] == (_lib.OP_EVENT_WAIT, 0)
+            assert seq[j + 1][2] == seq[j + 2][2]
+    assert sum(1 for k, s, e in seq if s == 1 and k not in (_lib.OP_EVENT_RECORD, _lib.OP_EVENT_WAIT)) == npairs
