@@ -432,7 +432,12 @@ int c3h_gemm(const c3h_gemm_args* a, void* stream);
  * (out_layout 1) or NCHW (out_layout 0).  GEMM view: M = n*ho*wo, N = o,
  * K = kh*kw*c_pack.  Group must be 1.  Replaces im2col + conv_contract +
  * conv_reshape + add_bias (+relu / +residual relu) of one Conv node
- * (c32/decompositions.py:300-375, kernel_registry.py:318-453). */
+ * (c32/decompositions.py:300-375, kernel_registry.py:318-453).
+ * 16-bit 3x3 / stride 1 / pad 1 convs with c = c_pack = c_stride = o = 64,
+ * NHWC output, width <= 78 and a bias / residual / ReLU epilogue run on a
+ * spatially tiled kernel whose results are bit-identical to the
+ * implicit-GEMM path (the environment variable C3H_DISABLE_CONV3X3 selects
+ * the latter). */
 typedef struct {
   const void* x;
   const void* w;
