@@ -975,9 +975,12 @@ class CompiledPlan:
         out = self._new(out_shape, self._out_dtype(st.final))
         self._finish_residual(st, out)
         mm = code
-        splits = self._splitk(m, n, k) if code == _lib.F32 else 1
+        if code == _lib.F32:
+            splits = self._splitk(m, n, k)
+        else:  # 16-bit: 128x128 tiles, K tiles of 64
+            splits = self._splitk(m, n, k, vec=64, tile=128, min_k=64)
         if splits > 1:
-            self._gemm_splitk(node, a2, w, out, st, m, n, k, splits, alpha, beta, bmode)
+            self._gemm_splitk(node, a2, w, out, st, m, n, k, splits, alpha, beta, bmode, in_code=code)
             return
 
         def build(r, a2=a2, w=w, out=out, st=st, m=m, n=n, k=k):
@@ -990,11 +993,12 @@ class CompiledPlan:
         self._emit(f"gemm:{node.op_type}", build, [a2, w] + self._epi_reads(st), [out], flops=2.0 * m * n * k)
         self.vals[st.final] = out
 
-    def _splitk(self, m: int, n: int, k: int, vec: int = 4) -> int:
-        """K splits for an fp32 GEMM whose 64x64 output tiles cannot fill two
-        blocks per CU: the largest split with K/split a multiple of `vec`, at
-        least 32 deep, and at most two blocks per CU in total (1 = no split)."""
-        tiles = -(-m // 64) * -(-n // 64)
+    def _splitk(self, m: int, n: int, k: int, vec: int = 4, tile: int = 64, min_k: int = 32) -> int:
+        """K splits for a GEMM whose tile x tile output tiles cannot fill two
+        blocks per CU (fp32: 64x64 tiles; 16-bit: 128x128): the largest split
+        with K/split a multiple of `vec`, at least `min_k` deep, and at most
+        two blocks per CU in total (1 = no split)."""
+        tiles = -(-m // tile) * -(-n // tile)
         target = 2 * self._cus
         if 2 * tiles > target or k < 128:
             return 1
@@ -1002,14 +1006,15 @@ class CompiledPlan:
         for s in range(2, 65):
             if tiles * s > target:
                 break
-            if k % s == 0 and (k // s) % vec == 0 and k // s >= 32:
+            if k % s == 0 and (k // s) % vec == 0 and k // s >= min_k:
                 best = s
         return best
 
     def _gemm_splitk(self, node, a2: Val, w: Val, out: Val, st: "_Epi", m: int, n: int, k: int, splits: int,
-                     alpha: float, beta: float, bmode) -> None:
+                     alpha: float, beta: float, bmode, in_code: int = _lib.F32) -> None:
         """Split-K: `splits` batched partial GEMMs over K/splits each into an fp32
-        workspace, then c3h_gemm_splitk_reduce (fixed summation order + epilogue)."""
+        workspace (fp32 accumulation for 16-bit operands too), then
+        c3h_gemm_splitk_reduce (fixed summation order + epilogue)."""
         ks = k // splits
         part = self._new((splits, m, n), np.float32)
 
@@ -1018,7 +1023,7 @@ class CompiledPlan:
             g.a, g.b, g.out = self._ptr(a2, r), self._ptr(w, r), self._ptr(part, r)
             g.m, g.n, g.k, g.lda, g.ldb, g.ldo, g.batch = m, n, ks, k, k, n, splits
             g.stride_a, g.stride_b, g.stride_out = ks, ks, m * n
-            g.trans_a, g.trans_b, g.in_dtype, g.out_dtype = 0, 1, _lib.F32, _lib.F32
+            g.trans_a, g.trans_b, g.in_dtype, g.out_dtype = 0, 1, in_code, _lib.F32
             g.epi.alpha, g.epi.beta = 1.0, 1.0
             return g
         self._emit(f"gemm:{node.op_type}", gbuild, [a2, w], [part], flops=2.0 * m * n * k)
