@@ -233,3 +233,29 @@ def test_compiled_concurrent_pairs_match_serial(gpu, name, policy, use_graph):
         a = _logits(conc, feed)["logits"]
         b = _logits(serial, feed)["logits"]
         np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("batch", [2, 64])
+def test_compiled_16bit_splitk_classifier(gpu, batch):
+    """ResNet-18 224's classifier (a 16-bit GEMM with too few 128x128 tiles to
+    fill the chip) runs as split-K: batched 16-bit partial GEMMs into fp32,
+    then the ordered reduce with the bias epilogue.  Logits against the
+    policy-rounded oracle within the 16-bit gate (2e-2 x logit range); the
+    serial-K result it replaces is not bit-identical (fp32 partial sums are
+    added in split order)."""
+    from hackathon_amd import models
+
+    kw = dict(SMALL["resnet18_224"])
+    kw["batch"] = batch
+    kw["widths"] = (16, 32, 64, 256)  # classifier K = 256: split into K/64-deep partials
+    m = models.build("resnet18_224", **kw)
+    plan, prog, weights = _compiled(m, "bf16")
+    assert "splitk_reduce" in prog.node_kinds
+    got = _logits(prog, m.inputs)["logits"]
+    ref = G.run_plan(plan, m.graph, weights, m.inputs, policy="bf16")["logits"]
+    ref32 = G.run_plan(plan, m.graph, weights, m.inputs)["logits"]
+    got = got.reshape(ref.shape)
+    scale = max(1.0, float(np.max(np.abs(ref32))))
+    diff = float(np.max(np.abs(got - ref)))
+    print(f"split-K classifier batch={batch}: max|diff| {diff:.3e} (range {scale:.2f})", flush=True)
+    assert diff <= 2e-2 * scale
