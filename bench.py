@@ -55,21 +55,9 @@ def _log(msg: str) -> None:
 
 
 def _prepare(name: str):
-    from hackathon_amd import models
-    from hackathon_amd.c32.strategy import PrecisionPolicy
-    from hackathon_amd.c33.pipeline import GraphPassPipeline
-    from hackathon_amd.c34.scheduler import ExecutionScheduler
-    from hackathon_amd.c35.compiled import CompiledPlan
-    from hackathon_amd.c35.executor import load_weights, fold_conv_batchnorm
+    from hackathon_amd.workloads import compile_workload
 
-    m = models.build(name)
-    GraphPassPipeline().run(m.graph)
-    host_w, host_c = load_weights(m.weights)
-    host_w.update(fold_conv_batchnorm(m.graph, host_w))
-    batch = next(iter(m.inputs.values())).shape[0]
-    plan = ExecutionScheduler(m.graph, batch_size=batch, precision_policy=PrecisionPolicy(m.precision)).build()
-    prog = CompiledPlan(m.graph, plan, host_w, host_c, policy=m.precision)
-    return m, plan, prog
+    return compile_workload(name)
 
 
 def _measure(name: str, steps: int, warmup: int) -> dict:

@@ -53,6 +53,8 @@ from . import engine as E
 _POLICY_ACT = {"fp32": np.dtype(np.float32), "bf16": BF16, "fp16": np.dtype(np.float16), "w8a8": BF16,
                "fp8": np.dtype(np.float16)}
 _MM_CODE = {"fp32": _lib.F32, "bf16": _lib.BF16, "fp16": _lib.F16, "w8a8": _lib.BF16, "fp8": _lib.F16}
+_DTYPE_NAME = {np.dtype(np.float32): "fp32", np.dtype(np.float16): "fp16", BF16: "bf16", np.dtype(np.int8): "int8",
+               np.dtype(np.int32): "int32", np.dtype(np.int64): "int64", np.dtype(np.uint8): "u8"}
 
 
 # ---------------------------------------------------------------- values and buffers
@@ -140,7 +142,8 @@ class CompiledPlan:
 
     def __init__(self, graph: Graph, plan: ExecutionPlan, host_weights: Dict[str, Any],
                  host_constants: Optional[Dict[str, Any]] = None, policy: str = "fp32",
-                 use_graph: bool = True, fuse_stem: bool = True, concurrent: bool = True) -> None:
+                 use_graph: bool = True, fuse_stem: bool = True, concurrent: bool = True,
+                 keep_values: bool = False) -> None:
         init()
         if policy not in _POLICY_ACT:
             raise ValueError(f"unknown precision policy {policy!r}")
@@ -166,6 +169,9 @@ class CompiledPlan:
         self.pairs: List[int] = []         # launch p and p + 1 run concurrently (p + 1 on the side stream)
         self.use_graph = use_graph
         self.fuse_stem = fuse_stem
+        # keep_values: every slab buffer gets memory of its own (no reuse), so
+        # each value the program stores can be read back after a run
+        self.keep_values = keep_values
         self._cus = int(device_props().compute_units)
         self._graph_exec = None
         self._stream = Stream()
@@ -231,10 +237,17 @@ class CompiledPlan:
             out = DeviceArray.empty(arr.shape, dtype)
             E.cast_into(arr, out)
             arr = out
+        self._note_weight_store(name, arr.dtype)
         host = np.asarray(src) if not isinstance(src, DeviceArray) and np.asarray(src).size <= 4096 else None
         v = Val(tuple(arr.shape), arr.dtype, self._persist(arr), host=host)
         cache[key] = v
         return v
+
+    def _note_weight_store(self, name: str, dtype) -> None:
+        """Remember the narrowest type a weight is stored in on the device."""
+        store = self.__dict__.setdefault("_weight_store", {})
+        if np.dtype(dtype).itemsize == 2 or name not in store:
+            store[name] = np.dtype(dtype)
 
     def _host_value(self, name: str) -> Optional[np.ndarray]:
         if name in self.weights_src:
@@ -353,7 +366,9 @@ class CompiledPlan:
         self.outputs: Dict[str, Val] = {}
         for t in self.graph.outputs:
             v = self.vals[t.name]
-            if v.dtype != np.float32 or not v.dense:
+            if v.dtype.kind in "iu":  # integer outputs (ArgMax) keep their type
+                v = v if v.dense else self._dense(v)
+            elif v.dtype != np.float32 or not v.dense:
                 v = self._dense(v, np.float32)
             self.outputs[t.name] = v
         end = len(self.launches)
@@ -419,7 +434,7 @@ class CompiledPlan:
                 slots[id(b)] = s
                 b.offset = pool.describe(s)[0]
             for b in by_last.get(i, []):
-                if i < len(self.launches):
+                if i < len(self.launches) and not self.keep_values:
                     pool.free(slots[id(b)])
         self.slab_bytes = max(pool.stats().peak_reserved_bytes, 256)
         self.slab = Buffer(self.slab_bytes)
@@ -485,6 +500,20 @@ class CompiledPlan:
     @property
     def num_launches(self) -> int:
         return len(self.launches)
+
+    def stored_dtypes(self) -> Dict[str, str]:
+        """Storage type ("fp32", "bf16", "fp16", "int8", ...) of every graph
+        tensor this program holds in memory.  Node outputs absent from the map
+        never leave a fused launch: they exist only as fp32 values in
+        registers (an absorbed bias, residual, activation or GELU step)."""
+        return {k: _DTYPE_NAME.get(v.dtype, str(v.dtype)) for k, v in self.vals.items()
+                if k not in self.weights_src and k not in self.inputs}
+
+    def weight_dtypes(self) -> Dict[str, str]:
+        """Storage type of every weight as the program's launches read it
+        (e.g. "bf16" for a table or contraction weight converted at compile
+        time; the narrowest when a weight has several device copies)."""
+        return {k: _DTYPE_NAME.get(d, str(d)) for k, d in self.__dict__.get("_weight_store", {}).items()}
 
     def stage_inputs(self, feed: Dict[str, Any]) -> None:
         """Copy the batch into the input buffers on the compiled stream."""
@@ -560,6 +589,7 @@ class CompiledPlan:
         self.launch()
         if sync:
             self._stream.synchronize()
+            self.check_errors()
         return dict(self.output_arrays)
 
     @property
@@ -754,6 +784,7 @@ class CompiledPlan:
         if arr is not dev32:
             E.cast_into(dev32, arr)
         v = Val((n, kp), np.dtype(dtype), self._persist(arr))
+        self._note_weight_store(name, dtype)
         cache[key] = (v, n, k)
         return cache[key]
 
@@ -1137,6 +1168,7 @@ class CompiledPlan:
             src_dev = src if isinstance(src, DeviceArray) else DeviceArray.from_host(w_host)
             packed = E.pack_conv_weight(src_dev, c_pack, kw_pack, k_stride, out_dtype=conv_dtype)
             wcache[wkey] = Val(packed.shape, packed.dtype, self._persist(packed))
+            self._note_weight_store(w_name, conv_dtype)
         wv = wcache[wkey]
         if narrow and residual_name is None and self._stem_pool(node, x, wv, bias_name, act, cin, o, kh, kw, sh, sw,
                                                                   dh, dw, pads, ho, wo, k_stride):
@@ -1342,17 +1374,105 @@ class CompiledPlan:
             data = data if data.dense else self._dense(data)
         axis = axis + len(data.shape) if axis < 0 else axis
         shape = data.shape[:axis] + idx.shape + data.shape[axis + 1:]
-        out = self._new(shape, data.dtype)
         outer, adim, inner = math.prod(data.shape[:axis]), data.shape[axis], math.prod(data.shape[axis + 1:])
+        add_node, addend = self._gather_addend(node, data, idx, axis, inner)
+        final = add_node.outputs[0] if add_node is not None else node.outputs[0]
+        od = self._out_dtype(final)
+        out = self._new(shape, od if addend is not None else data.dtype)
+        flag = self._error_flag()
 
-        def build(r, data=data, idx=idx, out=out):
+        def build(r, data=data, idx=idx, out=out, addend=addend):
             a = _lib.GatherArgs()
-            a.data, a.indices, a.out, a.error_flag = self._ptr(data, r), self._ptr(idx, r), self._ptr(out, r), None
+            a.data, a.indices, a.out = self._ptr(data, r), self._ptr(idx, r), self._ptr(out, r)
+            a.error_flag = flag.ptr
             a.outer, a.axis_dim, a.inner, a.n_indices, a.elem_bytes = outer, adim, inner, idx.size, data.dtype.itemsize
+            if addend is not None:
+                a.dtype, a.addend, a.addend_rows = dtype_code(out.dtype), self._ptr(addend, r), addend.size // inner
             return a
-        self._emit("gather", build, [data, idx], [out])
-        od = self._out_dtype(node.outputs[0])
-        self.vals[node.outputs[0]] = out if out.dtype == od else self._dense(out, od)
+        self._emit("gather_add" if addend is not None else "gather", build,
+                   [data, idx] + ([addend] if addend is not None else []), [out])
+        if addend is not None:
+            self.consumed.add(add_node.id)
+        self.vals[final] = out if out.dtype == od else self._dense(out, od)
+
+    def _gather_addend(self, node, data: Val, idx: Val, axis: int, inner: int):
+        """(Add node, addend Val) when the gather's single consumer adds a
+        constant table broadcast over the leading index dims -- the decoder's
+        Gather(tok, ids) -> Add(., pos) -- so one launch does both; else (None, None).
+
+        The table [rows, inner] must broadcast against [*idx.shape, inner] as
+        trailing dims (rows = the product of idx's last dims), the gathered
+        data must be 2-D (outer = 1), and the result is stored in the
+        activation type after one fp32 add, as the unfused Add would round it."""
+        add = self._single_consumer(node.outputs[0])
+        if add is None or add.op_type != "Add" or add.id in self.consumed or axis != 0 or len(data.shape) != 2:
+            return None, None
+        others = [i for i in add.inputs if i != node.outputs[0]]
+        if len(others) != 1 or others[0] not in self.weights_src or add.inputs.count(node.outputs[0]) != 1:
+            return None, None
+        w = self._weight_host(others[0])
+        wshape = list(w.shape)
+        while len(wshape) > 1 and wshape[0] == 1:
+            wshape.pop(0)
+        lead = wshape[:-1]
+        if not wshape or wshape[-1] != inner or len(lead) > len(idx.shape) or \
+                (lead and tuple(idx.shape[len(idx.shape) - len(lead):]) != tuple(lead)):
+            return None, None
+        od = self._out_dtype(add.outputs[0])
+        if data.dtype != od or od not in (np.dtype(np.float32), BF16, np.dtype(np.float16)) or inner % 8 or \
+                w.dtype != np.float32:
+            return None, None
+        return add, self._weight_val(others[0], od)
+
+    def _error_flag(self) -> DeviceArray:
+        """A device int32 that kernels set to 1 on an invalid index (sticky until read)."""
+        if getattr(self, "_errflag", None) is None:
+            self._errflag = self._keep(DeviceArray.from_host(np.zeros(1, np.int32)))
+        return self._errflag
+
+    def read_value(self, name: str, rows: Optional[int] = None) -> np.ndarray:
+        """Host copy of a value this program stores, in its logical (ONNX)
+        shape and layout -- NHWC activations come back NCHW, strided views
+        in their view order -- for the first `rows` entries of axis 0 (all if
+        None).  16-bit floats are widened to float32; integers keep their type.
+        Needs `keep_values=True` for anything but graph outputs and inputs
+        (otherwise the memory may have been reused); synchronizes the device."""
+        from ..device import bf16_to_f32
+
+        v = self.vals[name]
+        if v.buf is None:
+            raise ValueError(f"value '{name}' is a host constant")
+        if v.buf.kind == "slab" and not self.keep_values and name not in self.outputs:
+            raise ValueError("read_value of an intermediate value needs keep_values=True")
+        shape = list(v.shape)
+        if rows is not None and shape:
+            shape[0] = min(int(rows), shape[0])
+        if math.prod(shape) == 0:
+            return np.zeros(shape, np.float32)
+        st = v.logical_strides()
+        span = 1 + sum((d - 1) * s for d, s in zip(shape, st))
+        base = self._resolve(v.buf) + v.offset * v.dtype.itemsize
+        raw = DeviceArray(base, (span,), np.uint16 if v.dtype == BF16 else v.dtype, self.slab).get()
+        item = raw.itemsize
+        out = np.lib.stride_tricks.as_strided(raw, shape=shape, strides=[s * item for s in st]).copy()
+        if v.dtype == BF16:
+            return bf16_to_f32(out).reshape(shape)
+        if v.dtype == np.float16:
+            return out.astype(np.float32)
+        return out
+
+    def check_errors(self) -> None:
+        """Raise IndexError if a kernel of this program saw an out-of-range
+        index since the last check (the flag is cleared after reading).  A
+        synchronous 4-byte read: call it after the program's stream has
+        finished, outside any timed region."""
+        flag = getattr(self, "_errflag", None)
+        if flag is None:
+            return
+        if int(flag.get()[0]) != 0:
+            flag.copy_from_host(np.zeros(1, np.int32))
+            raise IndexError("Gather: an index is out of bounds for the gathered axis (ONNX Gather requires "
+                             "-axis_dim <= index < axis_dim)")
 
     # -- attention ----------------------------------------------------------------------------------
     def _flash_mask(self, mask_name: str, s_q: int, s_k: int) -> Optional[Tuple[int, Optional[str]]]:
@@ -1449,6 +1569,28 @@ class CompiledPlan:
                    flops=2.0 * max(q0, k0) * max(q1, k1) * rows * cols * inner)
         od = self._out_dtype(node.outputs[0])
         self.vals[node.outputs[0]] = out if od == np.float32 else self._dense(out, od)
+
+    # -- ArgMax ------------------------------------------------------------------------------------------
+    def _op_ArgMax(self, node):
+        """First index of the maximum along the last axis (NumPy/ONNX tie rule), int64."""
+        x = self._get(node.inputs[0])
+        axis = int(node.attributes.get("axis", 0))
+        axis = axis + len(x.shape) if axis < 0 else axis
+        if axis != len(x.shape) - 1 or int(node.attributes.get("select_last_index", 0)):
+            raise NotImplementedError("compiled ArgMax: last axis, first index only")
+        x = x if x.dense else self._dense(x)
+        cols = x.shape[-1]
+        rows = x.size // cols
+        keep = int(node.attributes.get("keepdims", 1))
+        out = self._new(tuple(x.shape[:-1]) + ((1,) if keep else ()), np.int64)
+
+        def build(r, x=x, out=out):
+            a = _lib.ArgmaxArgs()
+            a.in_, a.out, a.rows, a.cols, a.in_dtype = self._ptr(x, r), self._ptr(out, r), rows, cols, \
+                dtype_code(x.dtype)
+            return a
+        self._emit("argmax", build, [x], [out])
+        self.vals[node.outputs[0]] = out
 
     # -- W8A8 -----------------------------------------------------------------------------------------
     def _op_QuantizeLinear(self, node):

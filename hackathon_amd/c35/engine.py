@@ -334,6 +334,26 @@ def op_global_average_pool(inputs, attrs):
     return reduce(x, list(range(2, x.ndim)), True, 2, attrs)
 
 
+_GATHER_FLAG: Optional[DeviceArray] = None
+
+
+def gather_error_flag() -> DeviceArray:
+    """The device int32 every engine gather sets to 1 on an out-of-range index."""
+    global _GATHER_FLAG
+    if _GATHER_FLAG is None:
+        _GATHER_FLAG = DeviceArray.from_host(np.zeros(1, np.int32))
+    return _GATHER_FLAG
+
+
+def check_gather_errors() -> None:
+    """Raise IndexError (as np.take does) if a gather since the last check saw
+    an index outside [-axis_dim, axis_dim); clears the flag.  Synchronous."""
+    if _GATHER_FLAG is not None and int(_GATHER_FLAG.get()[0]) != 0:
+        _GATHER_FLAG.copy_from_host(np.zeros(1, np.int32))
+        raise IndexError("Gather: an index is out of bounds for the gathered axis (ONNX Gather requires "
+                         "-axis_dim <= index < axis_dim)")
+
+
 def gather(x: DeviceArray, idx: DeviceArray, axis: int, attrs, out_dtype=None) -> DeviceArray:
     axis = axis + x.ndim if axis < 0 else axis
     if not 0 <= axis < x.ndim:
@@ -345,7 +365,7 @@ def gather(x: DeviceArray, idx: DeviceArray, axis: int, attrs, out_dtype=None) -
     direct = out_dtype == x.dtype
     out = _planned(attrs, shape, out_dtype) if direct else DeviceArray.empty(shape, x.dtype)
     a = _lib.GatherArgs()
-    a.data, a.indices, a.out, a.error_flag = x.ptr, idx.ptr, out.ptr, None
+    a.data, a.indices, a.out, a.error_flag = x.ptr, idx.ptr, out.ptr, gather_error_flag().ptr
     a.outer, a.axis_dim, a.inner = math.prod(x.shape[:axis]), x.shape[axis], math.prod(x.shape[axis + 1:])
     a.n_indices, a.elem_bytes = idx.size, x.itemsize
     if out.size:

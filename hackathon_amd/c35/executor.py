@@ -26,7 +26,7 @@ import json
 import math
 import os
 import time
-from typing import Any, Dict, List, Optional, Tuple
+from typing import Any, Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -407,6 +407,7 @@ class PlannedGraphExecutor(GraphExecutor):
                 raise ValueError(f"Unsupported timeline action: {act.kind}")
         for s in streams.values():
             s.synchronize()
+        engine.check_gather_errors()
         self._resident_model_tensors.update(newly_resident)
         for name in self._preplanned_device_tensors & newly_resident.keys():
             self.host_weights.pop(name, None)
@@ -520,29 +521,44 @@ def _check_output(out: DeviceArray, out_name: str, tail: Optional[Tuple[int, ...
     return out.shape[1:]
 
 
-def _run_planned_batches(pipeline, arrays, total, batch, out_name, out_path) -> Tuple[int, ...]:
-    """Strict path: one batch at a time, logits gathered on the device (X:1137-1201)."""
+def _extra_path(out_path: str, name: str) -> str:
+    """File of a graph output after the first: <name>.npy beside logits.npy."""
+    return os.path.join(os.path.dirname(out_path), f"{name}.npy")
+
+
+def _run_planned_batches(pipeline, arrays, total, batch, out_name, out_path,
+                         extras: Sequence[str] = ()) -> Tuple[int, ...]:
+    """Strict path: one batch at a time, logits gathered on the device (X:1137-1201).
+    Further graph outputs (`extras`, e.g. an int64 ArgMax) are gathered on
+    the host and saved as <name>.npy."""
     final: Optional[DeviceArray] = None
+    extra_host: Dict[str, list] = {n: [] for n in extras}
     for start in range(0, total, batch):
         end = min(start + batch, total)
-        out = pipeline.run({name: DeviceArray.from_host(arr[start:end]) for name, arr in arrays.items()})[out_name]
+        outs = pipeline.run({name: DeviceArray.from_host(arr[start:end]) for name, arr in arrays.items()})
+        out = outs[out_name]
         tail = _check_output(out, out_name, final.shape[1:] if final is not None else None)
         if final is None:
             final = DeviceArray.empty((total,) + tail, np.float32)
         engine.copy_into(out, final.split_axis0(start, end))
+        for n in extras:
+            extra_host[n].append(outs[n].get())
     if final is None:
         raise RuntimeError("Inference produced no output batches")
     result = final.get()
     if not np.all(np.isfinite(result)):
         raise ValueError("Output contains non-finite values (NaN or Inf)")
     np.save(out_path, result)
+    for n in extras:
+        np.save(_extra_path(out_path, n), np.concatenate(extra_host[n], axis=0))
     return result.shape
 
 
 _CHUNK_BYTES = 64 << 20
 
 
-def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path) -> Tuple[int, ...]:
+def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path,
+                     extras: Sequence[str] = ()) -> Tuple[int, ...]:
     """Compiled path with host I/O overlapped with the GPU.
 
     Per batch: the input slice goes through a pinned buffer (two, used in
@@ -553,6 +569,8 @@ def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path) -> Tupl
     turn), and each chunk is checked for non-finite values and written into
     the memory-mapped logits.npy.  No whole-output device or host copy is
     ever built, so C5's 2.1 GB of logits cost one staging buffer per slot.
+    Further graph outputs (`extras`, e.g. the decoders' int64 ArgMax) are
+    staged the same way and drained whole into <name>.npy.
     """
     from ..device import Event, PinnedArray, Stream
 
@@ -563,12 +581,19 @@ def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path) -> Tupl
     ready = [Event(), Event()]
     chunks = [PinnedArray((_CHUNK_BYTES // 4,), np.float32) for _ in range(2)]
     chunk_done = [Event(), Event()]
+    flags = [PinnedArray((1,), np.int32) for _ in range(2)]  # each batch's gather error flag
+    progs: list = [None, None]
+    x_stage: list = [{}, {}]   # per slot: extra output name -> device staging buffer
+    x_host: list = [{}, {}]    # per slot: extra output name -> pinned host buffer
+    x_mm: Dict[str, Any] = {}
     mm = None
     tail: Optional[Tuple[int, ...]] = None
     pending = None  # (slot, start, end) of the batch still on the device
 
     def drain(slot, start, end):
         copy_stream.wait_event(ready[slot])
+        flag = progs[slot]._error_flag()
+        _lib.check(_lib.lib().c3h_memcpy_d2h_async(flags[slot].ptr, flag.ptr, 4, copy_stream.handle), "d2h")
         src = stage[slot]
         row = math.prod(tail)
         flat = mm.reshape(-1)
@@ -584,14 +609,29 @@ def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path) -> Tupl
 
         if spans:
             issue(0)
+        else:
+            copy_stream.synchronize()
+        if not spans and int(flags[slot].array[0]) != 0:
+            progs[slot].check_errors()  # clears the flag and raises IndexError
         for k, (o0, o1) in enumerate(spans):
             if k + 1 < len(spans):
                 issue(k + 1)
-            chunk_done[k % 2].synchronize()
+            chunk_done[k % 2].synchronize()  # the flag copy was queued before chunk 0
+            if k == 0 and int(flags[slot].array[0]) != 0:
+                progs[slot].check_errors()  # clears the flag and raises IndexError
             host = chunks[k % 2].array[: o1 - o0]
             if not np.all(np.isfinite(host)):
                 raise ValueError("Output contains non-finite values (NaN or Inf)")
             flat[o0:o1] = host
+        if extras:
+            for n in extras:
+                src_x = x_stage[slot][n]
+                _lib.check(_lib.lib().c3h_memcpy_d2h_async(x_host[slot][n].ptr, src_x.ptr,
+                                                           (end - start) * src_x.nbytes // src_x.shape[0],
+                                                           copy_stream.handle), "d2h")
+            copy_stream.synchronize()
+            for n in extras:
+                x_mm[n][start:end] = x_host[slot][n].array[: end - start]
 
     for i, start in enumerate(range(0, total, batch)):
         end = min(start + batch, total)
@@ -606,6 +646,7 @@ def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path) -> Tupl
             feed[n] = (pin_in[slot][n], view.nbytes)
         prog.stage_inputs(feed)
         prog.launch()
+        progs[slot] = prog
         out = prog.output_arrays[out_name]
         tail = _check_output(out, out_name, tail)
         if mm is None:
@@ -613,6 +654,16 @@ def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path) -> Tupl
         if stage[slot] is None:
             stage[slot] = DeviceArray.empty((batch,) + tail, np.float32)
         _lib.check(_lib.lib().c3h_memcpy_d2d_async(stage[slot].ptr, out.ptr, out.nbytes, prog.stream.handle), "d2d")
+        for n in extras:
+            xo = prog.output_arrays[n]
+            if n not in x_mm:
+                x_mm[n] = np.lib.format.open_memmap(_extra_path(out_path, n), mode="w+", dtype=xo.dtype,
+                                                    shape=(total,) + xo.shape[1:])
+            if n not in x_stage[slot]:
+                x_stage[slot][n] = DeviceArray.empty((batch,) + xo.shape[1:], xo.dtype)
+                x_host[slot][n] = PinnedArray((batch,) + xo.shape[1:], xo.dtype)
+            _lib.check(_lib.lib().c3h_memcpy_d2d_async(x_stage[slot][n].ptr, xo.ptr, xo.nbytes, prog.stream.handle),
+                       "d2d")
         ready[slot].record(prog.stream)
         if pending is not None:
             drain(*pending)
@@ -623,6 +674,9 @@ def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path) -> Tupl
     mm.flush()
     shape = mm.shape
     del mm
+    for n in extras:
+        x_mm[n].flush()
+    x_mm.clear()
     return shape
 
 
@@ -692,15 +746,16 @@ def load_and_infer(model_path: str, input_dir: str, output_dir: str, batch_size:
                                            qualify_optimizations=qualify_optimizations, engine_kind=engine_kind,
                                            precision=precision)
     out_name = graph.outputs[0].name if graph.outputs else "logits"
+    extras = [t.name for t in graph.outputs[1:]]
     os.makedirs(output_dir, exist_ok=True)
     out_path = os.path.join(output_dir, "logits.npy")
     ti = time.perf_counter()
     if engine_kind == "compiled":
         if qualify_optimizations:  # C3.3 check on the first batch (X:955-994), then the streamed run
             pipeline.run({name: DeviceArray.from_host(arr[:batch]) for name, arr in arrays.items()})
-        out_shape = _stream_compiled(pipeline, arrays, total, batch, out_name, out_path)
+        out_shape = _stream_compiled(pipeline, arrays, total, batch, out_name, out_path, extras)
     else:
-        out_shape = _run_planned_batches(pipeline, arrays, total, batch, out_name, out_path)
+        out_shape = _run_planned_batches(pipeline, arrays, total, batch, out_name, out_path, extras)
     ti_end = time.perf_counter()
     with open(os.path.join(output_dir, "manifest.json"), "w") as f:
         json.dump({"tensors": [{"name": out_name, "file": "logits.npy", "dtype": "float32",
@@ -718,6 +773,7 @@ def load_and_infer(model_path: str, input_dir: str, output_dir: str, batch_size:
     return {
         "model_path": model_path, "input_dir": input_dir, "output_dir": output_dir, "batch_size": batch,
         "backend": "libc3hip", "backend_evidence": evidence, "engine": engine_kind, "total_samples": total, "output_shape": list(out_shape),
+        "extra_outputs": {n: os.path.basename(_extra_path(out_path, n)) for n in extras},
         "parse_time_s": tp_end - tp, "infer_time_s": ti_end - ti, "total_time_s": t_end - t0,
         "cross_stage_reference": True, "optimized_graph_nodes": len(pipeline.graph.nodes),
         "fusion_stats": pipeline.fusion_result["Fusion"]["stats"],

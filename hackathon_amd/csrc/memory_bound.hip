@@ -497,6 +497,39 @@ __global__ void __launch_bounds__(kBlock) gather_kernel(c3h_gather_args a, int64
   }
 }
 
+// Gather with a fused per-row addend (token + positional embedding): one
+// thread per 8 elements of a row, 16-byte (16-bit) or 32-byte (fp32) loads
+// of the gathered row and the addend row, fp32 add, one rounding, one vector
+// store.  Consecutive threads take consecutive chunks of a row, so loads and
+// stores are coalesced; the index is read once per chunk from L1.
+template <typename T>
+__global__ void __launch_bounds__(kBlock) gather_add_kernel(c3h_gather_args a, int64_t row_vecs) {
+  const int64_t total = a.n_indices * row_vecs;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const T* data = static_cast<const T*>(a.data);
+  const T* add = static_cast<const T*>(a.addend);
+  T* out = static_cast<T*>(a.out);
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
+    const int64_t r = t / row_vecs;
+    const int64_t c = (t - r * row_vecs) * 8;
+    int64_t idx = a.indices[r];
+    if (idx < 0) idx += a.axis_dim;
+    float v[8], w[8];
+    if (idx < 0 || idx >= a.axis_dim) {
+      if (a.error_flag) *a.error_flag = 1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+      Elem<T>::store8(out + r * a.inner + c, v);
+      continue;
+    }
+    Elem<T>::load8(data + idx * a.inner + c, v);
+    Elem<T>::load8(add + (r % a.addend_rows) * a.inner + c, w);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] += w[e];
+    Elem<T>::store8(out + r * a.inner + c, v);
+  }
+}
+
 // ------------------------------------------------------------------ argmax
 // One 256-thread block per row; NaN counts as the maximum (NumPy rule) and
 // ties resolve to the lowest index.
@@ -1077,6 +1110,26 @@ int c3h_gather(const c3h_gather_args* a, void* stream) {
   int64_t total_rows = a->outer * a->n_indices;
   if (total_rows == 0 || row_bytes == 0) return C3H_OK;
   hipStream_t s = as_stream(stream);
+  if (a->addend) {
+    C3H_REQUIRE(a->outer == 1 && a->addend_rows >= 1, "gather: a fused addend needs outer == 1 and addend_rows >= 1");
+    C3H_REQUIRE(a->inner % 8 == 0, "gather: a fused addend needs rows of a multiple of 8 elements");
+    const int vec_bytes = a->dtype == C3H_F32 ? 32 : 16;
+    C3H_REQUIRE((a->dtype == C3H_F32 && a->elem_bytes == 4) ||
+                    ((a->dtype == C3H_BF16 || a->dtype == C3H_F16) && a->elem_bytes == 2),
+                "gather: a fused addend needs dtype F32, BF16 or F16 matching elem_bytes");
+    C3H_REQUIRE((reinterpret_cast<uintptr_t>(a->data) | reinterpret_cast<uintptr_t>(a->out) |
+                 reinterpret_cast<uintptr_t>(a->addend)) % vec_bytes == 0,
+                "gather: a fused addend needs vector-aligned data, addend and out");
+    const int64_t rv = a->inner / 8;
+    const dim3 grid(grid_for(total_rows * rv));
+    if (a->dtype == C3H_F32)
+      hipLaunchKernelGGL(gather_add_kernel<float>, grid, dim3(kBlock), 0, s, *a, rv);
+    else if (a->dtype == C3H_BF16)
+      hipLaunchKernelGGL(gather_add_kernel<bf16_t>, grid, dim3(kBlock), 0, s, *a, rv);
+    else
+      hipLaunchKernelGGL(gather_add_kernel<f16_t>, grid, dim3(kBlock), 0, s, *a, rv);
+    return launch_status("gather");
+  }
   bool aligned16 = (reinterpret_cast<uintptr_t>(a->data) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 15) == 0;
   if (row_bytes % 16 == 0 && aligned16) {
     int64_t rv = row_bytes / 16;

@@ -214,8 +214,11 @@ def _causal_mask(seq: int) -> np.ndarray:
 def build_decoder(batch: int = 64, seq: int = 256, d_model: int = 512, heads: int = 8, ffn: int = 2048,
                   layers: int = 6, vocab: int = 8192, precision: str = "fp16", quantized: bool = False,
                   seed: int = 0, name: Optional[str] = None,
-                  act_scales: Optional[Dict[str, float]] = None) -> Model:
-    """Pre-LN decoder; `quantized` routes every Linear through QDQ int8."""
+                  act_scales: Optional[Dict[str, float]] = None, argmax: bool = True) -> Model:
+    """Pre-LN decoder; `quantized` routes every Linear through QDQ int8.
+
+    Outputs: "logits" [N, seq, vocab] and, with `argmax`, "argmax" [N, seq]
+    (int64, first index of the maximum, ONNX ArgMax axis=-1 keepdims=0)."""
     rng = np.random.default_rng(seed)
     name = name or ("decoder_w8a8" if quantized else "decoder_fp16")
     b = GraphBuilder(name)
@@ -303,8 +306,10 @@ def build_decoder(batch: int = 64, seq: int = 256, d_model: int = 512, heads: in
         f = linear(g, ffn, d_model, f"{p}.ffn2")
         x = b.node("Add", [x, f], shape=["N", seq, d_model], name=f"{p}.residual2")
     hn = ln(x, "final.ln")
-    logits = linear(hn, d_model, vocab, "lm_head")
-    b.output(logits)
+    logits = b.output(linear(hn, d_model, vocab, "lm_head"))
+    if argmax:  # the predicted token per position ("output logits + argmax")
+        pred = b.node("ArgMax", [logits], shape=["N", seq], dtype=np.int64, name="predict", axis=-1, keepdims=0)
+        b.output(pred, "argmax")
     signature = f"b{batch}_s{seq}_d{d_model}_h{heads}_f{ffn}_l{layers}_v{vocab}_seed{seed}"
     model = Model(name, b.finish(), b.weights, {"input_ids": ids},
                   precision="w8a8" if quantized else precision, unit="tokens", tokens_per_sample=seq,

@@ -287,7 +287,15 @@ int c3h_bn_fold(const c3h_bnfold_args* a, void* stream);
 /* Gather along an axis: data viewed as [outer, axis_dim, inner] elements of
  * `elem_bytes`; int64 indices (negative wrap, out-of-range -> error flag).
  * Bit-exact row copy (kernel_registry.py:744-752, c35/engine.py:462-481).
- * If `error_flag` is non-NULL the kernel writes 1 there on a bad index. */
+ * If `error_flag` is non-NULL the kernel writes 1 there on a bad index (the
+ * flag is never cleared by the library; out-of-range rows are written as 0).
+ *
+ * Optional fused addend (the decoder's token + positional embedding, the
+ * Gather -> Add pair of c35/engine.py:462-481 and :226-244, in one pass):
+ * when `addend` is non-NULL, outer must be 1 and `dtype` (F32, BF16 or F16)
+ * names the element type of data, out and addend; output row r is
+ * data[idx[r]] + addend[r % addend_rows], added in fp32 and rounded once to
+ * `dtype`.  `addend` is [addend_rows, inner]. */
 typedef struct {
   const void* data;
   const int64_t* indices;
@@ -298,7 +306,9 @@ typedef struct {
   int64_t inner;
   int64_t n_indices;
   int32_t elem_bytes;
-  int32_t pad_;
+  int32_t dtype;
+  const void* addend;
+  int64_t addend_rows;
 } c3h_gather_args;
 int c3h_gather(const c3h_gather_args* a, void* stream);
 

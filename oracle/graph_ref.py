@@ -22,7 +22,7 @@ TEST INFRASTRUCTURE ONLY (see oracle/registry_ref.py).
 from __future__ import annotations
 
 import math
-from typing import Any, Dict, List, Optional, Tuple
+from typing import Any, Callable, Dict, List, Optional, Tuple
 
 import numpy as np
 
@@ -33,12 +33,23 @@ F32 = np.float32
 
 
 def round_bf16(x: np.ndarray) -> np.ndarray:
-    """Round float32 to bfloat16 (nearest even) and back to float32."""
-    u = np.ascontiguousarray(x, F32).view(np.uint32).astype(np.uint64)
-    nan = ((u & 0x7F800000) == 0x7F800000) & ((u & 0x007FFFFF) != 0)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
-    r = np.where(nan, u | 0x400000, r)
-    return r.astype(np.uint32).view(F32).reshape(np.shape(x))
+    """Round float32 to bfloat16 (nearest even) and back to float32.
+
+    Integer form of RNE on the top 16 bits: add 0x7FFF plus the kept LSB,
+    then truncate.  No finite input overflows 32 bits (the largest, -inf's
+    pattern 0xFF800000, plus 0x8000 stays below 2^32); NaNs keep their
+    payload with the quiet bit set.
+    """
+    x = np.ascontiguousarray(x, F32)
+    u = x.view(np.uint32)
+    r = (u >> 16) & np.uint32(1)
+    r += np.uint32(0x7FFF)
+    r += u
+    r &= np.uint32(0xFFFF0000)
+    nan = np.isnan(x)
+    if nan.any():
+        r[nan] = u[nan] | np.uint32(0x400000)
+    return r.view(F32).reshape(np.shape(x))
 
 
 def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
@@ -94,8 +105,27 @@ def _lookup_policy_kernel(name: str):
 
 
 def run_plan(plan, graph, weights: Dict[str, np.ndarray], feed: Dict[str, np.ndarray],
-             policy: str = "fp32") -> Dict[str, np.ndarray]:
-    """Evaluate the plan's kernel steps in order with the registry oracle."""
+             policy: str = "fp32", store: Optional[Dict[str, str]] = None,
+             teacher: Optional[Dict[str, np.ndarray]] = None,
+             on_forced: Optional[Callable[[str, np.ndarray, np.ndarray], None]] = None) -> Dict[str, np.ndarray]:
+    """Evaluate the plan's kernel steps in order with the registry oracle.
+
+    `store` (optional, with a 16-bit or W8A8 policy) names the storage type of
+    each node output as an executable program keeps it in memory
+    ({tensor: "bf16" | "fp16" | "fp32" | ...}).  Given it, a node output is
+    rounded to bf16/fp16 only where it is stored that way, and left in fp32
+    where the program keeps it inside one fused launch (absent from the map):
+    the same arithmetic, with the rounding points of that program instead of
+    one rounding per node.  Weights named in `store` are rounded to their
+    stored type (e.g. an embedding table kept in bf16); other weights and
+    the graph inputs are rounded as without it.
+
+    `teacher` (optional) holds values an executable produced for some node
+    outputs, in logical shape.  After the oracle computes such an output it
+    calls `on_forced(name, oracle value, teacher value)` and continues with
+    the teacher value, so each node is checked on the executable's own inputs
+    and no difference propagates past the node that made it.
+    """
     values: Dict[str, np.ndarray] = {}
     for name, arr in feed.items():
         values[name] = np.asarray(arr)
@@ -119,9 +149,12 @@ def run_plan(plan, graph, weights: Dict[str, np.ndarray], feed: Dict[str, np.nda
         ins = []
         for n in k.logical_inputs:
             v = values[n]
-            if round_inputs and prof.get("weight_dtype") in ("bf16", "fp16") and n in plan.weight_slots \
-                    and np.asarray(v).dtype == F32 and np.asarray(v).ndim >= 2:
-                v = round_to(v, prof["weight_dtype"])
+            if round_inputs and n in plan.weight_slots and np.asarray(v).dtype == F32:
+                if store is None or n not in store:
+                    if prof.get("weight_dtype") in ("bf16", "fp16") and np.asarray(v).ndim >= 2:
+                        v = round_to(v, prof["weight_dtype"])
+                elif store[n] in ("bf16", "fp16"):
+                    v = round_to(v, store[n])
             ins.append(v)
         if prof.get("compute_dtype") == "fp8":
             ins = _fp8_operands(ins, k.operator_params)
@@ -134,8 +167,18 @@ def run_plan(plan, graph, weights: Dict[str, np.ndarray], feed: Dict[str, np.nda
         fn(ins, outs, dict(k.operator_params), k.tuning_params)
         last = node_last_step[k.node_id] == k.step_index
         for n, o in zip(k.logical_outputs, outs):
-            if round_inputs and last and o.dtype == F32 and prof.get("output_dtype") in ("bf16", "fp16"):
-                o = round_to(o, prof["output_dtype"])
+            if round_inputs and last and o.dtype == F32:
+                if store is None:
+                    if prof.get("output_dtype") in ("bf16", "fp16"):
+                        o = round_to(o, prof["output_dtype"])
+                elif store.get(n) in ("bf16", "fp16"):
+                    o = round_to(o, store[n])
+            if teacher is not None and last and n in teacher:
+                t = np.asarray(teacher[n])
+                o = np.asarray(o).reshape(t.shape)
+                if on_forced is not None:
+                    on_forced(n, o, t)
+                o = t.astype(o.dtype, copy=False)
             values[n] = o
     return {t.name: values[t.name] for t in graph.outputs}
 

@@ -17,6 +17,7 @@ import copy
 import numpy as np
 import pytest
 
+import gates
 from oracle import graph_ref as G
 
 pytestmark = pytest.mark.gpu
@@ -74,25 +75,44 @@ def _agree(got: np.ndarray, ref: np.ndarray) -> float:
 @pytest.mark.parametrize("name,policy", [("resnet18_cifar", "bf16"), ("resnet18_224", "bf16"),
                                          ("decoder_fp16", "fp16"), ("decoder_fp16", "bf16")])
 def test_compiled_16bit_policy(gpu, name, policy):
+    """16-bit policies on the small variants (the full-size configs are in
+    test_gpu_fullsize.py).  Decoders: north_star as written, max|logits -
+    fp32| <= 2e-2, and argmax equal to fp32's wherever the fp32 top-2 margin
+    exceeds 4e-2.  ResNets: their random-init logits reach tens to hundreds,
+    where 2e-2 is below one bf16 ulp; gate: within one bf16 ulp at the logit
+    scale of the oracle rounding where the program stores bf16, and argmax
+    equal to fp32's wherever the margin exceeds twice the measured error."""
     from hackathon_amd import models
 
     m = models.build(name, **SMALL[name])
     plan, prog, weights = _compiled(m, policy)
     got = _logits(prog, m.inputs)["logits"]
-    ref = G.run_plan(plan, m.graph, weights, m.inputs, policy=policy)["logits"]
+    store = {**prog.weight_dtypes(), **prog.stored_dtypes()}
+    refs = G.run_plan(plan, m.graph, weights, m.inputs, policy=policy, store=store)["logits"]
     ref32 = G.run_plan(plan, m.graph, weights, m.inputs)["logits"]
-    got = got.reshape(ref.shape)
-    scale = max(1.0, float(np.max(np.abs(ref32))))
-    diff = float(np.max(np.abs(got - ref)))
-    print(f"{name}/{policy}: max|diff| vs policy oracle {diff:.3e} (logit range {scale:.2f}), "
-          f"vs fp32 {float(np.max(np.abs(got - ref32))):.3e}, argmax agree {_agree(got, ref32):.4f}")
-    assert diff <= 2e-2 * scale
-    # Random-init logits are nearly tied across classes, so argmax agreement
-    # is gated against the policy-rounded oracle rather than fp32.
-    assert _agree(got, ref) >= (0.99 if policy == "fp16" else 0.95)
+    got = got.reshape(ref32.shape)
+    d_emu = float(np.max(np.abs(got - refs)))
+    d32 = float(np.max(np.abs(got - ref32)))
+    top = float(np.max(np.abs(refs)))
+    print(f"{name}/{policy}: max|diff| vs {policy} oracle at the program's rounding points {d_emu:.3e}, "
+          f"vs fp32 {d32:.3e} (max|logit| {top:.2f}), argmax agree vs fp32 {gates.agree(got, ref32):.4f}")
+    if name.startswith("decoder"):
+        assert d32 <= 2e-2 and d_emu <= 2e-2
+        ok, share = gates.margin_agreement(got, ref32, 2e-2)
+    else:
+        assert d_emu <= gates.ulp_at(top, "bf16")
+        ok, share = gates.margin_agreement(got, ref32, d32)
+    print(f"  argmax vs fp32 on clear-margin rows {ok:.4f} ({share:.1%} of rows)")
+    assert ok == 1.0
 
 
 def test_compiled_w8a8_decoder(gpu):
+    """W8A8 on a small decoder: as accurate as the W8A8 definition (the
+    oracle's emulation at the program's rounding points) -- RMS logit error
+    against fp32 at most 1.1x the emulation's, argmax agreement with fp32 at
+    most 0.05 below it (128 positions: a few near-ties).  The int8 codes and
+    accumulators themselves are bit-exact per launch (full-size
+    teacher-forced test)."""
     from hackathon_amd import models
 
     kw = dict(batch=2, seq=64, d_model=128, heads=2, ffn=256, layers=2, vocab=300, quantized=True)
@@ -101,13 +121,16 @@ def test_compiled_w8a8_decoder(gpu):
     m = models.build_decoder(**kw, act_scales={n: max(v, 1e-8) / 127.0 for n, v in ranges.items()})
     plan, prog, weights = _compiled(m, "w8a8")
     got = _logits(prog, m.inputs)["logits"]
-    ref = G.run_plan(plan, m.graph, weights, m.inputs, policy="w8a8")["logits"]
-    got = got.reshape(ref.shape)
-    scale = max(1.0, float(np.max(np.abs(ref))))
-    diff = float(np.max(np.abs(got - ref)))
-    print(f"decoder_w8a8: max|diff| {diff:.3e} (logit range {scale:.2f}) argmax agree {_agree(got, ref):.4f}")
-    assert diff <= 5e-2 * scale
-    assert _agree(got, ref) >= 0.9
+    store = {**prog.weight_dtypes(), **prog.stored_dtypes()}
+    refs = G.run_plan(plan, m.graph, weights, m.inputs, policy="w8a8", store=store)["logits"]
+    ref32 = G.run_plan(plan, m.graph, weights, m.inputs)["logits"]
+    got = got.reshape(ref32.shape)
+    e_gpu, e_emu = gates.rms(got - ref32), gates.rms(refs - ref32)
+    a_gpu, a_emu = gates.agree(got, ref32), gates.agree(refs, ref32)
+    print(f"decoder_w8a8: RMS error vs fp32 {e_gpu:.3e} (emulation {e_emu:.3e}); argmax agree vs fp32 "
+          f"{a_gpu:.4f} (emulation {a_emu:.4f}); max|diff| vs emulation {float(np.max(np.abs(got - refs))):.3e}")
+    assert e_gpu <= 1.1 * e_emu
+    assert a_gpu >= a_emu - 0.05
 
 
 def _rms(x) -> float:
@@ -259,3 +282,21 @@ def test_compiled_16bit_splitk_classifier(gpu, batch):
     diff = float(np.max(np.abs(got - ref)))
     print(f"split-K classifier batch={batch}: max|diff| {diff:.3e} (range {scale:.2f})", flush=True)
     assert diff <= 2e-2 * scale
+
+
+def test_compiled_gather_out_of_range_ids_raise(gpu):
+    """Token ids outside the vocabulary make the compiled program raise
+    IndexError after the run (np.take's behaviour in the oracle) instead of
+    returning logits computed from zero rows; the next valid run is unaffected."""
+    from hackathon_amd import models
+
+    m = models.build("decoder_fp16", **SMALL["decoder_fp16"])
+    plan, prog, weights = _compiled(m, "fp16")
+    assert "gather_add" in prog.node_kinds
+    good = _logits(prog, m.inputs)["logits"].copy()
+    bad = dict(m.inputs)
+    bad["input_ids"] = m.inputs["input_ids"].copy()
+    bad["input_ids"][1, 5] = SMALL["decoder_fp16"]["vocab"] + 3
+    with pytest.raises(IndexError):
+        prog.run(bad)
+    np.testing.assert_array_equal(_logits(prog, m.inputs)["logits"], good)

@@ -827,3 +827,126 @@ def test_conv3x3_band_kernel_matches_implicit_gemm(gpu, kind, n, h, w, resid, ac
         t = t + (b32 if bias else 0) + (rv[b_, y, x_] if resid else 0)
         want = np.maximum(t, 0) if act == 1 else t
         np.testing.assert_allclose(got[b_, y, x_], want, rtol=1e-2, atol=4e-2)
+
+
+@pytest.mark.parametrize("kind", ["fp16", "bf16"])
+@pytest.mark.parametrize("mask_kind", [1, 2])
+def test_flash_attention_config5_shape(gpu, kind, mask_kind):
+    """Flash attention at the W8A8 decoder's shape: B=16, H=12, S=1024, dh=64,
+    causal (computed) or additive (causal -inf plus random finite values).
+    Every (batch, head) is checked against float64 at 40 query rows (tile
+    edges, the first and last rows, random rows), and one whole (b, h) at every
+    row, so a wrong batch/head/tile offset anywhere in the grid fails."""
+    from hackathon_amd import _lib
+    from hackathon_amd.device import DeviceArray
+
+    b, h, s, d = 16, 12, 1024, 64
+    rng = np.random.default_rng(1024 + mask_kind)
+    qkv = rng.standard_normal((b, s, 3, h, d), dtype=np.float32)
+    bits, val = _bits(qkv, kind)
+    del qkv
+    dev = _dev(bits)
+    out = DeviceArray.empty((b, s, h, d), bits.dtype)
+    mask = np.zeros((s, s), np.float32)
+    if mask_kind == 2:
+        mask = rng.standard_normal((s, s)).astype(np.float32)
+        mask[np.triu_indices(s, 1)] = -np.inf
+    mdev = _dev(mask)
+    a = _lib.FlashArgs()
+    item = 2
+    a.q, a.k, a.v = dev.ptr, dev.ptr + h * d * item, dev.ptr + 2 * h * d * item
+    a.mask, a.out = mdev.ptr, out.ptr
+    a.batch, a.heads, a.seq_q, a.seq_k, a.head_dim = b, h, s, s, d
+    a.dtype = _lib.BF16 if kind == "bf16" else _lib.F16
+    a.q_sb = a.k_sb = a.v_sb = s * 3 * h * d
+    a.q_sh = a.k_sh = a.v_sh = d
+    a.q_ss = a.k_ss = a.v_ss = 3 * h * d
+    a.o_sb, a.o_sh, a.o_ss = s * h * d, d, h * d
+    a.mask_ld, a.scale, a.mask_kind = s, 1.0 / math.sqrt(d), mask_kind
+    print(f"flash B={b} H={h} S={s} {kind} mask_kind={mask_kind}", flush=True)
+    _lib.launch(a, None)
+    got = _from16(out.get(), kind)  # [B, S, H, D]
+    add = np.triu(np.full((s, s), -np.inf), 1) if mask_kind == 1 else mask.astype(np.float64)
+
+    def ref_rows(bi, hi, rows):
+        q = val[bi, rows, 0, hi].astype(np.float64)
+        k = val[bi, :, 1, hi].astype(np.float64)
+        v = val[bi, :, 2, hi].astype(np.float64)
+        sc = q @ k.T / math.sqrt(d) + add[rows]
+        p = np.exp(sc - sc.max(-1, keepdims=True))
+        return (p / p.sum(-1, keepdims=True)) @ v
+
+    rows = np.unique(np.concatenate([[0, 1, 15, 16, 31, 63, 64, 65, 127, 128, 129, 255, 256, 511, 512, 767, 768,
+                                      1000, 1022, 1023], rng.integers(0, s, 20)]))
+    tol = 2e-2 if kind == "bf16" else 5e-3
+    worst = 0.0
+    for bi in range(b):
+        for hi in range(h):
+            want = ref_rows(bi, hi, rows)
+            err = np.abs(got[bi, rows, hi] - want)
+            worst = max(worst, float(err.max()))
+            np.testing.assert_allclose(got[bi, rows, hi], want, rtol=tol, atol=tol)
+    full = ref_rows(b - 1, h - 1, np.arange(s))
+    np.testing.assert_allclose(got[b - 1, :, h - 1], full, rtol=tol, atol=tol)
+    print(f"  max |err| at sampled rows {worst:.3e}, whole (b,h)=({b - 1},{h - 1}) "
+          f"{float(np.abs(got[b - 1, :, h - 1] - full).max()):.3e}", flush=True)
+
+
+@pytest.mark.parametrize("kind", ["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("n_idx,rows,inner", [(64 * 256, 256, 512), (16 * 1024, 1024, 768), (37, 5, 8)])
+def test_gather_fused_addend_bit_exact(gpu, kind, n_idx, rows, inner):
+    """c3h_gather with an addend: out[r] = data[idx[r]] + addend[r % rows],
+    fp32 add of the stored values and one rounding -- what Gather followed by
+    the broadcast Add gives -- including negative indices; the decoder
+    embedding shapes of configs 4 and 5 and a ragged small case."""
+    from hackathon_amd import _lib
+    from hackathon_amd.device import DeviceArray
+
+    rng = np.random.default_rng(n_idx + inner)
+    vocab = 300
+    table = rng.standard_normal((vocab, inner)).astype(np.float32)
+    pos = rng.standard_normal((rows, inner)).astype(np.float32)
+    idx = rng.integers(-vocab, vocab, size=n_idx).astype(np.int64)
+    if kind == "fp32":
+        t_st, t_val, p_st, p_val, code = table, table, pos, pos, _lib.F32
+    else:
+        (t_st, t_val), (p_st, p_val) = _bits(table, kind), _bits(pos, kind)
+        code = _lib.BF16 if kind == "bf16" else _lib.F16
+    want = t_val[idx] + p_val[np.arange(n_idx) % rows]
+    want = want if kind == "fp32" else G.round_to(want, kind)
+    td, pd, idd = _dev(t_st), _dev(p_st), _dev(idx)
+    out = DeviceArray.empty((n_idx, inner), t_st.dtype)
+    flag = _dev(np.zeros(1, np.int32))
+    a = _lib.GatherArgs()
+    a.data, a.indices, a.out, a.error_flag = td.ptr, idd.ptr, out.ptr, flag.ptr
+    a.outer, a.axis_dim, a.inner, a.n_indices, a.elem_bytes = 1, vocab, inner, n_idx, t_st.itemsize
+    a.dtype, a.addend, a.addend_rows = code, pd.ptr, rows
+    _lib.launch(a, None)
+    got = out.get() if kind == "fp32" else _from16(out.get(), kind)
+    np.testing.assert_array_equal(got, want)
+    assert int(flag.get()[0]) == 0
+
+
+def test_gather_out_of_range_sets_flag_and_zero_rows(gpu):
+    """An index outside [-axis_dim, axis_dim) writes a zero row and sets the
+    error flag (plain and fused-addend forms); in-range rows are unaffected."""
+    from hackathon_amd import _lib
+    from hackathon_amd.device import DeviceArray
+
+    table = np.arange(10 * 8, dtype=np.float32).reshape(10, 8) + 1.0
+    idx = np.array([0, 9, 10, -11, -10, 3], np.int64)
+    for fused in (False, True):
+        td, idd = _dev(table), _dev(idx)
+        pos = _dev(np.zeros((2, 8), np.float32))
+        out = DeviceArray.empty((6, 8), np.float32)
+        flag = _dev(np.zeros(1, np.int32))
+        a = _lib.GatherArgs()
+        a.data, a.indices, a.out, a.error_flag = td.ptr, idd.ptr, out.ptr, flag.ptr
+        a.outer, a.axis_dim, a.inner, a.n_indices, a.elem_bytes = 1, 10, 8, 6, 4
+        if fused:
+            a.dtype, a.addend, a.addend_rows = _lib.F32, pos.ptr, 2
+        _lib.launch(a, None)
+        got = out.get()
+        assert int(flag.get()[0]) == 1
+        np.testing.assert_array_equal(got[[0, 1, 4, 5]], table[[0, 9, 0, 3]])
+        np.testing.assert_array_equal(got[[2, 3]], 0.0)

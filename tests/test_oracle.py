@@ -272,6 +272,82 @@ def test_qlinear_acc_exact_and_requantize():
     assert R.requantize(np.array([[10 ** 6]], np.int32), np.float32(1), np.array([1], F32), np.float32(1), 0)[0, 0] == 127
 
 
+def test_dequantize_linear_closed_form():
+    """ONNX DequantizeLinear: y = (x - zero) * scale in int32 then fp32.  The
+    zero point is subtracted after widening: -128 - 127 must be -255, not the
+    int8 wrap-around 1; a missing zero point means 0."""
+    x = np.array([-128, -1, 0, 1, 127], np.int8)
+    got = _run("dequantize_linear", [x, np.float32(0.5), np.int8(-3)])
+    np.testing.assert_array_equal(got[:5], [-62.5, 1.0, 1.5, 2.0, 65.0])
+    got = _run("dequantize_linear", [x, np.float32(0.25), np.int8(127)])
+    np.testing.assert_array_equal(got[:5], [-63.75, -32.0, -31.75, -31.5, 0.0])
+    got = _run("dequantize_linear", [x, np.float32(2.0)])
+    np.testing.assert_array_equal(got[:5], [-256.0, -2.0, 0.0, 2.0, 254.0])
+    got = _run("dequantize_linear", [x, np.float32(3.0), None])
+    np.testing.assert_array_equal(got[:5], [-384.0, -3.0, 0.0, 3.0, 381.0])
+
+
+def test_batchnorm_closed_form_per_channel():
+    """R:573-584: y = (x - mean) / sqrt(var + eps) * scale + bias, parameters on
+    axis 1.  Hand values chosen so every result is exact in fp32; a channel
+    with var = 0 pins the default epsilon (1e-5): without it the output is
+    infinite, with another epsilon it is off by that ratio's square root."""
+    x = np.arange(2 * 3 * 2 * 2, dtype=F32).reshape(2, 3, 2, 2)
+    scale = np.array([2.0, 1.0, 3.0], F32)
+    bias = np.array([0.5, -1.0, 0.0], F32)
+    mean = np.array([1.0, 0.0, 4.0], F32)
+    var = np.array([3.0, 0.25, 15.0], F32)
+    got = _run("batchnorm_f32", [x, scale, bias, mean, var], {"epsilon": 1.0}).reshape(x.shape)
+    want = np.empty_like(x)
+    want[:, 0] = x[:, 0] - 0.5                       # (x - 1) / 2 * 2 + 0.5
+    want[:, 1] = x[:, 1] / np.sqrt(F32(1.25)) - 1.0  # (x - 0) / sqrt(1.25) * 1 - 1
+    want[:, 2] = (x[:, 2] - 4.0) * 0.75              # (x - 4) / 4 * 3
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6)
+    np.testing.assert_array_equal(got[:, 0], want[:, 0])
+    np.testing.assert_array_equal(got[:, 2], want[:, 2])
+    # default epsilon on a zero-variance channel
+    z = _run("batchnorm_f32", [x[:, :1], F32([1.0]), F32([0.0]), F32([1.0]), F32([0.0])], {}).reshape(2, 1, 2, 2)
+    np.testing.assert_allclose(z, (x[:, :1] - 1.0) / math.sqrt(1e-5), rtol=1e-5)
+
+
+@pytest.mark.parametrize("params,ndim,want", [
+    ({}, 3, ((0, 1, 2), False)),                                  # default: every axis
+    ({"keepdims": 1}, 2, ((0, 1), True)),
+    ({"axis": -1}, 3, ((2,), False)),                             # negative axis wraps
+    ({"axis": 1, "keepdims": 1}, 4, ((1,), True)),
+    ({"axes": [-2, -1], "keepdims": 1}, 4, ((2, 3), True)),       # GlobalAveragePool's decomposition
+    ({"axes": [0, -1]}, 3, ((0, 2), False)),
+    ({"axes": 2}, 3, ((2,), False)),                              # a scalar "axes"
+    ({"axes": [0], "axis": 1}, 2, ((0,), False)),                 # "axes" wins over "axis"
+])
+def test_reduction_axes_known_answers(params, ndim, want):
+    """R:272-287: axes (list or scalar) before axis before all axes, each taken mod ndim."""
+    assert R.reduction_axes(params, ndim) == want
+
+
+@pytest.mark.parametrize("kernel,fold", [("reduce_sum", lambda vs: sum(vs)), ("reduce_max", max),
+                                         ("reduce_mean", lambda vs: sum(vs) / len(vs))])
+@pytest.mark.parametrize("params", [{"axes": [-2, -1], "keepdims": 1}, {"axis": 1}, {"axes": [0, 2]}, {}])
+def test_reduce_kernels_match_loops(kernel, fold, params):
+    """Each reduce kernel against an explicit loop over the index space."""
+    import itertools
+
+    x = np.random.default_rng(9).integers(-8, 8, size=(2, 3, 4, 5)).astype(F32)  # exact sums
+    axes, keep = R.reduction_axes(params, x.ndim)
+    groups = {}
+    for idx in itertools.product(*(range(s) for s in x.shape)):
+        key = tuple(0 if d in axes else i for d, i in enumerate(idx))
+        groups.setdefault(key, []).append(float(x[idx]))
+    kept = tuple(1 if d in axes else s for d, s in enumerate(x.shape))
+    want = np.zeros(kept, np.float64)
+    for key, vs in groups.items():
+        want[key] = fold(vs)
+    if not keep:
+        want = want.reshape(tuple(s for d, s in enumerate(x.shape) if d not in axes))
+    got = _run(kernel, [x], params, out_elems=want.size).reshape(want.shape)
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6)
+
+
 def test_argmax_first_index_and_nan():
     x = np.array([[1, 3, 3, 2], [0, 0, 0, 0], [-1, np.nan, 5, np.nan]], F32)
     out = [np.zeros(3, np.int64)]
@@ -298,6 +374,25 @@ def test_round_bf16_and_f16():
     v = np.array([1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -2.5, 65504.0, np.inf], F32)
     np.testing.assert_array_equal(G.round_bf16(v), [1.0, 1.0, 1.0 + 2 ** -6, -2.5, 65536.0, np.inf])
     np.testing.assert_array_equal(G.round_to(np.array([1.0 + 2 ** -11], F32), "fp16"), [1.0])
+
+
+def test_round_bf16_equals_torch_bfloat16_conversion():
+    """round_bf16 against torch's float32 -> bfloat16 cast (round to nearest even)
+    on 2^22 random bit patterns plus every tie pattern of one binade, the
+    largest finite values, denormals and the infinities; NaNs stay NaN."""
+    import torch
+
+    rng = np.random.default_rng(11)
+    bits = [rng.integers(0, 2 ** 32, size=1 << 22, dtype=np.uint64).astype(np.uint32),
+            (np.arange(1 << 16, dtype=np.uint32) << 16) | np.uint32(0x8000),   # exact ties, all signs/exponents
+            np.array([0x7F7FFFFF, 0xFF7FFFFF, 0x7F7F8000, 0x00000001, 0x80008000, 0x007FFFFF,
+                      0x7F800000, 0xFF800000, 0x7FC00001, 0xFFFFFFFF], np.uint32)]
+    x = np.concatenate(bits).view(F32)
+    got = G.round_bf16(x)
+    want = torch.from_numpy(x.copy()).to(torch.bfloat16).to(torch.float32).numpy()
+    fin = ~np.isnan(x)
+    np.testing.assert_array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
+    assert np.isnan(got[~fin]).all()
 
 
 # -- plan evaluation == ONNX-semantics evaluation ------------------------------------------------
