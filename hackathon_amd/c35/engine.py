@@ -176,6 +176,13 @@ def gemm(a: DeviceArray, b: DeviceArray, out: DeviceArray, m: int, n: int, k: in
     _lib.launch(g, current_stream())
 
 
+def gemm_splitk(g: _lib.GemmArgs, splits: int, workspace: DeviceArray) -> None:
+    """c3h_gemm_splitk: the GEMM `g` cut along K into `splits` partial GEMMs
+    in `workspace` (fp32 [splits, m, n]), then the ordered reduce + epilogue."""
+    _lib.check(_lib.lib().c3h_gemm_splitk(C.byref(g), int(splits), workspace.ptr, workspace.nbytes,
+                                          current_stream()), "c3h_gemm_splitk")
+
+
 def _bias_mode(bias: Optional[DeviceArray], m: int, n: int) -> Tuple[int, int, int]:
     """(mode, rows, cols) of a Gemm C operand broadcast to [m, n] (E:771-793)."""
     if bias is None:

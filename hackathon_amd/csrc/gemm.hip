@@ -1930,6 +1930,76 @@ int c3h_gemm_splitk_reduce(const c3h_splitk_args* a, void* stream) {
   return launch_status("splitk_reduce");
 }
 
+}  // extern "C"
+
+namespace {
+
+// Bytes of fp32 partials a split-K GEMM needs, or -1 if the sizes overflow.
+int64_t splitk_partial_bytes(const c3h_gemm_args* a, int32_t splits) {
+  if (a->m < 0 || a->n < 0 || splits < 1) return -1;
+  const int64_t mn = a->m * a->n;
+  if (a->n != 0 && mn / a->n != a->m) return -1;
+  if (mn > (INT64_MAX / 4) / splits) return -1;
+  return mn * splits * 4;
+}
+
+// The split-K GEMM over a given fp32 partial buffer (the caller has checked
+// its size): `splits` batched partial GEMMs over K/splits each, plain
+// epilogue, then the ordered reduce with a's epilogue.
+int gemm_splitk_into(const c3h_gemm_args* a, int32_t splits, float* partial, hipStream_t s) {
+  C3H_REQUIRE(a->batch == 1, "gemm_splitk: batch must be 1 (one GEMM split along K)");
+  C3H_REQUIRE(splits >= 1 && splits <= 64, "gemm_splitk: splits %d outside [1, 64]", splits);
+  C3H_REQUIRE(a->k >= splits && a->k % splits == 0, "gemm_splitk: k %lld is not a multiple of splits %d",
+              static_cast<long long>(a->k), splits);
+  C3H_REQUIRE(a->out_dtype == C3H_F32 || a->out_dtype == C3H_BF16 || a->out_dtype == C3H_F16,
+              "gemm_splitk: output dtype must be fp32, bf16 or fp16");
+  int rc = check_epilogue(a->epi);
+  if (rc) return rc;
+  if (a->m == 0 || a->n == 0) return C3H_OK;
+  const int64_t ks = a->k / splits;
+  c3h_gemm_args g = *a;
+  g.out = partial;
+  g.k = ks;
+  g.ldo = a->n;
+  g.batch = splits;
+  g.stride_a = a->trans_a ? ks * a->lda : ks;
+  g.stride_b = a->trans_b ? ks : ks * a->ldb;
+  g.stride_out = a->m * a->n;
+  g.stride_bias = g.stride_res = 0;
+  g.out_dtype = C3H_F32;
+  memset(&g.epi, 0, sizeof(g.epi));
+  g.epi.alpha = 1.0f;
+  g.epi.beta = 1.0f;
+  rc = c3h_gemm(&g, s);
+  if (rc) return rc;
+  c3h_splitk_args r;
+  memset(&r, 0, sizeof(r));
+  r.partial = partial;
+  r.out = a->out;
+  r.m = a->m;
+  r.n = a->n;
+  r.ldo = a->ldo;
+  r.splits = splits;
+  r.out_dtype = a->out_dtype;
+  r.epi = a->epi;
+  return c3h_gemm_splitk_reduce(&r, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int c3h_gemm_splitk(const c3h_gemm_args* a, int32_t splits, void* workspace, size_t workspace_bytes, void* stream) {
+  C3H_REQUIRE(a != nullptr, "gemm_splitk: null args");
+  const int64_t need = splitk_partial_bytes(a, splits);
+  C3H_REQUIRE(need >= 0, "gemm_splitk: bad sizes or splits");
+  C3H_REQUIRE(need == 0 || (workspace != nullptr && static_cast<int64_t>(workspace_bytes) >= need),
+              "gemm_splitk: workspace of %zu bytes is smaller than the %lld bytes of partials (splits*m*n*4)",
+              workspace_bytes, static_cast<long long>(need));
+  C3H_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0, "gemm_splitk: workspace must be 16-byte aligned");
+  return gemm_splitk_into(a, splits, static_cast<float*>(workspace), as_stream(stream));
+}
+
 int c3h_gemm_fp8(const c3h_fp8_gemm_args* a, void* stream) {
   C3H_REQUIRE(a != nullptr, "gemm_fp8: null args");
   C3H_REQUIRE(a->m >= 0 && a->n >= 0 && a->k >= 1, "gemm_fp8: bad sizes");

@@ -608,6 +608,19 @@ typedef struct {
 } c3h_splitk_args;
 int c3h_gemm_splitk_reduce(const c3h_splitk_args* a, void* stream);
 
+/* Split-K GEMM in one call, over a caller workspace: the GEMM of `a`
+ * (batch 1) cut along K into `splits` partial GEMMs of K/splits each, fp32
+ * partials written to `workspace` ([splits][m][n], splits*m*n*4 bytes,
+ * 16-byte aligned), then the ordered reduce of c3h_gemm_splitk_reduce with
+ * a's epilogue into a->out.  The same two launches the compiled engine
+ * issues for a GEMM with too few output tiles to fill the chip (the MLP,
+ * the ResNet-18 224 classifier; fused_gemm_epilogue_f32, R:606-633), for
+ * callers outside the compiled engine.  k must be a multiple of splits
+ * (1 <= splits <= 64; 16-bit inputs: K/splits a multiple of 8); the
+ * workspace is written before it is read.  Deterministic for a given split. */
+int c3h_gemm_splitk(const c3h_gemm_args* a, int32_t splits, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* ------------------------------------------------------------------ */
 /* fp8 (OCP E4M3) GEMM: the executable form of the reference's         */
 /* structural `matmul_f8` (c32/hardware.py:80-81), chosen by the mixed  */

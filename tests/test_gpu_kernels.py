@@ -8,6 +8,7 @@ on the same (rounded) inputs; tolerances are stated per test.
 
 from __future__ import annotations
 
+import ctypes as C
 import math
 
 import numpy as np
@@ -950,3 +951,66 @@ def test_gather_out_of_range_sets_flag_and_zero_rows(gpu):
         assert int(flag.get()[0]) == 1
         np.testing.assert_array_equal(got[[0, 1, 4, 5]], table[[0, 9, 0, 3]])
         np.testing.assert_array_equal(got[[2, 3]], 0.0)
+
+
+def _splitk_case(rng, kind, m, n, k):
+    """A GEMM of the split-K shape family with bias + ReLU + residual: args and host operands."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    a32 = rng.standard_normal((m, k)).astype(np.float32)
+    b32 = rng.standard_normal((n, k)).astype(np.float32)
+    if kind == "fp32":
+        a_st, b_st, code, odt, ocode = a32, b32, _lib.F32, np.float32, _lib.F32
+        res_st = rng.standard_normal((m, n)).astype(np.float32)
+    else:
+        (a_st, _), (b_st, _) = _bits(a32, kind), _bits(b32, kind)
+        code = _lib.BF16 if kind == "bf16" else _lib.F16
+        odt, ocode = (BF16, _lib.BF16) if kind == "bf16" else (np.float16, _lib.F16)
+        res_st, _ = _bits(rng.standard_normal((m, n)).astype(np.float32), kind)
+    keep = [_dev(a_st), _dev(b_st), _dev(rng.standard_normal(n).astype(np.float32)), _dev(res_st)]
+    ad, bd, biasd, resd = keep
+    g = _lib.GemmArgs()
+    g.a, g.b, g.m, g.n, g.k, g.lda, g.ldb, g.ldo, g.batch = ad.ptr, bd.ptr, m, n, k, k, k, n, 1
+    g.trans_a, g.trans_b, g.in_dtype, g.out_dtype = 0, 1, code, ocode
+    g.epi = E.epilogue(bias=biasd, bias_mode=2, act=1, residual=resd, alpha=0.75)
+    return g, keep, odt
+
+
+@pytest.mark.parametrize("kind,m,n,k,splits", [("fp32", 256, 512, 784, 16), ("bf16", 256, 1000, 512, 8),
+                                               ("fp16", 100, 72, 1024, 4), ("fp32", 3, 7, 40, 5)])
+def test_gemm_splitk_one_call_equals_two_launches(gpu, kind, m, n, k, splits):
+    """c3h_gemm_splitk (partials in a caller workspace + ordered reduce) is bit
+    for bit the compiled engine's two launches (batched partial GEMM, then
+    c3h_gemm_splitk_reduce); a workspace one element short is refused."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import DeviceArray
+
+    rng = np.random.default_rng(m * 7 + n + k)
+    g, keep, odt = _splitk_case(rng, kind, m, n, k)
+    ws = DeviceArray.empty((splits, m, n), np.float32)
+    out1 = DeviceArray.empty((m, n), odt)
+    g.out = out1.ptr
+    E.gemm_splitk(g, splits, ws)
+    # the same two launches by hand
+    part = DeviceArray.empty((splits, m, n), np.float32)
+    out2 = DeviceArray.empty((m, n), odt)
+    p = _lib.GemmArgs()
+    C.memmove(C.byref(p), C.byref(g), C.sizeof(g))
+    ks = k // splits
+    p.out, p.k, p.batch, p.stride_a, p.stride_b, p.stride_out, p.out_dtype = part.ptr, ks, splits, ks, ks, m * n, _lib.F32
+    p.epi = E.epilogue()
+    _lib.launch(p, None)
+    r = _lib.SplitKArgs()
+    r.partial, r.out, r.m, r.n, r.ldo, r.splits, r.out_dtype, r.epi = part.ptr, out2.ptr, m, n, n, splits, \
+        g.out_dtype, g.epi
+    _lib.launch(r, None)
+    a, b = out1.get(), out2.get()
+    np.testing.assert_array_equal(a.view(np.uint8), b.view(np.uint8))
+    assert np.any(a.view(np.uint8) != 0)
+    # a workspace one byte short is refused before any launch
+    short = DeviceArray.empty((splits * m * n - 1,), np.float32)
+    rc = _lib.lib().c3h_gemm_splitk(C.byref(g), splits, short.ptr, short.nbytes, None)
+    assert rc != 0 and "workspace" in _lib.last_error()
