@@ -289,6 +289,7 @@ def _declare(lib: C.CDLL) -> None:
         "c3h_graph_destroy": ([vp], C.c_int),
         "c3h_abi_sizes": ([P(i64), i32], i32),
         "c3h_gemm_splitk": ([P(GemmArgs), i32, vp, C.c_size_t, vp], C.c_int),
+        "c3h_gemm_splitk_noalloc": ([P(GemmArgs), i32, vp], C.c_int),
     }
     for name, (argtypes, restype) in sig.items():
         fn = getattr(lib, name)

@@ -11,6 +11,9 @@ namespace c3h {
 // Thread-local last-error message (returned by c3h_last_error()).
 void set_error(const char* fmt, ...);
 int fail(int code, const char* fmt, ...);
+// Resolves the device address of gemm.hip's static split-K scratch array on
+// `device` (which must be current); called by c3h_init.  Returns a status.
+int gemm_scratch_setup(int device);
 
 #define C3H_HIP_CHECK(expr)                                                   \
   do {                                                                        \

@@ -12,6 +12,7 @@
 // remapped so that consecutive tiles (sharing an A row panel) land on the
 // same XCD and hit its L2.
 #include <stdlib.h>
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -1988,6 +1989,68 @@ int gemm_splitk_into(const c3h_gemm_args* a, int32_t splits, float* partial, hip
 }  // namespace
 
 extern "C" {
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------
+// Static split-K scratch for c3h_gemm_splitk_noalloc: fp32 partials live in
+// this file-scope device array instead of a caller or library allocation.
+// Each GPU the library runs on holds its own copy (kScratchBytes) until the
+// process ends.  In host code `scratch` only names the symbol: its device
+// address on a given GPU comes from hipGetSymbolAddress with that GPU
+// current, kept per device in g_scratch_ptr, and only that address is ever
+// passed to kernels.
+// ---------------------------------------------------------------------
+static constexpr int64_t kScratchBytes = int64_t{32} << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / 4];
+
+namespace {
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// The scratch address on the current device, resolved on first use.
+int scratch_for_current(void** out) {
+  int dev = 0;
+  C3H_HIP_CHECK(hipGetDevice(&dev));
+  C3H_REQUIRE(dev >= 0 && dev < kMaxDevices, "gemm scratch: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    C3H_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    C3H_REQUIRE(ptr != nullptr, "gemm scratch: hipGetSymbolAddress returned a null address on device %d", dev);
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return C3H_OK;
+}
+}  // namespace
+
+namespace c3h {
+int gemm_scratch_setup(int device) {
+  int cur = -1;
+  C3H_HIP_CHECK(hipGetDevice(&cur));
+  C3H_REQUIRE(cur == device, "gemm scratch: device %d is not current (%d is)", device, cur);
+  void* ptr = nullptr;
+  return scratch_for_current(&ptr);
+}
+}  // namespace c3h
+
+extern "C" {
+
+int c3h_gemm_splitk_noalloc(const c3h_gemm_args* a, int32_t splits, void* stream) {
+  C3H_REQUIRE(a != nullptr, "gemm_splitk_noalloc: null args");
+  const int64_t need = splitk_partial_bytes(a, splits);
+  C3H_REQUIRE(need >= 0, "gemm_splitk_noalloc: bad sizes or splits");
+  C3H_REQUIRE(need <= kScratchBytes,
+              "gemm_splitk_noalloc: the partials need %lld bytes (splits*m*n*4), above the %lld-byte static "
+              "scratch; use c3h_gemm_splitk with a workspace",
+              static_cast<long long>(need), static_cast<long long>(kScratchBytes));
+  void* ptr = nullptr;
+  int rc = scratch_for_current(&ptr);
+  if (rc) return rc;
+  return gemm_splitk_into(a, splits, static_cast<float*>(ptr), as_stream(stream));
+}
 
 int c3h_gemm_splitk(const c3h_gemm_args* a, int32_t splits, void* workspace, size_t workspace_bytes, void* stream) {
   C3H_REQUIRE(a != nullptr, "gemm_splitk: null args");

@@ -39,7 +39,7 @@ int c3h_init(int device) {
   C3H_REQUIRE(device >= 0 && device < count, "device %d out of range (count %d)", device, count);
   C3H_HIP_CHECK(hipSetDevice(device));
   C3H_HIP_CHECK(hipFree(nullptr));  // force context creation
-  return C3H_OK;
+  return gemm_scratch_setup(device);
 }
 
 int c3h_device_count(int* count) {

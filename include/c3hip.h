@@ -621,6 +621,19 @@ int c3h_gemm_splitk_reduce(const c3h_splitk_args* a, void* stream);
 int c3h_gemm_splitk(const c3h_gemm_args* a, int32_t splits, void* workspace, size_t workspace_bytes,
                     void* stream);
 
+/* c3h_gemm_splitk with no workspace and no allocation: the fp32 partials go
+ * to a static 32 MiB device array of the library (one per GPU, held until
+ * the process ends; its address is resolved per device by c3h_init or the
+ * first call on that device).  No counterpart in the reference: it is for
+ * callers that cannot allocate -- code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  Same kernels and result
+ * as c3h_gemm_splitk.  Fails with C3H_EINVAL, launching nothing, when the
+ * partials (splits*m*n*4 bytes) exceed 32 MiB.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (e.g. on two streams)
+ * race.  The partials are fully written before they are read, so the
+ * array's previous contents never matter. */
+int c3h_gemm_splitk_noalloc(const c3h_gemm_args* a, int32_t splits, void* stream);
+
 /* ------------------------------------------------------------------ */
 /* fp8 (OCP E4M3) GEMM: the executable form of the reference's         */
 /* structural `matmul_f8` (c32/hardware.py:80-81), chosen by the mixed  */
