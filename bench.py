@@ -17,7 +17,16 @@ launches / their time.  roofline.traffic: measured HBM bytes per dominant
 launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy) read
 from the committed summary that `--traffic-run` / `--traffic-summary` make.
 cpu_baseline: the NumPy oracle (a restatement of the reference
-decomposition) on a bounded sample, on this host's cores.
+decomposition) on a bounded sample, on this host's cores -- for the headline
+and for every per_config entry, with the thread settings and NumPy's BLAS.
+
+memory_bound (per config): every HBM-bound kernel family on that config's
+path (LayerNorm, gather + positional add, quantize, argmax, pooling, ...)
+replayed alone as a hipGraph, its algorithmic bytes (each operand read once,
+each output written once) over its time: achieved GB/s and the fraction of
+MI355X's 8 TB/s.  end_to_end (per config): the same program fed from and
+drained to pinned host memory every step (H2D, program, D2H serialized on
+one stream): the PCIe-inclusive rate, reported beside `value`, never as it.
 """
 
 from __future__ import annotations
@@ -47,6 +56,10 @@ DOMINANT = {
 }
 BASELINE_INDEX = {"mlp": 0, "resnet18_cifar": 1, "resnet18_224": 2, "decoder_fp16": 3, "decoder_w8a8": 4}
 CPU_SAMPLE = {"mlp": 4096, "resnet18_cifar": 128, "resnet18_224": 48, "decoder_fp16": 16, "decoder_w8a8": 2}
+# smaller samples for the per-config baselines (a few seconds of CPU each)
+CPU_SAMPLE_PER_CONFIG = {"mlp": 4096, "resnet18_cifar": 32, "resnet18_224": 8, "decoder_fp16": 8, "decoder_w8a8": 1}
+MEMORY_BOUND = ("layernorm", "layernorm_q", "gather_add", "gather", "quantize", "quantize_fp8", "dequantize", "argmax",
+                "maxpool", "gap", "layout", "splitk_reduce", "ew", "softmax", "cast", "copy")
 # decoder_fp8 is no BASELINE config: the decoder_fp16 model under the "fp8" policy (E4M3 GEMMs).
 
 
@@ -110,13 +123,92 @@ def _measure(name: str, steps: int, warmup: int) -> dict:
             "share_of_step": k_ms / (gpu_ms / steps) if gpu_ms > 0 else None,
         },
     }
+    res["memory_bound"] = _memory_bound(prog, reps=max(5, min(steps, 20)))
+    res["end_to_end"] = _end_to_end(prog, m, units, steps=max(3, min(steps, 10)))
     _log(f"{name}: {res['value']:.1f} {res['unit']}, {res['ms_per_step']:.3f} ms/step, "
-         f"{desc}: {achieved:.1f} TFLOP/s ({100 * achieved / PEAK[dtype]:.1f}% of peak)")
+         f"{desc}: {achieved:.1f} TFLOP/s ({100 * achieved / PEAK[dtype]:.1f}% of peak); "
+         f"with host transfers {res['end_to_end']['value']:.1f} {res['unit']}")
+    for kind, mb in res["memory_bound"].items():
+        _log(f"  {name} {kind}: {mb['launches_per_step']} launches, {mb['us_per_launch']:.1f} us, "
+             f"{mb['algorithmic_MB_per_launch']:.1f} MB -> {mb['achieved_GBps']:.0f} GB/s "
+             f"({100 * mb['frac_of_hbm_peak']:.1f}% of 8 TB/s)")
     del prog
     return res
 
 
-def _cpu_baseline(name: str) -> dict:
+def _memory_bound(prog, reps: int) -> dict:
+    """Achieved HBM bandwidth of each memory-bound kernel family of the program."""
+    out = {}
+    for kind in MEMORY_BOUND:
+        idx = prog.launches_of([kind])
+        if not idx:
+            continue
+        repeat = max(1, -(-32 // len(idx)))
+        ms = prog.time_subset(idx, reps=reps, repeat=repeat)
+        _, nbytes = prog.work(idx)
+        gbps = nbytes / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+        out[kind] = {"launches_per_step": len(idx), "us_per_launch": ms * 1e3 / len(idx),
+                     "algorithmic_MB_per_launch": nbytes / len(idx) / 1e6, "achieved_GBps": gbps,
+                     "peak_GBps": PEAK["hbm"], "frac_of_hbm_peak": gbps / PEAK["hbm"],
+                     "timing": f"hipGraph of the family's launches x{repeat}, HIP events, {reps} replays"}
+    return out
+
+
+def _end_to_end(prog, m, units: int, steps: int) -> dict:
+    """The program fed from pinned host memory and drained to it, every step."""
+    import numpy as np
+
+    from hackathon_amd import _lib
+    from hackathon_amd.device import PinnedArray, synchronize
+
+    pin_in = {}
+    for n, v in m.inputs.items():
+        pa = PinnedArray(v.shape, v.dtype)
+        pa.array[...] = v
+        pin_in[n] = pa
+    pin_out = {n: PinnedArray(a.shape, a.dtype) for n, a in prog.output_arrays.items()}
+    feed = {n: (pa, pa.array.nbytes) for n, pa in pin_in.items()}
+    h = prog.stream.handle
+
+    def step():
+        prog.stage_inputs(feed)
+        prog.launch()
+        for n, a in prog.output_arrays.items():
+            _lib.check(_lib.lib().c3h_memcpy_d2h_async(pin_out[n].ptr, a.ptr, a.nbytes, h), "d2h")
+
+    step()
+    prog.stream.synchronize()
+    synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    prog.stream.synchronize()
+    wall = time.perf_counter() - t0
+    in_bytes = sum(pa.array.nbytes for pa in pin_in.values())
+    out_bytes = sum(a.nbytes for a in prog.output_arrays.values())
+    return {"value": units * steps / wall, "ms_per_step": wall * 1e3 / steps, "steps": steps,
+            "h2d_bytes_per_step": in_bytes, "d2h_bytes_per_step": out_bytes,
+            "form": "pinned host input -> H2D -> program -> D2H of every output to pinned host, "
+                    "serialized on the program stream"}
+
+
+def _blas_info() -> dict:
+    """Thread settings and the BLAS NumPy is linked against (BASELINE.md's CPU-baseline plan)."""
+    import numpy as np
+
+    info = {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS")}
+    info["affinity_cores"] = len(os.sched_getaffinity(0))
+    info["numpy"] = np.__version__
+    try:
+        cfg = np.show_config(mode="dicts")
+        blas = cfg.get("Build Dependencies", {}).get("blas", {})
+        info["blas"] = {k: blas.get(k) for k in ("name", "version", "openblas configuration") if blas.get(k)}
+    except Exception as exc:  # noqa: BLE001 - informational only
+        info["blas"] = f"unavailable: {exc}"
+    return info
+
+
+def _cpu_baseline(name: str, sample: int = 0) -> dict:
     """The NumPy oracle on a bounded sample of the same workload (median of 3 after a warm-up)."""
     import numpy as np
 
@@ -129,7 +221,7 @@ def _cpu_baseline(name: str) -> dict:
     m = models.build(name)
     GraphPassPipeline().run(m.graph)
     w = {**m.weights, **graph_ref.fold_conv_bn(m.graph, m.weights)}
-    b = CPU_SAMPLE[name]
+    b = sample or CPU_SAMPLE[name]
     plan = ExecutionScheduler(m.graph, batch_size=b, precision_policy=PrecisionPolicy(m.precision)).build()
     feed = {k: v[:b] for k, v in m.inputs.items()}
     graph_ref.run_plan(plan, m.graph, w, feed, policy=m.precision)
@@ -147,22 +239,28 @@ def _cpu_baseline(name: str) -> dict:
     return {"value": units / t, "unit": f"{m.unit}/s", "cores": min(threads, affinity), "kind": "port",
             "sample": f"oracle.graph_ref.run_plan (NumPy restatement of the reference decomposition, "
                       f"{m.precision} policy rounding emulated in fp32) on the first {b} samples of the "
-                      f"batch, median of {len(times)} runs ({t:.2f} s each)"}
+                      f"batch, median of {len(times)} runs ({t:.2f} s each)",
+            "threads": _blas_info()}
 
 
-# -- HBM traffic of the dominant kernel (two rocprofv3 --pmc passes) -------------------------------
+# -- measured HBM traffic (two rocprofv3 --pmc passes) --------------------------------------------
 COPY_BYTES = 1 << 30
 TRAFFIC_PROFILE = ROOT / "profiles" / f"{HEADLINE}_conv_traffic.md"
 
 
-def _traffic_run(meta_path: str, reps: int = 3) -> int:
+def _traffic_profile(workload: str, label: str) -> Path:
+    return ROOT / "profiles" / f"{workload}_{label}_traffic.md"
+
+
+def _traffic_run(meta_path: str, workload: str = HEADLINE, kinds: str = "", reps: int = 3) -> int:
     """The dispatch stream the FETCH_SIZE and WRITE_SIZE passes count.
 
     First a plain copy of COPY_BYTES (strided_copy_kernel, 8-byte elements,
     dense): what the counters read for it against the bytes it must move is
-    the calibration factor.  Then the headline workload's dominant launches
-    (every conv of one step) replayed `reps` + 1 times as a hipGraph; the
-    per-launch algorithmic bytes go to `meta_path` for the summary."""
+    the calibration factor.  Then the workload's launches of `kinds` (default:
+    its dominant family) replayed `reps` + 1 times as one hipGraph, as the
+    run's last dispatches; their per-launch algorithmic bytes go to
+    `meta_path` for the summary."""
     import numpy as np
 
     from hackathon_amd.c35 import engine
@@ -175,15 +273,21 @@ def _traffic_run(meta_path: str, reps: int = 3) -> int:
         engine.strided_copy(src, dst, (n,), (1,))
     synchronize()
     del src, dst
-    m, plan, prog = _prepare(HEADLINE)
-    idx = prog.launches_of(DOMINANT[HEADLINE][0])
+    m, plan, prog = _prepare(workload)
+    kind_list = [k for k in kinds.split(",") if k] or DOMINANT[workload][0]
+    label = "conv" if kind_list == DOMINANT[HEADLINE][0] and workload == HEADLINE else \
+        ("dominant" if kind_list == DOMINANT[workload][0] else "memory_bound")
+    idx = prog.launches_of(kind_list)
+    if not idx:
+        raise ValueError(f"{workload} has no launches of kinds {kind_list}")
     prog.time_subset(idx, reps=reps)
     synchronize()
-    meta = {"workload": HEADLINE, "copy_bytes": COPY_BYTES, "copy_dispatches": 3, "replays": reps + 1,
+    meta = {"workload": workload, "label": label, "kinds": kind_list, "copy_bytes": COPY_BYTES,
+            "copy_dispatches": 3, "replays": reps + 1,
             "launches": [{k: prog.launch_meta[i][k] for k in ("kind", "flops", "bytes")} for i in idx]}
     with open(meta_path, "w") as f:
         json.dump(meta, f, indent=1)
-    _log(f"traffic run: {len(idx)} dominant launches x {reps + 1} replays, meta -> {meta_path}")
+    _log(f"traffic run: {workload} {kind_list}: {len(idx)} launches x {reps + 1} replays, meta -> {meta_path}")
     return 0
 
 
@@ -205,65 +309,86 @@ def _pmc_rows(run_dir: str, counter: str):
     return [(k, v) for _, k, v in rows]
 
 
+def _source_commit() -> str:
+    import subprocess
+
+    try:
+        return subprocess.run(["git", "-C", str(ROOT), "rev-parse", "--short=12", "HEAD"], capture_output=True,
+                              text=True, check=True).stdout.strip()
+    except (OSError, subprocess.CalledProcessError):
+        return "unknown"
+
+
 def _traffic_summary(fetch_dir: str, write_dir: str, meta_path: str) -> int:
-    """Calibrated HBM bytes per dominant launch -> profiles/<headline>_conv_traffic.md."""
+    """Calibrated HBM bytes per launch -> profiles/<workload>_<label>_traffic.md."""
     import numpy as np
 
     with open(meta_path) as f:
         meta = json.load(f)
     launches = meta["launches"]
+    nl, reps = len(launches), meta["replays"]
     out = {}
+    names = []
     for counter, run_dir in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         rows = _pmc_rows(run_dir, counter)
         copy = [v for k, v in rows if "strided_copy_kernel" in k]
-        conv = [v for k, v in rows if "mfma_gemm" in k or "conv_stem_pool" in k or "conv3x3_c64" in k]
-        if len(copy) != meta["copy_dispatches"] or len(conv) != len(launches) * meta["replays"]:
-            raise ValueError(f"{counter}: {len(copy)} copy / {len(conv)} conv dispatches, expected "
-                             f"{meta['copy_dispatches']} / {len(launches) * meta['replays']}")
+        if len(copy) != meta["copy_dispatches"] or len(rows) < nl * reps:
+            raise ValueError(f"{counter}: {len(copy)} copy dispatches (expected {meta['copy_dispatches']}), "
+                             f"{len(rows)} dispatches in all (need {nl * reps} for the replays)")
+        sub = rows[-nl * reps:]  # the subset graph's replays are the run's last dispatches
+        names = [k for k, _ in sub[:nl]]
         factor = meta["copy_bytes"] / (float(np.median(copy)) * 1024.0)
-        per = np.asarray(conv).reshape(meta["replays"], len(launches)).mean(axis=0) * 1024.0 * factor
+        per = np.asarray([v for _, v in sub]).reshape(reps, nl).mean(axis=0) * 1024.0 * factor
         out[counter] = (factor, float(np.median(copy)), per)
     f_fac, f_copy, fetch = out["FETCH_SIZE"]
     w_fac, w_copy, write = out["WRITE_SIZE"]
     alg = np.asarray([l["bytes"] for l in launches], float)
     traffic = fetch + write
+    wl, label = meta["workload"], meta.get("label", "conv")
+    kinds = ",".join(meta.get("kinds", DOMINANT[wl][0]))
+    dest = _traffic_profile(wl, label)
     lines = [
-        f"# {meta['workload']}: HBM traffic of the implicit-GEMM conv launches (rocprofv3 --pmc)", "",
+        f"# {wl}: HBM traffic of the {kinds} launches (rocprofv3 --pmc)", "",
         "Commands (repository root, MI355X box; one counter per pass):", "", "```",
-        "timeout -s KILL 180 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch -o run -- \\",
-        "    python3 bench.py --traffic-run gpurun_out/traffic_meta_fetch.json",
-        "timeout -s KILL 180 rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write -o run -- \\",
-        "    python3 bench.py --traffic-run gpurun_out/traffic_meta.json",
+        f"timeout -s KILL 180 rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch -o run -- \\",
+        f"    python3 bench.py --traffic-run gpurun_out/traffic_meta_fetch.json --workload {wl} --kinds {kinds}",
+        f"timeout -s KILL 180 rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write -o run -- \\",
+        f"    python3 bench.py --traffic-run gpurun_out/traffic_meta.json --workload {wl} --kinds {kinds}",
         "python3 bench.py --traffic-summary gpurun_out/pmc_fetch gpurun_out/pmc_write gpurun_out/traffic_meta.json",
         "```", "",
         f"Calibration: a dense copy of {meta['copy_bytes'] / 2**20:.0f} MiB (strided_copy_kernel) reads "
         f"FETCH_SIZE {f_copy:.0f} KiB and WRITE_SIZE {w_copy:.0f} KiB per dispatch; scale factors "
         f"{f_fac:.4f} (fetch) and {w_fac:.4f} (write) turn counter KiB into bytes moved.", "",
-        "| launch | algorithmic MB | fetched MB | written MB | traffic / algorithmic |",
-        "|---:|---:|---:|---:|---:|",
+        "| launch | kind | kernel | algorithmic MB | fetched MB | written MB | traffic / algorithmic |",
+        "|---:|---|---|---:|---:|---:|---:|",
     ]
-    for i in range(len(launches)):
-        lines.append(f"| {i} | {alg[i] / 1e6:.1f} | {fetch[i] / 1e6:.1f} | {write[i] / 1e6:.1f} | "
-                     f"{traffic[i] / alg[i]:.2f} |")
+    for i in range(nl):
+        kname = names[i].split("(")[0][:60]
+        lines.append(f"| {i} | {launches[i]['kind']} | `{kname}` | {alg[i] / 1e6:.1f} | {fetch[i] / 1e6:.1f} | "
+                     f"{write[i] / 1e6:.1f} | {traffic[i] / alg[i]:.2f} |")
     lines += ["", f"Per step: algorithmic {alg.sum() / 1e9:.3f} GB, measured {traffic.sum() / 1e9:.3f} GB "
               f"({traffic.sum() / alg.sum():.2f}x).", "",
               f"traffic_bytes_per_launch = {traffic.mean():.0f}",
-              f"algorithmic_bytes_per_launch = {alg.mean():.0f}", ""]
-    TRAFFIC_PROFILE.write_text("\n".join(lines))
-    _log(f"wrote {TRAFFIC_PROFILE}: {traffic.mean() / 1e6:.1f} MB per launch "
-         f"({traffic.sum() / alg.sum():.2f}x algorithmic)")
+              f"algorithmic_bytes_per_launch = {alg.mean():.0f}",
+              f"source_commit = {_source_commit()}", ""]
+    dest.write_text("\n".join(lines))
+    _log(f"wrote {dest}: {traffic.mean() / 1e6:.1f} MB per launch ({traffic.sum() / alg.sum():.2f}x algorithmic)")
     return 0
 
 
 def _committed_traffic():
-    """HBM bytes per dominant launch from the committed pmc summary, or None."""
+    """(HBM bytes per dominant launch, source note) from the committed pmc summary, or (None, None)."""
     import re
 
     try:
-        m = re.search(r"^traffic_bytes_per_launch = (\d+)$", TRAFFIC_PROFILE.read_text(), re.M)
+        text = TRAFFIC_PROFILE.read_text()
     except OSError:
-        return None
-    return int(m.group(1)) if m else None
+        return None, None
+    m = re.search(r"^traffic_bytes_per_launch = (\d+)$", text, re.M)
+    c = re.search(r"^source_commit = (\S+)$", text, re.M)
+    src = f"{TRAFFIC_PROFILE.relative_to(ROOT)} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of bench.py " \
+          f"--traffic-run, copy-calibrated; tree at commit {c.group(1) if c else 'unrecorded'})"
+    return (int(m.group(1)) if m else None), src
 
 
 def main() -> int:
@@ -275,7 +400,9 @@ def main() -> int:
                     help="comma-separated workloads to measure (the headline is always included)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-run", metavar="META_JSON",
-                    help="dispatch stream for a rocprofv3 --pmc pass (copy calibration + dominant launches)")
+                    help="dispatch stream for a rocprofv3 --pmc pass (copy calibration + a family's launches)")
+    ap.add_argument("--workload", default=HEADLINE, help="workload of --traffic-run")
+    ap.add_argument("--kinds", default="", help="launch kinds of --traffic-run (default: the dominant family)")
     ap.add_argument("--traffic-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "META_JSON"),
                     help="turn the two pmc passes into the committed traffic summary (no GPU)")
     args = ap.parse_args()
@@ -286,7 +413,7 @@ def main() -> int:
               "Run with --gpus 1.", file=sys.stderr)
         return 2
     if args.traffic_run:
-        return _traffic_run(args.traffic_run)
+        return _traffic_run(args.traffic_run, args.workload, args.kinds)
     from hackathon_amd.device import device_props, init
 
     init(0)
@@ -299,12 +426,19 @@ def main() -> int:
     for n in names:
         per[n] = _measure(n, args.steps, args.warmup)
     head = per[HEADLINE]
-    head["roofline"]["traffic"] = _committed_traffic()
+    head["roofline"]["traffic"], head["roofline"]["traffic_source"] = _committed_traffic()
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.time()
         cpu = _cpu_baseline(HEADLINE)
         _log(f"cpu baseline: {cpu['value']:.2f} {cpu['unit']} on {cpu['cores']} threads ({time.time() - t0:.0f}s)")
+        for n in names:
+            if n == HEADLINE or n not in CPU_SAMPLE_PER_CONFIG:
+                continue
+            t0 = time.time()
+            per[n]["cpu_baseline"] = _cpu_baseline(n, CPU_SAMPLE_PER_CONFIG[n])
+            _log(f"cpu baseline {n}: {per[n]['cpu_baseline']['value']:.2f} {per[n]['cpu_baseline']['unit']} "
+                 f"({time.time() - t0:.0f}s)")
     line = {
         "metric": METRIC, "value": head["value"], "unit": head["unit"], "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,

@@ -87,7 +87,8 @@ class SoftmaxArgs(C.Structure):
 class LayerNormArgs(C.Structure):
     _fields_ = [("x", vp), ("residual", vp), ("scale", vp), ("bias", vp), ("out", vp),
                 ("mean_out", vp), ("invstd_out", vp), ("rows", i64), ("cols", i64),
-                ("epsilon", f32), ("x_dtype", i32), ("out_dtype", i32), ("pad_", i32)]
+                ("epsilon", f32), ("x_dtype", i32), ("out_dtype", i32), ("out_scale", f32), ("out_zero", i32),
+                ("pad_", i32)]
 
 
 class BatchNormArgs(C.Structure):

@@ -163,6 +163,7 @@ class CompiledPlan:
         self.inputs: Dict[str, Val] = {}
         self.consumed: set = set()         # node ids already lowered into an earlier launch
         self.node_kinds: List[str] = []     # launch labels (for reporting)
+        self._rounded: Dict[str, str] = {}  # values rounded to a storage type in registers only
         self.launch_meta: List[Dict[str, Any]] = []  # per launch: kind, algorithmic flops and bytes
         self.launch_rw: List[Tuple[List[Buf], List[Buf]]] = []  # per launch: buffers read, buffers written
         self.concurrent = concurrent and not os.environ.get("C3H_SERIAL_PLAN")
@@ -276,11 +277,13 @@ class CompiledPlan:
         raise KeyError(f"compiled plan: value '{name}' is not available")
 
     def _emit(self, kind: str, build, reads: Sequence[Val] = (), writes: Sequence[Val] = (),
-              flops: float = 0.0) -> None:
+              flops: float = 0.0, skip_bytes: Sequence[Val] = (), extra_bytes: int = 0) -> None:
         """Append one launch; records buffer lifetimes and algorithmic work.
 
         `bytes` is the launch's algorithmic HBM traffic: every operand read
-        once and every output written once (logical sizes, no padding).
+        once and every output written once (logical sizes, no padding).  A
+        read the launch touches only partly (a gathered table) is named in
+        `skip_bytes` and its touched bytes given as `extra_bytes`.
         """
         idx = len(self.launches)
         seen = set()
@@ -293,7 +296,9 @@ class CompiledPlan:
             key = (id(v.buf), v.offset, v.shape, v.strides)
             if key not in seen:
                 seen.add(key)
-                nbytes += v.size * v.dtype.itemsize
+                if not any(v is sv for sv in skip_bytes):
+                    nbytes += v.size * v.dtype.itemsize
+        nbytes += int(extra_bytes)
         self.launches.append(_Launch(build))
         self.launch_rw.append(([v.buf for v in reads if v is not None and v.buf is not None],
                                [v.buf for v in writes if v is not None and v.buf is not None]))
@@ -509,6 +514,18 @@ class CompiledPlan:
         return {k: _DTYPE_NAME.get(v.dtype, str(v.dtype)) for k, v in self.vals.items()
                 if k not in self.weights_src and k not in self.inputs}
 
+    def rounding_map(self) -> Dict[str, str]:
+        """Every point where this program rounds a value to a storage type:
+        weights as its launches read them, stored values, and values rounded
+        in registers only (a LayerNorm output rounded to the activation type
+        inside the launch that quantizes it).  What an emulation needs to
+        round exactly where the program does."""
+        return {**self.weight_dtypes(), **self.stored_dtypes(), **self._rounded}
+
+    def rounded_in_registers(self) -> Dict[str, str]:
+        """Values rounded to a storage type inside a launch and never stored."""
+        return dict(self._rounded)
+
     def weight_dtypes(self) -> Dict[str, str]:
         """Storage type of every weight as the program's launches read it
         (e.g. "bf16" for a table or contraction weight converted at compile
@@ -548,16 +565,20 @@ class CompiledPlan:
         """Indices of launches whose kind (before any ':') is in `kinds`."""
         return [i for i, k in enumerate(self.node_kinds) if k.split(":")[0] in set(kinds)]
 
-    def time_subset(self, indices: Sequence[int], reps: int = 20) -> float:
-        """Milliseconds per replay of a hipGraph holding only the given launches.
+    def time_subset(self, indices: Sequence[int], reps: int = 20, repeat: int = 1) -> float:
+        """Milliseconds per pass over the given launches, from a hipGraph
+        holding only them (`repeat` passes back to back in one graph, so that
+        a few-microsecond launch is not dominated by graph-launch overhead).
 
         The launches reuse the compiled buffers, so they see realistic data;
         the timing comes from HIP events recorded on the compiled stream
-        around `reps` replays.
+        around `reps` replays.  No launch reads a buffer it writes (the slab
+        planner frees a launch's inputs only after placing its outputs), so
+        repeating a launch recomputes the same result.
         """
         from ..device import Event
 
-        idx = list(indices)
+        idx = list(indices) * max(1, int(repeat))
         if not idx:
             return 0.0
         sub = (_lib.Op * len(idx))()
@@ -575,7 +596,7 @@ class CompiledPlan:
                 _lib.check(_lib.lib().c3h_graph_launch(g.value, h), "c3h_graph_launch")
             end.record(self._stream)
             end.synchronize()
-            return start.elapsed_ms(end) / reps
+            return start.elapsed_ms(end) / reps / max(1, int(repeat))
         finally:
             _lib.lib().c3h_graph_destroy(g.value)
 
@@ -1318,8 +1339,15 @@ class CompiledPlan:
             residual = residual if (residual.dense and residual.dtype == x.dtype) else self._dense(residual, x.dtype)
         scale = self._weight_val(scale_name, np.float32)
         bias = self._weight_val(bias_name, np.float32) if bias_name else None
-        out = self._new(x.shape, self._out_dtype(node.outputs[0]))
         eps = float(node.attributes.get("epsilon", 1e-5))
+        # A QuantizeLinear that is the LayerNorm's only consumer runs in the same
+        # launch (W8A8): int8 codes of the activation-type LayerNorm output.
+        quant = self._fusable_quantize(node.outputs[0], cols)
+        ln_dtype = self._out_dtype(node.outputs[0])
+        if quant is not None and ln_dtype != x.dtype:
+            quant = None
+        out = self._new(x.shape, np.int8 if quant is not None else ln_dtype)
+        qscale, qzero = (quant[1], quant[2]) if quant is not None else (1.0, 0)
 
         def build(r, x=x, residual=residual, out=out, scale=scale, bias=bias):
             a = _lib.LayerNormArgs()
@@ -1327,9 +1355,30 @@ class CompiledPlan:
             a.scale, a.bias = self._ptr(scale, r), self._ptr(bias, r) if bias is not None else None
             a.out, a.mean_out, a.invstd_out = self._ptr(out, r), None, None
             a.rows, a.cols, a.epsilon, a.x_dtype, a.out_dtype = rows, cols, eps, dtype_code(x.dtype), dtype_code(out.dtype)
+            a.out_scale, a.out_zero = qscale, qzero
             return a
-        self._emit("layernorm", build, [x, scale] + ([bias] if bias else []) + ([residual] if residual else []), [out])
-        self.vals[node.outputs[0]] = out
+        self._emit("layernorm_q" if quant is not None else "layernorm", build,
+                   [x, scale] + ([bias] if bias else []) + ([residual] if residual else []), [out])
+        if quant is not None:
+            self.consumed.add(quant[0].id)
+            self._rounded[node.outputs[0]] = _DTYPE_NAME[ln_dtype]
+            self.vals[quant[0].outputs[0]] = out
+        else:
+            self.vals[node.outputs[0]] = out
+
+    def _fusable_quantize(self, tensor: str, cols: int):
+        """(QuantizeLinear node, scale, zero point) when `tensor`'s only consumer
+        is a QuantizeLinear with a constant scalar scale and zero point that
+        the fused LayerNorm can apply (not a graph output), else None."""
+        q = self._single_consumer(tensor)
+        if q is None or q.op_type != "QuantizeLinear" or q.id in self.consumed or self._is_output(tensor) or \
+                cols % 8 or q.inputs[0] != tensor:
+            return None
+        scale = self._scalar_const(q.inputs[1])
+        zero = int(self._scalar_const(q.inputs[2])) if len(q.inputs) > 2 and q.inputs[2] else 0
+        if scale is None or not scale > 0 or not -128 <= zero <= 127:
+            return None
+        return q, scale, zero
 
     def _op_FusedLayerNormalization(self, node):
         self._layernorm(node, self._get(node.inputs[0]), None, node.inputs[1],
@@ -1390,7 +1439,8 @@ class CompiledPlan:
                 a.dtype, a.addend, a.addend_rows = dtype_code(out.dtype), self._ptr(addend, r), addend.size // inner
             return a
         self._emit("gather_add" if addend is not None else "gather", build,
-                   [data, idx] + ([addend] if addend is not None else []), [out])
+                   [data, idx] + ([addend] if addend is not None else []), [out],
+                   skip_bytes=[data], extra_bytes=outer * idx.size * inner * data.dtype.itemsize)
         if addend is not None:
             self.consumed.add(add_node.id)
         self.vals[final] = out if out.dtype == od else self._dense(out, od)

@@ -158,9 +158,28 @@ __global__ void __launch_bounds__(256) transpose_tile_kernel(const T* __restrict
 }
 
 // ------------------------------------------------------------------ reductions
+// Cross-lane steps of a wave reduction within each row of 16 lanes, as DPP
+// moves (VALU, no LDS round trip): quad_perm [1,0,3,2] and [2,3,0,1] pair
+// lanes 1 and 2 apart; row_half_mirror (lane i <-> 7 - i of each 8) and
+// row_mirror (i <-> 15 - i of each 16) then pair whole quads and half-rows,
+// whose lanes already hold equal partial results.  Every lane ends with its
+// row's total; the last two steps (16, 32 lanes apart) cross rows.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+template <typename Op>
+__device__ __forceinline__ float row16_reduce(float v, Op op) {
+  v = op(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = op(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = op(v, dpp_mov<0x141>(v));  // row_half_mirror
+  v = op(v, dpp_mov<0x140>(v));  // row_mirror
+  return v;
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v = row16_reduce(v, [](float a, float b) { return a + b; });
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
   return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
@@ -372,75 +391,113 @@ __global__ void __launch_bounds__(kBlock) layernorm_kernel(c3h_layernorm_args a)
   }
 }
 
-// Vectorized LayerNorm: one wave per row, 8 consecutive columns per lane per
-// vector (16-byte loads of 16-bit data), up to kLnVec vectors per lane kept
-// in registers (NV = vectors per lane, chosen per width); statistics in fp32 (mean, then biased variance of the
-// centred values), as layernorm_kernel.  cols % 8 == 0, cols <= 512 * kLnVec.
+// Vectorized LayerNorm: each wave normalizes ROWS consecutive rows, 8
+// consecutive columns per lane per vector (16-byte loads of 16-bit data), NV
+// vectors per lane per row kept in registers.  Every row's loads are issued
+// before the first reduction, so a wave has ROWS * NV loads in flight (one
+// 1 KB row per wave left HBM latency uncovered: 38-44 % of 8 TB/s at d=512
+// and 768).  Statistics in fp32: mean, then the biased variance of the
+// centred values, as layernorm_kernel.  cols % 8 == 0, cols <= 512 * NV.
+//
+// TO = int8_t: the QuantizeLinear that is the LayerNorm's only consumer, in
+// the same pass.  Each output is first rounded to the activation type TX
+// (what the unfused LayerNorm stores), then q = saturate(rne(y / out_scale)
+// + out_zero) exactly as quantize_kernel computes it: bit-identical codes.
 constexpr int kLnVec = 8;
 
-template <typename TX, typename TO, int NV>
+template <typename TX, typename TO>
+struct LnStore {
+  static __device__ __forceinline__ void store8(TO* p, const float* y, float, int) { Elem<TO>::store8(p, y); }
+};
+template <typename TX>
+struct LnStore<TX, int8_t> {
+  static __device__ __forceinline__ void store8(int8_t* p, const float* y, float qs, int qz) {
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float r = Elem<TX>::to_f32(Elem<TX>::from_f32(y[e]));
+      float q = rintf(r / qs) + static_cast<float>(qz);
+      q = fminf(fmaxf(q, -128.0f), 127.0f);
+      w[e >> 2] |= (static_cast<uint32_t>(static_cast<int8_t>(q)) & 0xffu) << (8 * (e & 3));
+    }
+    *reinterpret_cast<uint2*>(p) = uint2{w[0], w[1]};
+  }
+};
+
+template <typename TX, typename TO, int NV, int ROWS>
 __global__ void __launch_bounds__(kBlock) layernorm_vec_kernel(c3h_layernorm_args a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + wave;
-  if (row >= a.rows) return;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + wave) * ROWS;
+  if (row0 >= a.rows) return;
   const int nvec = static_cast<int>(a.cols / 8);
-  const TX* x = static_cast<const TX*>(a.x) + row * a.cols;
-  const TX* res = a.residual ? static_cast<const TX*>(a.residual) + row * a.cols : nullptr;
-  float v[NV][8];
-  float sum = 0.0f;
+  float v[ROWS][NV][8];
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int vi = lane + 64 * j;
+  for (int r = 0; r < ROWS; ++r) {
+    const int64_t row = row0 + r;
+    const TX* x = static_cast<const TX*>(a.x) + row * a.cols;
+    const TX* res = a.residual ? static_cast<const TX*>(a.residual) + row * a.cols : nullptr;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[j][e] = 0.0f;
-    if (vi < nvec) {
-      Elem<TX>::load8(x + vi * 8, v[j]);
-      if (res) {
-        float r[8];
-        Elem<TX>::load8(res + vi * 8, r);
+    for (int j = 0; j < NV; ++j) {
+      const int vi = lane + 64 * j;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[j][e] += r[e];
-      }
+      for (int e = 0; e < 8; ++e) v[r][j][e] = 0.0f;
+      if (row < a.rows && vi < nvec) {
+        Elem<TX>::load8(x + vi * 8, v[r][j]);
+        if (res) {
+          float q[8];
+          Elem<TX>::load8(res + vi * 8, q);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sum += v[j][e];
-    }
-  }
-  const float mean = wave_sum(sum) / static_cast<float>(a.cols);
-  float sq = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    if (lane + 64 * j < nvec) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float d = v[j][e] - mean;
-        sq += d * d;
+          for (int e = 0; e < 8; ++e) v[r][j][e] += q[e];
+        }
       }
     }
   }
-  const float var = wave_sum(sq) / static_cast<float>(a.cols);
-  const float inv_std = 1.0f / sqrtf(var + a.epsilon);
   const float* scale = static_cast<const float*>(a.scale);
   const float* bias = static_cast<const float*>(a.bias);
-  TO* out = static_cast<TO*>(a.out) + row * a.cols;
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int vi = lane + 64 * j;
-    if (vi < nvec) {
-      float g[8], y[8];
-      Elem<float>::load8(scale + vi * 8, g);
-      float b[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      if (bias) Elem<float>::load8(bias + vi * 8, b);
+  for (int r = 0; r < ROWS; ++r) {
+    const int64_t row = row0 + r;
+    if (row >= a.rows) break;
+    float sum = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        y[e] = (v[j][e] - mean) * inv_std * g[e];
-        if (bias) y[e] += b[e];
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum += v[r][j][e];  // out-of-range vectors hold zeros
+    const float mean = wave_sum(sum) / static_cast<float>(a.cols);
+    float sq = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      if (lane + 64 * j < nvec) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = v[r][j][e] - mean;
+          sq += d * d;
+        }
       }
-      Elem<TO>::store8(out + vi * 8, y);
     }
-  }
-  if (lane == 0) {
-    if (a.mean_out) static_cast<float*>(a.mean_out)[row] = mean;
-    if (a.invstd_out) static_cast<float*>(a.invstd_out)[row] = inv_std;
+    const float var = wave_sum(sq) / static_cast<float>(a.cols);
+    const float inv_std = 1.0f / sqrtf(var + a.epsilon);
+    TO* out = static_cast<TO*>(a.out) + row * a.cols;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int vi = lane + 64 * j;
+      if (vi < nvec) {
+        float g[8], y[8];
+        Elem<float>::load8(scale + vi * 8, g);
+        float b[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (bias) Elem<float>::load8(bias + vi * 8, b);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          y[e] = (v[r][j][e] - mean) * inv_std * g[e];
+          if (bias) y[e] += b[e];
+        }
+        LnStore<TX, TO>::store8(out + vi * 8, y, a.out_scale, a.out_zero);
+      }
+    }
+    if (lane == 0) {
+      if (a.mean_out) static_cast<float*>(a.mean_out)[row] = mean;
+      if (a.invstd_out) static_cast<float*>(a.invstd_out)[row] = inv_std;
+    }
   }
 }
 
@@ -908,15 +965,19 @@ __global__ void __launch_bounds__(kBlock) maxpool_nhwc_vec_kernel(c3h_pool_args 
   }
 }
 
+// Rows per wave: 4 for rows of <= 512 columns, 2 for <= 1024 (measured
+// faster than 4 at 768 columns, where 4 rows keep 64 floats per lane
+// resident), else 1.
 template <typename TX, typename TO>
-void launch_ln(const c3h_layernorm_args& a, int blocks, int nv, void* stream) {
-  const dim3 g(blocks), b(kBlock);
+void launch_ln(const c3h_layernorm_args& a, int nv, void* stream) {
+  const dim3 b(kBlock);
   hipStream_t st = as_stream(stream);
+  auto grid = [&](int rows_per_wave) { return dim3(static_cast<unsigned>(ceil_div(a.rows, 4 * rows_per_wave))); };
   switch (nv) {
-    case 1: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 1>), g, b, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 2>), g, b, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 4>), g, b, 0, st, a); break;
-    default: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 8>), g, b, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 1, 4>), grid(4), b, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 2, 2>), grid(2), b, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 4, 1>), grid(1), b, 0, st, a); break;
+    default: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 8, 1>), grid(1), b, 0, st, a); break;
   }
 }
 
@@ -1071,18 +1132,28 @@ int c3h_layernorm(const c3h_layernorm_args* a, void* stream) {
   if (a->rows == 0) return C3H_OK;
   int blocks = static_cast<int>(ceil_div(a->rows, kBlock / 64));
   auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-  const bool vec = a->cols % 8 == 0 && a->cols <= 512 * kLnVec && al16(a->x) && al16(a->out) && al16(a->scale) &&
+  const bool quant = a->out_dtype == C3H_I8;
+  const bool vec = a->cols % 8 == 0 && a->cols <= 512 * kLnVec && al16(a->x) && al16(a->scale) &&
+                   (quant ? (reinterpret_cast<uintptr_t>(a->out) & 7) == 0 : al16(a->out)) &&
                    (!a->bias || al16(a->bias)) && (!a->residual || al16(a->residual)) &&
                    (a->x_dtype == C3H_F32 || a->x_dtype == C3H_BF16 || a->x_dtype == C3H_F16) &&
-                   (a->out_dtype == C3H_F32 || a->out_dtype == a->x_dtype);
+                   (a->out_dtype == C3H_F32 || a->out_dtype == a->x_dtype || quant);
+  C3H_REQUIRE(!quant || vec, "layernorm: an int8 (quantized) output needs cols %% 8 == 0, cols <= %d, "
+              "16-byte aligned inputs and an 8-byte aligned output", 512 * kLnVec);
+  C3H_REQUIRE(!quant || (a->out_scale > 0.0f && a->out_zero >= -128 && a->out_zero <= 127),
+              "layernorm: quantized output needs out_scale > 0 and an int8 zero point");
   if (vec) {
     const int nv = static_cast<int>(ceil_div(a->cols / 8, 64));
     const int NVsel = nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : 8;
-    if (a->x_dtype == C3H_F32) launch_ln<float, float>(*a, blocks, NVsel, stream);
-    else if (a->x_dtype == C3H_BF16 && a->out_dtype == C3H_F32) launch_ln<bf16_t, float>(*a, blocks, NVsel, stream);
-    else if (a->x_dtype == C3H_BF16) launch_ln<bf16_t, bf16_t>(*a, blocks, NVsel, stream);
-    else if (a->out_dtype == C3H_F32) launch_ln<f16_t, float>(*a, blocks, NVsel, stream);
-    else launch_ln<f16_t, f16_t>(*a, blocks, NVsel, stream);
+    if (quant) {
+      if (a->x_dtype == C3H_F32) launch_ln<float, int8_t>(*a, NVsel, stream);
+      else if (a->x_dtype == C3H_BF16) launch_ln<bf16_t, int8_t>(*a, NVsel, stream);
+      else launch_ln<f16_t, int8_t>(*a, NVsel, stream);
+    } else if (a->x_dtype == C3H_F32) launch_ln<float, float>(*a, NVsel, stream);
+    else if (a->x_dtype == C3H_BF16 && a->out_dtype == C3H_F32) launch_ln<bf16_t, float>(*a, NVsel, stream);
+    else if (a->x_dtype == C3H_BF16) launch_ln<bf16_t, bf16_t>(*a, NVsel, stream);
+    else if (a->out_dtype == C3H_F32) launch_ln<f16_t, float>(*a, NVsel, stream);
+    else launch_ln<f16_t, f16_t>(*a, NVsel, stream);
     return launch_status("layernorm_vec");
   }
   hipLaunchKernelGGL(layernorm_kernel, dim3(blocks), dim3(kBlock), 0, as_stream(stream), *a);

@@ -232,7 +232,12 @@ int c3h_softmax(const c3h_softmax_args* a, void* stream);
 
 /* LayerNorm over the trailing `cols` of each of `rows` rows, with optional
  * residual added first (FusedResidualNorm), optional bias, optional mean and
- * inverse-std outputs (c35/engine.py:484-532, 1078-1247). */
+ * inverse-std outputs (c35/engine.py:484-532, 1078-1247).
+ * out_dtype C3H_I8: the QuantizeLinear that consumes the LayerNorm, fused
+ * (W8A8 pre-LN inputs): each output is rounded to x_dtype -- the value the
+ * unfused LayerNorm would store -- then q = saturate(rne(y / out_scale) +
+ * out_zero), the codes c3h_quantize would produce from that stored value.
+ * Needs cols % 8 == 0 and cols <= 4096. */
 typedef struct {
   const void* x;
   const void* residual; /* may be NULL */
@@ -246,6 +251,8 @@ typedef struct {
   float epsilon;
   int32_t x_dtype;
   int32_t out_dtype;
+  float out_scale;      /* out_dtype C3H_I8 only */
+  int32_t out_zero;     /* out_dtype C3H_I8 only */
   int32_t pad_;
 } c3h_layernorm_args;
 int c3h_layernorm(const c3h_layernorm_args* a, void* stream);

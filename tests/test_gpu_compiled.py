@@ -87,7 +87,7 @@ def test_compiled_16bit_policy(gpu, name, policy):
     m = models.build(name, **SMALL[name])
     plan, prog, weights = _compiled(m, policy)
     got = _logits(prog, m.inputs)["logits"]
-    store = {**prog.weight_dtypes(), **prog.stored_dtypes()}
+    store = prog.rounding_map()
     refs = G.run_plan(plan, m.graph, weights, m.inputs, policy=policy, store=store)["logits"]
     ref32 = G.run_plan(plan, m.graph, weights, m.inputs)["logits"]
     got = got.reshape(ref32.shape)
@@ -121,7 +121,7 @@ def test_compiled_w8a8_decoder(gpu):
     m = models.build_decoder(**kw, act_scales={n: max(v, 1e-8) / 127.0 for n, v in ranges.items()})
     plan, prog, weights = _compiled(m, "w8a8")
     got = _logits(prog, m.inputs)["logits"]
-    store = {**prog.weight_dtypes(), **prog.stored_dtypes()}
+    store = prog.rounding_map()
     refs = G.run_plan(plan, m.graph, weights, m.inputs, policy="w8a8", store=store)["logits"]
     ref32 = G.run_plan(plan, m.graph, weights, m.inputs)["logits"]
     got = got.reshape(ref32.shape)

@@ -146,7 +146,7 @@ def test_fullsize_low_precision(gpu, name):
       0.02 below the emulation's.
     """
     m, folded, prog, out = _run_full(name)
-    store = {**prog.weight_dtypes(), **prog.stored_dtypes()}
+    store = prog.rounding_map()
     rows = SLICE[name]
     del prog
     _check_argmax_output(out)
@@ -218,8 +218,9 @@ def _teacher_forced(name: str):
     assert set(gpu_fold) == set(cpu_fold)
     fold_rel = _fold_difference(fused, m.weights, gpu_fold, cpu_fold)
     rows = SLICE[name] if name != "mlp" else 64
-    store = {**prog.weight_dtypes(), **prog.stored_dtypes()}
+    store = prog.rounding_map()
     teacher = {n: prog.read_value(n, rows) for n in prog.stored_dtypes()}
+    in_registers = set(prog.rounded_in_registers())
     del prog
     stats, ops = {}, {}
 
@@ -228,6 +229,13 @@ def _teacher_forced(name: str):
         st = {"kind": kind, "size": int(got.size), "max_ref": float(np.max(np.abs(ref))) if ref.size else 0.0}
         if kind in ("int8", "int32", "int64", "u8"):
             st["mismatch"] = int(np.count_nonzero(ref != got))
+            st["code_max"] = int(np.max(np.abs(ref.astype(np.int64) - got.astype(np.int64)))) if ref.size else 0
+            # codes of a QuantizeLinear fused into the LayerNorm launch: the
+            # oracle quantizes its own LayerNorm output (never stored, so not
+            # teacher-forced), which may sit one activation ulp away
+            prod_node = m.graph.nodes.get(m.graph.tensor_producer.get(n))
+            st["after_fused_ln"] = bool(prod_node is not None and prod_node.inputs and
+                                        prod_node.inputs[0] in in_registers)
         else:
             d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
             st["max_abs"] = float(d.max()) if d.size else 0.0
@@ -278,8 +286,10 @@ def _summarize(name, stats, ops):
     for (op, kind), items in sorted(by.items()):
         if kind in ("int8", "int32", "int64", "u8"):
             worst = max(items, key=lambda t: t[1]["mismatch"])
-            print(f"  {name} {op:>25} {kind:>5} x{len(items):3d}: mismatches max {worst[1]['mismatch']} "
-                  f"({worst[0]})", flush=True)
+            fused = sum(1 for t in items if t[1].get("after_fused_ln"))
+            print(f"  {name} {op:>25} {kind:>5} x{len(items):3d}: mismatches max {worst[1]['mismatch']} of "
+                  f"{worst[1]['size']}, |code diff| <= {worst[1]['code_max']} ({worst[0]}; {fused} quantized inside "
+                  f"a LayerNorm launch)", flush=True)
         elif kind in ("bf16", "fp16"):
             worst = max(items, key=lambda t: t[1]["max_abs"] / gates.ulp_at(t[1]["max_ref"], kind))
             gt1 = max(t[1]["frac_gt1"] for t in items)
@@ -298,7 +308,11 @@ def _summarize(name, stats, ops):
 def test_fullsize_per_value_teacher_forced(gpu, name):
     """Every value the full-size program stores, against the oracle's node
     recomputed from the program's own inputs (no error carried between nodes):
-      int8 (QuantizeLinear codes)            bit-exact
+      int8 (QuantizeLinear codes)            bit-exact; codes quantized inside the
+                                             LayerNorm launch (W8A8) within one code
+                                             on at most 1e-4 of elements, since the
+                                             oracle quantizes its own LayerNorm output
+                                             (one activation ulp at most, above)
       bf16 / fp16                            within one ulp at the tensor's
                                              largest magnitude, and at most
                                              0.1 % of elements more than one
@@ -320,7 +334,10 @@ def test_fullsize_per_value_teacher_forced(gpu, name):
     for n, st in stats.items():
         kind = st["kind"]
         if kind in ("int8", "int32", "int64", "u8"):
-            assert st["mismatch"] == 0, (n, st)
+            if st.get("after_fused_ln"):
+                assert st["code_max"] <= 1 and st["mismatch"] <= 1e-4 * st["size"], (n, st)
+            else:
+                assert st["mismatch"] == 0, (n, st)
         elif kind in ("bf16", "fp16"):
             assert st["max_abs"] <= gates.ulp_at(st["max_ref"], kind), (n, ops[n], st)
             if ops[n] != "MatMul":

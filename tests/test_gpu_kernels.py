@@ -1014,3 +1014,47 @@ def test_gemm_splitk_one_call_equals_two_launches(gpu, kind, m, n, k, splits):
     short = DeviceArray.empty((splits * m * n - 1,), np.float32)
     rc = _lib.lib().c3h_gemm_splitk(C.byref(g), splits, short.ptr, short.nbytes, None)
     assert rc != 0 and "workspace" in _lib.last_error()
+
+
+@pytest.mark.parametrize("rows,cols,dt,res", [(16 * 1024, 768, "bf16", False), (37, 512, "fp16", True),
+                                              (5, 1024, "fp32", True), (9, 24, "bf16", False),
+                                              (16 * 1024, 768, "bf16", True)])
+def test_layernorm_int8_output_equals_layernorm_then_quantize(gpu, rows, cols, dt, res):
+    """LayerNorm with the QuantizeLinear fused (out_dtype I8, the W8A8 pre-LN
+    inputs) gives exactly the codes of LayerNorm -> stored activation ->
+    c3h_quantize, including saturated codes and a nonzero zero point."""
+    from hackathon_amd import _lib
+    from hackathon_amd.device import BF16, DeviceArray
+
+    rng = np.random.default_rng(rows * 3 + cols)
+    x32 = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
+    r32 = rng.standard_normal((rows, cols)).astype(np.float32)
+    if dt == "fp32":
+        xd, rd, code, sdt = _dev(x32), _dev(r32), _lib.F32, np.float32
+    else:
+        xd, rd = _dev(_bits(x32, dt)[0]), _dev(_bits(r32, dt)[0])
+        code, sdt = (_lib.BF16, BF16) if dt == "bf16" else (_lib.F16, np.float16)
+    gd = _dev(rng.uniform(0.5, 1.5, cols).astype(np.float32))
+    bd = _dev(rng.standard_normal(cols).astype(np.float32) * 0.1)
+    qscale, qzero = 0.019, -3  # some codes saturate at +-127/-128
+    mid = DeviceArray.empty((rows, cols), sdt)
+    codes_a = DeviceArray.empty((rows, cols), np.int8)
+    codes_b = DeviceArray.empty((rows, cols), np.int8)
+
+    def ln(out, out_code):
+        a = _lib.LayerNormArgs()
+        a.x, a.residual, a.scale, a.bias, a.out = xd.ptr, rd.ptr if res else None, gd.ptr, bd.ptr, out.ptr
+        a.rows, a.cols, a.epsilon, a.x_dtype, a.out_dtype = rows, cols, 1e-5, code, out_code
+        a.out_scale, a.out_zero = qscale, qzero
+        _lib.launch(a, None)
+
+    print(f"layernorm->int8 rows={rows} cols={cols} {dt} res={res}", flush=True)
+    ln(mid, code)
+    q = _lib.QuantizeArgs()
+    q.x, q.out, q.count, q.scale, q.zero_point, q.x_dtype = mid.ptr, codes_a.ptr, rows * cols, qscale, qzero, code
+    _lib.launch(q, None)
+    codes_b.copy_from_host(np.full(rows * cols, 77, np.int8))
+    ln(codes_b, _lib.I8)
+    a_, b_ = codes_a.get(), codes_b.get()
+    np.testing.assert_array_equal(a_, b_)
+    assert (a_ == 127).any() and (a_ == -128).any()
