@@ -1,1592 +1,17 @@
-// Contraction kernels of libc3hip.so (gfx950): GEMM and implicit-GEMM Conv2d
-// on MFMA, fp32 accumulation, LDS double-buffered tiles and a fused epilogue.
-//
-//   fp32  : v_mfma_f32_16x16x4_f32   (configs 1-2, the reference's fp32 policy)
-//   bf16  : v_mfma_f32_16x16x32_bf16 (config 3)
-//   f16   : v_mfma_f32_16x16x32_f16  (config 4)
-//
-// A 256-thread workgroup (4 wave64s) computes a BM x BN macro tile; each wave
-// owns a (BM/WM) x (BN/WN) sub-tile of 16x16 MFMA tiles.  A and B tiles are
-// staged global -> registers -> LDS with two LDS buffers, so the loads of
-// tile k+1 are in flight while the MFMAs of tile k run.  Tile ids are
-// remapped so that consecutive tiles (sharing an A row panel) land on the
-// same XCD and hit its L2.
+// C entry points of the contraction kernels (GEMM, implicit-GEMM Conv2d,
+// split-K, int8 and fp8 GEMM).  The kernels and launch templates live in
+// gemm_kernels.h; the per-type launchers are instantiated in gemm_bf16.hip,
+// gemm_bf16_conv.hip, gemm_f16.hip, gemm_f16_conv.hip, gemm_i8.hip,
+// gemm_f8.hip and gemm_f32.hip.
 #include <stdlib.h>
 #include <mutex>
-#include <type_traits>
-#include <utility>
 
-#include "common.h"
+#include "gemm_kernels.h"
 
 using namespace c3h;
+using namespace c3h::gk;
 
 namespace {
-
-typedef __attribute__((ext_vector_type(4))) float f32x4;
-typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
-typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
-
-constexpr int kThreads = 256;
-
-// Kernel-argument view: the (single) by-value argument read in place through
-// the kernarg segment pointer (constant address space, scalar loads), so a
-// dynamically indexed epilogue program never makes the compiler copy the
-// argument struct into scratch memory.
-template <typename T>
-using KArg = __attribute__((address_space(4))) T;
-
-template <typename P>
-__device__ __forceinline__ const KArg<P>& kernel_arg() {
-  return *(const KArg<P>*)(__builtin_amdgcn_kernarg_segment_ptr());
-}
-
-// GELU as the decomposed ONNX chain Div -> Erf -> Add -> Mul -> Mul computes
-// it, operation for operation: ((x * (erf(x / c0) + c1)) * c2) with the
-// chain's constants (c0 = sqrt(2), c1 = 1, c2 = 0.5 in practice).
-__device__ __forceinline__ float gelu_erf(float x, float c0, float c1, float c2) {
-  const float t = erff(x / c0) + c1;
-  return (x * t) * c2;
-}
-
-// ---------------------------------------------------------------- epilogue
-// `e` is read straight from the kernel-argument segment (uniform scalar
-// loads); `bias_off` selects the batch's bias slice.
-__device__ __forceinline__ float apply_epilogue(const KArg<c3h_epilogue>& e, float acc, int64_t m, int64_t n,
-                                                int64_t ldb_bias, float res, int64_t bias_off = 0) {
-  float v = e.alpha * acc;
-  const float* bias = static_cast<const float*>(e.bias) + bias_off;
-  switch (e.bias_mode) {
-    case 1: v += e.beta * bias[0]; break;
-    case 2: v += e.beta * bias[n]; break;
-    case 3: v += e.beta * bias[m]; break;
-    case 4: v += e.beta * bias[m * ldb_bias + n]; break;
-    default: break;
-  }
-  v += res;
-  if (e.act == 1) v = fmaxf(v, 0.0f);
-  else if (e.act == 2) v = gelu_erf(v, e.imm[0], e.imm[1], e.imm[2]);
-  if (e.n_inst > 0) {
-    // Linear program: operand 0 = x (the value entering the program),
-    // 1 = previous result, 2 + j = imm[j].  No register file, so the
-    // program costs no scratch memory in register-heavy GEMM kernels.
-    const float x = v;
-    float prev = v;
-    for (int i = 0; i < e.n_inst; ++i) {
-      const int ca = e.inst[i].a, cb = e.inst[i].b;
-      const float oa = ca == 0 ? x : (ca == 1 ? prev : e.imm[ca - 2]);
-      const float ob = cb == 0 ? x : (cb == 1 ? prev : e.imm[cb - 2]);
-      prev = ew_apply(e.inst[i].op, oa, ob, e.inst[i].imm);
-    }
-    v = prev;
-  }
-  return v;
-}
-
-// Epilogue of 8 consecutive columns n..n+7 of row m, in the same order and
-// arithmetic as apply_epilogue.  Every decision is uniform across the wave
-// and is taken once per 8 values, and bias_mode 2 reads its 8 bias values
-// as two float4 loads when they are 16-byte aligned.
-__device__ __forceinline__ void apply_epilogue8(const KArg<c3h_epilogue>& e, float* v, int64_t m, int64_t n,
-                                                int64_t ldb_bias, const float* res, int64_t bias_off) {
-  const float alpha = e.alpha, beta = e.beta;
-  if (alpha != 1.0f) {
-#pragma unroll
-    for (int c = 0; c < 8; ++c) v[c] = alpha * v[c];
-  }
-  const float* bias = static_cast<const float*>(e.bias) + bias_off;
-  const int bm = e.bias_mode;
-  if (bm == 2) {
-    float b[8];
-    if ((reinterpret_cast<uintptr_t>(bias + n) & 15) == 0) {
-      const float4 b0 = *reinterpret_cast<const float4*>(bias + n), b1 = *reinterpret_cast<const float4*>(bias + n + 4);
-      b[0] = b0.x; b[1] = b0.y; b[2] = b0.z; b[3] = b0.w; b[4] = b1.x; b[5] = b1.y; b[6] = b1.z; b[7] = b1.w;
-    } else {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) b[c] = bias[n + c];
-    }
-#pragma unroll
-    for (int c = 0; c < 8; ++c) v[c] += beta * b[c];
-  } else if (bm == 1) {
-    const float b = beta * bias[0];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) v[c] += b;
-  } else if (bm == 3) {
-    const float b = beta * bias[m];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) v[c] += b;
-  } else if (bm == 4) {
-#pragma unroll
-    for (int c = 0; c < 8; ++c) v[c] += beta * bias[m * ldb_bias + n + c];
-  }
-#pragma unroll
-  for (int c = 0; c < 8; ++c) v[c] += res[c];
-  const int act = e.act;
-  if (act == 1) {
-#pragma unroll
-    for (int c = 0; c < 8; ++c) v[c] = fmaxf(v[c], 0.0f);
-  } else if (act == 2) {
-    const float c0 = e.imm[0], c1 = e.imm[1], c2 = e.imm[2];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) v[c] = gelu_erf(v[c], c0, c1, c2);
-  }
-  const int ni = e.n_inst;
-  if (ni > 0) {
-    float x[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) x[c] = v[c];
-    for (int i = 0; i < ni; ++i) {
-      const int op = e.inst[i].op, ca = e.inst[i].a, cb = e.inst[i].b;
-      const float imm = e.inst[i].imm;
-      const float ia = ca >= 2 ? e.imm[ca - 2] : 0.0f, ib = cb >= 2 ? e.imm[cb - 2] : 0.0f;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const float oa = ca == 0 ? x[c] : (ca == 1 ? v[c] : ia);
-        const float ob = cb == 0 ? x[c] : (cb == 1 ? v[c] : ib);
-        v[c] = ew_apply(op, oa, ob, imm);
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------- problem
-// Division by an invariant d for n < 2^31 (Granlund & Montgomery 1994, the
-// round-up multiplier with a 33-bit add): l = ceil(log2 d),
-// mul = floor(2^32 (2^l - d) / d) + 1, q = (mulhi(n, mul) + n) >> l.
-struct FastDiv {
-  uint32_t mul, shift;
-};
-
-// Buffer-load byte offset past every num_records used here: reads zeros.
-constexpr uint32_t kOobOffset = 0x80000000u;
-
-inline FastDiv make_fastdiv(uint32_t d) {
-  uint32_t l = 0;
-  while ((uint64_t{1} << l) < d) ++l;
-  const uint64_t mul = ((uint64_t{1} << 32) * ((uint64_t{1} << l) - d)) / d + 1;
-  return FastDiv{static_cast<uint32_t>(mul), l};
-}
-
-// Everything the kernels need, flattened from the gemm/conv args.
-struct Problem {
-  const void* a;
-  const void* b;
-  void* out;
-  int64_t m, n, k;
-  int64_t lda, ldb, ldo;
-  int64_t stride_a, stride_b, stride_out, stride_bias, stride_res;
-  int trans_a, trans_b;
-  int out_dtype;
-  // conv geometry (A_MODE == kConv)
-  int cn, cc, ch, cw, c_stride, c_pack, kh, kw, kw_pack, sh, sw, pt, pl, dh, dw, ho, wo;
-  int out_nchw;  // conv: write NCHW instead of NHWC
-  int tiles_m, tiles_n;
-  // conv index divisors: ho*wo, wo, c_pack, kw_pack
-  FastDiv fd_hw, fd_wo, fd_cpack, fd_kwpack;
-  // byte extents of A and B (buffer-resource bounds of the pipelined kernel)
-  int64_t a_bytes, b_bytes;
-  // int8 GEMM (c3h_qgemm): output mode and quantization parameters
-  int qmode, y_zero;
-  float a_scale, y_scale;
-  const float* b_scale;
-  const float* a_rows;  // fp8 GEMM (c3h_gemm_fp8): per-row A scale
-  c3h_epilogue epi;
-};
-
-enum AMode { kDenseK = 0, kDenseM = 1, kConv = 2 };
-
-// XCD-aware tile id: hardware dispatches workgroup i to XCD i % 8.  Give each
-// XCD a contiguous range of tile ids (N-fastest) so neighbouring tiles that
-// share an A panel share an L2.
-__device__ __forceinline__ void tile_coords(const Problem& p, int& tm, int& tn) {
-  const int total = p.tiles_m * p.tiles_n;
-  int bid = blockIdx.x;
-  int tile = bid;
-  if ((total & 7) == 0) {
-    const int per = total >> 3;
-    tile = (bid & 7) * per + (bid >> 3);
-  }
-  tm = tile / p.tiles_n;
-  tn = tile - tm * p.tiles_n;
-}
-
-// Decomposed conv output row m -> (input row base offset, hi0, wi0).
-struct ConvRow {
-  int64_t base;  // element offset of x[n][0][0][0]
-  int hi0, wi0;
-  bool valid;
-};
-
-__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
-  return (__umulhi(n, f.mul) + n) >> f.shift;
-}
-
-// m < 2^31 (checked on the host): 32-bit index math with invariant divisors.
-__device__ __forceinline__ ConvRow conv_row(const Problem& p, int64_t m) {
-  ConvRow r;
-  r.valid = m < p.m;
-  const uint32_t mm = r.valid ? static_cast<uint32_t>(m) : 0u;
-  const uint32_t img = fdiv(mm, p.fd_hw);
-  const uint32_t rem = mm - img * static_cast<uint32_t>(p.ho * p.wo);
-  const uint32_t ho = fdiv(rem, p.fd_wo);
-  const uint32_t wo = rem - ho * static_cast<uint32_t>(p.wo);
-  r.base = static_cast<int64_t>(img) * p.ch * p.cw * p.c_stride;
-  r.hi0 = static_cast<int>(ho) * p.sh - p.pt;
-  r.wi0 = static_cast<int>(wo) * p.sw - p.pl;
-  return r;
-}
-
-// Element offset in x of the VEC-wide K slice starting at k, or -1 when it is
-// padding.  K order is (kh, kw_pack, c_pack) with c fastest.
-__device__ __forceinline__ int64_t conv_k_offset(const Problem& p, const ConvRow& r, int64_t k) {
-  if (!r.valid || k >= p.k) return -1;
-  const uint32_t kk = static_cast<uint32_t>(k);
-  const uint32_t tap = fdiv(kk, p.fd_cpack);
-  const int c0 = static_cast<int>(kk - tap * static_cast<uint32_t>(p.c_pack));
-  const uint32_t khi = fdiv(tap, p.fd_kwpack);
-  const int kwi = static_cast<int>(tap - khi * static_cast<uint32_t>(p.kw_pack));
-  if (kwi >= p.kw || c0 >= p.cc) return -1;
-  const int hi = r.hi0 + static_cast<int>(khi) * p.dh;
-  const int wi = r.wi0 + kwi * p.dw;
-  if (hi < 0 || hi >= p.ch || wi < 0 || wi >= p.cw) return -1;
-  return r.base + (static_cast<int64_t>(hi) * p.cw + wi) * p.c_stride + c0;
-}
-
-// Epilogue through LDS: a wave stages one 16-row strip of its accumulator
-// sub-tile (16 x WTN fp32, row stride WTN + 4) and then stores it with
-// consecutive lanes on consecutive output addresses: row-major [m, n] output
-// is written as 4 lanes per row, WTN/4 contiguous columns each; NCHW conv
-// output is written one column (channel) per lane, 16 consecutive pixels.
-template <typename TO, int WTN>
-__device__ __forceinline__ void store_strip(const Problem& p, const float* stage, int lane, int64_t mrow0,
-                                            int64_t ncol0, TO* outp, const TO* resp, int64_t bias_off) {
-  constexpr int SS = WTN + 4;
-  if (!p.out_nchw) {
-    const int row = lane >> 2;
-    const int c0 = (lane & 3) * (WTN / 4);
-    const int64_t m = mrow0 + row;
-    if (m >= p.m) return;
-    for (int c = 0; c < WTN / 4; ++c) {
-      const int64_t n = ncol0 + c0 + c;
-      if (n >= p.n) break;
-      const int64_t o = m * p.ldo + n;
-      const float res = resp ? Elem<TO>::to_f32(resp[o]) : 0.0f;
-      outp[o] = Elem<TO>::from_f32(apply_epilogue(kernel_arg<Problem>().epi, stage[row * SS + c0 + c], m, n, p.n, res, bias_off));
-    }
-  } else {
-    const int64_t hw = static_cast<int64_t>(p.ho) * p.wo;
-    for (int col = lane; col < WTN; col += 64) {
-      const int64_t n = ncol0 + col;
-      if (n >= p.n) break;
-      for (int row = 0; row < 16; ++row) {
-        const int64_t m = mrow0 + row;
-        if (m >= p.m) break;
-        const int64_t img = m / hw, pix = m - img * hw;
-        const int64_t o = (img * p.n + n) * hw + pix;
-        const float res = resp ? Elem<TO>::to_f32(resp[o]) : 0.0f;
-        outp[o] = Elem<TO>::from_f32(apply_epilogue(kernel_arg<Problem>().epi, stage[row * SS + col], m, n, p.n, res, bias_off));
-      }
-    }
-  }
-}
-
-__device__ __forceinline__ void wave_sync_lds() {
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-  __builtin_amdgcn_wave_barrier();
-}
-
-// =====================================================================
-// fp32 kernel: v_mfma_f32_16x16x4_f32.  LDS tiles are stored k-major
-// (As[k][m], Bs[k][n]) so each lane's MFMA operand is one conflict-free
-// ds_read_b32.
-// =====================================================================
-template <int BM, int BN, int WM, int WN, int AM, bool B_KCONTIG>
-__global__ void __launch_bounds__(kThreads) gemm_f32_kernel(Problem p) {
-  constexpr int BK = 16;
-  constexpr int PADM = 16;  // row stride = BM + 16 floats -> 16-bank skew per k
-  constexpr int SA = BM + PADM, SB = BN + PADM;
-  constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
-  constexpr int WTN = BN / WN;
-  constexpr int kTileFloats = 2 * BK * SA + 2 * BK * SB;
-  constexpr int kStageFloats = 4 * 16 * (WTN + 4);
-  __shared__ __attribute__((aligned(16))) float smem[kTileFloats > kStageFloats ? kTileFloats : kStageFloats];
-  float (*As)[BK][SA] = reinterpret_cast<float (*)[BK][SA]>(smem);
-  float (*Bs)[BK][SB] = reinterpret_cast<float (*)[BK][SB]>(smem + 2 * BK * SA);
-
-  int tm, tn;
-  tile_coords(p, tm, tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
-  const int64_t bz = blockIdx.z;
-  const float* A = static_cast<const float*>(p.a) + bz * p.stride_a;
-  const float* B = static_cast<const float*>(p.b) + bz * p.stride_b;
-
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave / WN, wn = wave % WN;
-
-  // A tile: BM x BK floats.  K-contiguous modes: thread loads float4 along k
-  // (4 threads per row).  M-contiguous mode: float4 along m.
-  constexpr int A_VECS = BM * BK / 4 / kThreads;  // float4 per thread
-  constexpr int B_VECS = BN * BK / 4 / kThreads;
-  static_assert(A_VECS >= 1 && B_VECS >= 1, "tile too small");
-  float4 ra[A_VECS], rb[B_VECS];
-
-  ConvRow crow[A_VECS];
-  if (AM == kConv) {
-#pragma unroll
-    for (int i = 0; i < A_VECS; ++i) {
-      int e = tid + kThreads * i;
-      crow[i] = conv_row(p, m0 + e / (BK / 4));
-    }
-  }
-
-  auto load_a = [&](int64_t k0) {
-#pragma unroll
-    for (int i = 0; i < A_VECS; ++i) {
-      int e = tid + kThreads * i;
-      if (AM == kDenseM) {
-        int kr = e / (BM / 4), mc = (e % (BM / 4)) * 4;
-        int64_t k = k0 + kr, m = m0 + mc;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (k < p.k) {
-          const float* src = A + k * p.lda + m;
-          if (m + 3 < p.m) v = *reinterpret_cast<const float4*>(src);
-          else {
-            if (m < p.m) v.x = src[0];
-            if (m + 1 < p.m) v.y = src[1];
-            if (m + 2 < p.m) v.z = src[2];
-          }
-        }
-        ra[i] = v;
-      } else {
-        int mr = e / (BK / 4), kc = (e % (BK / 4)) * 4;
-        int64_t m = m0 + mr, k = k0 + kc;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (AM == kDenseK) {
-          if (m < p.m) {
-            const float* src = A + m * p.lda + k;
-            if (k + 3 < p.k) v = *reinterpret_cast<const float4*>(src);
-            else {
-              if (k < p.k) v.x = src[0];
-              if (k + 1 < p.k) v.y = src[1];
-              if (k + 2 < p.k) v.z = src[2];
-            }
-          }
-        } else {
-          int64_t off = conv_k_offset(p, crow[i], k);
-          if (off >= 0) v = *reinterpret_cast<const float4*>(A + off);
-        }
-        ra[i] = v;
-      }
-    }
-  };
-  auto load_b = [&](int64_t k0) {
-#pragma unroll
-    for (int i = 0; i < B_VECS; ++i) {
-      int e = tid + kThreads * i;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (B_KCONTIG) {  // B stored [n][k]
-        int nr = e / (BK / 4), kc = (e % (BK / 4)) * 4;
-        int64_t n = n0 + nr, k = k0 + kc;
-        if (n < p.n) {
-          const float* src = B + n * p.ldb + k;
-          if (k + 3 < p.k) v = *reinterpret_cast<const float4*>(src);
-          else {
-            if (k < p.k) v.x = src[0];
-            if (k + 1 < p.k) v.y = src[1];
-            if (k + 2 < p.k) v.z = src[2];
-          }
-        }
-      } else {  // B stored [k][n]
-        int kr = e / (BN / 4), nc = (e % (BN / 4)) * 4;
-        int64_t k = k0 + kr, n = n0 + nc;
-        if (k < p.k) {
-          const float* src = B + k * p.ldb + n;
-          if (n + 3 < p.n) v = *reinterpret_cast<const float4*>(src);
-          else {
-            if (n < p.n) v.x = src[0];
-            if (n + 1 < p.n) v.y = src[1];
-            if (n + 2 < p.n) v.z = src[2];
-          }
-        }
-      }
-      rb[i] = v;
-    }
-  };
-  auto store_tiles = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < A_VECS; ++i) {
-      int e = tid + kThreads * i;
-      if (AM == kDenseM) {
-        int kr = e / (BM / 4), mc = (e % (BM / 4)) * 4;
-        *reinterpret_cast<float4*>(&As[buf][kr][mc]) = ra[i];
-      } else {
-        int mr = e / (BK / 4), kc = (e % (BK / 4)) * 4;
-        As[buf][kc + 0][mr] = ra[i].x;
-        As[buf][kc + 1][mr] = ra[i].y;
-        As[buf][kc + 2][mr] = ra[i].z;
-        As[buf][kc + 3][mr] = ra[i].w;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < B_VECS; ++i) {
-      int e = tid + kThreads * i;
-      if (B_KCONTIG) {
-        int nr = e / (BK / 4), kc = (e % (BK / 4)) * 4;
-        Bs[buf][kc + 0][nr] = rb[i].x;
-        Bs[buf][kc + 1][nr] = rb[i].y;
-        Bs[buf][kc + 2][nr] = rb[i].z;
-        Bs[buf][kc + 3][nr] = rb[i].w;
-      } else {
-        int kr = e / (BN / 4), nc = (e % (BN / 4)) * 4;
-        *reinterpret_cast<float4*>(&Bs[buf][kr][nc]) = rb[i];
-      }
-    }
-  };
-
-  f32x4 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int64_t ktiles = ceil_div(p.k, BK);
-  load_a(0);
-  load_b(0);
-  store_tiles(0);
-  __syncthreads();
-  const int lrow = lane & 15, lk = lane >> 4;
-  for (int64_t kt = 0; kt < ktiles; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < ktiles) {
-      load_a((kt + 1) * BK);
-      load_b((kt + 1) * BK);
-    }
-#pragma unroll
-    for (int ks = 0; ks < BK / 4; ++ks) {
-      float av[TM], bv[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) av[i] = As[cur][ks * 4 + lk][wm * (BM / WM) + i * 16 + lrow];
-#pragma unroll
-      for (int j = 0; j < TN; ++j) bv[j] = Bs[cur][ks * 4 + lk][wn * (BN / WN) + j * 16 + lrow];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < ktiles) {
-      store_tiles(cur ^ 1);
-      __syncthreads();
-    }
-  }
-
-  // Epilogue: lane holds rows 4*(lane/16)+r, col lane%16 of each 16x16 tile;
-  // stage each 16-row strip through LDS and store it coalesced.
-  float* outp = static_cast<float*>(p.out) + bz * p.stride_out;
-  const float* resp = p.epi.residual ? static_cast<const float*>(p.epi.residual) + bz * p.stride_res : nullptr;
-  const int64_t bias_off = bz * p.stride_bias;
-  __syncthreads();
-  float* stage = smem + wave * 16 * (WTN + 4);
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) stage[(lk * 4 + r) * (WTN + 4) + j * 16 + lrow] = acc[i][j][r];
-    wave_sync_lds();
-    store_strip<float, WTN>(p, stage, lane, m0 + wm * (BM / WM) + i * 16, n0 + wn * WTN, outp, resp, bias_off);
-    wave_sync_lds();
-  }
-}
-
-// =====================================================================
-// MFMA kernel for 16-bit (v_mfma_f32_16x16x32_{bf16,f16}) and int8
-// (v_mfma_i32_16x16x64_i8, exact int32 accumulation) operands.  A tile row
-// is 128 bytes of K (64 16-bit or 128 int8 elements); LDS rows hold eight
-// 16-byte chunks XOR-swizzled by (row & 7), so a lane's MFMA operand is one
-// ds_read_b128 and 8 consecutive rows reading the same K chunk hit 8
-// distinct bank groups.  Every thread moves 16-byte vectors; since 256 % 8
-// == 0 a thread's vectors share one K chunk and step 32 rows apart.
-//
-// A operand modes:
-//   kDenseK    A[m][k] row-major (lda).
-//   kConvTap   implicit-GEMM conv with c_pack % 64 == 0: a 64-wide K tile lies
-//              inside one filter tap, so (kh, kw, c0) is uniform per tile and
-//              advanced incrementally; each row keeps its pixel base.
-//   kConv      generic implicit GEMM (c_pack % 8 == 0): per-vector tap math.
-//   kConvStem  c_pack == c_stride == 4, kw padded to 8: a vector is two taps
-//              of one input row (two 8-byte halves, each bounds-checked).
-// =====================================================================
-typedef __attribute__((ext_vector_type(4))) int i32x4;
-
-// kStep: 16-byte K chunks of a tile row one MFMA consumes per lane group
-// (4: two MFMA steps per 128-byte row; 8: one step).  kScaled: accumulators
-// are multiplied by a_rows[m] * b_scale[n] before the epilogue.
-struct MmaBF16 {
-  typedef bf16x8 vec;
-  typedef f32x4 acc_t;
-  static constexpr int ES = 2;
-  static constexpr bool kInt = false;
-  static constexpr int kStep = 4;
-  static constexpr bool kScaled = false;
-  static __device__ __forceinline__ acc_t mma(vec a, vec b, acc_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-};
-struct MmaF16 {
-  typedef f16x8 vec;
-  typedef f32x4 acc_t;
-  static constexpr int ES = 2;
-  static constexpr bool kInt = false;
-  static constexpr int kStep = 4;
-  static constexpr bool kScaled = false;
-  static __device__ __forceinline__ acc_t mma(vec a, vec b, acc_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
-struct MmaI8 {
-  typedef i32x4 vec;
-  typedef i32x4 acc_t;
-  static constexpr int ES = 1;
-  static constexpr bool kInt = true;
-  static constexpr int kStep = 4;
-  static constexpr bool kScaled = false;
-  static __device__ __forceinline__ acc_t mma(vec a, vec b, acc_t c) {
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-  }
-};
-// OCP E4M3 x E4M3 -> fp32 (v_mfma_f32_16x16x128_f8f6f4, format code 0 on
-// both operands, no block scales).  A lane supplies 32 K bytes: lane group g
-// (lane >> 4) takes tile-row chunks g and g + 4.  A and B use the same
-// lane/byte -> k assignment, so the dot product covers each k exactly once
-// whatever order the instruction walks K in.
-typedef __attribute__((ext_vector_type(8))) int i32x8;
-struct MmaF8 {
-  typedef i32x8 vec;
-  typedef f32x4 acc_t;
-  static constexpr int ES = 1;
-  static constexpr bool kInt = false;
-  static constexpr int kStep = 8;
-  static constexpr bool kScaled = true;
-  static __device__ __forceinline__ acc_t mma(vec a, vec b, acc_t c) {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
-  }
-};
-
-// MFMA operand of tile row `r` (row base `row`, XOR-swizzled 16-byte chunks)
-// for the K step starting at chunk ks.
-template <typename Mma>
-__device__ __forceinline__ typename Mma::vec read_operand(const uint8_t* row, int r, int ks, int lchunk) {
-  if constexpr (Mma::kStep == 8) {
-    const i32x4 lo = *reinterpret_cast<const i32x4*>(row + ((lchunk ^ (r & 7)) << 4));
-    const i32x4 hi = *reinterpret_cast<const i32x4*>(row + (((lchunk + 4) ^ (r & 7)) << 4));
-    return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  } else {
-    return *reinterpret_cast<const typename Mma::vec*>(row + (((ks + lchunk) ^ (r & 7)) << 4));
-  }
-}
-
-enum AMode16 { kConvTap = 3, kConvStem = 4 };
-
-// Grouped tile order: each XCD (blockIdx % 8) owns a contiguous range of tile
-// ids, walked in column-major groups of 8 tile rows so blocks resident at
-// the same time share both A and B panels in that XCD's L2.
-__device__ __forceinline__ void tile_coords_of(const Problem& p, int id, int& tm, int& tn) {
-  // XCD x = id % 8 receives ids x, x + 8, ...: count q + (x < r) of them for
-  // total = 8 q + r; its j-th one takes tile x q + min(x, r) + j, so every
-  // XCD walks a contiguous tile range (a bijection for any total).
-  const int total = p.tiles_m * p.tiles_n;
-  const int x = id & 7, q = total >> 3, r = total & 7;
-  const int tile = x * q + min(x, r) + (id >> 3);
-  constexpr int G = 8;
-  const int group = tile / (G * p.tiles_n);
-  const int first_m = group * G;
-  const int gsize = min(p.tiles_m - first_m, G);
-  const int in_group = tile - group * G * p.tiles_n;
-  tm = first_m + in_group % gsize;
-  tn = in_group / gsize;
-}
-__device__ __forceinline__ void tile_coords_grouped(const Problem& p, int& tm, int& tn) {
-  tile_coords_of(p, blockIdx.x, tm, tn);
-}
-
-// Vectorized epilogue of one 16-row strip (row-major [m, n] output): each
-// lane owns 8 consecutive columns, so a row is written as WTN/8 16-byte
-// (bf16/fp16) or 32-byte (fp32) stores.  Called from a runtime loop over
-// strips: the whole wave tile is staged in LDS first, so the accumulators are
-// only ever indexed by unrolled (constant) indices.
-template <typename TO, int WTN>
-__device__ __forceinline__ void store_strip_vec(const float* stage, int lane, int64_t mrow0, int64_t ncol0,
-                                                          TO* outp, const TO* resp, int64_t bias_off, bool vec_ok) {
-  const KArg<Problem>& p = kernel_arg<Problem>();
-  constexpr int SS = WTN + 4;
-  constexpr int LPR = WTN / 8;
-  constexpr int RPP = 64 / LPR;
-  static_assert(LPR >= 1 && 64 % LPR == 0 && RPP <= 16, "strip shape");
-  const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
-  for (int pass = 0; pass < 16 / RPP; ++pass) {
-    const int row = pass * RPP + lane / LPR;
-    const int c0 = (lane % LPR) * 8;
-    const int64_t m = mrow0 + row;
-    const int64_t n = ncol0 + c0;
-    if (m >= pm || n >= pn) continue;
-    const float4 lo = *reinterpret_cast<const float4*>(stage + row * SS + c0);
-    const float4 hi = *reinterpret_cast<const float4*>(stage + row * SS + c0 + 4);
-    float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-    const int64_t o = m * ldo + n;
-    if (vec_ok && n + 8 <= pn) {
-      float res[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      if (resp) Elem<TO>::load8(resp + o, res);
-      apply_epilogue8(p.epi, v, m, n, pn, res, bias_off);
-      Elem<TO>::store8(outp + o, v);
-    } else {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        if (n + c < pn) {
-          const float res = resp ? Elem<TO>::to_f32(resp[o + c]) : 0.0f;
-          outp[o + c] = Elem<TO>::from_f32(apply_epilogue(p.epi, v[c], m, n + c, pn, res, bias_off));
-        }
-      }
-    }
-  }
-}
-
-// int8 GEMM epilogue of one 16-row strip: the stage holds int32 accumulator
-// bits.  qmode 0 writes int32, 1 requantizes to int8, 2 dequantizes, 3
-// requantizes then dequantizes (QLinearMatMul -> DequantizeLinear); 2 and 3
-// continue through the float epilogue into TO.
-template <typename TO, int WTN>
-__device__ __forceinline__ void store_strip_q(const float* stage, int lane, int64_t mrow0, int64_t ncol0, TO* outp,
-                                              const TO* resp, bool vec_ok) {
-  const KArg<Problem>& p = kernel_arg<Problem>();
-  constexpr int SS = WTN + 4;
-  constexpr int LPR = WTN / 8;
-  constexpr int RPP = 64 / LPR;
-  const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
-  const int mode = p.qmode;
-  const float sa = p.a_scale, sy = p.y_scale, zy = static_cast<float>(p.y_zero);
-  const float* sb = p.b_scale;
-  for (int pass = 0; pass < 16 / RPP; ++pass) {
-    const int row = pass * RPP + lane / LPR;
-    const int c0 = (lane % LPR) * 8;
-    const int64_t m = mrow0 + row;
-    const int64_t n = ncol0 + c0;
-    if (m >= pm || n >= pn) continue;
-    const int4 lo = *reinterpret_cast<const int4*>(stage + row * SS + c0);
-    const int4 hi = *reinterpret_cast<const int4*>(stage + row * SS + c0 + 4);
-    const int acc[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-    const int64_t o = m * ldo + n;
-    const bool full = vec_ok && n + 8 <= pn;
-    if constexpr (std::is_same<TO, int32_t>::value) {
-      int32_t* out = outp;
-      if (full) {
-        reinterpret_cast<int4*>(out + o)[0] = lo;
-        reinterpret_cast<int4*>(out + o)[1] = hi;
-      } else {
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-          if (n + c < pn) out[o + c] = acc[c];
-      }
-    } else {
-      float v[8];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const float bsc = n + c < pn ? sb[n + c] : 0.0f;
-        if (mode == 1 || mode == 3) {
-          const float mult = (sa * bsc) / sy;
-          float y = rintf(static_cast<float>(acc[c]) * mult) + zy;
-          y = fminf(fmaxf(y, -128.0f), 127.0f);
-          v[c] = mode == 1 ? y : (y - zy) * sy;
-        } else {
-          v[c] = static_cast<float>(acc[c]) * (sa * bsc);
-        }
-      }
-      if constexpr (std::is_same<TO, int8_t>::value) {
-        int8_t* out = outp;
-        if (full) {
-          uint32_t w[2] = {0u, 0u};
-#pragma unroll
-          for (int c = 0; c < 8; ++c)
-            w[c >> 2] |= (static_cast<uint32_t>(static_cast<int8_t>(v[c])) & 0xffu) << (8 * (c & 3));
-          *reinterpret_cast<uint2*>(out + o) = uint2{w[0], w[1]};
-        } else {
-#pragma unroll
-          for (int c = 0; c < 8; ++c)
-            if (n + c < pn) out[o + c] = static_cast<int8_t>(v[c]);
-        }
-      } else if (full) {
-        float res[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (resp) Elem<TO>::load8(resp + o, res);
-        apply_epilogue8(p.epi, v, m, n, pn, res, 0);
-        Elem<TO>::store8(outp + o, v);
-      } else {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          if (n + c < pn) {
-            const float res = resp ? Elem<TO>::to_f32(resp[o + c]) : 0.0f;
-            outp[o + c] = Elem<TO>::from_f32(apply_epilogue(p.epi, v[c], m, n + c, pn, res, 0));
-          }
-        }
-      }
-    }
-  }
-}
-
-// Epilogue straight from C^T accumulators (16-bit and fp32 MFMA kernels,
-// which multiply with the operands swapped): acc[i][j][r] is output row
-// m = mbase + 16 i + l16, column n = nbase + 16 j + 4 lg + r, so a lane owns
-// 4 consecutive columns of a row and writes them as one 8-byte (16-bit) or
-// 16-byte (fp32) store after the epilogue, with no LDS round trip.
-// Calls f(std::integral_constant<int, 0>) ... f(<N - 1>): indices that are
-// constants before any loop unrolling, so register arrays indexed by them
-// never become addressable (scratch) memory.
-template <typename F, int... Is>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
-  (f(std::integral_constant<int, Is>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
-// The 16-bit and fp32 MFMA kernels multiply with the operands swapped, so
-// acc[i][j][r] is C^T: output row m = mbase + 16 i + l16, column
-// n = nbase + 16 j + 4 lg + r.  A lane owns 4 consecutive columns of a row.
-//
-// Common epilogue (row-major output, alpha = beta = 1, bias absent or per
-// column, optional residual, optional ReLU, no program) straight from the
-// accumulators: one 8-byte (16-bit) or 16-byte (fp32) store per 4 values, no
-// LDS round trip.  Same arithmetic as apply_epilogue: ((acc + b) + res), max 0.
-// G: the GELU form (act 2, gelu_erf with imm[0..2]), a separate
-// instantiation so the plain form carries no per-element GELU code.
-template <typename TO, int TM, int TN, bool G, typename Acc>
-__device__ __forceinline__ void epilogue_direct_impl(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase,
-                                                     int lane, TO* outp, const TO* resp, const float* bias, int act) {
-  const KArg<Problem>& p = kernel_arg<Problem>();
-  const bool relu = !G && act == 1;
-  constexpr bool gelu = G;
-  const float g0 = G ? p.epi.imm[0] : 0.0f, g1 = G ? p.epi.imm[1] : 0.0f, g2 = G ? p.epi.imm[2] : 0.0f;
-  const int l16 = lane & 15, lg = lane >> 4;
-  const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
-  // Bias of this lane's columns, for every column tile.
-  float b[TN][4];
-  static_for<TN>([&](auto jc) {
-    constexpr int j = decltype(jc)::value;
-    const int64_t n = nbase + 16 * j + 4 * lg;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) b[j][r] = 0.0f;
-    if (bias && n + 4 <= pn) {
-      const float4 q = *reinterpret_cast<const float4*>(bias + n);
-      b[j][0] = q.x; b[j][1] = q.y; b[j][2] = q.z; b[j][3] = q.w;
-    }
-  });
-  // Row by row: a row's column tiles share cache lines, so its residual
-  // loads and its stores go out back to back (interleaving rows makes L2
-  // write partial lines back more than once).
-  static_for<TM>([&](auto ic) {
-    constexpr int i = decltype(ic)::value;
-    const int64_t m = mbase + 16 * i + l16;
-    if (m < pm) {
-      float res[TN][4];
-      static_for<TN>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        const int64_t n = nbase + 16 * j + 4 * lg;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) res[j][r] = 0.0f;
-        if (resp && n + 4 <= pn) Elem<TO>::load4(resp + m * ldo + n, res[j]);
-      });
-      static_for<TN>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        const int64_t n = nbase + 16 * j + 4 * lg;
-        float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-        if (n + 4 <= pn) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float t = (v[r] + b[j][r]) + res[j][r];
-            v[r] = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t);
-          }
-          Elem<TO>::store4(outp + m * ldo + n, v);
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            if (n + r < pn) {
-              const int64_t o = m * ldo + n + r;
-              float t = (v[r] + (bias ? bias[n + r] : 0.0f)) + (resp ? Elem<TO>::to_f32(resp[o]) : 0.0f);
-              outp[o] = Elem<TO>::from_f32(relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t));
-            }
-          }
-        }
-      });
-    }
-  });
-}
-
-// GELU: act 2 is computed in registers only by the instantiations that ask
-// for it (the large-tile kernel, which has no staged epilogue).
-template <typename TO, int TM, int TN, bool GELU = false, typename Acc>
-__device__ __forceinline__ void epilogue_direct(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
-                                                TO* outp, const TO* resp, const float* bias, int act) {
-  if (GELU && act == 2) epilogue_direct_impl<TO, TM, TN, true>(acc, mbase, nbase, lane, outp, resp, bias, act);
-  else epilogue_direct_impl<TO, TM, TN, false>(acc, mbase, nbase, lane, outp, resp, bias, act);
-}
-
-// int8 GEMM (c3h_qgemm) counterpart of epilogue_direct for C^T int32
-// accumulators: qmode 0 stores int32, 1 requantizes to int8 (4 bytes per
-// lane), 2 dequantizes and 3 requantizes then dequantizes, both followed by
-// the common float epilogue (simple_epi).  Arithmetic as store_strip_q.
-template <typename TO, int TM, int TN, bool G, typename Acc>
-__device__ __forceinline__ void epilogue_direct_q_impl(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase,
-                                                       int lane, TO* outp, const TO* resp, const float* bias, int act) {
-  const KArg<Problem>& p = kernel_arg<Problem>();
-  const bool relu = !G && act == 1;
-  constexpr bool gelu = G;
-  const float g0 = G ? p.epi.imm[0] : 0.0f, g1 = G ? p.epi.imm[1] : 0.0f, g2 = G ? p.epi.imm[2] : 0.0f;
-  const int l16 = lane & 15, lg = lane >> 4;
-  const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
-  const int mode = p.qmode;
-  const float sa = p.a_scale, sy = p.y_scale, zy = static_cast<float>(p.y_zero);
-  float sb[TN][4], b[TN][4];
-  static_for<TN>([&](auto jc) {
-    constexpr int j = decltype(jc)::value;
-    const int64_t n = nbase + 16 * j + 4 * lg;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      sb[j][r] = 0.0f;
-      b[j][r] = 0.0f;
-      if (n + r < pn) {
-        if (mode != 0) sb[j][r] = p.b_scale[n + r];
-        if (bias) b[j][r] = bias[n + r];
-      }
-    }
-  });
-  // Row by row, as epilogue_direct: a row's stores go out back to back.
-  static_for<TM>([&](auto ic) {
-    constexpr int i = decltype(ic)::value;
-    const int64_t m = mbase + 16 * i + l16;
-    if (m < pm) {
-      float res[TN][4];
-      static_for<TN>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        const int64_t n = nbase + 16 * j + 4 * lg;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) res[j][r] = 0.0f;
-        if constexpr (!std::is_same<TO, int32_t>::value && !std::is_same<TO, int8_t>::value) {
-          if (resp && n + 4 <= pn) Elem<TO>::load4(resp + m * ldo + n, res[j]);
-        }
-      });
-      static_for<TN>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        const int64_t n = nbase + 16 * j + 4 * lg;
-        const bool nfull = n + 4 <= pn;
-        const int64_t o = m * ldo + n;
-        if (n < pn) {
-          if constexpr (std::is_same<TO, int32_t>::value) {
-            if (nfull) {
-              *reinterpret_cast<int4*>(outp + o) = int4{acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-            } else {
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                if (n + r < pn) outp[o + r] = acc[i][j][r];
-            }
-          } else {
-            float v[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float a = static_cast<float>(acc[i][j][r]);
-              if (mode == 1 || mode == 3) {
-                const float mult = (sa * sb[j][r]) / sy;
-                float y = rintf(a * mult) + zy;
-                y = fminf(fmaxf(y, -128.0f), 127.0f);
-                v[r] = mode == 1 ? y : (y - zy) * sy;
-              } else {
-                v[r] = a * (sa * sb[j][r]);
-              }
-            }
-            if constexpr (std::is_same<TO, int8_t>::value) {
-              if (nfull) {
-                uint32_t w = 0u;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) w |= (static_cast<uint32_t>(static_cast<int8_t>(v[r])) & 0xffu) << (8 * r);
-                *reinterpret_cast<uint32_t*>(outp + o) = w;
-              } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                  if (n + r < pn) outp[o + r] = static_cast<int8_t>(v[r]);
-              }
-            } else {
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                float rr = res[j][r];
-                if (resp && !nfull && n + r < pn) rr = Elem<TO>::to_f32(resp[o + r]);
-                const float t = (v[r] + b[j][r]) + rr;
-                v[r] = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t);
-              }
-              if (nfull) {
-                Elem<TO>::store4(outp + o, v);
-              } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                  if (n + r < pn) outp[o + r] = Elem<TO>::from_f32(v[r]);
-              }
-            }
-          }
-        }
-      });
-    }
-  });
-}
-
-// fp8 GEMM: C^T accumulators (row m = mbase + 16 i + l16, column
-// n = nbase + 16 j + 4 lg + r) times a_rows[m] * b_scale[n], in registers,
-// before either epilogue.  Rows / columns past the edge get scale 0 (never
-// stored).
-template <int TM, int TN>
-__device__ __forceinline__ void scale_acc(f32x4 (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane) {
-  const KArg<Problem>& p = kernel_arg<Problem>();
-  const int l16 = lane & 15, lg = lane >> 4;
-  float sb[TN][4];
-  static_for<TN>([&](auto jc) {
-    constexpr int j = decltype(jc)::value;
-    const int64_t n = nbase + 16 * j + 4 * lg;
-    if (n + 4 <= p.n) {
-      const float4 q = *reinterpret_cast<const float4*>(p.b_scale + n);
-      sb[j][0] = q.x; sb[j][1] = q.y; sb[j][2] = q.z; sb[j][3] = q.w;
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sb[j][r] = n + r < p.n ? p.b_scale[n + r] : 0.0f;
-    }
-  });
-  static_for<TM>([&](auto ic) {
-    constexpr int i = decltype(ic)::value;
-    const int64_t m = mbase + 16 * i + l16;
-    const float sa = m < p.m ? p.a_rows[m] : 0.0f;
-    static_for<TN>([&](auto jc) {
-      constexpr int j = decltype(jc)::value;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[i][j][r] = (acc[i][j][r] * sa) * sb[j][r];
-    });
-  });
-}
-
-template <typename TO, int TM, int TN, bool GELU = false, typename Acc>
-__device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
-                                                  TO* outp, const TO* resp, const float* bias, int act) {
-  if (GELU && act == 2) epilogue_direct_q_impl<TO, TM, TN, true>(acc, mbase, nbase, lane, outp, resp, bias, act);
-  else epilogue_direct_q_impl<TO, TM, TN, false>(acc, mbase, nbase, lane, outp, resp, bias, act);
-}
-
-// Whether epilogue_direct_q applies: int32 / int8 outputs need only aligned
-// row-major stores; dequantized ones also need the common float epilogue.
-__device__ __forceinline__ bool epilogue_q_direct_ok(const KArg<Problem>& p, bool vec4);
-
-// Whether epilogue_direct applies (uniform): see its comment.
-__device__ __forceinline__ bool epilogue_is_simple(const KArg<Problem>& p, bool vec4) {
-  const int bm = p.epi.bias_mode;
-  return vec4 && !p.out_nchw && p.epi.alpha == 1.0f && p.epi.beta == 1.0f && (bm == 0 || bm == 2) &&
-         p.epi.act <= 1 && p.epi.n_inst == 0 &&
-         (bm == 0 || (reinterpret_cast<uintptr_t>(p.epi.bias) & 15) == 0);
-}
-__device__ __forceinline__ bool epilogue_q_direct_ok(const KArg<Problem>& p, bool vec4) {
-  return p.qmode <= 1 ? (vec4 && !p.out_nchw) : epilogue_is_simple(p, vec4);
-}
-
-// BUF: operands read with buffer loads at 32-bit byte offsets (A and B below
-// 2^31 bytes, no batch): row bases are precomputed once, out-of-range lanes
-// use an offset past num_records and read zeros, so a K step costs a few
-// VALU per load instead of 64-bit address math and branches.
-template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, bool BUF = false>
-__global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
-  constexpr bool DIRECT_GELU = false;  // GELU epilogues take the staged path here
-  constexpr int ES = Mma::ES;
-  constexpr int VE = 16 / ES;        // elements per 16-byte vector
-  constexpr int BK = 128 / ES;       // elements per 128-byte tile row
-  constexpr int RB = 128;            // LDS row bytes
-  constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int RSTEP = kThreads / 8;  // rows between a thread's vectors
-  constexpr int A_V = BM / RSTEP, B_V = BN / RSTEP;
-  static_assert(WM * WN == kThreads / 64, "wave grid");
-  static_assert(A_V >= 1 && B_V >= 1 && BM % RSTEP == 0 && BN % RSTEP == 0, "tile too small");
-  static_assert(AM == kDenseK || ES == 2, "conv modes are 16-bit");
-  constexpr int kTileBytes = 2 * (BM + BN) * RB;
-  constexpr int kStageBytes = (kThreads / 64) * WTM * (WTN + 4) * 4;  // whole wave tiles, 32-bit
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kTileBytes > kStageBytes ? kTileBytes : kStageBytes];
-  uint8_t (*As)[BM][RB] = reinterpret_cast<uint8_t (*)[BM][RB]>(smem);
-  uint8_t (*Bs)[BN][RB] = reinterpret_cast<uint8_t (*)[BN][RB]>(smem + 2 * BM * RB);
-  typedef typename Mma::vec vec;
-  typedef typename Mma::acc_t acc_t;
-
-  int tm, tn;
-  tile_coords_grouped(p, tm, tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
-  const int64_t bz = blockIdx.z;
-  const uint8_t* A = static_cast<const uint8_t*>(p.a) + bz * p.stride_a * ES;
-  const uint8_t* B = static_cast<const uint8_t*>(p.b) + bz * p.stride_b * ES;
-
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave / WN, wn = wave % WN;
-  const int trow = tid >> 3;         // first tile row of this thread
-  const int kchunk = tid & 7;        // 16-byte K chunk of all of this thread's vectors
-  const int kc = kchunk * VE;        // ... as an element column
-
-  // Two register sets: the loads of tile kt + 2 are issued while tile kt is
-  // multiplied and tile kt + 1 is still in flight.
-  uint4 ra0[A_V], rb0[B_V], ra1[A_V], rb1[B_V];
-
-  // Per-row conv state (conv modes): pixel base offset, top-left input coords.
-  int64_t rbase[AM == kDenseK ? 1 : A_V];
-  int rhi[AM == kDenseK ? 1 : A_V], rwi[AM == kDenseK ? 1 : A_V];
-  ConvRow crow[AM == kConv ? A_V : 1];
-  static_assert(!BUF || AM == kDenseK || AM == kConvTap, "buffer loads: dense or tap-uniform conv");
-  __amdgpu_buffer_rsrc_t rs_a, rs_b;
-  int32_t a_off[BUF ? A_V : 1];   // dense: row byte offset (-1: out of range); tap: pixel byte offset
-  int32_t b_off[BUF ? B_V : 1];
-  if constexpr (BUF) {
-    rs_a = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.a), 0, static_cast<int>(p.a_bytes), 0x00020000);
-    rs_b = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.b), 0, static_cast<int>(p.b_bytes), 0x00020000);
-#pragma unroll
-    for (int i = 0; i < B_V; ++i) {
-      const int64_t n = n0 + trow + RSTEP * i;
-      b_off[i] = n < p.n ? static_cast<int32_t>(n * p.ldb * ES) : -1;
-    }
-    if (AM == kDenseK) {
-#pragma unroll
-      for (int i = 0; i < A_V; ++i) {
-        const int64_t m = m0 + trow + RSTEP * i;
-        a_off[i] = m < p.m ? static_cast<int32_t>(m * p.lda * ES) : -1;
-      }
-    }
-  }
-  if (AM == kConvTap || AM == kConvStem) {
-#pragma unroll
-    for (int i = 0; i < A_V; ++i) {
-      const ConvRow r = conv_row(p, m0 + trow + RSTEP * i);
-      rbase[i] = r.base;
-      rhi[i] = r.valid ? r.hi0 : -(1 << 28);  // invalid rows fail every bounds check
-      rwi[i] = r.wi0;
-      if constexpr (BUF)
-        a_off[i] = static_cast<int32_t>(
-            (r.base + (static_cast<int64_t>(r.hi0) * p.cw + r.wi0) * p.c_stride) * ES);
-    }
-  } else if (AM == kConv) {
-#pragma unroll
-    for (int i = 0; i < A_V; ++i) crow[i] = conv_row(p, m0 + trow + RSTEP * i);
-  }
-  // kConvTap: the next tile's filter tap and channel base.
-  int t_kh = 0, t_kw = 0, t_c0 = 0;
-
-  // `live` is false for the tiles past the end that the fixed-depth prefetch
-  // still issues: their loads read zeros, so every issue() is the same number
-  // of load instructions and the compiler's vmcnt waits stay exact.
-  auto load_a = [&](int64_t k0, uint4 (&ra)[A_V], bool live) {
-    if constexpr (BUF) {
-      if (AM == kDenseK) {
-        const bool kok = live && k0 + kc < p.k;
-        const int32_t koff = static_cast<int32_t>((k0 + kc) * ES);
-#pragma unroll
-        for (int i = 0; i < A_V; ++i) {
-          const uint32_t voff = (kok && a_off[i] >= 0) ? static_cast<uint32_t>(a_off[i] + koff) : kOobOffset;
-          ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs_a, voff, 0, 0));
-        }
-      } else {
-        const int dh = t_kh * p.dh, dw = t_kw * p.dw;
-        const int32_t tap = static_cast<int32_t>(((dh * p.cw + dw) * p.c_stride + t_c0 + kc) * ES);
-#pragma unroll
-        for (int i = 0; i < A_V; ++i) {
-          const bool ok = live && static_cast<unsigned>(rhi[i] + dh) < static_cast<unsigned>(p.ch) &&
-                          static_cast<unsigned>(rwi[i] + dw) < static_cast<unsigned>(p.cw);
-          const uint32_t voff = ok ? static_cast<uint32_t>(a_off[i] + tap) : kOobOffset;
-          ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs_a, voff, 0, 0));
-        }
-      }
-      return;
-    }
-    if (AM == kDenseK) {
-      const int64_t k = k0 + kc;
-#pragma unroll
-      for (int i = 0; i < A_V; ++i) {
-        const int64_t m = m0 + trow + RSTEP * i;
-        uint4 v = {0u, 0u, 0u, 0u};
-        if (m < p.m && k < p.k) v = *reinterpret_cast<const uint4*>(A + (m * p.lda + k) * ES);
-        ra[i] = v;
-      }
-    } else if (AM == kConvTap) {
-      const int dh = t_kh * p.dh, dw = t_kw * p.dw;
-      const int64_t tap_off = (static_cast<int64_t>(dh) * p.cw + dw) * p.c_stride + t_c0 + kc;
-#pragma unroll
-      for (int i = 0; i < A_V; ++i) {
-        const int hi = rhi[i] + dh, wi = rwi[i] + dw;
-        uint4 v = {0u, 0u, 0u, 0u};
-        if (live && static_cast<unsigned>(hi) < static_cast<unsigned>(p.ch) &&
-            static_cast<unsigned>(wi) < static_cast<unsigned>(p.cw))
-          v = *reinterpret_cast<const uint4*>(
-              A + (rbase[i] + (static_cast<int64_t>(rhi[i]) * p.cw + rwi[i]) * p.c_stride + tap_off) * ES);
-        ra[i] = v;
-      }
-    } else if (AM == kConvStem) {
-      // K order (kh, kw_pack = 8, c = 4): vector kc covers taps kw0, kw0 + 1.
-      const int64_t k = k0 + kc;
-      const int tap = static_cast<int>(k >> 2);
-      const int khi = tap >> 3, kw0 = tap & 7;
-#pragma unroll
-      for (int i = 0; i < A_V; ++i) {
-        uint2 lo = {0u, 0u}, hi2 = {0u, 0u};
-        if (k < p.k) {
-          const int hi = rhi[i] + khi * p.dh;
-          if (static_cast<unsigned>(hi) < static_cast<unsigned>(p.ch)) {
-            const int wa = rwi[i] + kw0 * p.dw, wb = wa + p.dw;
-            const int64_t rowoff = rbase[i] + static_cast<int64_t>(hi) * p.cw * 4;
-            if (kw0 < p.kw && static_cast<unsigned>(wa) < static_cast<unsigned>(p.cw))
-              lo = *reinterpret_cast<const uint2*>(A + (rowoff + static_cast<int64_t>(wa) * 4) * ES);
-            if (kw0 + 1 < p.kw && static_cast<unsigned>(wb) < static_cast<unsigned>(p.cw))
-              hi2 = *reinterpret_cast<const uint2*>(A + (rowoff + static_cast<int64_t>(wb) * 4) * ES);
-          }
-        }
-        ra[i] = uint4{lo.x, lo.y, hi2.x, hi2.y};
-      }
-    } else {
-      const int64_t k = k0 + kc;
-#pragma unroll
-      for (int i = 0; i < A_V; ++i) {
-        const int64_t off = conv_k_offset(p, crow[i], k);
-        uint4 v = {0u, 0u, 0u, 0u};
-        if (off >= 0) v = *reinterpret_cast<const uint4*>(A + off * ES);
-        ra[i] = v;
-      }
-    }
-  };
-  auto advance_tap = [&]() {
-    if (AM == kConvTap) {
-      t_c0 += BK;
-      if (t_c0 >= p.c_pack) {
-        t_c0 = 0;
-        if (++t_kw >= p.kw) {
-          t_kw = 0;
-          ++t_kh;
-        }
-      }
-    }
-  };
-  auto load_b = [&](int64_t k0, uint4 (&rb)[B_V], bool live) {
-    const int64_t k = k0 + kc;
-    if constexpr (BUF) {
-      const bool kok = live && k < p.k;
-      const int32_t koff = static_cast<int32_t>(k * ES);
-#pragma unroll
-      for (int i = 0; i < B_V; ++i) {
-        const uint32_t voff = (kok && b_off[i] >= 0) ? static_cast<uint32_t>(b_off[i] + koff) : kOobOffset;
-        rb[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs_b, voff, 0, 0));
-      }
-      return;
-    }
-#pragma unroll
-    for (int i = 0; i < B_V; ++i) {
-      const int64_t n = n0 + trow + RSTEP * i;
-      uint4 v = {0u, 0u, 0u, 0u};
-      if (n < p.n && k < p.k) v = *reinterpret_cast<const uint4*>(B + (n * p.ldb + k) * ES);
-      rb[i] = v;
-    }
-  };
-  // Byte offset of 16-byte chunk c of row r (XOR swizzle).
-  auto swz = [](int r, int c) { return (c ^ (r & 7)) << 4; };
-  auto store_tiles = [&](int buf, const uint4 (&ra)[A_V], const uint4 (&rb)[B_V]) {
-#pragma unroll
-    for (int i = 0; i < A_V; ++i) {
-      const int r = trow + RSTEP * i;
-      *reinterpret_cast<uint4*>(&As[buf][r][swz(r, kchunk)]) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_V; ++i) {
-      const int r = trow + RSTEP * i;
-      *reinterpret_cast<uint4*>(&Bs[buf][r][swz(r, kchunk)]) = rb[i];
-    }
-  };
-
-  acc_t acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
-
-  const int64_t ktiles = ceil_div(p.k, BK);
-  const int lrow = lane & 15, lchunk = lane >> 4;
-  auto compute = [&](int cur) {
-#pragma unroll
-    for (int ks = 0; ks < 8; ks += Mma::kStep) {  // MFMA K steps of 16 * kStep bytes
-      vec av[TM], bv[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int r = wm * WTM + i * 16 + lrow;
-        av[i] = read_operand<Mma>(&As[cur][r][0], r, ks, lchunk);
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int r = wn * WTN + j * 16 + lrow;
-        bv[j] = read_operand<Mma>(&Bs[cur][r][0], r, ks, lchunk);
-      }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          acc[i][j] = Mma::mma(bv[j], av[i], acc[i][j]);  // C^T: see epilogue_direct
-        }
-    }
-  };
-  // LDS barrier that leaves global loads in flight: this wave's LDS stores
-  // are complete (lgkmcnt 0); __syncthreads would also wait for vmcnt(0).
-  auto lds_barrier = [&]() {
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-  };
-  auto issue = [&](int64_t kt, uint4 (&ra)[A_V], uint4 (&rb)[B_V]) {
-    const bool live = kt < ktiles;
-    load_a(kt * BK, ra, live);
-    load_b(kt * BK, rb, live);
-    advance_tap();
-  };
-
-  issue(0, ra0, rb0);
-  issue(1, ra1, rb1);
-  store_tiles(0, ra0, rb0);
-  lds_barrier();
-  int64_t kt = 0;
-  for (; kt + 2 <= ktiles; kt += 2) {
-    // LDS buffer 0 holds tile kt; ra1/rb1 carry tile kt + 1.
-    issue(kt + 2, ra0, rb0);
-    compute(0);
-    store_tiles(1, ra1, rb1);
-    lds_barrier();
-    // LDS buffer 1 holds tile kt + 1; ra0/rb0 carry tile kt + 2.
-    issue(kt + 3, ra1, rb1);
-    compute(1);
-    if (kt + 2 < ktiles) {
-      store_tiles(0, ra0, rb0);
-      lds_barrier();
-    }
-  }
-  if (kt < ktiles) compute(0);  // odd tile count: the last tile sits in buffer 0
-  if constexpr (Mma::kScaled) scale_acc<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane);
-
-  // Epilogue: a lane holds (m = 4*(lane/16)+r, n = lane%16) of each 16x16
-  // tile.  The whole wave tile is staged in LDS (accumulators only ever
-  // indexed by unrolled constants), then stored 16 rows at a time with 8
-  // columns per lane.
-  TO* outp = static_cast<TO*>(p.out) + bz * p.stride_out;
-  const TO* resp = p.epi.residual ? static_cast<const TO*>(p.epi.residual) + bz * p.stride_res : nullptr;
-  const int64_t bias_off = bz * p.stride_bias;
-  {
-    constexpr uintptr_t kA = 4 * sizeof(TO) - 1;
-    const bool vec4 = (p.ldo % 4 == 0) && (p.stride_out % 4 == 0) && (p.stride_res % 4 == 0) &&
-                      (p.stride_bias % 4 == 0) && ((reinterpret_cast<uintptr_t>(outp) & kA) == 0) &&
-                      ((reinterpret_cast<uintptr_t>(resp) & kA) == 0);
-    if constexpr (Mma::kInt) {
-      if (bz == 0 && epilogue_q_direct_ok(kernel_arg<Problem>(), vec4)) {
-        const float* bias = p.epi.bias_mode == 2 ? static_cast<const float*>(p.epi.bias) : nullptr;
-        epilogue_direct_q<TO, TM, TN, DIRECT_GELU>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act);
-        return;
-      }
-    } else if (epilogue_is_simple(kernel_arg<Problem>(), vec4)) {
-      const float* bias = p.epi.bias_mode == 2 ? static_cast<const float*>(p.epi.bias) + bias_off : nullptr;
-      epilogue_direct<TO, TM, TN, DIRECT_GELU>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act);
-      return;
-    }
-  }
-  const bool vec_ok = !p.out_nchw && (p.ldo % 8 == 0) && (p.stride_out % 8 == 0) && (p.stride_res % 8 == 0) &&
-                      ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0) &&
-                      ((reinterpret_cast<uintptr_t>(p.epi.residual) & 15) == 0);
-  __syncthreads();
-  float* stage = reinterpret_cast<float*>(smem) + wave * WTM * (WTN + 4);
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float* dst = &stage[(i * 16 + lrow) * (WTN + 4) + j * 16 + (lane >> 4) * 4 + r];  // C^T accumulators
-        if constexpr (Mma::kInt) *reinterpret_cast<int*>(dst) = acc[i][j][r];
-        else *dst = acc[i][j][r];
-      }
-  wave_sync_lds();
-#pragma nounroll
-  for (int i = 0; i < TM; ++i) {
-    const int64_t mrow0 = m0 + wm * WTM + i * 16, ncol0 = n0 + wn * WTN;
-    const float* strip = stage + i * 16 * (WTN + 4);
-    if constexpr (Mma::kInt) {
-      store_strip_q<TO, WTN>(strip, lane, mrow0, ncol0, outp, resp, vec_ok);
-    } else {
-      if (p.out_nchw) store_strip<TO, WTN>(p, strip, lane, mrow0, ncol0, outp, resp, bias_off);
-      else store_strip_vec<TO, WTN>(strip, lane, mrow0, ncol0, outp, resp, bias_off, vec_ok);
-    }
-  }
-}
-
-// =====================================================================
-// Pipelined variant: operand tiles go straight from global memory to LDS
-// (buffer_load_dwordx4 ... lds) through S stages, so S-1 tiles are in flight
-// while one is multiplied, without staging registers.  Lane i of a DMA load
-// writes LDS bytes [16 i, 16 i + 16) from the wave's base (M0); a wave load
-// covers 8 tile rows, and each lane fetches the logical K chunk that the XOR
-// swizzle places at its slot.  Out-of-range lanes (M/N/K tails, conv
-// padding) get a byte offset beyond the buffer's num_records and so write
-// zeros.  One barrier per K tile: after it, every wave has finished the
-// previous tile, whose buffer then receives tile kt + S - 1.
-//
-// Requirements (checked on the host): A and B each below 2^31 bytes; A mode
-// kDenseK or kConvTap.
-// =====================================================================
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
-}
-
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// NW waves per block.  NW = 8 is the large-tile form (256 x 256, wave tiles
-// 64 x 128, one block per CU): half the operand bytes per flop of 128 x 128,
-// direct epilogues only (its LDS cannot also hold a staged epilogue).
-template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, int S, int NW = 4>
-__global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
-  constexpr bool DIRECT = NW > 4;
-  constexpr bool DIRECT_GELU = DIRECT;
-  constexpr int ES = Mma::ES;
-  constexpr int VE = 16 / ES;
-  constexpr int BK = 128 / ES;
-  constexpr int RB = 128;
-  constexpr int TM = BM / WM / 16, TN = BN / WN / 16;
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int GROUPS = (BM + BN) / 8;   // 8-row wave loads per stage
-  constexpr int LPW = GROUPS / NW;        // wave loads per wave per stage
-  constexpr int STAGE = (BM + BN) * RB;
-  static_assert(WM * WN == NW && GROUPS % NW == 0 && BM % 8 == 0, "shape");
-  static_assert(AM == kDenseK || AM == kConvTap, "dma kernel: dense or tap-uniform conv only");
-  static_assert(S >= 2 && S <= 4 && LPW * (S - 2) < 64, "stages");
-  constexpr int kStageBytes = DIRECT ? 0 : NW * WTM * (WTN + 4) * 4;
-  constexpr int kSmem = S * STAGE > kStageBytes ? S * STAGE : kStageBytes;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
-  typedef typename Mma::vec vec;
-  typedef typename Mma::acc_t acc_t;
-
-  int tm, tn;
-  tile_coords_grouped(p, tm, tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
-  // wave index via readfirstlane: provably uniform, so each DMA's LDS base
-  // (M0) is a scalar and needs no per-lane waterfall loop
-  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int wm = wave / WN, wn = wave % WN;
-
-  const __amdgpu_buffer_rsrc_t rs_a = make_rsrc(p.a, p.a_bytes);
-  const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(p.b, p.b_bytes);
-  const int lchunk_ld = (lane & 7) ^ (lane >> 3);  // logical K chunk this lane fetches
-  const int kc = lchunk_ld * VE;
-
-  // Per load slot j (group g = wave + NW j): the byte offset of this lane's
-  // chunk at K tile 0 (conv: at tap (0, 0), which may lie in the padding, so
-  // it can be negative), or -1 for a row past M / N; conv rows also keep
-  // their top-left input coordinates (rows past M get hi0 far out of range,
-  // so every tap's bounds check fails).  A and B byte extents are below 2^31
-  // (dma_eligible), so 32-bit offsets cover them.  Slots j < A_SLOTS hold A
-  // rows for every wave (BM / 8 is a multiple of NW), a compile-time split.
-  constexpr int A_SLOTS = BM / 8 / NW;
-  static_assert((BM / 8) % NW == 0, "A/B slot split");
-  int32_t slot_off[LPW];
-  int slot_hi[LPW], slot_wi[LPW];
-#pragma unroll
-  for (int j = 0; j < LPW; ++j) {
-    const int g = wave + NW * j;
-    const int r = g * 8 + (lane >> 3);
-    slot_hi[j] = 0;
-    slot_wi[j] = 0;
-    if (j < A_SLOTS) {
-      const int64_t m = m0 + r;
-      if (AM == kConvTap) {
-        const ConvRow cr = conv_row(p, m);
-        slot_off[j] = static_cast<int32_t>(
-            (cr.base + (static_cast<int64_t>(cr.hi0) * p.cw + cr.wi0) * p.c_stride + kc) * ES);
-        slot_hi[j] = cr.valid ? cr.hi0 : -0x40000000;
-        slot_wi[j] = cr.wi0;
-      } else {
-        slot_off[j] = m < p.m ? static_cast<int32_t>((m * p.lda + kc) * ES) : -1;
-      }
-    } else {
-      const int64_t n = n0 + (r - BM);
-      slot_off[j] = n < p.n ? static_cast<int32_t>((n * p.ldb + kc) * ES) : -1;
-    }
-  }
-  int t_kh = 0, t_kw = 0, t_c0 = 0;  // kConvTap: tap of the next tile to issue
-
-  auto issue = [&](int64_t kt, int buf) {
-    const bool k_ok = kt * BK + kc < p.k;
-    const int32_t k_bytes = static_cast<int32_t>(kt * BK * ES);  // dense operands: uniform
-    const int dh = t_kh * p.dh, dw = t_kw * p.dw;
-    // conv: the tap's uniform byte offset from tap (0, 0)
-    const int32_t tap_bytes = ((dh * p.cw + dw) * p.c_stride + t_c0) * ES;
-#pragma unroll
-    for (int j = 0; j < LPW; ++j) {
-      const int g = wave + NW * j;
-      uint32_t voff = kOobOffset;
-      if (j < A_SLOTS) {
-        if (AM == kConvTap) {
-          const int hi = slot_hi[j] + dh, wi = slot_wi[j] + dw;
-          if (static_cast<unsigned>(hi) < static_cast<unsigned>(p.ch) &&
-              static_cast<unsigned>(wi) < static_cast<unsigned>(p.cw))
-            voff = static_cast<uint32_t>(slot_off[j] + tap_bytes);
-        } else if (slot_off[j] >= 0 && k_ok) {
-          voff = static_cast<uint32_t>(slot_off[j] + k_bytes);
-        }
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, (lds_void_ptr)(smem + buf * STAGE + g * 1024), 16, voff, 0,
-                                                 0, 0);
-      } else {
-        if (slot_off[j] >= 0 && k_ok) voff = static_cast<uint32_t>(slot_off[j] + k_bytes);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, (lds_void_ptr)(smem + buf * STAGE + g * 1024), 16, voff, 0,
-                                                 0, 0);
-      }
-    }
-    if (AM == kConvTap) {
-      t_c0 += BK;
-      if (t_c0 >= p.c_pack) {
-        t_c0 = 0;
-        if (++t_kw >= p.kw) {
-          t_kw = 0;
-          ++t_kh;
-        }
-      }
-    }
-  };
-
-  acc_t acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
-
-  const int64_t ktiles = ceil_div(p.k, BK);
-#pragma unroll
-  for (int st = 0; st < S - 1; ++st)
-    if (st < ktiles) issue(st, st);
-  const int lrow = lane & 15, lchunk = lane >> 4;
-  for (int64_t kt = 0; kt < ktiles; ++kt) {
-    // Tiles issued after kt (at most S - 2 of them) may stay in flight.
-    const int64_t later = min(static_cast<int64_t>(S - 2), ktiles - 1 - kt);
-    if (later >= 2) wait_vmcnt<2 * LPW>();
-    else if (later == 1) wait_vmcnt<LPW>();
-    else wait_vmcnt<0>();
-    // Barrier without __syncthreads' release fence: that fence would wait for
-    // every outstanding DMA (vmcnt(0)) and drain the pipeline.  This wave's
-    // tile-kt DMA is complete (the wait above) and its earlier LDS reads were
-    // consumed by MFMAs; the empty asm statements keep the compiler from
-    // moving memory operations across the barrier.
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    if (kt + S - 1 < ktiles) issue(kt + S - 1, static_cast<int>((kt + S - 1) % S));
-    const uint8_t* As = smem + (kt % S) * STAGE;
-    const uint8_t* Bs = As + BM * RB;
-    // Every K step's operand fragments are read from LDS before the first
-    // MFMA (a scheduling barrier keeps them there), so the later steps'
-    // reads complete under the earlier steps' MFMAs.  Left to itself the
-    // scheduler issues each step's reads just before its MFMAs and waits on
-    // them (lgkmcnt(0) several times per K tile).
-    constexpr int KS = 8 / Mma::kStep;
-    vec av[KS][TM], bv[KS][TN];
-#pragma unroll
-    for (int q = 0; q < KS; ++q) {
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int r = wm * WTM + i * 16 + lrow;
-        av[q][i] = read_operand<Mma>(As + r * RB, r, q * Mma::kStep, lchunk);
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int r = wn * WTN + j * 16 + lrow;
-        bv[q][j] = read_operand<Mma>(Bs + r * RB, r, q * Mma::kStep, lchunk);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int q = 0; q < KS; ++q)
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          acc[i][j] = Mma::mma(bv[q][j], av[q][i], acc[i][j]);  // C^T: see epilogue_direct
-        }
-  }
-
-  if constexpr (Mma::kScaled) scale_acc<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane);
-  TO* outp = static_cast<TO*>(p.out);
-  const TO* resp = p.epi.residual ? static_cast<const TO*>(p.epi.residual) : nullptr;
-  {
-    constexpr uintptr_t kA = 4 * sizeof(TO) - 1;
-    const bool vec4 = (p.ldo % 4 == 0) && ((reinterpret_cast<uintptr_t>(outp) & kA) == 0) &&
-                      ((reinterpret_cast<uintptr_t>(resp) & kA) == 0);
-    const float* bias = p.epi.bias_mode == 2 ? static_cast<const float*>(p.epi.bias) : nullptr;
-    if constexpr (Mma::kInt) {
-      // DIRECT: the host admitted only epilogues epilogue_direct_q computes
-      // (big_tile_wins), GELU included; there is no staged path to fall to.
-      if (DIRECT || epilogue_q_direct_ok(kernel_arg<Problem>(), vec4)) {
-        epilogue_direct_q<TO, TM, TN, DIRECT_GELU>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act);
-        return;
-      }
-    } else if (DIRECT || epilogue_is_simple(kernel_arg<Problem>(), vec4)) {
-      epilogue_direct<TO, TM, TN, DIRECT_GELU>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act);
-      return;
-    }
-  }
-  if constexpr (!DIRECT) {
-  const bool vec_ok = !p.out_nchw && (p.ldo % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0) &&
-                      ((reinterpret_cast<uintptr_t>(p.epi.residual) & 15) == 0);
-  __syncthreads();
-  float* stage = reinterpret_cast<float*>(smem) + wave * WTM * (WTN + 4);
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float* dst = &stage[(i * 16 + lrow) * (WTN + 4) + j * 16 + (lane >> 4) * 4 + r];  // C^T accumulators
-        if constexpr (Mma::kInt) *reinterpret_cast<int*>(dst) = acc[i][j][r];
-        else *dst = acc[i][j][r];
-      }
-  wave_sync_lds();
-#pragma nounroll
-  for (int i = 0; i < TM; ++i) {
-    const int64_t mrow0 = m0 + wm * WTM + i * 16, ncol0 = n0 + wn * WTN;
-    const float* strip = stage + i * 16 * (WTN + 4);
-    if constexpr (Mma::kInt) {
-      store_strip_q<TO, WTN>(strip, lane, mrow0, ncol0, outp, resp, vec_ok);
-    } else {
-      if (p.out_nchw) store_strip<TO, WTN>(p, strip, lane, mrow0, ncol0, outp, resp, 0);
-      else store_strip_vec<TO, WTN>(strip, lane, mrow0, ncol0, outp, resp, 0, vec_ok);
-    }
-  }
-  }
-}
-
-// =====================================================================
-// Split-K finish (c3h_gemm_splitk_reduce): one thread per output, the
-// partial products summed in split order, then the common epilogue.
-// =====================================================================
-template <typename TO>
-__global__ void __launch_bounds__(256) splitk_reduce_kernel(c3h_splitk_args a) {
-  const KArg<c3h_splitk_args>& p = kernel_arg<c3h_splitk_args>();
-  const int64_t mn = p.m * p.n;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= mn) return;
-  const int64_t row = i / p.n, col = i - row * p.n;
-  float v = p.partial[i];
-  for (int s = 1; s < p.splits; ++s) v += p.partial[s * mn + i];
-  const int64_t o = row * p.ldo + col;
-  const float res = p.epi.residual ? Elem<TO>::to_f32(static_cast<const TO*>(p.epi.residual)[o]) : 0.0f;
-  static_cast<TO*>(a.out)[o] = Elem<TO>::from_f32(apply_epilogue(p.epi, v, row, col, p.n, res, 0));
-}
 
 // =====================================================================
 // SIMT fp32 GEMM for operands the MFMA path cannot vector-load (odd K,
@@ -1610,181 +35,6 @@ __global__ void __launch_bounds__(256) gemm_simple_kernel(Problem p) {
   const float res = p.epi.residual ? static_cast<const float*>(p.epi.residual)[bz * p.stride_res + o] : 0.0f;
   outp[o] = apply_epilogue(kernel_arg<Problem>().epi, acc, m, n, p.n, res, bz * p.stride_bias);
 }
-
-// ---------------------------------------------------------------- dispatch
-template <int BM, int BN>
-void grid_of(Problem& p, int64_t batch, dim3& grid) {
-  p.tiles_m = static_cast<int>(ceil_div(p.m, BM));
-  p.tiles_n = static_cast<int>(ceil_div(p.n, BN));
-  grid = dim3(static_cast<unsigned>(p.tiles_m) * static_cast<unsigned>(p.tiles_n), 1, static_cast<unsigned>(batch));
-}
-
-template <int AM, bool BK_>
-int launch_f32(Problem p, int64_t batch, hipStream_t s) {
-  dim3 grid;
-  if (p.n <= 64 && p.m >= 4096) {
-    grid_of<256, 64>(p, batch, grid);
-    hipLaunchKernelGGL((gemm_f32_kernel<256, 64, 4, 1, AM, BK_>), grid, dim3(kThreads), 0, s, p);
-  } else if (p.m <= 64 || p.n <= 64 || ceil_div(p.m, 128) * ceil_div(p.n, 128) * batch < 256) {
-    // narrow operands, or too few 128x128 tiles to fill the chip
-    grid_of<64, 64>(p, batch, grid);
-    hipLaunchKernelGGL((gemm_f32_kernel<64, 64, 2, 2, AM, BK_>), grid, dim3(kThreads), 0, s, p);
-  } else {
-    grid_of<128, 128>(p, batch, grid);
-    hipLaunchKernelGGL((gemm_f32_kernel<128, 128, 2, 2, AM, BK_>), grid, dim3(kThreads), 0, s, p);
-  }
-  return launch_status("gemm_f32");
-}
-
-// The pipelined kernel needs byte offsets that fit the 32-bit buffer offset
-// with room for the out-of-range sentinel, and no batch strides.
-inline bool dma_eligible(const Problem& p, int64_t batch, int am) {
-  if (getenv("C3H_DISABLE_DMA")) return false;
-  // Narrow implicit-GEMM convs (N <= 64) stay on the register-prefetch
-  // kernel, which measured faster there; wider ones use the DMA kernel.
-  if (am == kConvTap && p.n <= 64) return false;
-  return batch == 1 && (am == kDenseK || am == kConvTap) && p.a_bytes > 0 && p.b_bytes > 0 &&
-         p.a_bytes < (int64_t{1} << 31) && p.b_bytes < (int64_t{1} << 31);
-}
-
-// Whether the 256 x 256 eight-wave DMA kernel beats 128 x 128 at two blocks
-// per CU: rounds of resident tiles, a 256-tile round costing 1.66 rounds of
-// 128-tiles (measured: 8192^3 GEMM, 1195 vs 994 us), and an epilogue that
-// epilogue_direct(_q) handles (host-side restatement of epilogue_is_simple;
-// plus GELU for int8, which the large-tile instantiation computes in
-// registers).
-// int8 GEMMs writing int32 / int8 (qmode 0 / 1) need only aligned row-major
-// stores (epilogue_q_direct_ok).
-bool big_tile_wins(const Problem& p, int cus, size_t out_size, bool int_mma) {
-  if (getenv("C3H_DISABLE_BIGTILE") || p.n <= 128) return false;
-  const c3h_epilogue& e = p.epi;
-  const uintptr_t al = 4 * out_size - 1;
-  const bool stores = !p.out_nchw && p.ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(p.out) & al) == 0;
-  // GELU in registers measured slower than the staged 128 x 128 epilogue for
-  // 16-bit GEMMs (16384x2048x512: 101 vs 95 us) and faster for int8 ones.
-  const int max_act = int_mma ? 2 : 1;
-  const bool simple = stores && e.alpha == 1.0f && e.beta == 1.0f && (e.bias_mode == 0 || e.bias_mode == 2) &&
-                      e.act <= max_act && e.n_inst == 0 &&
-                      (e.bias_mode == 0 || (reinterpret_cast<uintptr_t>(e.bias) & 15) == 0) &&
-                      (reinterpret_cast<uintptr_t>(e.residual) & al) == 0;
-  if (!(int_mma && p.qmode <= 1 ? stores : simple)) return false;
-  const int64_t t128 = ceil_div(p.m, 128) * ceil_div(p.n, 128), t256 = ceil_div(p.m, 256) * ceil_div(p.n, 256);
-  const double r128 = static_cast<double>(ceil_div(t128, 2 * cus));
-  const double r256 = static_cast<double>(ceil_div(t256, cus)) * 1.66;
-  return r256 < 0.9 * r128;  // a clear margin: near-ties measured slower (16384x2304x768 int8)
-}
-
-int device_cus() {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    return 256;
-  return cus;
-}
-
-template <typename Mma, typename TO, int AM>
-int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
-  dim3 grid;
-  if constexpr (AM == kDenseK || AM == kConvTap) {
-    if (dma_eligible(p, batch, AM) && big_tile_wins(p, device_cus(), sizeof(TO), Mma::kInt)) {
-      grid_of<256, 256>(p, 1, grid);
-      hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 256, 4, 2, AM, 2, 8>), grid, dim3(512), 0, s, p);
-      return launch_status(what);
-    }
-    if (dma_eligible(p, batch, AM)) {
-      // Two stages (one tile in flight): 64-80 KB of LDS, so two blocks share
-      // a CU and one's fill and epilogue overlap the other's MFMAs -- this
-      // measured faster than deeper pipelines at one block per CU.
-      if (p.n <= 64) {
-        grid_of<256, 64>(p, 1, grid);
-        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 64, 4, 1, AM, 2>), grid, dim3(kThreads), 0, s, p);
-      } else {
-        grid_of<128, 128>(p, 1, grid);
-        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 128, 128, 2, 2, AM, 2>), grid, dim3(kThreads), 0, s, p);
-      }
-      return launch_status(what);
-    }
-  }
-  if constexpr (AM == kDenseK || AM == kConvTap) {
-    if (batch == 1 && p.a_bytes > 0 && p.b_bytes > 0 && p.a_bytes < (int64_t{1} << 31) &&
-        p.b_bytes < (int64_t{1} << 31) && !getenv("C3H_DISABLE_BUF")) {
-      if (p.n <= 64) {
-        grid_of<256, 64>(p, 1, grid);
-        hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 256, 64, 4, 1, AM, true>), grid, dim3(kThreads), 0, s, p);
-      } else {
-        grid_of<128, 128>(p, 1, grid);
-        hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 128, 128, 2, 2, AM, true>), grid, dim3(kThreads), 0, s, p);
-      }
-      return launch_status(what);
-    }
-  }
-  if (p.n <= 64) {
-    grid_of<256, 64>(p, batch, grid);
-    hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 256, 64, 4, 1, AM>), grid, dim3(kThreads), 0, s, p);
-  } else {
-    grid_of<128, 128>(p, batch, grid);
-    hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 128, 128, 2, 2, AM>), grid, dim3(kThreads), 0, s, p);
-  }
-  return launch_status(what);
-}
-
-// 16-bit inputs write either the same 16-bit type or fp32.
-template <typename Mma, typename T, int AM>
-int launch_h(Problem p, int64_t batch, hipStream_t s, int in_dtype) {
-  if (p.out_dtype == C3H_F32) return launch_mfma<Mma, float, AM>(p, batch, s, "gemm_h");
-  if (p.out_dtype == in_dtype) return launch_mfma<Mma, T, AM>(p, batch, s, "gemm_h");
-  return fail(C3H_EUNSUPPORTED, "gemm: 16-bit inputs write fp32 or the input dtype, not %d", p.out_dtype);
-}
-
-template <int AM>
-int launch_h_any(Problem p, int64_t batch, hipStream_t s, int in_dtype) {
-  return in_dtype == C3H_BF16 ? launch_h<MmaBF16, bf16_t, AM>(p, batch, s, in_dtype)
-                              : launch_h<MmaF16, f16_t, AM>(p, batch, s, in_dtype);
-}
-
-// fp8 GEMM: the two-stage DMA kernel where its 32-bit buffer offsets reach,
-// else the register-prefetch kernel.
-template <typename TO>
-int launch_fp8(Problem p, hipStream_t s) {
-  dim3 grid;
-  if (dma_eligible(p, 1, kDenseK) && big_tile_wins(p, device_cus(), sizeof(TO), false)) {
-    grid_of<256, 256>(p, 1, grid);
-    hipLaunchKernelGGL((mfma_gemm_dma_kernel<MmaF8, TO, 256, 256, 4, 2, kDenseK, 2, 8>), grid, dim3(512), 0, s, p);
-  } else if (dma_eligible(p, 1, kDenseK)) {
-    if (p.n <= 64) {
-      grid_of<256, 64>(p, 1, grid);
-      hipLaunchKernelGGL((mfma_gemm_dma_kernel<MmaF8, TO, 256, 64, 4, 1, kDenseK, 2>), grid, dim3(kThreads), 0, s, p);
-    } else {
-      grid_of<128, 128>(p, 1, grid);
-      hipLaunchKernelGGL((mfma_gemm_dma_kernel<MmaF8, TO, 128, 128, 2, 2, kDenseK, 2>), grid, dim3(kThreads), 0, s, p);
-    }
-  } else if (p.n <= 64) {
-    grid_of<256, 64>(p, 1, grid);
-    hipLaunchKernelGGL((mfma_gemm_kernel<MmaF8, TO, 256, 64, 4, 1, kDenseK>), grid, dim3(kThreads), 0, s, p);
-  } else {
-    grid_of<128, 128>(p, 1, grid);
-    hipLaunchKernelGGL((mfma_gemm_kernel<MmaF8, TO, 128, 128, 2, 2, kDenseK>), grid, dim3(kThreads), 0, s, p);
-  }
-  return launch_status("gemm_fp8");
-}
-
-int check_epilogue(const c3h_epilogue& e) {
-  C3H_REQUIRE(e.bias_mode >= 0 && e.bias_mode <= 4, "epilogue: bad bias_mode %d", e.bias_mode);
-  C3H_REQUIRE(e.bias_mode == 0 || e.bias != nullptr, "epilogue: bias_mode %d needs a bias pointer", e.bias_mode);
-  C3H_REQUIRE(e.act >= 0 && e.act <= 2, "epilogue: bad act %d", e.act);
-  C3H_REQUIRE(e.act != 2 || e.n_imm >= 3, "epilogue: act 2 (gelu) reads imm[0..2]");
-  C3H_REQUIRE(e.n_imm >= 0 && e.n_imm <= 8, "epilogue: n_imm %d out of range", e.n_imm);
-  C3H_REQUIRE(e.n_inst >= 0 && e.n_inst <= C3H_EW_MAX_INST, "epilogue: n_inst %d out of range", e.n_inst);
-  for (int i = 0; i < e.n_inst; ++i) {
-    int limit = 2 + e.n_imm;
-    C3H_REQUIRE(e.inst[i].a >= 0 && e.inst[i].a < limit && e.inst[i].b >= 0 && e.inst[i].b < limit,
-                "epilogue: instruction %d operand outside [0,%d)", i, limit);
-    C3H_REQUIRE(e.inst[i].op >= 0 && e.inst[i].op <= C3H_EW_COPY, "epilogue: bad opcode %d", e.inst[i].op);
-  }
-  return C3H_OK;
-}
-
-inline bool aligned(const void* ptr, int bytes) { return (reinterpret_cast<uintptr_t>(ptr) & (bytes - 1)) == 0; }
 
 }  // namespace
 
@@ -1831,16 +81,16 @@ int c3h_gemm(const c3h_gemm_args* a, void* stream) {
       return launch_status("gemm_simple");
     }
     if (a->trans_a) {
-      return a->trans_b ? launch_f32<kDenseM, true>(p, a->batch, s) : launch_f32<kDenseM, false>(p, a->batch, s);
+      return launch_f32_modes(p, a->batch, s, kDenseM, a->trans_b != 0);
     }
-    return a->trans_b ? launch_f32<kDenseK, true>(p, a->batch, s) : launch_f32<kDenseK, false>(p, a->batch, s);
+    return launch_f32_modes(p, a->batch, s, kDenseK, a->trans_b != 0);
   }
   if (a->in_dtype == C3H_BF16 || a->in_dtype == C3H_F16) {
     C3H_REQUIRE(!a->trans_a && a->trans_b, "gemm: 16-bit path needs A [m,k] and B packed [n,k] (trans_b=1)");
     C3H_REQUIRE(a->k % 8 == 0 && a->lda % 8 == 0 && a->ldb % 8 == 0 && a->stride_a % 8 == 0 && a->stride_b % 8 == 0,
                 "gemm: 16-bit path needs k, lda, ldb multiples of 8");
     C3H_REQUIRE(aligned(a->a, 16) && aligned(a->b, 16), "gemm: 16-bit operands must be 16-byte aligned");
-    return launch_h_any<kDenseK>(p, a->batch, s, a->in_dtype);
+    return a->in_dtype == C3H_BF16 ? launch_bf16_dense(p, a->batch, s) : launch_f16_dense(p, a->batch, s);
   }
   return fail(C3H_EUNSUPPORTED, "gemm: input dtype %d unsupported", a->in_dtype);
 }
@@ -1884,7 +134,7 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
     p.fd_kwpack = make_fastdiv(static_cast<uint32_t>(p.kw_pack));
     p.k = static_cast<int64_t>(a->kh) * a->kw * a->c_pack;
     p.ldb = p.k;
-    return launch_f32<kConv, true>(p, 1, s);
+    return launch_f32_modes(p, 1, s, kConv, true);
   }
   if (a->in_dtype == C3H_BF16 || a->in_dtype == C3H_F16) {
     C3H_REQUIRE(aligned(a->x, 16) && aligned(a->w, 16), "conv2d: x and w must be 16-byte aligned");
@@ -1898,8 +148,8 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
       rc = conv3x3_c64_launch(a, s, &handled);
       if (handled || rc) return rc;
       // A 64-wide K tile stays inside one filter tap when c_pack % 64 == 0.
-      if (a->c_pack % 64 == 0) return launch_h_any<kConvTap>(p, 1, s, a->in_dtype);
-      return launch_h_any<kConv>(p, 1, s, a->in_dtype);
+      const int am = a->c_pack % 64 == 0 ? kConvTap : kConv;
+      return a->in_dtype == C3H_BF16 ? launch_bf16_conv(p, s, am) : launch_f16_conv(p, s, am);
     }
     // Narrow-channel stem: c_pack = c_stride = 4, kw padded to a multiple of
     // 2 so each 32-wide K tile covers whole pixels (8-byte vectors).
@@ -1908,7 +158,7 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
     p.fd_kwpack = make_fastdiv(static_cast<uint32_t>(p.kw_pack));
     p.k = static_cast<int64_t>(a->kh) * p.kw_pack * 4;
     p.ldb = p.k;
-    return launch_h_any<kConvStem>(p, 1, s, a->in_dtype);
+    return a->in_dtype == C3H_BF16 ? launch_bf16_conv(p, s, kConvStem) : launch_f16_conv(p, s, kConvStem);
   }
   return fail(C3H_EUNSUPPORTED, "conv2d: input dtype %d unsupported", a->in_dtype);
 }
@@ -2089,9 +339,7 @@ int c3h_gemm_fp8(const c3h_fp8_gemm_args* a, void* stream) {
   p.a_bytes = (a->m - 1) * a->lda + a->k;
   p.b_bytes = (a->n - 1) * a->ldb + a->k;
   hipStream_t s = as_stream(stream);
-  if (a->out_dtype == C3H_F32) return launch_fp8<float>(p, s);
-  if (a->out_dtype == C3H_BF16) return launch_fp8<bf16_t>(p, s);
-  return launch_fp8<f16_t>(p, s);
+  return launch_f8(p, s, a->out_dtype);
 }
 
 int c3h_qgemm(const c3h_qgemm_args* a, void* stream) {
@@ -2119,11 +367,7 @@ int c3h_qgemm(const c3h_qgemm_args* a, void* stream) {
   p.a_bytes = (a->m - 1) * a->lda + a->k;
   p.b_bytes = (a->n - 1) * a->ldb + a->k;
   hipStream_t s = as_stream(stream);
-  if (a->mode == 0) return launch_mfma<MmaI8, int32_t, kDenseK>(p, 1, s, "qgemm");
-  if (a->mode == 1) return launch_mfma<MmaI8, int8_t, kDenseK>(p, 1, s, "qgemm");
-  if (a->out_dtype == C3H_F32) return launch_mfma<MmaI8, float, kDenseK>(p, 1, s, "qgemm");
-  if (a->out_dtype == C3H_BF16) return launch_mfma<MmaI8, bf16_t, kDenseK>(p, 1, s, "qgemm");
-  return launch_mfma<MmaI8, f16_t, kDenseK>(p, 1, s, "qgemm");
+  return launch_i8(p, s, a->mode, a->out_dtype);
 }
 
 }  // extern "C"
