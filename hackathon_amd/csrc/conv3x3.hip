@@ -272,6 +272,9 @@ __global__ void __launch_bounds__(kWaves * 64, 2) conv3x3_c64_kernel(Conv3x3Args
         dst[i] = *reinterpret_cast<const vec*>(base + (ks ? (aaddr[i] ^ 64u) : aaddr[i]));
     };
     load_a(std::integral_constant<int, 0>{}, av[0]);
+    // MFMA section at raised wave priority (the other block on this CU's
+    // SIMDs does its DMA issue and epilogue in the gaps).
+    __builtin_amdgcn_s_setprio(1);
     static_for<18>([&](auto uc) {
       constexpr int u = decltype(uc)::value;
       if constexpr (u + 1 < 18) load_a(std::integral_constant<int, u + 1>{}, av[(u + 1) & 1]);
@@ -281,6 +284,7 @@ __global__ void __launch_bounds__(kWaves * 64, 2) conv3x3_c64_kernel(Conv3x3Args
         for (int j = 0; j < kTN; ++j) acc[i][j] = Frag<F16>::mma(bw[j][u], av[u & 1][i], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
     });
+    __builtin_amdgcn_s_setprio(0);
 
     // Epilogue from the C^T accumulators: acc[i][j][r] is output pixel
     // q = wm * 64 + 16 i + l16 of the band, channel wn * 32 + 16 j + 4 lg + r.

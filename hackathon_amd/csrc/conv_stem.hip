@@ -222,6 +222,7 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
     for (int i = 0; i < TPW; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    __builtin_amdgcn_s_setprio(1);  // MFMA section at raised wave priority
 #pragma unroll
     for (int kh = 0; kh < KH; ++kh) {
 #pragma unroll
@@ -235,6 +236,7 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     // bias (+ the absent residual's +0, as c3h_conv2d) + ReLU, rounded, into the conv tile [pixel][channel].
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {

@@ -1357,7 +1357,30 @@ __device__ __forceinline__ void wait_vmcnt() {
 // NW waves per block.  NW = 8 is the large-tile form (256 x 256, wave tiles
 // 64 x 128, one block per CU): half the operand bytes per flop of 128 x 128,
 // direct epilogues only (its LDS cannot also hold a staged epilogue).
-template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, int S, int NW = 4>
+// Raised wave priority around the MFMA sections of the DMA kernel.
+#ifndef C3H_MFMA_PRIO
+#define C3H_MFMA_PRIO 1
+#endif
+constexpr bool kPrio = C3H_MFMA_PRIO != 0;
+
+// s_waitcnt with only the LDS/scalar-memory counter constrained to 0.
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xF | (0x7 << 4) | (0x3 << 14)); }
+
+// vmcnt(n * per) for a runtime n in [0, 3] (the wait needs an immediate).
+template <int PER>
+__device__ __forceinline__ void wait_vmcnt_groups(int64_t n) {
+  if (n >= 3) wait_vmcnt<3 * PER>();
+  else if (n == 2) wait_vmcnt<2 * PER>();
+  else if (n == 1) wait_vmcnt<PER>();
+  else wait_vmcnt<0>();
+}
+
+// RP (register pipelining): the operand fragments of K tile kt + 1 are read
+// from LDS into a second register set while the MFMAs of tile kt run from
+// the first, and all S stages hold tiles in flight (DMA lead S - 1 tiles).
+// The K order and every accumulation are those of the RP = false kernel, so
+// the two are bit-identical.
+template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, int S, int NW = 4, bool RP = false>
 __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
   constexpr bool DIRECT = NW > 4;
   constexpr bool DIRECT_GELU = DIRECT;
@@ -1473,10 +1496,79 @@ __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
     for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
 
   const int64_t ktiles = ceil_div(p.k, BK);
+  const int lrow = lane & 15, lchunk = lane >> 4;
+  if constexpr (RP) {
+    static_assert(LPW * (S - 1) < 64, "vmcnt range");
+    constexpr int KS = 8 / Mma::kStep;
+    constexpr int N_MFMA = KS * TM * TN;
+    constexpr int N_DSR = KS * (TM + TN) * (Mma::kStep == 8 ? 2 : 1);
+    constexpr int PER = N_MFMA / N_DSR;
+    vec av[2][KS][TM], bv[2][KS][TN];
+    auto read_frags = [&](auto set_c, int stage) {
+      constexpr int SET = decltype(set_c)::value;
+      const uint8_t* As = smem + stage * STAGE;
+      const uint8_t* Bs = As + BM * RB;
+#pragma unroll
+      for (int q = 0; q < KS; ++q) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int r = wm * WTM + i * 16 + lrow;
+          av[SET][q][i] = read_operand<Mma>(As + r * RB, r, q * Mma::kStep, lchunk);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int r = wn * WTN + j * 16 + lrow;
+          bv[SET][q][j] = read_operand<Mma>(Bs + r * RB, r, q * Mma::kStep, lchunk);
+        }
+      }
+    };
+    // Prologue: every stage receives a tile; tile 0's fragments go to set 0.
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+      if (st < ktiles) issue(st, st);
+    wait_vmcnt_groups<LPW>(min(static_cast<int64_t>(S - 1), ktiles - 1));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    read_frags(std::integral_constant<int, 0>{}, 0);
+    auto body = [&](auto set_c, int64_t kt) {
+      constexpr int SET = decltype(set_c)::value;
+      // This wave's reads of tile kt are done and its part of tile kt + 1
+      // has landed; after the barrier every wave is there, so tile kt's
+      // stage may be refilled and tile kt + 1 read.
+      wait_lgkmcnt0();
+      wait_vmcnt_groups<LPW>(max(static_cast<int64_t>(0), min(static_cast<int64_t>(S - 2), ktiles - 2 - kt)));
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (kt + S < ktiles) issue(kt + S, static_cast<int>(kt % S));
+      __builtin_amdgcn_sched_barrier(0);
+      // Tile kt + 1's fragments into the other set (past the last tile this
+      // reads a stale, in-bounds stage into the unused set), one LDS read
+      // between every PER MFMAs of tile kt.
+      read_frags(std::integral_constant<int, SET ^ 1>{}, static_cast<int>((kt + 1) % S));
+#pragma unroll
+      for (int q = 0; q < KS; ++q)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = Mma::mma(bv[SET][q][j], av[SET][q][i], acc[i][j]);
+#pragma unroll
+      for (int g = 0; g < N_DSR; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // one LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);  // PER MFMAs
+      }
+      if constexpr (N_MFMA > PER * N_DSR) __builtin_amdgcn_sched_group_barrier(0x008, N_MFMA - PER * N_DSR, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int64_t kt = 0; kt < ktiles; kt += 2) {
+      body(std::integral_constant<int, 0>{}, kt);
+      if (kt + 1 < ktiles) body(std::integral_constant<int, 1>{}, kt + 1);
+    }
+  } else {
 #pragma unroll
   for (int st = 0; st < S - 1; ++st)
     if (st < ktiles) issue(st, st);
-  const int lrow = lane & 15, lchunk = lane >> 4;
   for (int64_t kt = 0; kt < ktiles; ++kt) {
     // Tiles issued after kt (at most S - 2 of them) may stay in flight.
     const int64_t later = min(static_cast<int64_t>(S - 2), ktiles - 1 - kt);
@@ -1515,6 +1607,10 @@ __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
       }
     }
     __builtin_amdgcn_sched_barrier(0);
+    // The MFMA section runs at raised wave priority: of the two blocks
+    // sharing a CU, the one multiplying keeps the matrix pipe fed while the
+    // other waits on its DMA, barrier and LDS reads.
+    if constexpr (kPrio) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int q = 0; q < KS; ++q)
 #pragma unroll
@@ -1523,6 +1619,9 @@ __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
         for (int j = 0; j < TN; ++j) {
           acc[i][j] = Mma::mma(bv[q][j], av[q][i], acc[i][j]);  // C^T: see epilogue_direct
         }
+    if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   }
 
   if constexpr (Mma::kScaled) scale_acc<TM, TN>(acc, m0 + wm * WTM, n0 + wn * WTN, lane);
@@ -1657,6 +1756,13 @@ inline bool big_tile_wins(const Problem& p, int cus, size_t out_size, bool int_m
   return r256 < 0.9 * r128;  // a clear margin: near-ties measured slower (16384x2304x768 int8)
 }
 
+// Register-pipelined form of the 4-wave DMA kernel: C3H_DMA_RP = 2, 3 or 4
+// LDS stages (0: the two-stage kernel without register pipelining).
+inline int dma_rp_stages() {
+  const char* v = getenv("C3H_DMA_RP");
+  return v ? atoi(v) : 0;
+}
+
 inline int device_cus() {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
@@ -1675,15 +1781,28 @@ int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
       return launch_status(what);
     }
     if (dma_eligible(p, batch, AM)) {
-      // Two stages (one tile in flight): 64-80 KB of LDS, so two blocks share
-      // a CU and one's fill and epilogue overlap the other's MFMAs -- this
-      // measured faster than deeper pipelines at one block per CU.
+      const int rp = dma_rp_stages();
       if (p.n <= 64) {
         grid_of<256, 64>(p, 1, grid);
-        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 64, 4, 1, AM, 2>), grid, dim3(kThreads), 0, s, p);
+        if (rp == 2)
+          hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 64, 4, 1, AM, 2, 4, true>), grid, dim3(kThreads), 0, s, p);
+        else if (rp == 3)
+          hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 64, 4, 1, AM, 3, 4, true>), grid, dim3(kThreads), 0, s, p);
+        else
+          hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 64, 4, 1, AM, 2>), grid, dim3(kThreads), 0, s, p);
       } else {
         grid_of<128, 128>(p, 1, grid);
-        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 128, 128, 2, 2, AM, 2>), grid, dim3(kThreads), 0, s, p);
+        if (rp == 2)
+          hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 128, 128, 2, 2, AM, 2, 4, true>), grid, dim3(kThreads), 0, s,
+                             p);
+        else if (rp == 3)
+          hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 128, 128, 2, 2, AM, 3, 4, true>), grid, dim3(kThreads), 0, s,
+                             p);
+        else if (rp == 4)
+          hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 128, 128, 2, 2, AM, 4, 4, true>), grid, dim3(kThreads), 0, s,
+                             p);
+        else
+          hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 128, 128, 2, 2, AM, 2>), grid, dim3(kThreads), 0, s, p);
       }
       return launch_status(what);
     }

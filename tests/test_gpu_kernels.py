@@ -1058,3 +1058,113 @@ def test_layernorm_int8_output_equals_layernorm_then_quantize(gpu, rows, cols, d
     a_, b_ = codes_a.get(), codes_b.get()
     np.testing.assert_array_equal(a_, b_)
     assert (a_ == 127).any() and (a_ == -128).any()
+
+
+def _with_env(var, value, fn):
+    import os
+
+    old = os.environ.get(var)
+    if value is None:
+        os.environ.pop(var, None)
+    else:
+        os.environ[var] = value
+    try:
+        return fn()
+    finally:
+        if old is None:
+            os.environ.pop(var, None)
+        else:
+            os.environ[var] = old
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16", "int8"])
+@pytest.mark.parametrize("m,n,k", [(300, 200, 64), (256, 128, 128), (130, 70, 192), (1000, 256, 320),
+                                   (4096, 512, 1152), (512, 64, 576), (2048, 2048, 512)])
+def test_gemm_register_pipelined_matches_two_stage(gpu, kind, m, n, k):
+    """The register-pipelined DMA kernel (2, 3 or 4 LDS stages) is bit for bit
+    the two-stage kernel: same K order, same accumulation, same epilogue --
+    for K tile counts below, at and above the stage count, ragged M/N and a
+    bias + residual + ReLU epilogue (int8: requantize -> dequantize mode 3)."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    rng = np.random.default_rng(m + 3 * n + 7 * k)
+    bias = _dev(rng.standard_normal(n).astype(np.float32))
+    if kind == "int8":
+        a = _dev(rng.integers(-128, 128, size=(m, k), dtype=np.int8))
+        b = _dev(rng.integers(-127, 128, size=(n, k), dtype=np.int8))
+        sb = _dev((rng.random(n) * 0.01 + 0.001).astype(np.float32))
+        res = _dev(_bits(rng.standard_normal((m, n)).astype(np.float32), "bf16")[0])
+        out = DeviceArray.empty((m, n), BF16)
+    else:
+        a = _dev(_bits(rng.standard_normal((m, k)).astype(np.float32), kind)[0])
+        b = _dev(_bits(rng.standard_normal((n, k)).astype(np.float32), kind)[0])
+        res = _dev(_bits(rng.standard_normal((m, n)).astype(np.float32), kind)[0])
+        out = DeviceArray.empty((m, n), BF16 if kind == "bf16" else np.float16)
+
+    def run():
+        out.copy_from_host(np.zeros(out.nbytes, np.uint8))
+        if kind == "int8":
+            g = _lib.QGemmArgs()
+            g.a, g.b, g.out, g.m, g.n, g.k, g.lda, g.ldb, g.ldo = a.ptr, b.ptr, out.ptr, m, n, k, k, k, n
+            g.a_scale, g.y_scale, g.b_scale, g.mode, g.out_dtype = 0.02, 0.37, sb.ptr, 3, _lib.BF16
+            g.epi = E.epilogue(bias=bias, bias_mode=2, act=1, residual=res)
+        else:
+            g = _lib.GemmArgs()
+            g.a, g.b, g.out, g.m, g.n, g.k, g.lda, g.ldb, g.ldo, g.batch = a.ptr, b.ptr, out.ptr, m, n, k, k, k, n, 1
+            code = _lib.BF16 if kind == "bf16" else _lib.F16
+            g.trans_a, g.trans_b, g.in_dtype, g.out_dtype = 0, 1, code, code
+            g.epi = E.epilogue(bias=bias, bias_mode=2, act=1, residual=res)
+        _lib.launch(g, None)
+        return out.get().copy()
+
+    print(f"register pipelining {kind} {m}x{n}x{k}", flush=True)
+    want = _with_env("C3H_DISABLE_BIGTILE", "1", lambda: _with_env("C3H_DMA_RP", "0", run))
+    assert np.any(want.view(np.uint8) != 0)
+    for rp in ("2", "3", "4"):
+        got = _with_env("C3H_DISABLE_BIGTILE", "1", lambda: _with_env("C3H_DMA_RP", rp, run))
+        np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8), err_msg=f"RP stages {rp}")
+
+
+@pytest.mark.parametrize("n,hw,c,o,kh,stride", [(256, 28, 128, 128, 3, 1), (256, 56, 64, 128, 3, 2),
+                                                (8, 14, 256, 256, 3, 1), (16, 7, 512, 512, 3, 1),
+                                                (32, 28, 128, 256, 1, 2)])
+def test_conv_register_pipelined_matches_two_stage(gpu, n, hw, c, o, kh, stride):
+    """Tap-uniform implicit-GEMM convs (the ResNet-18 layer 2-4 shapes) on the
+    register-pipelined kernel are bit-identical to the two-stage kernel."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    rng = np.random.default_rng(n + hw + c + o + kh)
+    pad = kh // 2
+    ho = (hw + 2 * pad - kh) // stride + 1
+    x, _ = _bits(rng.standard_normal((n, hw, hw, c)).astype(np.float32), "bf16")
+    kpack = ((kh * kh * c + 31) // 32) * 32
+    w = np.zeros((o, kpack), np.float32)
+    w[:, :kh * kh * c] = rng.standard_normal((o, kh * kh * c)).astype(np.float32) * 0.05
+    wb, _ = _bits(w, "bf16")
+    res, _ = _bits(rng.standard_normal((n, ho, ho, o)).astype(np.float32), "bf16")
+    xd, wd, rd = _dev(x), _dev(wb), _dev(res)
+    bd = _dev(rng.standard_normal(o).astype(np.float32))
+    out = DeviceArray.empty((n, ho, ho, o), BF16)
+
+    def run():
+        out.copy_from_host(np.zeros(out.nbytes, np.uint8))
+        a = _lib.ConvArgs()
+        a.x, a.w, a.out = xd.ptr, wd.ptr, out.ptr
+        a.n, a.c, a.h, a.w_, a.c_stride, a.c_pack, a.o = n, c, hw, hw, c, c, o
+        a.kh, a.kw, a.sh, a.sw, a.pad_top, a.pad_left, a.dh, a.dw, a.ho, a.wo = kh, kh, stride, stride, pad, pad, \
+            1, 1, ho, ho
+        a.out_layout, a.in_dtype, a.out_dtype = 1, _lib.BF16, _lib.BF16
+        a.epi = E.epilogue(bias=bd, bias_mode=2, act=1, residual=rd)
+        _lib.launch(a, None)
+        return out.get().copy()
+
+    print(f"register pipelining conv n={n} {hw}x{hw} c={c} o={o} k={kh} s={stride}", flush=True)
+    want = _with_env("C3H_DISABLE_BIGTILE", "1", lambda: _with_env("C3H_DMA_RP", "0", run))
+    assert np.any(want.view(np.uint8) != 0)
+    for rp in ("2", "3", "4"):
+        got = _with_env("C3H_DISABLE_BIGTILE", "1", lambda: _with_env("C3H_DMA_RP", rp, run))
+        np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8), err_msg=f"RP stages {rp}")
