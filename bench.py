@@ -53,6 +53,8 @@ DOMINANT = {
     "decoder_fp16": (["gemm"], "fp16", "GEMM + fused epilogues (fp16 MFMA 16x16x32)"),
     "decoder_w8a8": (["qgemm"], "int8", "int8 GEMM + requant/dequant epilogue (MFMA i32 16x16x64)"),
     "decoder_fp8": (["gemm_fp8"], "fp8", "E4M3 GEMM + scale/epilogue (MFMA f32 16x16x128 f8f6f4)"),
+    "decoder_fp4": (["gemm_w4a16"], "fp16", "W4A16 GEMM: MXFP4 weights widened to fp16 in registers "
+                    "(fp16 MFMA 16x16x32)"),
 }
 BASELINE_INDEX = {"mlp": 0, "resnet18_cifar": 1, "resnet18_224": 2, "decoder_fp16": 3, "decoder_w8a8": 4}
 CPU_SAMPLE = {"mlp": 4096, "resnet18_cifar": 128, "resnet18_224": 48, "decoder_fp16": 16, "decoder_w8a8": 2}
@@ -60,7 +62,8 @@ CPU_SAMPLE = {"mlp": 4096, "resnet18_cifar": 128, "resnet18_224": 48, "decoder_f
 CPU_SAMPLE_PER_CONFIG = {"mlp": 4096, "resnet18_cifar": 32, "resnet18_224": 8, "decoder_fp16": 8, "decoder_w8a8": 1}
 MEMORY_BOUND = ("layernorm", "layernorm_q", "gather_add", "gather", "quantize", "quantize_fp8", "dequantize", "argmax",
                 "maxpool", "gap", "layout", "splitk_reduce", "ew", "softmax", "cast", "copy")
-# decoder_fp8 is no BASELINE config: the decoder_fp16 model under the "fp8" policy (E4M3 GEMMs).
+# decoder_fp8 and decoder_fp4 are no BASELINE configs: the decoder_fp16 model under the "fp8" policy
+# (E4M3 GEMMs) and the "fp4" policy (W4A16 GEMMs, the reference's fp4 choice made executable).
 
 
 def _log(msg: str) -> None:
@@ -396,7 +399,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="mlp,resnet18_cifar,resnet18_224,decoder_fp16,decoder_w8a8",
+    ap.add_argument("--configs", default="mlp,resnet18_cifar,resnet18_224,decoder_fp16,decoder_w8a8,decoder_fp4",
                     help="comma-separated workloads to measure (the headline is always included)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-run", metavar="META_JSON",

@@ -34,7 +34,7 @@ OP_NOP, OP_EVENT_RECORD, OP_EVENT_WAIT, OP_COPY = 0, 1, 2, 3
 OP_FILL, OP_CAST, OP_EW, OP_STRIDED_COPY, OP_REDUCE, OP_SOFTMAX, OP_LAYERNORM, OP_BATCHNORM, \
     OP_GATHER, OP_ARGMAX, OP_IM2COL, OP_LAYOUT, OP_MAXPOOL, OP_GEMM, OP_CONV, OP_ATTN_SCORES, \
     OP_FLASH, OP_QUANTIZE, OP_QGEMM, OP_DEQUANTIZE, OP_BNFOLD, OP_PACK, OP_CONV_POOL, OP_QUANT_FP8, \
-    OP_GEMM_FP8, OP_SPLITK = range(10, 36)
+    OP_GEMM_FP8, OP_SPLITK, OP_QUANT_MXFP4, OP_GEMM_W4A16 = range(10, 38)
 
 vp = C.c_void_p
 i32 = C.c_int32
@@ -197,6 +197,17 @@ class Fp8GemmArgs(C.Structure):
                 ("pad_", i32), ("epi", Epilogue)]
 
 
+class Mxfp4QuantArgs(C.Structure):
+    _fields_ = [("x", vp), ("codes", vp), ("scales", vp), ("rows", i64), ("cols", i64), ("ldx", i64),
+                ("ldc", i64), ("lds", i64), ("x_dtype", i32), ("pad_", i32)]
+
+
+class W4A16GemmArgs(C.Structure):
+    _fields_ = [("a", vp), ("b_codes", vp), ("b_scales", vp), ("out", vp), ("m", i64), ("n", i64),
+                ("k", i64), ("lda", i64), ("ldb", i64), ("ldbs", i64), ("ldo", i64), ("out_dtype", i32),
+                ("pad_", i32), ("epi", Epilogue)]
+
+
 class SplitKArgs(C.Structure):
     _fields_ = [("partial", vp), ("out", vp), ("m", i64), ("n", i64), ("ldo", i64), ("splits", i32),
                 ("out_dtype", i32), ("epi", Epilogue)]
@@ -217,7 +228,7 @@ ABI_ORDER = [Props, FillArgs, CastArgs, EwArgs, CopyArgs, ReduceArgs, SoftmaxArg
              BatchNormArgs, BnFoldArgs, GatherArgs, ArgmaxArgs, Im2colArgs, LayoutArgs, PoolArgs,
              Epilogue, GemmArgs, ConvArgs, AttnScoresArgs, FlashArgs, QuantizeArgs, QGemmArgs,
              DequantizeArgs, Op, PackArgs, ConvPoolArgs, Fp8QuantArgs, Fp8GemmArgs,
-             SplitKArgs]
+             SplitKArgs, Mxfp4QuantArgs, W4A16GemmArgs]
 
 # Kernel entry points: name -> args struct (all take (const args*, void* stream)).
 KERNELS = {
@@ -230,7 +241,8 @@ KERNELS = {
     "c3h_quantize": QuantizeArgs, "c3h_qgemm": QGemmArgs, "c3h_dequantize": DequantizeArgs,
     "c3h_pack_conv_weight": PackArgs, "c3h_conv_stem_pool": ConvPoolArgs,
     "c3h_quantize_fp8_rows": Fp8QuantArgs, "c3h_gemm_fp8": Fp8GemmArgs,
-    "c3h_gemm_splitk_reduce": SplitKArgs,
+    "c3h_gemm_splitk_reduce": SplitKArgs, "c3h_quantize_mxfp4": Mxfp4QuantArgs,
+    "c3h_gemm_w4a16": W4A16GemmArgs,
 }
 
 OP_KIND = {
@@ -242,6 +254,7 @@ OP_KIND = {
     QuantizeArgs: OP_QUANTIZE, QGemmArgs: OP_QGEMM, DequantizeArgs: OP_DEQUANTIZE,
     BnFoldArgs: OP_BNFOLD, PackArgs: OP_PACK, ConvPoolArgs: OP_CONV_POOL,
     Fp8QuantArgs: OP_QUANT_FP8, Fp8GemmArgs: OP_GEMM_FP8, SplitKArgs: OP_SPLITK,
+    Mxfp4QuantArgs: OP_QUANT_MXFP4, W4A16GemmArgs: OP_GEMM_W4A16,
 }
 
 KERNEL_OF_ARGS = {v: k for k, v in KERNELS.items()}
@@ -266,6 +279,7 @@ def _declare(lib: C.CDLL) -> None:
         "c3h_device_props": ([C.c_int, P(Props)], C.c_int),
         "c3h_last_error": ([], C.c_char_p),
         "c3h_device_synchronize": ([], C.c_int),
+        "c3h_reload_switches": ([], C.c_int),
         "c3h_malloc": ([P(vp), C.c_size_t], C.c_int),
         "c3h_free": ([vp], C.c_int),
         "c3h_host_alloc": ([P(vp), C.c_size_t], C.c_int),

@@ -31,6 +31,9 @@ class HardwareCapability:
     supports_fp16: bool = True
     supports_bf16: bool = True
     supports_fp8: bool = True
+    # CDNA4 decodes MXFP4 (E2M1 + E8M0 block exponents) natively; "fp4" is run
+    # as W4A16 (c32/strategy.py:101-108) by c3h_gemm_w4a16.
+    supports_fp4: bool = True
     supports_int8: bool = True
     supports_winograd: bool = True
     extra_gemm_kernels: Set[str] = field(default_factory=set)
@@ -43,6 +46,8 @@ class HardwareCapability:
             out.append("bf16")
         if self.supports_fp8:
             out.append("fp8")
+        if self.supports_fp4:
+            out.append("fp4")
         if self.supports_int8:
             out.append("int8")
         return out
@@ -64,12 +69,14 @@ class HardwareCapability:
 
         props = device_props(device)
         lds = int(props.lds_bytes_per_block)
+        arch = props.arch.decode("utf-8", "replace")
         return cls(
             name=props.name.decode("utf-8", "replace"),
             source="c3h_device_props",
             verified=True,
             compute_capability=(int(props.major), int(props.minor)),
-            arch=props.arch.decode("utf-8", "replace"),
+            arch=arch,
+            supports_fp4=arch.startswith("gfx950"),
             compute_units=int(props.compute_units),
             wavefront_size=int(props.warp_size),
             max_threads_per_block=int(props.max_threads_per_block),

@@ -16,13 +16,19 @@ the planner passes through to `KernelStep.precision_profile`:
   * "w8a8" - QLinearMatMul computes int8 x int8 -> int32; float activations
     are stored in bf16 as in "bf16";
   * "fp8"  - the executable form of the reference's mixed-precision choice
-    (c32/strategy.py:124-160): a constant-weight GEMM that the reference's
-    rule gives fp8 (or fp4, which falls back to fp8 on a profile without
-    fp4, c32/strategy.py:113-122) computes OCP E4M3 x E4M3 with fp32
+    (c32/strategy.py:124-160) on a profile without fp4: a constant-weight
+    GEMM that the reference's rule gives fp8 (or fp4, which then falls back
+    to fp8, c32/strategy.py:113-122) computes OCP E4M3 x E4M3 with fp32
     accumulation (row-wise dynamic activation scales, per-output-channel
     weight scales); every other contraction, and every activation in
     storage, is fp16.  The reference also picks fp8 for aligned 1x1 convs;
     no fp8 conv kernel exists here, so those run fp16.
+  * "fp4"  - the same rule on this profile, which declares fp4: the large
+    aligned constant-weight GEMMs it gives fp4 (c32/strategy.py:150-154) run
+    W4A16 -- MXFP4 weights (E2M1, one E8M0 exponent per 32 k) widened to
+    fp16 in registers, fp16 activations, fp32 accumulation
+    (c32/strategy.py:101-108); those it gives fp8 run E4M3 as under "fp8";
+    the rest, and every activation in storage, fp16.
 """
 
 from __future__ import annotations
@@ -68,24 +74,29 @@ SAFE_FALLBACKS: Dict[str, List[str]] = {
 METADATA_KERNELS: Set[str] = {"constant", "flatten", "reshape", "transpose", "split", "gather"}
 
 
+POLICY_NAMES = ("fp32", "bf16", "fp16", "w8a8", "fp8", "fp4")
+
+
 @dataclass(frozen=True)
 class PrecisionPolicy:
-    """Executable precision policy (name in {"fp32", "bf16", "fp16", "w8a8", "fp8"})."""
+    """Executable precision policy (name in {"fp32", "bf16", "fp16", "w8a8", "fp8", "fp4"})."""
 
     name: str = "fp32"
 
     def __post_init__(self) -> None:
-        if self.name not in ("fp32", "bf16", "fp16", "w8a8", "fp8"):
+        if self.name not in POLICY_NAMES:
             raise ValueError(f"unknown precision policy {self.name!r}")
 
     @property
     def activation_dtype(self) -> str:
-        return {"fp32": "fp32", "bf16": "bf16", "fp16": "fp16", "w8a8": "bf16", "fp8": "fp16"}[self.name]
+        return {"fp32": "fp32", "bf16": "bf16", "fp16": "fp16", "w8a8": "bf16", "fp8": "fp16",
+                "fp4": "fp16"}[self.name]
 
     @property
     def contraction_dtype(self) -> str:
-        """Contraction type of nodes the policy does not single out (fp8: the fp16 fallback)."""
-        return {"fp32": "fp32", "bf16": "bf16", "fp16": "fp16", "w8a8": "bf16", "fp8": "fp16"}[self.name]
+        """Contraction type of nodes the policy does not single out (fp8, fp4: the fp16 fallback)."""
+        return {"fp32": "fp32", "bf16": "bf16", "fp16": "fp16", "w8a8": "bf16", "fp8": "fp16",
+                "fp4": "fp16"}[self.name]
 
 
 FP32_POLICY = PrecisionPolicy("fp32")
@@ -129,7 +140,11 @@ class Strategy:
         if node.op_type == "DequantizeLinear":
             return PrecisionProfile(compute_dtype="fp32", input_dtype="int8", output_dtype=out)
         if node.op_type in CONTRACTION_OPS:
-            if self.policy.name == "fp8" and self.executable_fp8(node, graph):
+            low = self.executable_low_precision(node, graph)
+            if low == "fp4":
+                return PrecisionProfile(compute_dtype="fp4", accumulator_dtype="fp32", input_dtype="fp16",
+                                        weight_dtype="fp4", output_dtype=out)
+            if low == "fp8":
                 return PrecisionProfile(compute_dtype="fp8", accumulator_dtype="fp32", input_dtype="fp8",
                                         weight_dtype="fp8", output_dtype=out)
             c = self.policy.contraction_dtype
@@ -138,8 +153,10 @@ class Strategy:
         return PrecisionProfile(compute_dtype="fp32", accumulator_dtype="fp32", input_dtype=act,
                                 output_dtype=out)
 
-    def _supported_fallback(self, preferred: str) -> str:
+    def _supported_fallback(self, preferred: str, allow_fp4: bool = True) -> str:
         supported = set(self.hardware.supported_precisions())
+        if not allow_fp4:
+            supported.discard("fp4")
         for prec in SAFE_FALLBACKS[preferred]:
             if prec == "fp4" and "fp16" not in supported:
                 continue
@@ -151,17 +168,26 @@ class Strategy:
     _GEMM_FORMS = {"MatMul": "MatMul", "Linear": "Linear", "Gemm": "Gemm", "FusedMatMulBias": "MatMul",
                    "FusedGemmEpilogue": "Gemm"}
 
-    def executable_fp8(self, node: Node, graph: Graph) -> bool:
-        """Whether the "fp8" policy runs `node` on the E4M3 GEMM: a GEMM-shaped
-        node with a constant rank-2 weight that the reference's rule sends to
-        fp8 (directly, or fp4 falling back to fp8 on this profile)."""
+    def executable_low_precision(self, node: Node, graph: Graph) -> Optional[str]:
+        """"fp4" / "fp8" where the policy runs `node` on the W4A16 / E4M3 GEMM,
+        else None: a GEMM-shaped node with a constant rank-2 weight, and the
+        reference's rule's choice for it -- under "fp8" on the profile
+        without fp4 (fp4 falls back to fp8), under "fp4" on this one."""
+        if self.policy.name not in ("fp8", "fp4"):
+            return None
         form = self._GEMM_FORMS.get(node.op_type)
         if form is None or len(node.inputs) < 2:
-            return False
+            return None
         w = graph.get_tensor(node.inputs[1])
         if w is None or not (w.is_initializer or w.is_constant) or len(w.shape) != 2:
-            return False
-        return self._supported_fallback(self._preferred_tunable_precision(node, graph, form)) == "fp8"
+            return None
+        chosen = self._supported_fallback(self._preferred_tunable_precision(node, graph, form),
+                                          allow_fp4=self.policy.name == "fp4")
+        return chosen if chosen in ("fp8", "fp4") else None
+
+    def executable_fp8(self, node: Node, graph: Graph) -> bool:
+        """Whether the policy runs `node` on the E4M3 GEMM."""
+        return self.executable_low_precision(node, graph) == "fp8"
 
     def _preferred_tunable_precision(self, node: Node, graph: Graph, op_type: Optional[str] = None) -> str:
         op_type = op_type or node.op_type

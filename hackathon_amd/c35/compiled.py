@@ -16,6 +16,8 @@ the MI355X instead:
   Under the "fp8" policy a GEMM the plan marks fp8 becomes a row-wise E4M3
   quantization of its activation plus one E4M3 GEMM (weights quantized per
   output channel once at compile time) with the same absorbed epilogue.
+  Under the "fp4" policy a GEMM the plan marks fp4 becomes one W4A16 GEMM on
+  its fp16 activation (weights quantized to MXFP4 once at compile time).
 * Views: Reshape / Flatten / Split / Transpose produce strided views (no
   copies, no host syncs: shape tensors are read at compile time); a consumer
   that needs dense data materializes once.
@@ -23,7 +25,7 @@ the MI355X instead:
   padded to a vector multiple) between convolutions; graph inputs are
   converted once, and channel-last data feeds GlobalAveragePool / MaxPool /
   elementwise chains directly.
-* Precision: the plan's policy ("fp32" | "bf16" | "fp16" | "w8a8" | "fp8") picks the
+* Precision: the plan's policy ("fp32" | "bf16" | "fp16" | "w8a8" | "fp8" | "fp4") picks the
   storage dtype of every activation and the MFMA input type of every
   contraction; weights are packed and converted once at compile time.
 * Memory: activation buffers are re-planned over the grouped launch order
@@ -51,8 +53,9 @@ from ..device import BF16, Buffer, DeviceArray, PinnedArray, Stream, device_prop
 from . import engine as E
 
 _POLICY_ACT = {"fp32": np.dtype(np.float32), "bf16": BF16, "fp16": np.dtype(np.float16), "w8a8": BF16,
-               "fp8": np.dtype(np.float16)}
-_MM_CODE = {"fp32": _lib.F32, "bf16": _lib.BF16, "fp16": _lib.F16, "w8a8": _lib.BF16, "fp8": _lib.F16}
+               "fp8": np.dtype(np.float16), "fp4": np.dtype(np.float16)}
+_MM_CODE = {"fp32": _lib.F32, "bf16": _lib.BF16, "fp16": _lib.F16, "w8a8": _lib.BF16, "fp8": _lib.F16,
+            "fp4": _lib.F16}
 _DTYPE_NAME = {np.dtype(np.float32): "fp32", np.dtype(np.float16): "fp16", BF16: "bf16", np.dtype(np.int8): "int8",
                np.dtype(np.int32): "int32", np.dtype(np.int64): "int64", np.dtype(np.uint8): "u8"}
 
@@ -955,6 +958,46 @@ class CompiledPlan:
                           Val((n,), np.dtype(np.float32), self._persist(scales)), n, k)
         return cache[key]
 
+    def _fp4_weight(self, name: str, trans_b: int) -> Tuple[Val, Val, int, int]:
+        """Weight as MXFP4: E2M1 codes of B^T [n][k/2] + E8M0 block exponents [n][k/32] (quantized on the GPU)."""
+        cache = self.__dict__.setdefault("_f4cache", {})
+        key = (name, trans_b)
+        if key not in cache:
+            w32, n, k = self._packed_weight_nk(name, trans_b, np.float32)
+            if k % 32:
+                raise NotImplementedError(f"MXFP4 weight {name}: K={k} is not a multiple of 32")
+            codes = DeviceArray.empty((n, k // 2), np.uint8)
+            scales = DeviceArray.empty((n, k // 32), np.uint8)
+            q = _lib.Mxfp4QuantArgs()
+            q.x, q.codes, q.scales = w32.buf.array.ptr, codes.ptr, scales.ptr
+            q.rows, q.cols, q.ldx, q.ldc, q.lds, q.x_dtype = n, k, k, k // 2, k // 32, _lib.F32
+            _lib.launch(q, None)
+            cache[key] = (Val((n, k // 2), np.dtype(np.uint8), self._persist(codes)),
+                          Val((n, k // 32), np.dtype(np.uint8), self._persist(scales)), n, k)
+        return cache[key]
+
+    def _gemm_w4a16(self, node, a: Val, w_name: str, trans_b: int, st: "_Epi", alpha: float, beta: float,
+                    bmode, out_shape: Tuple[int, ...]) -> Val:
+        """W4A16 GEMM of the fp16 activation with the MXFP4 weight and the epilogue `st`."""
+        m, k = math.prod(a.shape[:-1]), a.shape[-1]
+        wc, ws, n, kw = self._fp4_weight(w_name, trans_b)
+        if kw != k:
+            raise NotImplementedError(f"GEMM {node.id}: K={k} vs weight K={kw}")
+        a2 = a if (a.dense and a.dtype == np.dtype(np.float16)) else self._dense(a, np.dtype(np.float16))
+        out = self._new(out_shape, self._out_dtype(st.final))
+        self._finish_residual(st, out)
+
+        def build(r, a2=a2, out=out, st=st):
+            g = _lib.W4A16GemmArgs()
+            g.a, g.b_codes, g.b_scales, g.out = self._ptr(a2, r), self._ptr(wc, r), self._ptr(ws, r), self._ptr(out, r)
+            g.m, g.n, g.k, g.lda, g.ldb, g.ldbs, g.ldo = m, n, k, k, k // 2, k // 32, n
+            g.out_dtype = dtype_code(out.dtype)
+            self._fill_epi(g.epi, st, r, alpha, beta, bmode)
+            return g
+        self._emit(f"gemm_w4a16:{node.op_type}", build, [a2, wc, ws] + self._epi_reads(st), [out],
+                   flops=2.0 * m * n * k)
+        return out
+
     def _gemm_fp8(self, node, a: Val, w_name: str, trans_b: int, st: "_Epi", alpha: float, beta: float,
                   bmode, out_shape: Tuple[int, ...]) -> Val:
         """Row-wise E4M3 quantization of A, then the E4M3 GEMM with the epilogue `st`."""
@@ -1008,13 +1051,14 @@ class CompiledPlan:
                    beta: float, act: int, lead: Tuple[int, ...]) -> None:
         """out[lead..., n] = epilogue(alpha * A @ W + beta * bias) with absorbed tails."""
         m, k = math.prod(a.shape[:-1]), a.shape[-1]
-        if self._node_compute.get(node.id) == "fp8":
-            if self.policy != "fp8":
-                raise ValueError(f"GEMM {node.id}: plan computes fp8 but the engine policy is {self.policy!r}")
-            n = self._fp8_weight(w_name, trans_b)[2]
+        low = self._node_compute.get(node.id)
+        if low in ("fp8", "fp4"):
+            if (low, self.policy) not in (("fp8", "fp8"), ("fp8", "fp4"), ("fp4", "fp4")):
+                raise ValueError(f"GEMM {node.id}: plan computes {low} but the engine policy is {self.policy!r}")
+            n = (self._fp8_weight if low == "fp8" else self._fp4_weight)(w_name, trans_b)[2]
             st, bmode = self._gemm_epi_state(node, bias_name, act, m, n, tuple(lead) + (n,))
-            self.vals[st.final] = self._gemm_fp8(node, a, w_name, trans_b, st, alpha, beta, bmode,
-                                                 tuple(lead) + (n,))
+            lower = self._gemm_fp8 if low == "fp8" else self._gemm_w4a16
+            self.vals[st.final] = lower(node, a, w_name, trans_b, st, alpha, beta, bmode, tuple(lead) + (n,))
             return
         code = self.mm_code
         in_dtype = np.dtype(np.float32) if code == _lib.F32 else self.act_dtype

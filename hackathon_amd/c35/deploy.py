@@ -41,7 +41,7 @@ def _parser() -> argparse.ArgumentParser:
     p.add_argument("--output", required=True, help="Directory to write output logits.npy and manifest.json")
     p.add_argument("--batch-size", type=validate_batch_size, default=None,
                    help="Maximum batch size for inference (default: process all at once)")
-    p.add_argument("--precision", choices=["fp32", "bf16", "fp16", "w8a8", "fp8"], default="fp32",
+    p.add_argument("--precision", choices=["fp32", "bf16", "fp16", "w8a8", "fp8", "fp4"], default="fp32",
                    help="Precision policy for the C3.4 plan (default fp32)")
     p.add_argument("--engine", choices=["compiled", "planned"], default="compiled",
                    help="compiled: fused launch groups + hipGraph; planned: one launch per plan step")

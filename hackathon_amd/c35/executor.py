@@ -175,6 +175,7 @@ class PlannedGraphExecutor(GraphExecutor):
         self._resident_model_tensors: Dict[str, DeviceArray] = {}
         self._streams: Dict[int, Stream] = {}
         self._events_by_plan: Dict[int, Tuple[ExecutionPlan, Dict[str, Event]]] = {}
+        self._validated_plans: Dict[int, ExecutionPlan] = {}
         self._stream_objects_created = 0
         self._event_objects_created = 0
         self._planned_runs = 0
@@ -327,9 +328,15 @@ class PlannedGraphExecutor(GraphExecutor):
         return {**self.host_weights, **self._resident_model_tensors}
 
     def run_planned(self, feed_dict: Dict[str, Any], plan: ExecutionPlan) -> Dict[str, DeviceArray]:
-        issues = plan.validate()
-        if issues:
-            raise ValueError("C3.4 execution plan is invalid: " + "; ".join(issues[:10]))
+        # The structural checks run on the first batch a plan object sees, not
+        # on every batch as c35/executor.py:728 does; a plan edited after its
+        # first run is the caller's to re-validate.  The feed and graph checks
+        # below still run per batch.
+        if self._validated_plans.get(id(plan)) is not plan:
+            issues = plan.validate()
+            if issues:
+                raise ValueError("C3.4 execution plan is invalid: " + "; ".join(issues[:10]))
+            self._validated_plans[id(plan)] = plan
         counts = {int(np.shape(a)[0]) for a in feed_dict.values() if len(np.shape(a)) > 0}
         if len(counts) != 1:
             raise ValueError("Planned execution requires equal input batch sizes")

@@ -15,6 +15,17 @@ int fail(int code, const char* fmt, ...);
 // `device` (which must be current); called by c3h_init.  Returns a status.
 int gemm_scratch_setup(int device);
 
+// Kernel-selection switches from the environment, read at the first launch
+// and again by c3h_reload_switches() (launch paths read these, not getenv).
+struct Switches {
+  bool disable_dma = false;      // C3H_DISABLE_DMA: no direct-to-LDS GEMM kernel
+  bool disable_bigtile = false;  // C3H_DISABLE_BIGTILE: no 256 x 256 tile
+  bool disable_buf = false;      // C3H_DISABLE_BUF: no buffer-load GEMM kernel
+  bool disable_conv3x3 = false;  // C3H_DISABLE_CONV3X3: no 64-channel band conv
+  int dma_rp = 0;                // C3H_DMA_RP: register-pipelined DMA stages (0 = off)
+};
+const Switches& switches();
+
 #define C3H_HIP_CHECK(expr)                                                   \
   do {                                                                        \
     hipError_t err__ = (expr);                                                \

@@ -336,7 +336,7 @@ int device_cu_count() {
 // *handled; otherwise leaves *handled false and launches nothing.
 int conv3x3_c64_launch(const c3h_conv_args* a, hipStream_t s, bool* handled) {
   *handled = false;
-  if (getenv("C3H_DISABLE_CONV3X3")) return C3H_OK;
+  if (switches().disable_conv3x3) return C3H_OK;
   const c3h_epilogue& e = a->epi;
   const bool shape = (a->in_dtype == C3H_BF16 || a->in_dtype == C3H_F16) && a->out_dtype == a->in_dtype &&
                      a->kh == 3 && a->kw == 3 && a->sh == 1 && a->sw == 1 && a->dh == 1 && a->dw == 1 &&

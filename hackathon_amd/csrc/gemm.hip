@@ -1,8 +1,8 @@
 // C entry points of the contraction kernels (GEMM, implicit-GEMM Conv2d,
-// split-K, int8 and fp8 GEMM).  The kernels and launch templates live in
-// gemm_kernels.h; the per-type launchers are instantiated in gemm_bf16.hip,
-// gemm_bf16_conv.hip, gemm_f16.hip, gemm_f16_conv.hip, gemm_i8.hip,
-// gemm_f8.hip and gemm_f32.hip.
+// split-K, int8, fp8 and W4A16 GEMM).  The kernels and launch templates
+// live in gemm_kernels.h; the per-type launchers are instantiated in
+// gemm_bf16.hip, gemm_bf16_conv.hip, gemm_f16.hip, gemm_f16_conv.hip,
+// gemm_i8.hip, gemm_f8.hip, gemm_w4.hip and gemm_f32.hip.
 #include <stdlib.h>
 #include <mutex>
 
@@ -340,6 +340,39 @@ int c3h_gemm_fp8(const c3h_fp8_gemm_args* a, void* stream) {
   p.b_bytes = (a->n - 1) * a->ldb + a->k;
   hipStream_t s = as_stream(stream);
   return launch_f8(p, s, a->out_dtype);
+}
+
+int c3h_gemm_w4a16(const c3h_w4a16_gemm_args* a, void* stream) {
+  C3H_REQUIRE(a != nullptr, "gemm_w4a16: null args");
+  C3H_REQUIRE(a->m >= 0 && a->n >= 0 && a->k >= 1, "gemm_w4a16: bad sizes");
+  C3H_REQUIRE(a->k % 32 == 0, "gemm_w4a16: k must be a multiple of 32 (the MXFP4 block)");
+  C3H_REQUIRE(a->lda % 8 == 0 && a->lda >= a->k, "gemm_w4a16: lda must be a multiple of 8 and >= k");
+  C3H_REQUIRE(a->ldb % 4 == 0 && a->ldb >= a->k / 2, "gemm_w4a16: ldb (bytes) must be a multiple of 4 and >= k/2");
+  C3H_REQUIRE(a->ldbs >= a->k / 32 && a->ldo >= a->n, "gemm_w4a16: ldbs >= k/32 and ldo >= n required");
+  C3H_REQUIRE(aligned(a->a, 16) && aligned(a->b_codes, 4), "gemm_w4a16: A must be 16-byte and codes 4-byte aligned");
+  C3H_REQUIRE(a->b_scales != nullptr, "gemm_w4a16: b_scales required");
+  C3H_REQUIRE(a->out_dtype == C3H_F32 || a->out_dtype == C3H_F16, "gemm_w4a16: output dtype must be fp32 or fp16");
+  int rc = check_epilogue(a->epi);
+  if (rc) return rc;
+  if (a->m == 0 || a->n == 0) return C3H_OK;
+  const int64_t a_bytes = ((a->m - 1) * a->lda + a->k) * 2;
+  const int64_t b_bytes = (a->n - 1) * a->ldb + a->k / 2;
+  const int64_t s_bytes = (a->n - 1) * a->ldbs + a->k / 32;
+  C3H_REQUIRE(a_bytes < (int64_t{1} << 31) && b_bytes < (int64_t{1} << 31) && s_bytes < (int64_t{1} << 31),
+              "gemm_w4a16: A, codes and scales must each be below 2^31 bytes");
+  C3H_REQUIRE(ceil_div(a->m, 64) * ceil_div(a->n, 64) < (int64_t{1} << 31), "gemm_w4a16: too many tiles");
+  Problem p;
+  memset(&p, 0, sizeof(p));
+  p.a = a->a; p.b = a->b_codes; p.out = a->out;
+  p.m = a->m; p.n = a->n; p.k = a->k; p.lda = a->lda; p.ldb = a->ldb; p.ldo = a->ldo;
+  p.b_blk = a->b_scales; p.ldbs = a->ldbs; p.bs_bytes = s_bytes;
+  p.trans_b = 1;
+  p.out_dtype = a->out_dtype;
+  p.epi = a->epi;
+  p.ho = 1; p.wo = 1;
+  p.a_bytes = a_bytes;
+  p.b_bytes = b_bytes;
+  return launch_w4a16(p, as_stream(stream), a->out_dtype);
 }
 
 int c3h_qgemm(const c3h_qgemm_args* a, void* stream) {

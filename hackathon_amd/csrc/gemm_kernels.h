@@ -194,6 +194,10 @@ struct Problem {
   float a_scale, y_scale;
   const float* b_scale;
   const float* a_rows;  // fp8 GEMM (c3h_gemm_fp8): per-row A scale
+  // W4A16 GEMM (c3h_gemm_w4a16): B holds E2M1 codes [n][ldb bytes]; b_blk the
+  // E8M0 exponents [n][ldbs] of its 32-element blocks (bs_bytes in all)
+  const uint8_t* b_blk;
+  int64_t ldbs, bs_bytes;
   c3h_epilogue epi;
 };
 
@@ -998,7 +1002,25 @@ __device__ __forceinline__ bool epilogue_q_direct_ok(const KArg<Problem>& p, boo
 // 2^31 bytes, no batch): row bases are precomputed once, out-of-range lanes
 // use an offset past num_records and read zeros, so a K step costs a few
 // VALU per load instead of 64-bit address math and branches.
-template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, bool BUF = false>
+// Eight fp16 weights of one MXFP4 block: `codes` holds E2M1 elements 2j
+// (low nibble) and 2j+1 of byte j, `e8` the block's biased exponent.  The
+// scale is 2^(e8 - 127) as an fp32 (0xFF: NaN); v_cvt_scalef32_pk_f16_fp4
+// decodes two elements of one byte and multiplies by it.
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 mxfp4_to_f16x8(uint32_t codes, uint32_t e8) {
+  const float sc = __uint_as_float((e8 << 23) | (e8 == 0xFFu ? 0x400000u : 0u));
+  const f16x2_t h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(codes, sc, 0);
+  const f16x2_t h1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(codes, sc, 1);
+  const f16x2_t h2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(codes, sc, 2);
+  const f16x2_t h3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(codes, sc, 3);
+  return uint4{__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1), __builtin_bit_cast(uint32_t, h2),
+               __builtin_bit_cast(uint32_t, h3)};
+}
+
+// BQ: B is MXFP4 (W4A16, c3h_gemm_w4a16): each thread loads the 4 code bytes
+// and the exponent byte behind its 8-element K chunk and widens them to fp16
+// when it stores the tile to LDS, so the MFMA loop is the fp16 one.
+template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, bool BUF = false, bool BQ = false>
 __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
   constexpr bool DIRECT_GELU = false;  // GELU epilogues take the staged path here
   constexpr int ES = Mma::ES;
@@ -1012,6 +1034,7 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
   static_assert(WM * WN == kThreads / 64, "wave grid");
   static_assert(A_V >= 1 && B_V >= 1 && BM % RSTEP == 0 && BN % RSTEP == 0, "tile too small");
   static_assert(AM == kDenseK || ES == 2, "conv modes are 16-bit");
+  static_assert(!BQ || (std::is_same<Mma, MmaF16>::value && AM == kDenseK && BUF), "W4A16: fp16, dense, buffer loads");
   constexpr int kTileBytes = 2 * (BM + BN) * RB;
   constexpr int kStageBytes = (kThreads / 64) * WTM * (WTN + 4) * 4;  // whole wave tiles, 32-bit
   __shared__ __attribute__((aligned(16))) uint8_t smem[kTileBytes > kStageBytes ? kTileBytes : kStageBytes];
@@ -1035,24 +1058,31 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
   const int kc = kchunk * VE;        // ... as an element column
 
   // Two register sets: the loads of tile kt + 2 are issued while tile kt is
-  // multiplied and tile kt + 1 is still in flight.
-  uint4 ra0[A_V], rb0[B_V], ra1[A_V], rb1[B_V];
+  // multiplied and tile kt + 1 is still in flight.  (BQ: codes, exponent.)
+  typedef std::conditional_t<BQ, uint2, uint4> breg;
+  uint4 ra0[A_V], ra1[A_V];
+  breg rb0[B_V], rb1[B_V];
 
   // Per-row conv state (conv modes): pixel base offset, top-left input coords.
   int64_t rbase[AM == kDenseK ? 1 : A_V];
   int rhi[AM == kDenseK ? 1 : A_V], rwi[AM == kDenseK ? 1 : A_V];
   ConvRow crow[AM == kConv ? A_V : 1];
   static_assert(!BUF || AM == kDenseK || AM == kConvTap, "buffer loads: dense or tap-uniform conv");
-  __amdgpu_buffer_rsrc_t rs_a, rs_b;
+  __amdgpu_buffer_rsrc_t rs_a, rs_b, rs_s;
   int32_t a_off[BUF ? A_V : 1];   // dense: row byte offset (-1: out of range); tap: pixel byte offset
   int32_t b_off[BUF ? B_V : 1];
+  int32_t s_off[BQ ? B_V : 1];    // BQ: exponent row byte offset
   if constexpr (BUF) {
     rs_a = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.a), 0, static_cast<int>(p.a_bytes), 0x00020000);
     rs_b = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.b), 0, static_cast<int>(p.b_bytes), 0x00020000);
+    if constexpr (BQ)
+      rs_s = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.b_blk), 0, static_cast<int>(p.bs_bytes),
+                                               0x00020000);
 #pragma unroll
     for (int i = 0; i < B_V; ++i) {
       const int64_t n = n0 + trow + RSTEP * i;
-      b_off[i] = n < p.n ? static_cast<int32_t>(n * p.ldb * ES) : -1;
+      b_off[i] = n < p.n ? static_cast<int32_t>(n * p.ldb * (BQ ? 1 : ES)) : -1;
+      if constexpr (BQ) s_off[i] = n < p.n ? static_cast<int32_t>(n * p.ldbs) : -1;
     }
     if (AM == kDenseK) {
 #pragma unroll
@@ -1172,9 +1202,21 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
       }
     }
   };
-  auto load_b = [&](int64_t k0, uint4 (&rb)[B_V], bool live) {
+  auto load_b = [&](int64_t k0, breg (&rb)[B_V], bool live) {
     const int64_t k = k0 + kc;
-    if constexpr (BUF) {
+    if constexpr (BQ) {
+      // Out-of-range chunks read code bytes 0 (weight 0) and exponent 0.
+      const bool kok = live && k < p.k;
+      const int32_t koff = static_cast<int32_t>(k >> 1), soff = static_cast<int32_t>(k >> 5);
+#pragma unroll
+      for (int i = 0; i < B_V; ++i) {
+        const bool ok = kok && b_off[i] >= 0;
+        const uint32_t voff = ok ? static_cast<uint32_t>(b_off[i] + koff) : kOobOffset;
+        const uint32_t eoff = ok ? static_cast<uint32_t>(s_off[i] + soff) : kOobOffset;
+        rb[i].x = __builtin_amdgcn_raw_buffer_load_b32(rs_b, voff, 0, 0);
+        rb[i].y = __builtin_amdgcn_raw_buffer_load_b8(rs_s, eoff, 0, 0);
+      }
+    } else if constexpr (BUF) {
       const bool kok = live && k < p.k;
       const int32_t koff = static_cast<int32_t>(k * ES);
 #pragma unroll
@@ -1182,19 +1224,19 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
         const uint32_t voff = (kok && b_off[i] >= 0) ? static_cast<uint32_t>(b_off[i] + koff) : kOobOffset;
         rb[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs_b, voff, 0, 0));
       }
-      return;
-    }
+    } else {
 #pragma unroll
-    for (int i = 0; i < B_V; ++i) {
-      const int64_t n = n0 + trow + RSTEP * i;
-      uint4 v = {0u, 0u, 0u, 0u};
-      if (n < p.n && k < p.k) v = *reinterpret_cast<const uint4*>(B + (n * p.ldb + k) * ES);
-      rb[i] = v;
+      for (int i = 0; i < B_V; ++i) {
+        const int64_t n = n0 + trow + RSTEP * i;
+        uint4 v = {0u, 0u, 0u, 0u};
+        if (n < p.n && k < p.k) v = *reinterpret_cast<const uint4*>(B + (n * p.ldb + k) * ES);
+        rb[i] = v;
+      }
     }
   };
   // Byte offset of 16-byte chunk c of row r (XOR swizzle).
   auto swz = [](int r, int c) { return (c ^ (r & 7)) << 4; };
-  auto store_tiles = [&](int buf, const uint4 (&ra)[A_V], const uint4 (&rb)[B_V]) {
+  auto store_tiles = [&](int buf, const uint4 (&ra)[A_V], const breg (&rb)[B_V]) {
 #pragma unroll
     for (int i = 0; i < A_V; ++i) {
       const int r = trow + RSTEP * i;
@@ -1203,7 +1245,8 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
 #pragma unroll
     for (int i = 0; i < B_V; ++i) {
       const int r = trow + RSTEP * i;
-      *reinterpret_cast<uint4*>(&Bs[buf][r][swz(r, kchunk)]) = rb[i];
+      if constexpr (BQ) *reinterpret_cast<uint4*>(&Bs[buf][r][swz(r, kchunk)]) = mxfp4_to_f16x8(rb[i].x, rb[i].y);
+      else *reinterpret_cast<uint4*>(&Bs[buf][r][swz(r, kchunk)]) = rb[i];
     }
   };
 
@@ -1245,7 +1288,7 @@ __global__ void __launch_bounds__(kThreads) mfma_gemm_kernel(Problem p) {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
-  auto issue = [&](int64_t kt, uint4 (&ra)[A_V], uint4 (&rb)[B_V]) {
+  auto issue = [&](int64_t kt, uint4 (&ra)[A_V], breg (&rb)[B_V]) {
     const bool live = kt < ktiles;
     load_a(kt * BK, ra, live);
     load_b(kt * BK, rb, live);
@@ -1721,7 +1764,7 @@ int launch_f32(Problem p, int64_t batch, hipStream_t s) {
 // The pipelined kernel needs byte offsets that fit the 32-bit buffer offset
 // with room for the out-of-range sentinel, and no batch strides.
 inline bool dma_eligible(const Problem& p, int64_t batch, int am) {
-  if (getenv("C3H_DISABLE_DMA")) return false;
+  if (switches().disable_dma) return false;
   // Narrow implicit-GEMM convs (N <= 64) stay on the register-prefetch
   // kernel, which measured faster there; wider ones use the DMA kernel.
   if (am == kConvTap && p.n <= 64) return false;
@@ -1738,7 +1781,7 @@ inline bool dma_eligible(const Problem& p, int64_t batch, int am) {
 // int8 GEMMs writing int32 / int8 (qmode 0 / 1) need only aligned row-major
 // stores (epilogue_q_direct_ok).
 inline bool big_tile_wins(const Problem& p, int cus, size_t out_size, bool int_mma) {
-  if (getenv("C3H_DISABLE_BIGTILE") || p.n <= 128) return false;
+  if (switches().disable_bigtile || p.n <= 128) return false;
   const c3h_epilogue& e = p.epi;
   const uintptr_t al = 4 * out_size - 1;
   const bool stores = !p.out_nchw && p.ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(p.out) & al) == 0;
@@ -1758,10 +1801,7 @@ inline bool big_tile_wins(const Problem& p, int cus, size_t out_size, bool int_m
 
 // Register-pipelined form of the 4-wave DMA kernel: C3H_DMA_RP = 2, 3 or 4
 // LDS stages (0: the two-stage kernel without register pipelining).
-inline int dma_rp_stages() {
-  const char* v = getenv("C3H_DMA_RP");
-  return v ? atoi(v) : 0;
-}
+inline int dma_rp_stages() { return switches().dma_rp; }
 
 inline int device_cus() {
   int dev = 0, cus = 0;
@@ -1809,7 +1849,7 @@ int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
   }
   if constexpr (AM == kDenseK || AM == kConvTap) {
     if (batch == 1 && p.a_bytes > 0 && p.b_bytes > 0 && p.a_bytes < (int64_t{1} << 31) &&
-        p.b_bytes < (int64_t{1} << 31) && !getenv("C3H_DISABLE_BUF")) {
+        p.b_bytes < (int64_t{1} << 31) && !switches().disable_buf) {
       if (p.n <= 64) {
         grid_of<256, 64>(p, 1, grid);
         hipLaunchKernelGGL((mfma_gemm_kernel<Mma, TO, 256, 64, 4, 1, AM, true>), grid, dim3(kThreads), 0, s, p);
@@ -1870,6 +1910,21 @@ int launch_fp8(Problem p, hipStream_t s) {
   return launch_status("gemm_fp8");
 }
 
+// W4A16 GEMM: the register-prefetch kernel with MXFP4 B and buffer loads.
+template <typename TO>
+int launch_w4(Problem p, hipStream_t s) {
+  dim3 grid;
+  if (p.n <= 64) {
+    grid_of<256, 64>(p, 1, grid);
+    hipLaunchKernelGGL((mfma_gemm_kernel<MmaF16, TO, 256, 64, 4, 1, kDenseK, true, true>), grid, dim3(kThreads), 0, s, p);
+  } else {
+    grid_of<128, 128>(p, 1, grid);
+    hipLaunchKernelGGL((mfma_gemm_kernel<MmaF16, TO, 128, 128, 2, 2, kDenseK, true, true>), grid, dim3(kThreads), 0, s,
+                       p);
+  }
+  return launch_status("gemm_w4a16");
+}
+
 inline int check_epilogue(const c3h_epilogue& e) {
   C3H_REQUIRE(e.bias_mode >= 0 && e.bias_mode <= 4, "epilogue: bad bias_mode %d", e.bias_mode);
   C3H_REQUIRE(e.bias_mode == 0 || e.bias != nullptr, "epilogue: bias_mode %d needs a bias pointer", e.bias_mode);
@@ -1898,6 +1953,7 @@ int launch_f16_dense(Problem p, int64_t batch, hipStream_t s);    // gemm_f16.hi
 int launch_f16_conv(Problem p, hipStream_t s, int am);             // gemm_f16_conv.hip
 int launch_i8(Problem p, hipStream_t s, int mode, int out_dtype);  // gemm_i8.hip
 int launch_f8(Problem p, hipStream_t s, int out_dtype);            // gemm_f8.hip
+int launch_w4a16(Problem p, hipStream_t s, int out_dtype);         // gemm_w4.hip
 int launch_f32_modes(Problem p, int64_t batch, hipStream_t s, int am, bool b_kcontig);  // gemm_f32.hip
 
 }  // namespace gk

@@ -895,6 +895,51 @@ __global__ void __launch_bounds__(kBlock) quantize_fp8_rows_kernel(c3h_fp8_quant
   if (lane == 0) a.scale[row] = bad ? __builtin_nanf("") : amax / 448.0f;
 }
 
+// MXFP4 block quantization (c3h_quantize_mxfp4): one thread per block of 32
+// columns of one row.  Weights are quantized once per compiled plan, so the
+// kernel favours plain arithmetic over bandwidth: the exponent comes from
+// ilogbf (floor(log2 amax), subnormals included) and the element code from
+// comparisons against the round-to-nearest-even boundaries of the E2M1
+// magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6 (ties 0.25, 1.25, 2.5 and 5 go down
+// to the even code, ties 0.75, 1.75 and 3.5 up), saturating above 5.
+__device__ __forceinline__ uint32_t e2m1_code(float x, float inv) {
+  const float m = fabsf(x) * inv;
+  const uint32_t c = m <= 0.25f ? 0u : m < 0.75f ? 1u : m <= 1.25f ? 2u : m < 1.75f ? 3u
+                   : m <= 2.5f ? 4u : m < 3.5f ? 5u : m <= 5.0f ? 6u : 7u;
+  return (c != 0u && x < 0.0f) ? (c | 8u) : c;
+}
+
+__global__ void __launch_bounds__(kBlock) quantize_mxfp4_kernel(c3h_mxfp4_quant_args a) {
+  const int64_t nblk = a.cols / 32;
+  const int64_t id = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (id >= a.rows * nblk) return;
+  const int64_t row = id / nblk, blk = id - row * nblk;
+  const int64_t x0 = row * a.ldx + blk * 32;
+  float v[32];
+  float amax = 0.0f;
+  bool bad = false;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    v[e] = load_as_f32(a.x, a.x_dtype, x0 + e);
+    const float m = fabsf(v[e]);
+    bad |= !(m <= 3.402823466e38f);  // Inf or NaN
+    amax = fmaxf(amax, m);
+  }
+  int ex = -13;
+  if (amax > 0.0f) ex = min(max(ilogbf(amax) - 2, -13), 13);
+  const float inv = __uint_as_float(static_cast<uint32_t>(127 - ex) << 23);  // 2^-ex
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t word = 0u;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) word |= (bad ? 0u : e2m1_code(v[8 * j + e], inv)) << (4 * e);
+    w[j] = word;
+  }
+  *reinterpret_cast<uint4*>(a.codes + row * a.ldc + blk * 16) = uint4{w[0], w[1], w[2], w[3]};
+  a.scales[row * a.lds + blk] = bad ? uint8_t{0xFF} : static_cast<uint8_t>(ex + 127);
+}
+
 template <typename TX>
 int launch_fp8_rows(const c3h_fp8_quant_args& a, hipStream_t s) {
   const dim3 g(static_cast<unsigned>(ceil_div(a.rows, kBlock / 64))), b(kBlock);
@@ -1328,6 +1373,24 @@ int c3h_quantize_fp8_rows(const c3h_fp8_quant_args* a, void* stream) {
   if (a->x_dtype == C3H_F32) return launch_fp8_rows<float>(*a, st);
   if (a->x_dtype == C3H_BF16) return launch_fp8_rows<bf16_t>(*a, st);
   return launch_fp8_rows<f16_t>(*a, st);
+}
+
+int c3h_quantize_mxfp4(const c3h_mxfp4_quant_args* a, void* stream) {
+  C3H_REQUIRE(a && a->rows >= 0 && a->cols >= 0, "quantize_mxfp4: bad args");
+  C3H_REQUIRE(a->cols % 32 == 0, "quantize_mxfp4: cols must be a multiple of 32");
+  C3H_REQUIRE(a->ldx >= a->cols && a->ldc >= a->cols / 2 && a->lds >= a->cols / 32,
+              "quantize_mxfp4: ldx >= cols, ldc >= cols/2 and lds >= cols/32 required");
+  C3H_REQUIRE(a->ldc % 16 == 0 && (reinterpret_cast<uintptr_t>(a->codes) & 15) == 0,
+              "quantize_mxfp4: ldc must be a multiple of 16 and codes 16-byte aligned");
+  C3H_REQUIRE(a->x_dtype == C3H_F32 || a->x_dtype == C3H_BF16 || a->x_dtype == C3H_F16,
+              "quantize_mxfp4: x dtype must be fp32, bf16 or fp16");
+  C3H_REQUIRE(a->x != nullptr && a->codes != nullptr && a->scales != nullptr, "quantize_mxfp4: null pointer");
+  const int64_t blocks = a->rows * (a->cols / 32);
+  if (blocks == 0) return C3H_OK;
+  C3H_REQUIRE(ceil_div(blocks, kBlock) < (int64_t{1} << 31), "quantize_mxfp4: too many blocks");
+  hipLaunchKernelGGL(quantize_mxfp4_kernel, dim3(static_cast<unsigned>(ceil_div(blocks, kBlock))), dim3(kBlock), 0,
+                     as_stream(stream), *a);
+  return launch_status("quantize_mxfp4");
 }
 
 int c3h_dequantize(const c3h_dequantize_args* a, void* stream) {

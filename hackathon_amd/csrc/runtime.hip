@@ -3,6 +3,7 @@
 // capture.  Realizes the resource model of c35/executor.py:673-709 and
 // :757-868 in C++ so a compiled plan replays without Python in the loop.
 #include <stdarg.h>
+#include <stdlib.h>
 #include <vector>
 #include "common.h"
 
@@ -25,6 +26,21 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+static Switches read_switches() {
+  Switches w;
+  w.disable_dma = getenv("C3H_DISABLE_DMA") != nullptr;
+  w.disable_bigtile = getenv("C3H_DISABLE_BIGTILE") != nullptr;
+  w.disable_buf = getenv("C3H_DISABLE_BUF") != nullptr;
+  w.disable_conv3x3 = getenv("C3H_DISABLE_CONV3X3") != nullptr;
+  const char* rp = getenv("C3H_DMA_RP");
+  w.dma_rp = rp ? atoi(rp) : 0;
+  return w;
+}
+
+static Switches g_switches = read_switches();
+
+const Switches& switches() { return g_switches; }
+
 }  // namespace c3h
 
 using namespace c3h;
@@ -32,6 +48,11 @@ using namespace c3h;
 extern "C" {
 
 const char* c3h_last_error(void) { return g_last_error; }
+
+int c3h_reload_switches(void) {
+  g_switches = read_switches();
+  return C3H_OK;
+}
 
 int c3h_init(int device) {
   int count = 0;
@@ -230,6 +251,9 @@ static int dispatch_op(const c3h_op& op, hipStream_t s, void* const* events, int
     case C3H_OP_CONV_POOL: return c3h_conv_stem_pool(static_cast<const c3h_conv_pool_args*>(op.args), s);
     case C3H_OP_QUANT_FP8: return c3h_quantize_fp8_rows(static_cast<const c3h_fp8_quant_args*>(op.args), s);
     case C3H_OP_GEMM_FP8: return c3h_gemm_fp8(static_cast<const c3h_fp8_gemm_args*>(op.args), s);
+    case C3H_OP_QUANT_MXFP4:
+      return c3h_quantize_mxfp4(static_cast<const c3h_mxfp4_quant_args*>(op.args), s);
+    case C3H_OP_GEMM_W4A16: return c3h_gemm_w4a16(static_cast<const c3h_w4a16_gemm_args*>(op.args), s);
     case C3H_OP_SPLITK: return c3h_gemm_splitk_reduce(static_cast<const c3h_splitk_args*>(op.args), s);
     default: return fail(C3H_EINVAL, "unknown op kind %d", op.kind);
   }
@@ -317,7 +341,8 @@ int32_t c3h_abi_sizes(int64_t* out, int32_t capacity) {
       sizeof(c3h_attn_scores_args), sizeof(c3h_flash_args),   sizeof(c3h_quantize_args),
       sizeof(c3h_qgemm_args),     sizeof(c3h_dequantize_args), sizeof(c3h_op),
       sizeof(c3h_pack_args),      sizeof(c3h_conv_pool_args), sizeof(c3h_fp8_quant_args),
-      sizeof(c3h_fp8_gemm_args), sizeof(c3h_splitk_args)};
+      sizeof(c3h_fp8_gemm_args), sizeof(c3h_splitk_args), sizeof(c3h_mxfp4_quant_args),
+      sizeof(c3h_w4a16_gemm_args)};
   const int32_t n = static_cast<int32_t>(sizeof(sizes) / sizeof(sizes[0]));
   for (int32_t i = 0; i < n && i < capacity && out; ++i) out[i] = sizes[i];
   return n;

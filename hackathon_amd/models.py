@@ -17,6 +17,9 @@ Configs (BASELINE.json:7-11):
 Extra workload (not a BASELINE config):
     decoder_fp8    config 4's model under the "fp8" policy (E4M3 GEMMs for every
                    aligned constant-weight Linear, fp16 elsewhere)
+    decoder_fp4    config 4's model under the "fp4" policy (W4A16 GEMMs -- MXFP4
+                   weights, fp16 activations -- for the large aligned
+                   constant-weight Linears, fp16 elsewhere)
 """
 
 from __future__ import annotations
@@ -364,6 +367,7 @@ CONFIGS: Dict[str, Callable[..., Model]] = {
     "resnet18_224": build_resnet18_224,
     "decoder_fp16": lambda **kw: build_decoder(**{"precision": "fp16", **kw}),
     "decoder_fp8": lambda **kw: build_decoder(**{"precision": "fp8", "name": "decoder_fp8", **kw}),
+    "decoder_fp4": lambda **kw: build_decoder(**{"precision": "fp4", "name": "decoder_fp4", **kw}),
     "decoder_w8a8": lambda **kw: build_decoder(**{"batch": 16, "seq": 1024, "d_model": 768, "heads": 12,
                                                   "ffn": 3072, "layers": 12, "vocab": 32000,
                                                   "quantized": True, **kw}),

@@ -105,6 +105,12 @@ int c3h_device_count(int* count);
 int c3h_device_props(int device, c3h_props* out);
 const char* c3h_last_error(void);
 int c3h_device_synchronize(void);
+/* Re-reads the kernel-selection switches (C3H_DISABLE_DMA, C3H_DISABLE_BIGTILE,
+ * C3H_DISABLE_BUF, C3H_DISABLE_CONV3X3, C3H_DMA_RP) from the environment.
+ * They are read once, at the first launch, otherwise; call this between
+ * launches after changing them, never while another thread launches.  No
+ * counterpart in the reference (its kernel choice has no switches). */
+int c3h_reload_switches(void);
 
 /* One slab per plan arena (replaces cp.empty(peak_reserved_bytes), c35/executor.py:761-765). */
 int c3h_malloc(void** ptr, size_t bytes);
@@ -684,6 +690,54 @@ typedef struct {
 int c3h_gemm_fp8(const c3h_fp8_gemm_args* a, void* stream);
 
 /* ------------------------------------------------------------------ */
+/* W4A16: the executable form of the reference's structural fp4 choice */
+/* for large aligned constant-weight GEMMs (c32/strategy.py:150-154),  */
+/* with fp16 activations and fp32 accumulation (c32/strategy.py:       */
+/* 101-108).  Weights are OCP MX FP4: E2M1 elements, one E8M0 exponent */
+/* per 32 consecutive k.                                                */
+/* ------------------------------------------------------------------ */
+
+/* Block quantization of rows (weights packed B^T [n][k], rows = output
+ * channels) to MXFP4.  Per row r and block b of 32 columns: amax = max |x|;
+ * e = clamp(floor(log2 amax) - 2, -13, 13) (e = -13 for an all-zero block),
+ * so every dequantized element is zero or a normal fp16 exactly;
+ * scales[r][b] = e + 127; the element code is E2M1(|x| * 2^-e) rounded to
+ * nearest even and saturated at 6 (magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6),
+ * with the sign in bit 3 unless the magnitude code is 0.  A block holding
+ * Inf/NaN gets scale 0xFF (NaN) and zero codes.  codes[r][j] packs columns
+ * 2j (low nibble) and 2j+1 (high nibble).  cols % 32 == 0; ldc >= cols/2,
+ * ldc % 16 == 0 and codes 16-byte aligned; lds >= cols/32. */
+typedef struct {
+  const void* x;    /* [rows][ldx] fp32 / fp16 / bf16 */
+  uint8_t* codes;   /* [rows][ldc] */
+  uint8_t* scales;  /* [rows][lds] */
+  int64_t rows, cols, ldx, ldc, lds;
+  int32_t x_dtype;
+  int32_t pad_;
+} c3h_mxfp4_quant_args;
+int c3h_quantize_mxfp4(const c3h_mxfp4_quant_args* a, void* stream);
+
+/* out[m,n] = epilogue(sum_k A[m,k] * W[n,k]) with A fp16 [m][lda] and
+ * W[n,k] = E2M1(codes) * 2^(scales[n][k/32] - 127) widened to fp16 in
+ * registers (exact under c3h_quantize_mxfp4's exponent range), fp16 MFMA
+ * with fp32 accumulation, and the common epilogue into fp32 or fp16.
+ * Equals c3h_gemm on the dequantized fp16 weights bit for bit.  k % 32 == 0,
+ * lda % 8 == 0, ldb (bytes) % 4 == 0 and >= k/2, ldbs >= k/32; A 16-byte
+ * aligned; A, codes and scales each below 2^31 bytes. */
+typedef struct {
+  const void* a;           /* [m][lda] fp16 */
+  const uint8_t* b_codes;  /* [n][ldb] */
+  const uint8_t* b_scales; /* [n][ldbs] */
+  void* out;
+  int64_t m, n, k;
+  int64_t lda, ldb, ldbs, ldo;
+  int32_t out_dtype;
+  int32_t pad_;
+  c3h_epilogue epi;
+} c3h_w4a16_gemm_args;
+int c3h_gemm_w4a16(const c3h_w4a16_gemm_args* a, void* stream);
+
+/* ------------------------------------------------------------------ */
 /* Native timeline interpreter and graph capture                        */
 /* ------------------------------------------------------------------ */
 
@@ -720,7 +774,9 @@ enum c3h_op_kind {
   C3H_OP_CONV_POOL = 32,
   C3H_OP_QUANT_FP8 = 33,
   C3H_OP_GEMM_FP8 = 34,
-  C3H_OP_SPLITK = 35
+  C3H_OP_SPLITK = 35,
+  C3H_OP_QUANT_MXFP4 = 36,
+  C3H_OP_GEMM_W4A16 = 37
 };
 
 typedef struct {
@@ -754,7 +810,7 @@ int c3h_graph_destroy(void* graph_exec);
  * c3h_gemm_args, c3h_conv_args, c3h_attn_scores_args, c3h_flash_args,
  * c3h_quantize_args, c3h_qgemm_args, c3h_dequantize_args, c3h_op,
  * c3h_pack_args, c3h_conv_pool_args, c3h_fp8_quant_args, c3h_fp8_gemm_args,
- * c3h_splitk_args.
+ * c3h_splitk_args, c3h_mxfp4_quant_args, c3h_w4a16_gemm_args.
  * Returns the number of sizes available (host-only; needs no GPU). */
 int32_t c3h_abi_sizes(int64_t* out, int32_t capacity);
 

@@ -12,7 +12,8 @@ TEST INFRASTRUCTURE ONLY (see oracle/registry_ref.py).
   every node output stored in the activation type.  Under the "fp8" policy a
   step whose profile computes fp8 sees its activation quantized row-wise and
   its weight per output channel to E4M3 and back (oracle.fp8_ref), then the
-  fp32 kernel.
+  fp32 kernel; under "fp4" a step whose profile computes fp4 sees its fp16
+  activation and its weight quantized to MXFP4 and back (oracle.fp4_ref).
 * `run_graph` evaluates the unfused graph node by node with ONNX opset-17
   semantics (the reference's GraphExecutor, c35/executor.py:221-321).
 * `calibration_ranges` runs `run_graph` with every QDQ pair bypassed and
@@ -26,6 +27,7 @@ from typing import Any, Callable, Dict, List, Optional, Tuple
 
 import numpy as np
 
+from . import fp4_ref as F4
 from . import fp8_ref as F8
 from . import registry_ref as R
 
@@ -135,8 +137,8 @@ def run_plan(plan, graph, weights: Dict[str, np.ndarray], feed: Dict[str, np.nda
     node_last_step: Dict[str, int] = {}
     for k in plan.kernel_steps:
         node_last_step[k.node_id] = k.step_index
-    round_inputs = policy in ("bf16", "fp16", "w8a8", "fp8")
-    act = {"bf16": "bf16", "fp16": "fp16", "w8a8": "bf16", "fp8": "fp16"}.get(policy, "fp32")
+    round_inputs = policy in ("bf16", "fp16", "w8a8", "fp8", "fp4")
+    act = {"bf16": "bf16", "fp16": "fp16", "w8a8": "bf16", "fp8": "fp16", "fp4": "fp16"}.get(policy, "fp32")
     if round_inputs:
         for name in feed:
             if np.asarray(feed[name]).dtype == np.float32:
@@ -158,6 +160,8 @@ def run_plan(plan, graph, weights: Dict[str, np.ndarray], feed: Dict[str, np.nda
             ins.append(v)
         if prof.get("compute_dtype") == "fp8":
             ins = _fp8_operands(ins, k.operator_params)
+        elif prof.get("compute_dtype") == "fp4":
+            ins = _fp4_operands(ins, k.operator_params)
         outs = []
         for n in k.logical_outputs:
             count = max(_elements(plan, n, graph, plan.batch_size), 1)
@@ -181,6 +185,18 @@ def run_plan(plan, graph, weights: Dict[str, np.ndarray], feed: Dict[str, np.nda
                 o = t.astype(o.dtype, copy=False)
             values[n] = o
     return {t.name: values[t.name] for t in graph.outputs}
+
+
+def _fp4_operands(ins: List[np.ndarray], params: Dict[str, Any]) -> List[np.ndarray]:
+    """W4A16 operands of a GEMM step: the activation in fp16, the weight (as
+    B^T [n][k]) through MXFP4 and back."""
+    a16 = round_to(np.asarray(ins[0], F32), "fp16")
+    w = np.asarray(ins[1], F32)
+    if int(params.get("transB", 0)):
+        w4 = F4.dequantize_mxfp4(*F4.quantize_mxfp4(w))
+    else:
+        w4 = np.ascontiguousarray(F4.dequantize_mxfp4(*F4.quantize_mxfp4(np.ascontiguousarray(w.T))).T)
+    return [a16, w4] + list(ins[2:])
 
 
 def _fp8_operands(ins: List[np.ndarray], params: Dict[str, Any]) -> List[np.ndarray]:

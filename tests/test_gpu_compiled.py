@@ -192,6 +192,36 @@ def test_compiled_fp8_decoder(gpu):
     assert _agree(got, ref32) >= _agree(ref8, ref32) - 0.05
 
 
+def test_compiled_fp4_decoder(gpu):
+    """The "fp4" policy on a decoder whose every Linear is large enough for the
+    reference's fp4 rule (k, n >= 128, k n >= 32768): each runs as one W4A16
+    GEMM (MXFP4 weights quantized once on the GPU, fp16 activations).  The
+    engine implements the W4A16 definition, so the 16-bit workload gate
+    applies against the oracle's emulation of it at the program's rounding
+    points: max|diff| <= 2e-2, argmax equal wherever the emulation's top-2
+    margin exceeds 4e-2.  The distance to fp32 (the 4-bit weights' own
+    error) is printed."""
+    from hackathon_amd import models
+
+    m = models.build("decoder_fp4", batch=2, seq=64, d_model=256, heads=4, ffn=512, layers=2, vocab=320)
+    plan, prog, weights = _compiled(m, "fp4")
+    comp = [(k.precision_profile or {}).get("compute_dtype") for k in plan.kernel_steps]
+    n4 = comp.count("fp4")
+    assert n4 == 4 * 2 + 1 and comp.count("fp8") == 0
+    assert sum(k.startswith("gemm_w4a16:") for k in prog.node_kinds) == n4
+    got = _logits(prog, m.inputs)["logits"]
+    refs = G.run_plan(plan, m.graph, weights, m.inputs, policy="fp4", store=prog.rounding_map())["logits"]
+    ref32 = G.run_plan(plan, m.graph, weights, m.inputs)["logits"]
+    got = got.reshape(ref32.shape)
+    d = float(np.max(np.abs(got - refs)))
+    ok, share = gates.margin_agreement(got, refs, 2e-2)
+    print(f"decoder_fp4: max|diff| vs W4A16 emulation {d:.3e}; argmax vs emulation on clear-margin rows {ok:.4f} "
+          f"({share:.1%}); vs fp32: max {float(np.max(np.abs(got - ref32))):.3e}, RMS {gates.rms(got - ref32):.3e} "
+          f"(emulation {gates.rms(refs - ref32):.3e})")
+    assert d <= 2e-2
+    assert ok == 1.0
+
+
 class _AllOnes(dict):
     """Unit scales for every name (the calibration forward bypasses QDQ)."""
 

@@ -16,6 +16,8 @@ Gates (c35/test_c35.py:88-93 for fp32; north_star for 16-bit and int8):
                              emulated, and the measured distance to fp32
                              printed; see each test for the asserted bounds
   W8A8                       against the oracle with W8A8 emulated
+  W4A16 (config 4's decoder under the "fp4" policy, no BASELINE config)
+                             against the oracle with MXFP4 weights emulated
 """
 
 from __future__ import annotations
@@ -31,7 +33,8 @@ from oracle import graph_ref as G
 pytestmark = pytest.mark.gpu
 
 # rows of the batch the oracle evaluates (the GPU always runs the full batch)
-SLICE = {"mlp": 256, "resnet18_cifar": 8, "resnet18_224": 16, "decoder_fp16": 16, "decoder_w8a8": 1}
+SLICE = {"mlp": 256, "resnet18_cifar": 8, "resnet18_224": 16, "decoder_fp16": 16, "decoder_w8a8": 1,
+         "decoder_fp4": 16}
 
 
 def _oracle(m, folded, rows: int, policy: str, store=None):
@@ -124,7 +127,7 @@ def _check_argmax_output(out: dict) -> None:
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("name", ["resnet18_224", "decoder_fp16", "decoder_w8a8"])
+@pytest.mark.parametrize("name", ["resnet18_224", "decoder_fp16", "decoder_w8a8", "decoder_fp4"])
 def test_fullsize_low_precision(gpu, name):
     """End-to-end gates at full size (the per-launch proof is the teacher-forced test below).
 
@@ -144,6 +147,11 @@ def test_fullsize_low_precision(gpu, name):
       accurate as the W8A8 definition -- its RMS logit error against fp32 is at
       most 1.1x the emulation's, and its argmax agreement with fp32 at most
       0.02 below the emulation's.
+    decoder_fp4: 4-bit weights move the logits away from fp32 by design
+      (printed); the program implements the W4A16 definition, so the
+      16-bit gate applies against its emulation: max|logits - emulation| <=
+      2e-2 and argmax equal to the emulation's wherever its top-2 margin
+      exceeds 4e-2.
     """
     m, folded, prog, out = _run_full(name)
     store = prog.rounding_map()
@@ -171,6 +179,12 @@ def test_fullsize_low_precision(gpu, name):
         agree, share = gates.margin_agreement(got, ref32, 2e-2)
         print(f"  argmax vs fp32 on positions with margin > 4e-2: {agree:.4f} ({share:.1%} of positions); "
               f"overall {vs32['agree']:.4f}", flush=True)
+        assert agree == 1.0
+    elif name == "decoder_fp4":
+        assert vs_emu["max_abs"] <= 2e-2
+        agree, share = gates.margin_agreement(got, refs, 2e-2)
+        print(f"  argmax vs the W4A16 emulation on positions with margin > 4e-2: {agree:.4f} ({share:.1%} of "
+              f"positions); overall {vs_emu['agree']:.4f}", flush=True)
         assert agree == 1.0
     else:
         assert vs32["rms"] <= 1.1 * emu32["rms"]
@@ -304,7 +318,8 @@ def _summarize(name, stats, ops):
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("name", ["mlp", "resnet18_cifar", "resnet18_224", "decoder_fp16", "decoder_w8a8"])
+@pytest.mark.parametrize("name", ["mlp", "resnet18_cifar", "resnet18_224", "decoder_fp16", "decoder_w8a8",
+                                  "decoder_fp4"])
 def test_fullsize_per_value_teacher_forced(gpu, name):
     """Every value the full-size program stores, against the oracle's node
     recomputed from the program's own inputs (no error carried between nodes):

@@ -14,6 +14,7 @@ import math
 import numpy as np
 import pytest
 
+import switches
 from oracle import graph_ref as G
 from oracle import registry_ref as R
 
@@ -583,15 +584,8 @@ def test_layernorm_vec_against_float64(gpu, rows, cols, res, bias, dt):
 
 def _bigtile_pair(launch):
     """Run `launch` with the 256x256 eight-wave kernel allowed, then with it disabled."""
-    import os
-
-    os.environ.pop("C3H_DISABLE_BIGTILE", None)
-    a = launch()
-    os.environ["C3H_DISABLE_BIGTILE"] = "1"
-    try:
-        b = launch()
-    finally:
-        os.environ.pop("C3H_DISABLE_BIGTILE", None)
+    a = _with_env("C3H_DISABLE_BIGTILE", None, launch)
+    b = _with_env("C3H_DISABLE_BIGTILE", "1", launch)
     return a, b
 
 
@@ -808,14 +802,12 @@ def test_conv3x3_band_kernel_matches_implicit_gemm(gpu, kind, n, h, w, resid, ac
         a.out_layout, a.in_dtype, a.out_dtype = 1, code, code
         a.epi = E.epilogue(bias=bd if bias else None, bias_mode=2 if bias else 0, act=act,
                            residual=rd if resid else None)
-        if disable:
-            os.environ["C3H_DISABLE_CONV3X3"] = "1"
-        try:
+        def go():
             print(f"conv3x3 {kind} n={n} h={h} w={w} resid={resid} act={act} bias={bias} generic={disable}", flush=True)
             _lib.launch(a, None)
             return out.get().copy()
-        finally:
-            os.environ.pop("C3H_DISABLE_CONV3X3", None)
+
+        return _with_env("C3H_DISABLE_CONV3X3", "1" if disable else None, go)
 
     band = launch(False)
     generic = launch(True)
@@ -1060,21 +1052,7 @@ def test_layernorm_int8_output_equals_layernorm_then_quantize(gpu, rows, cols, d
     assert (a_ == 127).any() and (a_ == -128).any()
 
 
-def _with_env(var, value, fn):
-    import os
-
-    old = os.environ.get(var)
-    if value is None:
-        os.environ.pop(var, None)
-    else:
-        os.environ[var] = value
-    try:
-        return fn()
-    finally:
-        if old is None:
-            os.environ.pop(var, None)
-        else:
-            os.environ[var] = old
+_with_env = switches.with_switch
 
 
 @pytest.mark.parametrize("kind", ["bf16", "fp16", "int8"])

@@ -63,3 +63,29 @@ def test_strict_plan_matches_oracle_fp32(gpu, name):
     assert [t["kind"] for t in trace] == [a.kind for a in plan.timeline]
     # D2H landed in the reused pinned buffer
     np.testing.assert_array_equal(ex.host_output("logits").reshape(got["logits"].shape), got["logits"])
+
+
+def test_strict_plan_validated_once_per_plan(gpu, monkeypatch):
+    """Structural validation runs on a plan's first batch only; the outputs of
+    later batches equal the first's."""
+    m, _, _ = _prepare("mlp", **SMALL["mlp"])
+    plan, ex, first = _strict(m)
+    from hackathon_amd.c34.execution_plan import ExecutionPlan
+    from hackathon_amd.device import DeviceArray
+
+    calls = []
+    real = ExecutionPlan.validate
+    monkeypatch.setattr(ExecutionPlan, "validate", lambda self: calls.append(1) or real(self))
+    feed = {k: DeviceArray.from_host(v) for k, v in m.inputs.items()}
+    for _ in range(3):
+        out = ex.run_planned(feed, plan)
+        np.testing.assert_array_equal(out["logits"].get(), first["logits"])
+    assert calls == []
+    # a different plan object is validated on its first batch
+    from hackathon_amd.c32.strategy import PrecisionPolicy
+    from hackathon_amd.c34.scheduler import ExecutionScheduler
+    other = ExecutionScheduler(m.graph, batch_size=plan.batch_size, precision_policy=PrecisionPolicy("fp32")).build()
+    other.kernel_steps[0].tuning_params = None
+    with pytest.raises(ValueError, match="execution plan is invalid"):
+        ex.run_planned(feed, other)
+    assert calls == [1]
