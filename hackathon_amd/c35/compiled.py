@@ -1782,7 +1782,8 @@ def _gelu_program_to_act(st: "_Epi") -> None:
     The program Div(x, c0) -> Erf -> Add(., c1) -> Mul(x, .) -> Mul(., c2) is
     what the Div/Erf/Add/Mul/Mul chain of a GELU lowers to; act 2 evaluates
     the same five operations in the same order (Add and Mul operands may come
-    in either order: they commute exactly), so results are unchanged.
+    in either order: they commute exactly), with the division and the erf
+    each within an fp32 ulp or two of the correctly rounded ones.
     """
     if st.act or len(st.prog) != 5:
         return

@@ -45,12 +45,40 @@ __device__ __forceinline__ const KArg<P>& kernel_arg() {
   return *(const KArg<P>*)(__builtin_amdgcn_kernarg_segment_ptr());
 }
 
+// erf for the GELU epilogues, one branch-free formula: erf(u) =
+// sign(u) (1 - erfc(|u|)) with erfc(z) = t exp(-z^2 - 1.26551223 + t P(t)),
+// t = 1 / (1 + z / 2), the Chebyshev fit of Numerical Recipes (Press et al.,
+// 2nd ed., section 6.2, erfcc), fractional error below 1.2e-7 for all z >= 0.
+// Evaluated in fp32 it stays within 1e-6 of erfc relative for z < 4 (1e-5
+// beyond, from the exponent's rounding), i.e. erf within an fp32 ulp or two.
+__device__ __forceinline__ float erf_cheb(float u) {
+  const float z = fabsf(u);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = fmaf(t, p, -0.82215223f);
+  p = fmaf(t, p, 1.48851587f);
+  p = fmaf(t, p, -1.13520398f);
+  p = fmaf(t, p, 0.27886807f);
+  p = fmaf(t, p, -0.18628806f);
+  p = fmaf(t, p, 0.09678418f);
+  p = fmaf(t, p, 0.37409196f);
+  p = fmaf(t, p, 1.00002368f);
+  const float ec = t * __expf(fmaf(-z, z, fmaf(t, p, -1.26551223f)));
+  return u >= 0.0f ? 1.0f - ec : ec - 1.0f;
+}
+
 // GELU as the decomposed ONNX chain Div -> Erf -> Add -> Mul -> Mul computes
-// it, operation for operation: ((x * (erf(x / c0) + c1)) * c2) with the
-// chain's constants (c0 = sqrt(2), c1 = 1, c2 = 0.5 in practice).
+// it: ((x * (erf(x / c0) + c1)) * c2) with the chain's constants (c0 =
+// sqrt(2), c1 = 1, c2 = 0.5 in practice).  x / c0 is x * (1 / c0) with one
+// residual correction and erf is erf_cheb, each within an fp32 ulp or two of
+// the chain's correctly rounded division and erf, at a fraction of their
+// instructions.
 __device__ __forceinline__ float gelu_erf(float x, float c0, float c1, float c2) {
-  const float t = erff(x / c0) + c1;
-  return (x * t) * c2;
+  const float r0 = __builtin_amdgcn_rcpf(c0);
+  float q = x * r0;
+  const float rr = fmaf(-q, c0, x);
+  q = rr == rr ? fmaf(rr, r0, q) : q;  // x = +-Inf: keep Inf
+  return (x * (erf_cheb(q) + c1)) * c2;
 }
 
 // ---------------------------------------------------------------- epilogue
@@ -673,10 +701,19 @@ __device__ __forceinline__ void store_strip_q(const float* stage, int lane, int6
   const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
   const int mode = p.qmode;
   const float sa = p.a_scale, sy = p.y_scale, zy = static_cast<float>(p.y_zero);
-  const float* sb = p.b_scale;
+  const bool requant = mode == 1 || mode == 3;
+  // A lane's 8 columns are the same in every pass: their multipliers
+  // ((sa * sb) / sy requantizing, sa * sb for mode 2) are computed once.
+  const int c0 = (lane % LPR) * 8;
+  float mult[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int64_t nc = ncol0 + c0 + c;
+    const float bsc = (mode != 0 && nc < pn) ? p.b_scale[nc] : 0.0f;
+    mult[c] = requant ? (sa * bsc) / sy : sa * bsc;
+  }
   for (int pass = 0; pass < 16 / RPP; ++pass) {
     const int row = pass * RPP + lane / LPR;
-    const int c0 = (lane % LPR) * 8;
     const int64_t m = mrow0 + row;
     const int64_t n = ncol0 + c0;
     if (m >= pm || n >= pn) continue;
@@ -699,14 +736,12 @@ __device__ __forceinline__ void store_strip_q(const float* stage, int lane, int6
       float v[8];
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const float bsc = n + c < pn ? sb[n + c] : 0.0f;
-        if (mode == 1 || mode == 3) {
-          const float mult = (sa * bsc) / sy;
-          float y = rintf(static_cast<float>(acc[c]) * mult) + zy;
+        if (requant) {
+          float y = rintf(static_cast<float>(acc[c]) * mult[c]) + zy;
           y = fminf(fmaxf(y, -128.0f), 127.0f);
           v[c] = mode == 1 ? y : (y - zy) * sy;
         } else {
-          v[c] = static_cast<float>(acc[c]) * (sa * bsc);
+          v[c] = static_cast<float>(acc[c]) * mult[c];
         }
       }
       if constexpr (std::is_same<TO, int8_t>::value) {
@@ -853,18 +888,22 @@ __device__ __forceinline__ void epilogue_direct_q_impl(const Acc (&acc)[TM][TN],
   const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
   const int mode = p.qmode;
   const float sa = p.a_scale, sy = p.y_scale, zy = static_cast<float>(p.y_zero);
-  float sb[TN][4], b[TN][4];
+  const bool requant = mode == 1 || mode == 3;
+  // Per-column multiplier, once per lane: (sa * sb) / sy for requantizing
+  // modes, sa * sb for mode 2 (the same roundings as per element).
+  float mult[TN][4], b[TN][4];
   static_for<TN>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
     const int64_t n = nbase + 16 * j + 4 * lg;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      sb[j][r] = 0.0f;
+      float sbv = 0.0f;
       b[j][r] = 0.0f;
       if (n + r < pn) {
-        if (mode != 0) sb[j][r] = p.b_scale[n + r];
+        if (mode != 0) sbv = p.b_scale[n + r];
         if (bias) b[j][r] = bias[n + r];
       }
+      mult[j][r] = requant ? (sa * sbv) / sy : sa * sbv;
     }
   });
   // Row by row, as epilogue_direct: a row's stores go out back to back.
@@ -901,13 +940,12 @@ __device__ __forceinline__ void epilogue_direct_q_impl(const Acc (&acc)[TM][TN],
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const float a = static_cast<float>(acc[i][j][r]);
-              if (mode == 1 || mode == 3) {
-                const float mult = (sa * sb[j][r]) / sy;
-                float y = rintf(a * mult) + zy;
+              if (requant) {
+                float y = rintf(a * mult[j][r]) + zy;
                 y = fminf(fmaxf(y, -128.0f), 127.0f);
                 v[r] = mode == 1 ? y : (y - zy) * sy;
               } else {
-                v[r] = a * (sa * sb[j][r]);
+                v[r] = a * mult[j][r];
               }
             }
             if constexpr (std::is_same<TO, int8_t>::value) {

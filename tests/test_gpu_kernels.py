@@ -91,12 +91,15 @@ def test_gemm_16bit_out_and_program_epilogue(gpu, kind):
     ref = 0.5 * v * (1 + erf(v / math.sqrt(2.0)))
     got = _from16(out.get(), kind)
     np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-2)
-    # The compiled GELU activation (act 2) performs the same five operations: bit-identical.
+    # The compiled GELU activation (act 2) performs the same five operations,
+    # its division and erf within an fp32 ulp or two of the program's
+    # correctly rounded ones: at most one 16-bit step apart, on at most 0.1 %.
     out2 = DeviceArray.empty((m, n), a.dtype)
     e2 = E.epilogue(residual=resd, imm=[math.sqrt(2.0), 1.0, 0.5])
     e2.act = 2
     E.gemm(ad, btd, out2, m, n, k, lda=k, ldb=k, ldo=n, trans_b=1, in_dtype=code, epi=e2)
-    np.testing.assert_array_equal(out2.get().view(np.uint16), out.get().view(np.uint16))
+    step = np.abs(out2.get().view(np.int16).astype(np.int32) - out.get().view(np.int16).astype(np.int32))
+    assert step.max() <= 1 and np.mean(step != 0) <= 1e-3, (int(step.max()), float(np.mean(step != 0)))
 
 
 def _conv_case(rng, n, c, h, w, o, kh, kw, s, p):
@@ -642,6 +645,51 @@ def test_gemm_big_tile_matches_128_tiles(gpu, kind, out_kind, act):
     got = big[rows] if out_kind == "fp32" else _from16(big[rows], out_kind)
     tol = 1e-4 if out_kind == "fp32" else 1e-2
     np.testing.assert_allclose(got, want, rtol=tol, atol=tol * 4)
+
+
+def test_gemm_gelu_epilogue_matches_the_chain(gpu):
+    """The GEMM GELU epilogue (act 2) on exact accumulators x (A = [x, 0, 0, 0],
+    B row 0 = 1): equal to the decomposed chain ((x * (erf(x / sqrt 2) + 1)) *
+    0.5) evaluated in fp32 with a correctly rounded erf, within 2^-21 relative
+    plus |x| 2^-22 (two fp32 steps of erf near +-1, where the chain's own
+    rounding of erf dominates), over [-12, 12] and the special values."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import DeviceArray
+    from scipy.special import erf
+
+    x = np.concatenate([np.linspace(-12, 12, 48000, dtype=np.float32),
+                        np.array([0.0, -0.0, 1e-30, -1e-30, 1e-8, -1e-8, 3.0, -3.0, np.inf, -np.inf, np.nan],
+                                 np.float32)])
+    m = ((x.size + 63) // 64) * 64
+    a = np.zeros((m, 4), np.float32)
+    a[: x.size, 0] = x
+    n = 16
+    b = np.zeros((4, n), np.float32)
+    b[0] = 1.0
+    ad, bd = _dev(a), _dev(b)
+    out = DeviceArray.empty((m, n), np.float32)
+    g = _lib.GemmArgs()
+    g.a, g.b, g.out = ad.ptr, bd.ptr, out.ptr
+    g.m, g.n, g.k, g.lda, g.ldb, g.ldo, g.batch = m, n, 4, 4, n, n, 1
+    g.trans_a, g.trans_b, g.in_dtype, g.out_dtype = 0, 0, _lib.F32, _lib.F32
+    g.epi = E.epilogue(act=2, imm=[math.sqrt(2.0), 1.0, 0.5])
+    print(f"gemm fp32 gelu epilogue m={m}", flush=True)
+    _lib.launch(g, None)
+    got = out.get()[: x.size]
+    np.testing.assert_array_equal(got, np.repeat(got[:, :1], n, axis=1))
+    got = got[:, 0].astype(np.float64)
+    f = np.float32
+    q = (x / f(math.sqrt(2.0))).astype(f)
+    e = erf(q.astype(np.float64)).astype(f)
+    with np.errstate(invalid="ignore"):
+        ref = ((x * (e + f(1.0))).astype(f) * f(0.5)).astype(f).astype(np.float64)
+    fin = np.isfinite(ref)
+    tol = 2.0 ** -21 * np.abs(ref[fin]) + np.abs(x[fin].astype(np.float64)) * 2.0 ** -22 + 1e-38
+    err = np.abs(got[fin] - ref[fin])
+    assert np.all(err <= tol), (float(np.max(err / tol)), float(x[fin][np.argmax(err / tol)]))
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    assert got[np.isposinf(x)][0] == np.inf
 
 
 def test_conv_big_tile_matches_128_tiles(gpu):
