@@ -262,12 +262,30 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
     if (t + 1 < t_end) stash();  // every wave is past its patch reads
     // 3x3 / stride 2 max over the valid conv pixels of each pooled pixel, 8 channels per thread.
     {
+      // Whether every window of the tile lies inside the conv output (uniform).
+      const bool interior = pt > 0 && qt > 0 && 2 * (PH * pt + PH - 1) + 1 < g.ho && 2 * (PW * qt + PW - 1) + 1 < g.wo;
       const int px = tid >> 3, cg = tid & 7;
       const int pr = px / PW, qc = px - pr * PW;
       const int P = PH * pt + pr, Q = PW * qt + qc;
       if (P < g.po && Q < g.qo) {
         uint4 res;
-        if (g.relu) {
+        if (g.relu && interior) {
+          // Every window position is a conv pixel of the image: constant
+          // offsets from the window's corner, no checks.
+          const uint8_t* c0 = ctile + ((2 * pr) * CTW + 2 * qc) * CS + cg * 16;
+          uint32_t mx[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+          for (int dr = 0; dr < 3; ++dr)
+#pragma unroll
+            for (int dc = 0; dc < 3; ++dc) {
+              const uint4 v = *reinterpret_cast<const uint4*>(c0 + (dr * CTW + dc) * CS);
+              mx[0] = umax16x2(mx[0], v.x);
+              mx[1] = umax16x2(mx[1], v.y);
+              mx[2] = umax16x2(mx[2], v.z);
+              mx[3] = umax16x2(mx[3], v.w);
+            }
+          res = uint4{mx[0], mx[1], mx[2], mx[3]};
+        } else if (g.relu) {
           // Every window holds the valid pixel (2 pr + 1, 2 qc + 1); invalid
           // positions re-read it, which leaves the maximum unchanged.
           uint32_t mx[4] = {0u, 0u, 0u, 0u};

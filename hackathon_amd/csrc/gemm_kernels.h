@@ -1026,10 +1026,10 @@ __device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int6
 __device__ __forceinline__ bool epilogue_q_direct_ok(const KArg<Problem>& p, bool vec4);
 
 // Whether epilogue_direct applies (uniform): see its comment.
-__device__ __forceinline__ bool epilogue_is_simple(const KArg<Problem>& p, bool vec4) {
+__device__ __forceinline__ bool epilogue_is_simple(const KArg<Problem>& p, bool vec4, bool gelu_ok = false) {
   const int bm = p.epi.bias_mode;
   return vec4 && !p.out_nchw && p.epi.alpha == 1.0f && p.epi.beta == 1.0f && (bm == 0 || bm == 2) &&
-         p.epi.act <= 1 && p.epi.n_inst == 0 &&
+         p.epi.act <= (gelu_ok ? 2 : 1) && p.epi.n_inst == 0 &&
          (bm == 0 || (reinterpret_cast<uintptr_t>(p.epi.bias) & 15) == 0);
 }
 __device__ __forceinline__ bool epilogue_q_direct_ok(const KArg<Problem>& p, bool vec4) {
@@ -1464,7 +1464,9 @@ __device__ __forceinline__ void wait_vmcnt_groups(int64_t n) {
 template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, int S, int NW = 4, bool RP = false>
 __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
   constexpr bool DIRECT = NW > 4;
-  constexpr bool DIRECT_GELU = DIRECT;
+  // GELU in registers (epilogue_direct) for 16-bit outputs as well: with the
+  // branch-free erf it beats the staged epilogue.
+  constexpr bool DIRECT_GELU = DIRECT || !Mma::kInt;
   constexpr int ES = Mma::ES;
   constexpr int VE = 16 / ES;
   constexpr int BK = 128 / ES;
@@ -1720,7 +1722,7 @@ __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
         epilogue_direct_q<TO, TM, TN, DIRECT_GELU>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act);
         return;
       }
-    } else if (DIRECT || epilogue_is_simple(kernel_arg<Problem>(), vec4)) {
+    } else if (DIRECT || epilogue_is_simple(kernel_arg<Problem>(), vec4, DIRECT_GELU)) {
       epilogue_direct<TO, TM, TN, DIRECT_GELU>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act);
       return;
     }
@@ -1823,9 +1825,8 @@ inline bool big_tile_wins(const Problem& p, int cus, size_t out_size, bool int_m
   const c3h_epilogue& e = p.epi;
   const uintptr_t al = 4 * out_size - 1;
   const bool stores = !p.out_nchw && p.ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(p.out) & al) == 0;
-  // GELU in registers measured slower than the staged 128 x 128 epilogue for
-  // 16-bit GEMMs (16384x2048x512: 101 vs 95 us) and faster for int8 ones.
-  const int max_act = int_mma ? 2 : 1;
+  // GELU is computed in registers by both tile sizes.
+  const int max_act = 2;
   const bool simple = stores && e.alpha == 1.0f && e.beta == 1.0f && (e.bias_mode == 0 || e.bias_mode == 2) &&
                       e.act <= max_act && e.n_inst == 0 &&
                       (e.bias_mode == 0 || (reinterpret_cast<uintptr_t>(e.bias) & 15) == 0) &&
