@@ -85,6 +85,11 @@ constexpr int QG = 2;         // 16-query groups per wave
 constexpr int kBQ = 64 * QG;  // queries per workgroup
 constexpr int kBK = 64;       // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
+// Lazy rescaling: the exponent base of a query moves to its running maximum
+// only when some query of the wave has exceeded its base by more than this
+// (in exp2 units), so p = exp2(s c - base) <= 2^8, exact in range for the
+// 16-bit P operand, and O, l stay consistent with the base they were summed at.
+constexpr float kLazy = 8.0f;
 
 template <typename T> struct FlashMma;
 template <> struct FlashMma<bf16_t> {
@@ -130,8 +135,12 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
   const int qt = blockIdx.x % qtiles;
   const int bh = blockIdx.x / qtiles;
   const int head = bh % a.heads, batch = bh / a.heads;
+  // (`wave` is left as a per-lane value: declaring it uniform made the
+  // causal checks scalar branches and the kernel measured 17 % slower.)
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, g = lane >> 4;
+  // ds_bpermute byte addresses of lanes lane ^ 16 and lane ^ 32.
+  const int xor16 = (lane ^ 16) << 2, xor32 = (lane ^ 32) << 2;
 
   const uint16_t* Q = static_cast<const uint16_t*>(a.q) + batch * a.q_sb + head * a.q_sh;
   const uint16_t* K = static_cast<const uint16_t*>(a.k) + batch * a.k_sb + head * a.k_sh;
@@ -158,18 +167,28 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
   }
 
   f32x4 o_acc[QG][4];  // O^T tiles: dims 16*d + 4*g + j, query q[u]
+  // Row sums of P by the MFMA: a ones A operand makes every element of
+  // l_acc[u] the sum over the tile's keys of query q[u]'s 16-bit P values,
+  // the same P values O is summed from.
+  f32x4 l_acc[QG];
 #pragma unroll
-  for (int u = 0; u < QG; ++u)
+  for (int u = 0; u < QG; ++u) {
+    l_acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < 4; ++d) o_acc[u][d] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // Softmax state in raw score units: p = exp2(s * c - m * c), c = scale * log2 e.
+  }
+  const uint32_t one2 = pack2<T>(1.0f, 1.0f);
+  const vec8 ones = __builtin_bit_cast(vec8, uint4{one2, one2, one2, one2});
+  // Softmax state in raw score units: p = exp2(s * c - base), c = scale * log2 e.
   const float c = a.scale * kLog2e;
   const float inv_scale = 1.0f / a.scale;
-  float m_run[QG], l_part[QG];  // running max (raw) and this lane's partial row sum
+  // running max (raw), the max the exponent base was taken at, and the base
+  float m_run[QG], m_base[QG], base[QG];
 #pragma unroll
   for (int u = 0; u < QG; ++u) {
     m_run[u] = -INFINITY;
-    l_part[u] = 0.0f;
+    m_base[u] = -INFINITY;
+    base[u] = 0.0f;
   }
 
   const float* mask = static_cast<const float*>(a.mask);
@@ -273,26 +292,30 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, s_acc[u][kt4][j]);
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = fmaxf(tmax, __int_as_float(__builtin_amdgcn_ds_bpermute(xor16, __float_as_int(tmax))));
+        tmax = fmaxf(tmax, __int_as_float(__builtin_amdgcn_ds_bpermute(xor32, __float_as_int(tmax))));
         const float m_new = fmaxf(m_run[u], tmax);
-        const float base = m_new == -INFINITY ? 0.0f : m_new * c;
-        const float corr =
-            m_run[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(m_run[u], c, -base));
         m_run[u] = m_new;
-        l_part[u] *= corr;
+        // A finite maximum past the base by more than kLazy (any base is
+        // exceeded by a finite maximum while the base is still -inf).
+        const bool grow = m_new > m_base[u] && (m_base[u] == -INFINITY || (m_new - m_base[u]) * c > kLazy);
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // uniform: the whole wave moves its bases
+          const float nb = m_new == -INFINITY ? 0.0f : m_new * c;
+          const float corr = m_base[u] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(base[u] - nb);
+          m_base[u] = m_new;
+          base[u] = nb;
+          l_acc[u] *= corr;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) o_acc[u][d] *= corr;
+          for (int d = 0; d < 4; ++d) o_acc[u][d] *= corr;
+        }
         // P^T fragments for the two 32-key halves: element i of half ks is
         // key 32*ks + 16*(i/4) + 4*g + (i%4), i.e. s_acc[2*ks + i/4][i%4].
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           float pv[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[u][2 * ks + i / 4][i % 4], c, -base));
-            l_part[u] += pv[i];
-          }
+          for (int i = 0; i < 8; ++i)
+            pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[u][2 * ks + i / 4][i % 4], c, -base[u]));
           const uint4 packed = {pack2<T>(pv[0], pv[1]), pack2<T>(pv[2], pv[3]), pack2<T>(pv[4], pv[5]),
                                 pack2<T>(pv[6], pv[7])};
           pf[u][ks] = __builtin_bit_cast(vec8, packed);
@@ -310,14 +333,17 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
           for (int u = 0; u < QG; ++u) o_acc[u][d] = FlashMma<T>::mma(vf, pf[u][ks], o_acc[u][d]);
         }
       }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int u = 0; u < QG; ++u) l_acc[u] = FlashMma<T>::mma(ones, pf[u][ks], l_acc[u]);
     }
     __syncthreads();
   }
 
 #pragma unroll
   for (int u = 0; u < QG; ++u) {
-    float l_tot = l_part[u] + __shfl_xor(l_part[u], 16, 64);
-    l_tot += __shfl_xor(l_tot, 32, 64);
+    const float l_tot = l_acc[u][0];
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (q_valid[u]) {
 #pragma unroll
