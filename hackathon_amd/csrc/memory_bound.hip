@@ -402,25 +402,22 @@ __global__ void __launch_bounds__(kBlock) layernorm_kernel(c3h_layernorm_args a)
 // TO = int8_t: the QuantizeLinear that is the LayerNorm's only consumer, in
 // the same pass.  Each output is first rounded to the activation type TX
 // (what the unfused LayerNorm stores), then q = saturate(rne(y / out_scale)
-// + out_zero) exactly as quantize_kernel computes it: bit-identical codes.
+// + out_zero) by the same QuantDiv as quantize_kernel: bit-identical codes.
 constexpr int kLnVec = 8;
 
 template <typename TX, typename TO>
 struct LnStore {
-  static __device__ __forceinline__ void store8(TO* p, const float* y, float, int) { Elem<TO>::store8(p, y); }
+  static __device__ __forceinline__ void store8(TO* p, const float* y, const QuantDiv&, int) {
+    Elem<TO>::store8(p, y);
+  }
 };
 template <typename TX>
 struct LnStore<TX, int8_t> {
-  static __device__ __forceinline__ void store8(int8_t* p, const float* y, float qs, int qz) {
-    uint32_t w[2] = {0u, 0u};
+  static __device__ __forceinline__ void store8(int8_t* p, const float* y, const QuantDiv& qd, int qz) {
+    float r[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float r = Elem<TX>::to_f32(Elem<TX>::from_f32(y[e]));
-      float q = rintf(r / qs) + static_cast<float>(qz);
-      q = fminf(fmaxf(q, -128.0f), 127.0f);
-      w[e >> 2] |= (static_cast<uint32_t>(static_cast<int8_t>(q)) & 0xffu) << (8 * (e & 3));
-    }
-    *reinterpret_cast<uint2*>(p) = uint2{w[0], w[1]};
+    for (int e = 0; e < 8; ++e) r[e] = Elem<TX>::to_f32(Elem<TX>::from_f32(y[e]));
+    *reinterpret_cast<uint2*>(p) = qd.codes8(r, qz);
   }
 };
 
@@ -454,6 +451,7 @@ __global__ void __launch_bounds__(kBlock) layernorm_vec_kernel(c3h_layernorm_arg
   }
   const float* scale = static_cast<const float*>(a.scale);
   const float* bias = static_cast<const float*>(a.bias);
+  const QuantDiv qd(std::is_same<TO, int8_t>::value ? a.out_scale : 1.0f);
 #pragma unroll
   for (int r = 0; r < ROWS; ++r) {
     const int64_t row = row0 + r;
@@ -491,7 +489,7 @@ __global__ void __launch_bounds__(kBlock) layernorm_vec_kernel(c3h_layernorm_arg
           y[e] = (v[r][j][e] - mean) * inv_std * g[e];
           if (bias) y[e] += b[e];
         }
-        LnStore<TX, TO>::store8(out + vi * 8, y, a.out_scale, a.out_zero);
+        LnStore<TX, TO>::store8(out + vi * 8, y, qd, a.out_zero);
       }
     }
     if (lane == 0) {
@@ -793,32 +791,25 @@ __global__ void __launch_bounds__(kBlock) maxpool_kernel(c3h_pool_args a) {
 
 // ------------------------------------------------------------------ quantize / dequantize
 __global__ void quantize_kernel(c3h_quantize_args a) {
+  const QuantDiv qd(a.scale);
   int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < a.count; i += stride) {
-    float v = rintf(load_as_f32(a.x, a.x_dtype, i) / a.scale) + static_cast<float>(a.zero_point);
-    v = fminf(fmaxf(v, -128.0f), 127.0f);
-    a.out[i] = static_cast<int8_t>(v);
+    a.out[i] = qd.code(load_as_f32(a.x, a.x_dtype, i), a.zero_point);
   }
 }
 
 // 8 elements per thread: one 16-byte (16-bit input) or 32-byte (fp32) load,
-// one 8-byte int8 store; same rintf / saturate arithmetic as quantize_kernel.
+// one 8-byte int8 store; the same QuantDiv codes as quantize_kernel.
 template <typename TX>
 __global__ void __launch_bounds__(kBlock) quantize_vec_kernel(c3h_quantize_args a) {
   const int64_t nvec = a.count / 8;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   const TX* x = static_cast<const TX*>(a.x);
+  const QuantDiv qd(a.scale);
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec; i += stride) {
     float v[8];
     Elem<TX>::load8(x + i * 8, v);
-    uint32_t w[2] = {0u, 0u};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float q = rintf(v[e] / a.scale) + static_cast<float>(a.zero_point);
-      q = fminf(fmaxf(q, -128.0f), 127.0f);
-      w[e >> 2] |= (static_cast<uint32_t>(static_cast<int8_t>(q)) & 0xffu) << (8 * (e & 3));
-    }
-    *reinterpret_cast<uint2*>(a.out + i * 8) = uint2{w[0], w[1]};
+    *reinterpret_cast<uint2*>(a.out + i * 8) = qd.codes8(v, a.zero_point);
   }
 }
 

@@ -392,6 +392,66 @@ def test_quantize_vectorized_bit_exact(gpu, kind):
     np.testing.assert_array_equal(out.get(), R.quantize(xr, np.float32(0.5), 0))
 
 
+def _f32(bits):
+    return np.array([bits], np.uint32).view(np.float32)[0]
+
+
+# Scales for the division-free quantizer: all-ones significands (the divisors
+# where a reciprocal-only quotient is most often misrounded), the edges of the
+# range it serves (2^-100 .. 2^100) and just outside them, where the kernels
+# divide directly.
+_QUANT_SCALES = [0.5, 0.019, 1 / 127, 0.0123, 3.0, 40.11176,
+                 _f32(0x3FFFFFFF), _f32(0x3F7FFFFF), _f32(0x3C7FFFFF),     # 2 - 2^-22, 1 - 2^-24, 2^-6 (2 - 2^-23)
+                 _f32(0x0D800000), _f32(0x0D7FFFFF),                        # 2^-100 and just below
+                 _f32(0x71800000), _f32(0x71800001),                        # 2^100 and just above
+                 1e-30, 7e30]
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("zero", [0, -3, 5])
+def test_quantize_every_code_boundary_bit_exact(gpu, kind, zero):
+    """c3h_quantize (vectorized and scalar kernels) equals rne(x / scale) with a
+    correctly rounded fp32 division, for every finite and infinite bf16 / fp16
+    value, and for fp32 values within a few ulps of every half-integer
+    quotient (the rounding boundaries of the codes), over the scales above."""
+    from hackathon_amd import _lib
+    from hackathon_amd.device import DeviceArray
+
+    code = {"fp32": _lib.F32, "bf16": _lib.BF16, "fp16": _lib.F16}[kind]
+    for scale in _QUANT_SCALES:
+        s = np.float32(scale)
+        if kind == "bf16":
+            bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+            xr = (bits.astype(np.uint32) << 16).view(np.float32)
+            keep = ~np.isnan(xr)
+            bits, xr = bits[keep], xr[keep]
+            host = bits
+        elif kind == "fp16":
+            h = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+            h = h[~np.isnan(h)]
+            host, xr = h, h.astype(np.float32)
+        else:
+            k = np.arange(-140.5, 140.0, 1.0)                      # half-integer quotients around every code
+            near = [(k * np.float64(s)).astype(np.float32)]
+            for _ in range(2):                                     # and 1, 2 ulps either side
+                near = [np.nextafter(near[0], np.float32(-np.inf))] + near + [np.nextafter(near[-1], np.float32(np.inf))]
+            specials = np.array([np.inf, -np.inf, 0.0, -0.0, 3e38, -3e38, 1e-40, -1e-40], np.float32)
+            xr = np.concatenate(near + [specials]).astype(np.float32)
+            xr = xr[~np.isnan(xr)]
+            host = xr
+        want = R.quantize(xr, s, zero)
+        for count in (xr.size - xr.size % 8, xr.size - xr.size % 8 - 1):   # vectorized, then the scalar kernel
+            xd = _dev(np.ascontiguousarray(host[:count]))
+            out = DeviceArray.empty((count,), np.int8)
+            a = _lib.QuantizeArgs()
+            a.x, a.out, a.count, a.scale, a.zero_point, a.x_dtype = xd.ptr, out.ptr, count, float(s), zero, code
+            print(f"quantize {kind} scale={float(s)!r} zero={zero} count={count}", flush=True)
+            _lib.launch(a, None)
+            got = out.get()
+            bad = np.nonzero(got != want[:count])[0]
+            assert bad.size == 0, (float(s), xr[bad[:5]], got[bad[:5]], want[:count][bad[:5]])
+
+
 @pytest.mark.parametrize("kind", ["bf16", "fp16"])
 @pytest.mark.parametrize("n,h,w,relu,in_kind", [(2, 64, 64, 1, "fp32"), (3, 70, 57, 1, "fp32"), (1, 45, 83, 0, "fp32"),
                                                 (2, 38, 40, 1, "same")])
