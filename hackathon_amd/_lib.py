@@ -173,7 +173,8 @@ class QGemmArgs(C.Structure):
     _fields_ = [("a", vp), ("b", vp), ("out", vp), ("m", i64), ("n", i64), ("k", i64),
                 ("lda", i64), ("ldb", i64), ("ldo", i64), ("a_zero", i32), ("b_zero", i32),
                 ("a_scale", f32), ("y_scale", f32), ("b_scale", vp), ("y_zero", i32),
-                ("mode", i32), ("out_dtype", i32), ("pad_", i32), ("epi", Epilogue)]
+                ("mode", i32), ("out_dtype", i32), ("act_dtype", i32), ("q_scale", f32), ("q_zero", i32),
+                ("epi", Epilogue)]
 
 
 class DequantizeArgs(C.Structure):

@@ -1745,18 +1745,36 @@ class CompiledPlan:
             return
         self.consumed.add(deq.id)
         st = self._absorb_tail(deq.outputs[0], shape, _Epi())
-        out = self._new(shape, self._out_dtype(st.final))
+        act_dtype = self._out_dtype(st.final)
+        # A QuantizeLinear that is the epilogue output's only consumer (W8A8:
+        # the GELU output ahead of FFN2) runs in the same launch: the value is
+        # rounded to the activation type it would have been stored in, then
+        # quantized -- the codes of the unfused pair.
+        quant = self._fusable_quantize(st.final, n) if st.residual is None and not st.prog else None
+        if quant is not None and act_dtype not in (np.float32, np.float16, BF16):
+            quant = None
+        out = self._new(shape, np.int8 if quant is not None else act_dtype)
         self._finish_residual(st, out)
-        self._qgemm(a, bt, sbv, out, m, n, k, 3, sa, sy, st)
-        self.vals[st.final] = out
+        q = (dtype_code(act_dtype), quant[1], quant[2]) if quant is not None else None
+        self._qgemm(a, bt, sbv, out, m, n, k, 3, sa, sy, st, q)
+        if quant is not None:
+            self.consumed.add(quant[0].id)
+            self._rounded[st.final] = _DTYPE_NAME[act_dtype]
+            self.vals[quant[0].outputs[0]] = out
+        else:
+            self.vals[st.final] = out
 
-    def _qgemm(self, a, bt, sbv, out, m, n, k, mode, sa, sy, st: _Epi):
+    def _qgemm(self, a, bt, sbv, out, m, n, k, mode, sa, sy, st: _Epi, quant=None):
+        """quant: (act dtype code, scale, zero) of a QuantizeLinear applied to
+        the epilogue's output (int8 `out`, modes 2 / 3)."""
         def build(r, a=a, bt=bt, sbv=sbv, out=out, st=st):
             g = _lib.QGemmArgs()
             g.a, g.b, g.out = self._ptr(a, r), self._ptr(bt, r), self._ptr(out, r)
             g.m, g.n, g.k, g.lda, g.ldb, g.ldo = m, n, k, k, k, n
             g.a_scale, g.y_scale, g.b_scale = sa, sy, self._ptr(sbv, r)
             g.y_zero, g.mode, g.out_dtype = 0, mode, dtype_code(out.dtype)
+            if quant is not None:
+                g.act_dtype, g.q_scale, g.q_zero = quant
             self._fill_epi(g.epi, st, r)
             return g
         self._emit("qgemm", build, [a, bt, sbv] + self._epi_reads(st), [out], flops=2.0 * m * n * k)

@@ -201,53 +201,59 @@ __device__ __forceinline__ void store_vec16(T* p, const float* v) {
   }
 }
 
+// x rounded to the storage type dt (bf16 / fp16; fp32 unchanged) and back:
+// the value a consumer reads after the producer stores x as dt.
+__device__ __forceinline__ float round_to_dtype(float x, int dt) {
+  if (dt == C3H_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
+  if (dt == C3H_F16) return f16_bits_to_f32(f32_to_f16_bits(x));
+  return x;
+}
+
 // x / scale rounded to nearest, for the int8 QuantizeLinear codes, without an
 // IEEE division per element (about ten VALU operations, which made the
-// quantizing kernels issue-bound rather than HBM-bound).  inv = RN(1/scale)
-// once, then Markstein's correction: q0 = RN(x * inv), r = fma(-q0, scale, x)
-// (exact), q = RN(q0 + r * inv) is the correctly rounded quotient when scale
-// and 1/scale are normal and nothing overflows (P. Markstein, IBM J. Res.
-// Dev. 34(1), 1990; Muller et al., Handbook of Floating-Point Arithmetic,
-// the division-by-FMA theorems).  q0 is first clamped to +-2^20: a quotient
-// that large saturates every int8 code whatever its rounding, and the clamp
-// keeps an infinite q0 (x = +-Inf, or x / scale overflowing) from turning r
-// into NaN; a NaN x stays NaN.  Outside 2^-100 <= scale <= 2^100, where r or
-// 1/scale could leave the normal range, the division is done directly.
-// Whenever |x / scale| >= 1/4 (the only quotients whose rounding can move a
-// code) the result equals x / scale bit for bit; smaller ones round to code
-// zero_point either way.
+// quantizing kernels issue-bound rather than HBM-bound).  With
+// scale = m 2^e (1 <= m < 2) and inv = RN(1/m), once: y = x 2^-e (exact
+// wherever the quotient matters), then Markstein's correction
+// q0 = RN(y inv), r = fma(-q0, m, y) (exact), q = RN(q0 + r inv) -- the
+// correctly rounded y / m = x / scale whenever y and r are normal
+// (P. Markstein, IBM J. Res. Dev. 34(1), 1990; Muller et al., Handbook of
+// Floating-Point Arithmetic, the division-by-FMA theorems).  q0 is first
+// clamped to +-2^20: a quotient that large saturates every int8 code whatever
+// its rounding, and the clamp keeps an infinite q0 (x = +-Inf, or y
+// overflowing) from turning r into NaN; a NaN x stays NaN.  Whenever
+// |x / scale| >= 1/4 (the only quotients whose rounding can move a code) the
+// result equals x / scale bit for bit, for every positive finite scale;
+// smaller ones round to code zero_point either way.  One branch-free form.
+// Scales QuantDiv serves (and the quantizing entry points accept): positive,
+// normal, finite.
+inline bool quant_scale_ok(float s) { return s >= 0x1p-126f && s <= 3.4028235e38f; }
+
 struct QuantDiv {
-  float scale, inv;
-  bool fast;
-  __device__ __forceinline__ explicit QuantDiv(float s)
-      : scale(s), inv(1.0f / s), fast(s >= 0x1p-100f && s <= 0x1p100f) {}
-  __device__ __forceinline__ float quotient(float x) const {
-    const float q0 = fminf(fmaxf(x * inv, -0x1p20f), 0x1p20f);
-    return fmaf(fmaf(-q0, scale, x), inv, q0);
+  float m, inv;
+  int e;
+  __device__ __forceinline__ explicit QuantDiv(float scale) {
+    int ex = 0;
+    m = 2.0f * frexpf(scale, &ex);
+    e = ex - 1;
+    inv = 1.0f / m;
   }
-  // saturate(rne(x / scale) + zero_point) as an int8 code, for 8 values packed
-  // little-endian into two words.
+  __device__ __forceinline__ float quotient(float x) const {
+    const float y = ldexpf(x, -e);
+    const float q0 = fminf(fmaxf(y * inv, -0x1p20f), 0x1p20f);
+    return fmaf(fmaf(-q0, m, y), inv, q0);
+  }
+  // saturate(rne(x / scale) + zero_point) as an int8 code
+  __device__ __forceinline__ int8_t code(float x, int zero_point) const {
+    const float c = fminf(fmaxf(rintf(quotient(x)) + static_cast<float>(zero_point), -128.0f), 127.0f);
+    return static_cast<int8_t>(c);
+  }
+  // 8 codes packed little-endian into two words.
   __device__ __forceinline__ uint2 codes8(const float* x, int zero_point) const {
-    const float z = static_cast<float>(zero_point);
-    float q[8];
-    if (fast) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) q[e] = quotient(x[e]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) q[e] = x[e] / scale;
-    }
     uint32_t w[2] = {0u, 0u};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float c = fminf(fmaxf(rintf(q[e]) + z, -128.0f), 127.0f);
-      w[e >> 2] |= (static_cast<uint32_t>(static_cast<int8_t>(c)) & 0xffu) << (8 * (e & 3));
-    }
+    for (int k = 0; k < 8; ++k)
+      w[k >> 2] |= (static_cast<uint32_t>(code(x[k], zero_point)) & 0xffu) << (8 * (k & 3));
     return uint2{w[0], w[1]};
-  }
-  __device__ __forceinline__ int8_t code(float x, int zero_point) const {
-    const float q = fast ? quotient(x) : x / scale;
-    return static_cast<int8_t>(fminf(fmaxf(rintf(q) + static_cast<float>(zero_point), -128.0f), 127.0f));
   }
 };
 

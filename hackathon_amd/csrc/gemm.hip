@@ -384,8 +384,15 @@ int c3h_qgemm(const c3h_qgemm_args* a, void* stream) {
   C3H_REQUIRE((a->mode != 1 && a->mode != 3) || a->y_scale != 0.0f, "qgemm: y_scale must be nonzero");
   C3H_REQUIRE(a->k % 16 == 0 && a->lda % 16 == 0 && a->ldb % 16 == 0, "qgemm: k, lda, ldb must be multiples of 16");
   C3H_REQUIRE(aligned(a->a, 16) && aligned(a->b, 16), "qgemm: operands must be 16-byte aligned");
-  C3H_REQUIRE(a->mode < 2 || a->out_dtype == C3H_F32 || a->out_dtype == C3H_BF16 || a->out_dtype == C3H_F16,
-              "qgemm: dequantized output dtype must be float");
+  C3H_REQUIRE(a->mode < 2 || a->out_dtype == C3H_F32 || a->out_dtype == C3H_BF16 || a->out_dtype == C3H_F16 ||
+                  a->out_dtype == C3H_I8,
+              "qgemm: dequantized output dtype must be float, or int8 (quantized again)");
+  const bool requant_out = a->mode >= 2 && a->out_dtype == C3H_I8;
+  C3H_REQUIRE(!requant_out || (quant_scale_ok(a->q_scale) && a->q_zero >= -128 && a->q_zero <= 127),
+              "qgemm: an int8 output of mode %d needs a positive normal q_scale and an int8 q_zero", a->mode);
+  C3H_REQUIRE(!requant_out || a->act_dtype == C3H_F32 || a->act_dtype == C3H_BF16 || a->act_dtype == C3H_F16,
+              "qgemm: act_dtype must be fp32, bf16 or fp16");
+  C3H_REQUIRE(!requant_out || a->epi.residual == nullptr, "qgemm: no residual into an int8 output");
   int rc = check_epilogue(a->epi);
   if (rc) return rc;
   if (a->m == 0 || a->n == 0) return C3H_OK;
@@ -395,6 +402,7 @@ int c3h_qgemm(const c3h_qgemm_args* a, void* stream) {
   p.m = a->m; p.n = a->n; p.k = a->k; p.lda = a->lda; p.ldb = a->ldb; p.ldo = a->ldo;
   p.a_scale = a->a_scale; p.y_scale = a->y_scale; p.b_scale = a->b_scale;
   p.y_zero = a->y_zero; p.qmode = a->mode; p.out_dtype = a->out_dtype;
+  p.q_scale = requant_out ? a->q_scale : 1.0f; p.q_zero = a->q_zero; p.act_dtype = a->act_dtype;
   p.epi = a->epi;
   p.ho = 1; p.wo = 1;
   p.a_bytes = (a->m - 1) * a->lda + a->k;

@@ -217,10 +217,14 @@ struct Problem {
   FastDiv fd_hw, fd_wo, fd_cpack, fd_kwpack;
   // byte extents of A and B (buffer-resource bounds of the pipelined kernel)
   int64_t a_bytes, b_bytes;
-  // int8 GEMM (c3h_qgemm): output mode and quantization parameters
+  // int8 GEMM (c3h_qgemm): output mode and quantization parameters; with an
+  // int8 output in modes 2 / 3 the epilogue's value is rounded to act_dtype
+  // and quantized by (q_scale, q_zero)
   int qmode, y_zero;
   float a_scale, y_scale;
   const float* b_scale;
+  float q_scale;
+  int q_zero, act_dtype;
   const float* a_rows;  // fp8 GEMM (c3h_gemm_fp8): per-row A scale
   // W4A16 GEMM (c3h_gemm_w4a16): B holds E2M1 codes [n][ldb bytes]; b_blk the
   // E8M0 exponents [n][ldbs] of its 32-element blocks (bs_bytes in all)
@@ -702,6 +706,7 @@ __device__ __forceinline__ void store_strip_q(const float* stage, int lane, int6
   const int mode = p.qmode;
   const float sa = p.a_scale, sy = p.y_scale, zy = static_cast<float>(p.y_zero);
   const bool requant = mode == 1 || mode == 3;
+  const QuantDiv qd(p.q_scale);  // int8 output of modes 2 / 3
   // A lane's 8 columns are the same in every pass: their multipliers
   // ((sa * sb) / sy requantizing, sa * sb for mode 2) are computed once.
   const int c0 = (lane % LPR) * 8;
@@ -746,6 +751,20 @@ __device__ __forceinline__ void store_strip_q(const float* stage, int lane, int6
       }
       if constexpr (std::is_same<TO, int8_t>::value) {
         int8_t* out = outp;
+        if (mode >= 2) {
+          // the float epilogue (no residual into an int8 output), rounded to
+          // the activation type, then QuantizeLinear: codes in v
+          float res[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+          if (full) {
+            apply_epilogue8(p.epi, v, m, n, pn, res, 0);
+          } else {
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+              if (n + c < pn) v[c] = apply_epilogue(p.epi, v[c], m, n + c, pn, 0.0f, 0);
+          }
+#pragma unroll
+          for (int c = 0; c < 8; ++c) v[c] = static_cast<float>(qd.code(round_to_dtype(v[c], p.act_dtype), p.q_zero));
+        }
         if (full) {
           uint32_t w[2] = {0u, 0u};
 #pragma unroll
@@ -866,9 +885,69 @@ __device__ __forceinline__ void epilogue_direct_impl(const Acc (&acc)[TM][TN], i
 
 // GELU: act 2 is computed in registers only by the instantiations that ask
 // for it (the large-tile kernel, which has no staged epilogue).
+// epilogue_direct for a wave tile wholly inside the output: no bounds tests,
+// the activation fixed at compile time (ACT: 0 none, 1 ReLU, 2 GELU).  Same
+// arithmetic: ((acc + b) + res), then the activation.
+template <typename TO, int TM, int TN, int ACT, typename Acc>
+__device__ __forceinline__ void epilogue_direct_interior(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase,
+                                                         int lane, TO* outp, const TO* resp, const float* bias) {
+#pragma clang fp contract(off)
+  const KArg<Problem>& p = kernel_arg<Problem>();
+  const float g0 = p.epi.imm[0], g1 = p.epi.imm[1], g2 = p.epi.imm[2];
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int64_t ldo = p.ldo;
+  float b[TN][4];
+  static_for<TN>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) b[j][r] = 0.0f;
+    if (bias) {
+      const float4 q = *reinterpret_cast<const float4*>(bias + nbase + 16 * j + 4 * lg);
+      b[j][0] = q.x; b[j][1] = q.y; b[j][2] = q.z; b[j][3] = q.w;
+    }
+  });
+  TO* base = outp + (mbase + l16) * ldo + nbase + 4 * lg;
+  const TO* rbase = resp ? resp + (mbase + l16) * ldo + nbase + 4 * lg : nullptr;
+  static_for<TM>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    float res[TN][4];
+    static_for<TN>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) res[j][r] = 0.0f;
+      if (rbase) Elem<TO>::load4(rbase + 16 * i * ldo + 16 * j, res[j]);
+    });
+    static_for<TN>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float t = (acc[i][j][r] + b[j][r]) + res[j][r];
+        v[r] = ACT == 1 ? fmaxf(t, 0.0f) : (ACT == 2 ? gelu_erf(t, g0, g1, g2) : t);
+      }
+      Elem<TO>::store4(base + 16 * i * ldo + 16 * j, v);
+    });
+  });
+}
+
 template <typename TO, int TM, int TN, bool GELU = false, typename Acc>
 __device__ __forceinline__ void epilogue_direct(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
                                                 TO* outp, const TO* resp, const float* bias, int act) {
+  const KArg<Problem>& p = kernel_arg<Problem>();
+  if (mbase + 16 * TM <= p.m && nbase + 16 * TN <= p.n) {
+    if (act == 0) {
+      epilogue_direct_interior<TO, TM, TN, 0>(acc, mbase, nbase, lane, outp, resp, bias);
+      return;
+    }
+    if (act == 1) {
+      epilogue_direct_interior<TO, TM, TN, 1>(acc, mbase, nbase, lane, outp, resp, bias);
+      return;
+    }
+    if constexpr (GELU) {
+      epilogue_direct_interior<TO, TM, TN, 2>(acc, mbase, nbase, lane, outp, resp, bias);
+      return;
+    }
+  }
   if (GELU && act == 2) epilogue_direct_impl<TO, TM, TN, true>(acc, mbase, nbase, lane, outp, resp, bias, act);
   else epilogue_direct_impl<TO, TM, TN, false>(acc, mbase, nbase, lane, outp, resp, bias, act);
 }
@@ -889,6 +968,8 @@ __device__ __forceinline__ void epilogue_direct_q_impl(const Acc (&acc)[TM][TN],
   const int mode = p.qmode;
   const float sa = p.a_scale, sy = p.y_scale, zy = static_cast<float>(p.y_zero);
   const bool requant = mode == 1 || mode == 3;
+  const QuantDiv qd(p.q_scale);  // int8 output of modes 2 / 3
+  const int act_dt = p.act_dtype, qz = p.q_zero;
   // Per-column multiplier, once per lane: (sa * sb) / sy for requantizing
   // modes, sa * sb for mode 2 (the same roundings as per element).
   float mult[TN][4], b[TN][4];
@@ -949,6 +1030,16 @@ __device__ __forceinline__ void epilogue_direct_q_impl(const Acc (&acc)[TM][TN],
               }
             }
             if constexpr (std::is_same<TO, int8_t>::value) {
+              if (mode >= 2) {
+                // dequantized value, bias and activation, rounded to the
+                // activation type, then QuantizeLinear: codes in v
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const float t = v[r] + b[j][r];
+                  const float y = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t);
+                  v[r] = static_cast<float>(qd.code(round_to_dtype(y, act_dt), qz));
+                }
+              }
               if (nfull) {
                 uint32_t w = 0u;
 #pragma unroll
@@ -1014,9 +1105,140 @@ __device__ __forceinline__ void scale_acc(f32x4 (&acc)[TM][TN], int64_t mbase, i
   });
 }
 
+// epilogue_direct_q for a wave tile that lies wholly inside the output (every
+// row < m, every column < n), the case of all but the edge tiles: no bounds
+// tests, and the output kind, activation and (int8 output of modes 2 / 3)
+// rounding type fixed at compile time, so the per-element work is the
+// arithmetic alone (the general form's per-element selects and bounds
+// branches made the epilogue cost more VALU issue than a K = 768 main loop).
+// KIND: 0 int32 accumulators (mode 0), 1 int8 codes (mode 1), 2 / 3 float
+// output of mode 2 / 3, 4 / 5 int8 output of mode 2 / 3 quantized from the
+// bf16-rounded epilogue value.  ACT: 0 none, 1 ReLU, 2 GELU.  Arithmetic
+// identical to epilogue_direct_q_impl.
+template <typename TO, int TM, int TN, int KIND, int ACT, typename Acc>
+__device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
+                                                    TO* outp, const TO* resp, const float* bias) {
+  // Each product and sum rounds on its own, as in the general form (no
+  // multiply-add contraction of the dequantization with the bias).
+#pragma clang fp contract(off)
+  const KArg<Problem>& p = kernel_arg<Problem>();
+  constexpr bool kReq = KIND == 1 || KIND == 3 || KIND == 5;
+  constexpr bool kQuantOut = KIND >= 4;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int64_t ldo = p.ldo;
+  const float sa = p.a_scale, sy = p.y_scale, zy = static_cast<float>(p.y_zero);
+  const float g0 = p.epi.imm[0], g1 = p.epi.imm[1], g2 = p.epi.imm[2];
+  const QuantDiv qd(kQuantOut ? p.q_scale : 1.0f);
+  const int qz = p.q_zero;
+  float mult[TN][4], b[TN][4];
+  if constexpr (KIND != 0) {
+    static_for<TN>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      const int64_t n = nbase + 16 * j + 4 * lg;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float sbv = p.b_scale[n + r];
+        b[j][r] = bias ? bias[n + r] : 0.0f;
+        mult[j][r] = kReq ? (sa * sbv) / sy : sa * sbv;
+      }
+    });
+  }
+  TO* base = outp + (mbase + l16) * ldo + nbase + 4 * lg;
+  const TO* rbase = resp ? resp + (mbase + l16) * ldo + nbase + 4 * lg : nullptr;
+  static_for<TM>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    TO* row = base + 16 * i * ldo;
+    if constexpr (KIND == 0) {
+      static_for<TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        *reinterpret_cast<int4*>(row + 16 * j) = int4{acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+      });
+    } else {
+      float res[TN][4];
+      static_for<TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) res[j][r] = 0.0f;
+        if constexpr (KIND == 2 || KIND == 3) {
+          if (rbase) Elem<TO>::load4(rbase + 16 * i * ldo + 16 * j, res[j]);
+        }
+      });
+      static_for<TN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float a = static_cast<float>(acc[i][j][r]);
+          if constexpr (kReq) {
+            const float y = fminf(fmaxf(rintf(a * mult[j][r]) + zy, -128.0f), 127.0f);
+            v[r] = KIND == 1 ? y : (y - zy) * sy;
+          } else {
+            v[r] = a * mult[j][r];
+          }
+          if constexpr (KIND >= 2) {
+            const float t = kQuantOut ? v[r] + b[j][r] : (v[r] + b[j][r]) + res[j][r];
+            v[r] = ACT == 1 ? fmaxf(t, 0.0f) : (ACT == 2 ? gelu_erf(t, g0, g1, g2) : t);
+          }
+          if constexpr (kQuantOut) v[r] = static_cast<float>(qd.code(bf16_bits_to_f32(f32_to_bf16_bits(v[r])), qz));
+        }
+        if constexpr (std::is_same<TO, int8_t>::value) {
+          uint32_t w = 0u;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) w |= (static_cast<uint32_t>(static_cast<int8_t>(v[r])) & 0xffu) << (8 * r);
+          *reinterpret_cast<uint32_t*>(row + 16 * j) = w;
+        } else {
+          Elem<TO>::store4(row + 16 * j, v);
+        }
+      });
+    }
+  });
+}
+
 template <typename TO, int TM, int TN, bool GELU = false, typename Acc>
 __device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
                                                   TO* outp, const TO* resp, const float* bias, int act) {
+  const KArg<Problem>& p = kernel_arg<Problem>();
+  // Interior wave tile: the specialized form (int8 outputs of modes 2 / 3
+  // only when rounded through bf16, the W8A8 activation type).
+  if (mbase + 16 * TM <= p.m && nbase + 16 * TN <= p.n && act <= (GELU ? 2 : 1)) {
+    const int mode = p.qmode;
+    if constexpr (std::is_same<TO, int32_t>::value) {
+      epilogue_q_interior<TO, TM, TN, 0, 0>(acc, mbase, nbase, lane, outp, resp, bias);
+      return;
+    } else if constexpr (std::is_same<TO, int8_t>::value) {
+      if (mode == 1) {
+        epilogue_q_interior<TO, TM, TN, 1, 0>(acc, mbase, nbase, lane, outp, resp, bias);
+        return;
+      }
+      if (p.act_dtype == C3H_BF16) {
+        const bool m3 = mode == 3;
+        if (act == 0) {
+          if (m3) epilogue_q_interior<TO, TM, TN, 5, 0>(acc, mbase, nbase, lane, outp, resp, bias);
+          else epilogue_q_interior<TO, TM, TN, 4, 0>(acc, mbase, nbase, lane, outp, resp, bias);
+        } else if (act == 1) {
+          if (m3) epilogue_q_interior<TO, TM, TN, 5, 1>(acc, mbase, nbase, lane, outp, resp, bias);
+          else epilogue_q_interior<TO, TM, TN, 4, 1>(acc, mbase, nbase, lane, outp, resp, bias);
+        } else if constexpr (GELU) {
+          if (m3) epilogue_q_interior<TO, TM, TN, 5, 2>(acc, mbase, nbase, lane, outp, resp, bias);
+          else epilogue_q_interior<TO, TM, TN, 4, 2>(acc, mbase, nbase, lane, outp, resp, bias);
+        }
+        return;
+      }
+    } else {
+      const bool m3 = mode == 3;
+      if (act == 0) {
+        if (m3) epilogue_q_interior<TO, TM, TN, 3, 0>(acc, mbase, nbase, lane, outp, resp, bias);
+        else epilogue_q_interior<TO, TM, TN, 2, 0>(acc, mbase, nbase, lane, outp, resp, bias);
+      } else if (act == 1) {
+        if (m3) epilogue_q_interior<TO, TM, TN, 3, 1>(acc, mbase, nbase, lane, outp, resp, bias);
+        else epilogue_q_interior<TO, TM, TN, 2, 1>(acc, mbase, nbase, lane, outp, resp, bias);
+      } else if constexpr (GELU) {
+        if (m3) epilogue_q_interior<TO, TM, TN, 3, 2>(acc, mbase, nbase, lane, outp, resp, bias);
+        else epilogue_q_interior<TO, TM, TN, 2, 2>(acc, mbase, nbase, lane, outp, resp, bias);
+      }
+      return;
+    }
+  }
   if (GELU && act == 2) epilogue_direct_q_impl<TO, TM, TN, true>(acc, mbase, nbase, lane, outp, resp, bias, act);
   else epilogue_direct_q_impl<TO, TM, TN, false>(acc, mbase, nbase, lane, outp, resp, bias, act);
 }

@@ -1176,8 +1176,8 @@ int c3h_layernorm(const c3h_layernorm_args* a, void* stream) {
                    (a->out_dtype == C3H_F32 || a->out_dtype == a->x_dtype || quant);
   C3H_REQUIRE(!quant || vec, "layernorm: an int8 (quantized) output needs cols %% 8 == 0, cols <= %d, "
               "16-byte aligned inputs and an 8-byte aligned output", 512 * kLnVec);
-  C3H_REQUIRE(!quant || (a->out_scale > 0.0f && a->out_zero >= -128 && a->out_zero <= 127),
-              "layernorm: quantized output needs out_scale > 0 and an int8 zero point");
+  C3H_REQUIRE(!quant || (quant_scale_ok(a->out_scale) && a->out_zero >= -128 && a->out_zero <= 127),
+              "layernorm: quantized output needs a positive normal out_scale and an int8 zero point");
   if (vec) {
     const int nv = static_cast<int>(ceil_div(a->cols / 8, 64));
     const int NVsel = nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : 8;
@@ -1333,7 +1333,9 @@ int c3h_pack_conv_weight(const c3h_pack_args* a, void* stream) {
 }
 
 int c3h_quantize(const c3h_quantize_args* a, void* stream) {
-  C3H_REQUIRE(a && a->count >= 0 && a->scale != 0.0f, "quantize: bad args");
+  C3H_REQUIRE(a && a->count >= 0, "quantize: bad args");
+  C3H_REQUIRE(quant_scale_ok(a->scale), "quantize: scale must be a positive normal float, got %g",
+              static_cast<double>(a->scale));
   if (a->count == 0) return C3H_OK;
   if (a->count % 8 == 0 && (reinterpret_cast<uintptr_t>(a->x) & 15) == 0 &&
       (reinterpret_cast<uintptr_t>(a->out) & 7) == 0 &&

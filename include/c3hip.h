@@ -572,7 +572,13 @@ int c3h_quantize(const c3h_quantize_args* a, void* stream);
  * to int8 (QLinearMatMul); mode 2: dequantize to float out_dtype
  * v = acc * (a_scale * b_scale[n]) then the epilogue (bias, act/program);
  * mode 3: QLinearMatMul followed by DequantizeLinear(y_scale, y_zero) --
- * the mode-1 int8 y, then v = (y - zy) * y_scale, then the epilogue. */
+ * the mode-1 int8 y, then v = (y - zy) * y_scale, then the epilogue.
+ * Modes 2 and 3 with out_dtype C3H_I8 also apply the QuantizeLinear that
+ * consumes the epilogue's output: each value is rounded to act_dtype (F32,
+ * BF16 or F16: the type the unfused epilogue would store), then
+ * out = saturate(rne(v / q_scale) + q_zero) -- the codes the separate
+ * c3h_quantize of that stored tensor gives.  No residual with this form.
+ * (The QuantizeLinear after W8A8's FFN1 GELU, ahead of FFN2's QLinearMatMul.) */
 typedef struct {
   const int8_t* a;
   const int8_t* b;
@@ -587,7 +593,9 @@ typedef struct {
   int32_t y_zero;
   int32_t mode;
   int32_t out_dtype;
-  int32_t pad_;
+  int32_t act_dtype;  /* modes 2 / 3 with an int8 out: see above */
+  float q_scale;
+  int32_t q_zero;
   c3h_epilogue epi;
 } c3h_qgemm_args;
 int c3h_qgemm(const c3h_qgemm_args* a, void* stream);

@@ -244,11 +244,12 @@ def _teacher_forced(name: str):
         if kind in ("int8", "int32", "int64", "u8"):
             st["mismatch"] = int(np.count_nonzero(ref != got))
             st["code_max"] = int(np.max(np.abs(ref.astype(np.int64) - got.astype(np.int64)))) if ref.size else 0
-            # codes of a QuantizeLinear fused into the LayerNorm launch: the
-            # oracle quantizes its own LayerNorm output (never stored, so not
-            # teacher-forced), which may sit one activation ulp away
+            # codes of a QuantizeLinear fused into its producer's launch (a
+            # LayerNorm, or FFN1's GEMM + GELU): the oracle quantizes its own
+            # producer output (never stored, so not teacher-forced), which may
+            # sit one activation ulp away
             prod_node = m.graph.nodes.get(m.graph.tensor_producer.get(n))
-            st["after_fused_ln"] = bool(prod_node is not None and prod_node.inputs and
+            st["after_fused_producer"] = bool(prod_node is not None and prod_node.inputs and
                                         prod_node.inputs[0] in in_registers)
         else:
             d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
@@ -300,10 +301,10 @@ def _summarize(name, stats, ops):
     for (op, kind), items in sorted(by.items()):
         if kind in ("int8", "int32", "int64", "u8"):
             worst = max(items, key=lambda t: t[1]["mismatch"])
-            fused = sum(1 for t in items if t[1].get("after_fused_ln"))
+            fused = sum(1 for t in items if t[1].get("after_fused_producer"))
             print(f"  {name} {op:>25} {kind:>5} x{len(items):3d}: mismatches max {worst[1]['mismatch']} of "
                   f"{worst[1]['size']}, |code diff| <= {worst[1]['code_max']} ({worst[0]}; {fused} quantized inside "
-                  f"a LayerNorm launch)", flush=True)
+                  f"the producing launch)", flush=True)
         elif kind in ("bf16", "fp16"):
             worst = max(items, key=lambda t: t[1]["max_abs"] / gates.ulp_at(t[1]["max_ref"], kind))
             gt1 = max(t[1]["frac_gt1"] for t in items)
@@ -324,10 +325,11 @@ def test_fullsize_per_value_teacher_forced(gpu, name):
     """Every value the full-size program stores, against the oracle's node
     recomputed from the program's own inputs (no error carried between nodes):
       int8 (QuantizeLinear codes)            bit-exact; codes quantized inside the
-                                             LayerNorm launch (W8A8) within one code
-                                             on at most 1e-4 of elements, since the
-                                             oracle quantizes its own LayerNorm output
-                                             (one activation ulp at most, above)
+                                             producing launch (W8A8: LayerNorm, FFN1
+                                             GEMM + GELU) within one code on at most
+                                             1e-4 of elements, since the oracle
+                                             quantizes its own producer output (one
+                                             activation ulp at most, above)
       bf16 / fp16                            within one ulp at the tensor's
                                              largest magnitude, and at most
                                              0.1 % of elements more than one
@@ -349,7 +351,7 @@ def test_fullsize_per_value_teacher_forced(gpu, name):
     for n, st in stats.items():
         kind = st["kind"]
         if kind in ("int8", "int32", "int64", "u8"):
-            if st.get("after_fused_ln"):
+            if st.get("after_fused_producer"):
                 assert st["code_max"] <= 1 and st["mismatch"] <= 1e-4 * st["size"], (n, st)
             else:
                 assert st["mismatch"] == 0, (n, st)

@@ -397,14 +397,13 @@ def _f32(bits):
 
 
 # Scales for the division-free quantizer: all-ones significands (the divisors
-# where a reciprocal-only quotient is most often misrounded), the edges of the
-# range it serves (2^-100 .. 2^100) and just outside them, where the kernels
-# divide directly.
+# where a reciprocal-only quotient is most often misrounded), tiny and huge
+# exponents (the quotient is formed from x 2^-e), the smallest normal scale.
 _QUANT_SCALES = [0.5, 0.019, 1 / 127, 0.0123, 3.0, 40.11176,
                  _f32(0x3FFFFFFF), _f32(0x3F7FFFFF), _f32(0x3C7FFFFF),     # 2 - 2^-22, 1 - 2^-24, 2^-6 (2 - 2^-23)
                  _f32(0x0D800000), _f32(0x0D7FFFFF),                        # 2^-100 and just below
                  _f32(0x71800000), _f32(0x71800001),                        # 2^100 and just above
-                 1e-30, 7e30]
+                 1e-30, 7e30, _f32(0x00800000), _f32(0x7F7FFFFF)]           # 2^-126, the largest float
 
 
 @pytest.mark.parametrize("kind", ["bf16", "fp16", "fp32"])
@@ -833,6 +832,84 @@ def test_qgemm_big_tile_matches_128_tiles(gpu, mode, act):
     if mode == 0:
         rows = np.arange(0, m, 61)
         np.testing.assert_array_equal(big[rows], a[rows].astype(np.int64) @ bt.T.astype(np.int64))
+
+
+@pytest.mark.parametrize("m,n,k,mode,act,act_kind,switch", [
+    (4096, 4096, 256, 3, 2, "bf16", None),                      # 256x256 tile, GELU in registers
+    (4096, 4096, 256, 3, 2, "bf16", "C3H_DISABLE_BIGTILE"),     # 128x128 DMA tile, staged GELU epilogue
+    (300, 200, 256, 3, 1, "fp16", None),                        # 128x128, direct epilogue
+    (300, 70, 256, 2, 0, "fp32", None),                         # unaligned rows: staged, partial stores
+    (300, 200, 256, 3, 2, "bf16", "C3H_DISABLE_DMA"),           # register-prefetch kernel
+    (16384, 3072, 768, 3, 2, "bf16", None),                     # W8A8 FFN1
+])
+def test_qgemm_int8_output_equals_qgemm_then_quantize(gpu, m, n, k, mode, act, act_kind, switch):
+    """Modes 2 / 3 with an int8 output (the QuantizeLinear after the epilogue
+    in the same launch) give exactly the codes of the two-launch form: the
+    float epilogue stored in act_kind, then c3h_quantize -- with saturated
+    codes and a nonzero zero point."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    rng = np.random.default_rng(m + n + k + act)
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    bt = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    sb = (rng.random(n) * 0.01 + 0.001).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    ad, bd, sbd, biasd = _dev(a), _dev(bt), _dev(sb), _dev(bias)
+    code, sdt = {"fp32": (_lib.F32, np.float32), "bf16": (_lib.BF16, BF16), "fp16": (_lib.F16, np.float16)}[act_kind]
+    qscale, qzero = 0.0417, 3
+    mid = DeviceArray.empty((m, n), sdt)
+    want = DeviceArray.empty((m, n), np.int8)
+    got = DeviceArray.empty((m, n), np.int8)
+
+    def qgemm(out, out_code, quant):
+        g = _lib.QGemmArgs()
+        g.a, g.b, g.out, g.m, g.n, g.k, g.lda, g.ldb, g.ldo = ad.ptr, bd.ptr, out.ptr, m, n, k, k, k, n
+        g.a_scale, g.y_scale, g.b_scale, g.mode, g.out_dtype = 0.02, 0.37, sbd.ptr, mode, out_code
+        if quant:
+            g.act_dtype, g.q_scale, g.q_zero = code, qscale, qzero
+        g.epi = E.epilogue(bias=biasd, bias_mode=2, act=act, imm=[math.sqrt(2.0), 1.0, 0.5] if act == 2 else [])
+        print(f"qgemm {m}x{n}x{k} mode {mode} act {act} {act_kind} quant={quant} switch={switch}", flush=True)
+        _lib.launch(g, None)
+
+    def run():
+        qgemm(mid, code, False)
+        q = _lib.QuantizeArgs()
+        q.x, q.out, q.count, q.scale, q.zero_point, q.x_dtype = mid.ptr, want.ptr, m * n, qscale, qzero, code
+        _lib.launch(q, None)
+        got.copy_from_host(np.full(m * n, 77, np.int8))
+        qgemm(got, _lib.I8, True)
+        return want.get(), got.get()
+
+    w, g_ = _with_env(switch, "1", run) if switch else run()
+    bad = np.argwhere(w != g_)
+    assert bad.size == 0, (bad[:5], w[tuple(bad[:5].T)], g_[tuple(bad[:5].T)])
+    assert (w == 127).any() and (act != 0 or (w == -128).any()) and len(np.unique(w)) > 50
+
+
+def test_qgemm_int8_output_host_checks(gpu):
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import DeviceArray
+
+    a = DeviceArray.empty((32, 64), np.int8)
+    out = DeviceArray.empty((32, 32), np.int8)
+    sb = DeviceArray.empty((32,), np.float32)
+    g = _lib.QGemmArgs()
+    g.a, g.b, g.out, g.m, g.n, g.k, g.lda, g.ldb, g.ldo = a.ptr, a.ptr, out.ptr, 32, 32, 64, 64, 64, 32
+    g.a_scale, g.y_scale, g.b_scale, g.mode, g.out_dtype = 0.02, 0.37, sb.ptr, 3, _lib.I8
+    g.act_dtype, g.q_scale, g.q_zero = _lib.BF16, 0.0, 0
+    g.epi = E.epilogue()
+    with pytest.raises(_lib.C3HError, match="q_scale"):
+        _lib.launch(g, None)
+    g.q_scale, g.act_dtype = 0.5, _lib.I32
+    with pytest.raises(_lib.C3HError, match="act_dtype"):
+        _lib.launch(g, None)
+    g.act_dtype = _lib.BF16
+    g.epi = E.epilogue(residual=out)
+    with pytest.raises(_lib.C3HError, match="residual"):
+        _lib.launch(g, None)
 
 
 def test_gemm_fp8_big_tile_matches_128_tiles(gpu):
