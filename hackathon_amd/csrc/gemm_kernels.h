@@ -1132,14 +1132,29 @@ __device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], in
   const int qz = p.q_zero;
   float mult[TN][4], b[TN][4];
   if constexpr (KIND != 0) {
+    // Requantizing, each of the wave tile's 16 TN columns forms its
+    // multiplier (sa * sb) / sy once -- column c on lane c % 64 -- and the
+    // lanes that use it read it with ds_bpermute: one IEEE division per
+    // column instead of one per column and row lane (the 16 row lanes of a
+    // column group each needed all of theirs).
+    static_assert(TN % 4 == 0, "whole 64-column groups");
+    float own[TN / 4];
+    if constexpr (kReq) {
+#pragma unroll
+      for (int t = 0; t < TN / 4; ++t) own[t] = (sa * p.b_scale[nbase + lane + 64 * t]) / sy;
+    }
     static_for<TN>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
       const int64_t n = nbase + 16 * j + 4 * lg;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float sbv = p.b_scale[n + r];
         b[j][r] = bias ? bias[n + r] : 0.0f;
-        mult[j][r] = kReq ? (sa * sbv) / sy : sa * sbv;
+        if constexpr (kReq) {
+          const int src = (16 * (j % 4) + 4 * lg + r) << 2;  // byte address of lane (column % 64)
+          mult[j][r] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(own[j / 4])));
+        } else {
+          mult[j][r] = sa * p.b_scale[n + r];
+        }
       }
     });
   }
