@@ -34,7 +34,7 @@ OP_NOP, OP_EVENT_RECORD, OP_EVENT_WAIT, OP_COPY = 0, 1, 2, 3
 OP_FILL, OP_CAST, OP_EW, OP_STRIDED_COPY, OP_REDUCE, OP_SOFTMAX, OP_LAYERNORM, OP_BATCHNORM, \
     OP_GATHER, OP_ARGMAX, OP_IM2COL, OP_LAYOUT, OP_MAXPOOL, OP_GEMM, OP_CONV, OP_ATTN_SCORES, \
     OP_FLASH, OP_QUANTIZE, OP_QGEMM, OP_DEQUANTIZE, OP_BNFOLD, OP_PACK, OP_CONV_POOL, OP_QUANT_FP8, \
-    OP_GEMM_FP8, OP_SPLITK, OP_QUANT_MXFP4, OP_GEMM_W4A16 = range(10, 38)
+    OP_GEMM_FP8, OP_SPLITK, OP_QUANT_MXFP4, OP_GEMM_W4A16, OP_ARGMAX_FINISH = range(10, 39)
 
 vp = C.c_void_p
 i32 = C.c_int32
@@ -113,6 +113,11 @@ class ArgmaxArgs(C.Structure):
                 ("pad_", i32)]
 
 
+class ArgmaxFinishArgs(C.Structure):
+    _fields_ = [("parts", vp), ("in_", vp), ("out", vp), ("rows", i64), ("cols", i64), ("n_parts", i64),
+                ("ld", i64), ("in_ld", i64), ("in_dtype", i32), ("pad_", i32)]
+
+
 class Im2colArgs(C.Structure):
     _fields_ = [(n, i32) for n in ("n", "c", "h", "w", "kh", "kw", "sh", "sw", "pad_top",
                                    "pad_left", "dh", "dw", "ho", "wo", "dtype", "pad_")]
@@ -133,7 +138,7 @@ class PoolArgs(C.Structure):
 class Epilogue(C.Structure):
     _fields_ = [("bias", vp), ("residual", vp), ("alpha", f32), ("beta", f32),
                 ("bias_mode", i32), ("act", i32), ("n_imm", i32), ("n_inst", i32),
-                ("imm", f32 * 8), ("inst", EwInst * EW_MAX_INST)]
+                ("imm", f32 * 8), ("inst", EwInst * EW_MAX_INST), ("row_max", vp), ("row_max_ld", i64)]
 
 
 class GemmArgs(C.Structure):
@@ -229,7 +234,7 @@ ABI_ORDER = [Props, FillArgs, CastArgs, EwArgs, CopyArgs, ReduceArgs, SoftmaxArg
              BatchNormArgs, BnFoldArgs, GatherArgs, ArgmaxArgs, Im2colArgs, LayoutArgs, PoolArgs,
              Epilogue, GemmArgs, ConvArgs, AttnScoresArgs, FlashArgs, QuantizeArgs, QGemmArgs,
              DequantizeArgs, Op, PackArgs, ConvPoolArgs, Fp8QuantArgs, Fp8GemmArgs,
-             SplitKArgs, Mxfp4QuantArgs, W4A16GemmArgs]
+             SplitKArgs, Mxfp4QuantArgs, W4A16GemmArgs, ArgmaxFinishArgs]
 
 # Kernel entry points: name -> args struct (all take (const args*, void* stream)).
 KERNELS = {
@@ -243,7 +248,7 @@ KERNELS = {
     "c3h_pack_conv_weight": PackArgs, "c3h_conv_stem_pool": ConvPoolArgs,
     "c3h_quantize_fp8_rows": Fp8QuantArgs, "c3h_gemm_fp8": Fp8GemmArgs,
     "c3h_gemm_splitk_reduce": SplitKArgs, "c3h_quantize_mxfp4": Mxfp4QuantArgs,
-    "c3h_gemm_w4a16": W4A16GemmArgs,
+    "c3h_gemm_w4a16": W4A16GemmArgs, "c3h_argmax_finish": ArgmaxFinishArgs,
 }
 
 OP_KIND = {
@@ -255,7 +260,7 @@ OP_KIND = {
     QuantizeArgs: OP_QUANTIZE, QGemmArgs: OP_QGEMM, DequantizeArgs: OP_DEQUANTIZE,
     BnFoldArgs: OP_BNFOLD, PackArgs: OP_PACK, ConvPoolArgs: OP_CONV_POOL,
     Fp8QuantArgs: OP_QUANT_FP8, Fp8GemmArgs: OP_GEMM_FP8, SplitKArgs: OP_SPLITK,
-    Mxfp4QuantArgs: OP_QUANT_MXFP4, W4A16GemmArgs: OP_GEMM_W4A16,
+    Mxfp4QuantArgs: OP_QUANT_MXFP4, W4A16GemmArgs: OP_GEMM_W4A16, ArgmaxFinishArgs: OP_ARGMAX_FINISH,
 }
 
 KERNEL_OF_ARGS = {v: k for k, v in KERNELS.items()}

@@ -126,6 +126,7 @@ class _Epi:
     x_name: str = ""
     final: str = ""
     absorbed: List[str] = field(default_factory=list)
+    row_max: Optional["Val"] = None    # block-maxima side output (c3h_epilogue.row_max)
 
 
 def _numel_bytes(shape, dtype) -> int:
@@ -927,6 +928,21 @@ class CompiledPlan:
             e.imm[i] = v
         for i, (op, ra, rb, iv) in enumerate(st.prog):
             e.inst[i].op, e.inst[i].a, e.inst[i].b, e.inst[i].imm = op, ra, rb, iv
+        if st.row_max is not None:
+            e.row_max, e.row_max_ld = self._ptr(st.row_max, r), st.row_max.shape[-1]
+
+    def _note_row_max_site(self, st: "_Epi", out: Val, m: int, n: int, alpha: float = 1.0, beta: float = 1.0,
+                            bias_mode: Optional[int] = None) -> None:
+        """Remember the launch just emitted as able to write its rows' block
+        maxima (c3h_epilogue.row_max): a GEMM whose epilogue the kernels keep
+        in registers (alpha = beta = 1, no bias or a per-column one, at most
+        ReLU, no program) into a dense float output with n % 4 == 0."""
+        bm = (2 if st.bias is not None else 0) if bias_mode is None else bias_mode
+        if st.prog or st.act > 1 or alpha != 1.0 or beta != 1.0 or bm not in (0, 2) or n % 4:
+            return
+        if out.dtype not in (np.dtype(np.float32), np.dtype(np.float16), BF16) or not out.dense or out.offset:
+            return
+        self.__dict__.setdefault("_row_max_sites", {})[st.final] = (len(self.launches) - 1, st, m, n, out)
 
     def _epi_reads(self, st: "_Epi") -> List[Val]:
         return [v for v in (st.bias, st.residual) if v is not None]
@@ -996,6 +1012,7 @@ class CompiledPlan:
             return g
         self._emit(f"gemm_w4a16:{node.op_type}", build, [a2, wc, ws] + self._epi_reads(st), [out],
                    flops=2.0 * m * n * k)
+        self._note_row_max_site(st, out, m, n, alpha, beta, bmode)
         return out
 
     def _gemm_fp8(self, node, a: Val, w_name: str, trans_b: int, st: "_Epi", alpha: float, beta: float,
@@ -1028,6 +1045,7 @@ class CompiledPlan:
             return g
         self._emit(f"gemm_fp8:{node.op_type}", build, [qa, sa, wq, ws] + self._epi_reads(st), [out],
                    flops=2.0 * m * n * k)
+        self._note_row_max_site(st, out, m, n, alpha, beta, bmode)
         return out
 
     def _gemm_epi_state(self, node, bias_name: Optional[str], act: int, m: int, n: int,
@@ -1087,6 +1105,8 @@ class CompiledPlan:
             self._fill_epi(g.epi, st, r, alpha, beta, bmode)
             return g
         self._emit(f"gemm:{node.op_type}", build, [a2, w] + self._epi_reads(st), [out], flops=2.0 * m * n * k)
+        if mm != _lib.F32:
+            self._note_row_max_site(st, out, m, n, alpha, beta, bmode)
         self.vals[st.final] = out
 
     def _splitk(self, m: int, n: int, k: int, vec: int = 4, tile: int = 64, min_k: int = 32) -> int:
@@ -1677,6 +1697,30 @@ class CompiledPlan:
         rows = x.size // cols
         keep = int(node.attributes.get("keepdims", 1))
         out = self._new(tuple(x.shape[:-1]) + ((1,) if keep else ()), np.int64)
+        site = self.__dict__.get("_row_max_sites", {}).get(node.inputs[0])
+        if site is not None and site[4] is x and site[2] == rows and site[3] == cols:
+            # The producing GEMM also writes each row's 64-column block maxima
+            # (its epilogue's row_max side output); the ArgMax finishes from
+            # those and reads only the blocks that can hold the answer.
+            gi, st = site[0], site[1]
+            n_parts = -(-cols // 64)
+            parts = self._new((rows, n_parts), np.int64)       # c3h_block_max entries (8 bytes)
+            parts.buf.touch(gi)
+            self.launch_rw[gi][1].append(parts.buf)
+            self.launch_meta[gi]["bytes"] += parts.size * 8
+            st.row_max = parts
+
+            def fbuild(r, parts=parts, x=x, out=out):
+                a = _lib.ArgmaxFinishArgs()
+                a.parts, a.in_, a.out = self._ptr(parts, r), self._ptr(x, r), self._ptr(out, r)
+                a.rows, a.cols, a.n_parts, a.ld, a.in_ld, a.in_dtype = rows, cols, n_parts, n_parts, cols, \
+                    dtype_code(x.dtype)
+                return a
+            # algorithmic bytes: the block maxima, plus about one 64-column block of each row
+            self._emit("argmax_finish", fbuild, [parts, x], [out], skip_bytes=[x],
+                       extra_bytes=rows * 64 * x.dtype.itemsize)
+            self.vals[node.outputs[0]] = out
+            return
 
         def build(r, x=x, out=out):
             a = _lib.ArgmaxArgs()
@@ -1757,6 +1801,8 @@ class CompiledPlan:
         self._finish_residual(st, out)
         q = (dtype_code(act_dtype), quant[1], quant[2]) if quant is not None else None
         self._qgemm(a, bt, sbv, out, m, n, k, 3, sa, sy, st, q)
+        if quant is None:
+            self._note_row_max_site(st, out, m, n)
         if quant is not None:
             self.consumed.add(quant[0].id)
             self._rounded[st.final] = _DTYPE_NAME[act_dtype]

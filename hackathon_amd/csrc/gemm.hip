@@ -44,7 +44,9 @@ int c3h_gemm(const c3h_gemm_args* a, void* stream) {
   C3H_REQUIRE(a != nullptr, "gemm: null args");
   C3H_REQUIRE(a->m >= 0 && a->n >= 0 && a->k >= 0 && a->batch >= 1, "gemm: bad sizes");
   C3H_REQUIRE(a->batch <= 65535, "gemm: batch %lld too large", static_cast<long long>(a->batch));
-  int rc = check_epilogue(a->epi);
+  int rc = check_epilogue(a->epi, a->in_dtype == C3H_BF16 || a->in_dtype == C3H_F16);
+  if (rc) return rc;
+  rc = check_row_max(a->epi, a->n, a->ldo, a->out, a->out_dtype, a->batch);
   if (rc) return rc;
   if (a->m == 0 || a->n == 0) return C3H_OK;
   C3H_REQUIRE(a->k >= 1, "gemm: k must be >= 1 for a non-empty output");
@@ -324,7 +326,9 @@ int c3h_gemm_fp8(const c3h_fp8_gemm_args* a, void* stream) {
   C3H_REQUIRE(a->out_dtype == C3H_F32 || a->out_dtype == C3H_BF16 || a->out_dtype == C3H_F16,
               "gemm_fp8: output dtype must be fp32, bf16 or fp16");
   C3H_REQUIRE(a->m < (int64_t{1} << 31) && a->n < (int64_t{1} << 31), "gemm_fp8: m and n must be below 2^31");
-  int rc = check_epilogue(a->epi);
+  int rc = check_epilogue(a->epi, true);
+  if (rc) return rc;
+  rc = check_row_max(a->epi, a->n, a->ldo, a->out, a->out_dtype, 1);
   if (rc) return rc;
   if (a->m == 0 || a->n == 0) return C3H_OK;
   C3H_REQUIRE(ceil_div(a->m, 64) * ceil_div(a->n, 64) < (int64_t{1} << 31), "gemm_fp8: too many tiles");
@@ -352,7 +356,9 @@ int c3h_gemm_w4a16(const c3h_w4a16_gemm_args* a, void* stream) {
   C3H_REQUIRE(aligned(a->a, 16) && aligned(a->b_codes, 4), "gemm_w4a16: A must be 16-byte and codes 4-byte aligned");
   C3H_REQUIRE(a->b_scales != nullptr, "gemm_w4a16: b_scales required");
   C3H_REQUIRE(a->out_dtype == C3H_F32 || a->out_dtype == C3H_F16, "gemm_w4a16: output dtype must be fp32 or fp16");
-  int rc = check_epilogue(a->epi);
+  int rc = check_epilogue(a->epi, true);
+  if (rc) return rc;
+  rc = check_row_max(a->epi, a->n, a->ldo, a->out, a->out_dtype, 1);
   if (rc) return rc;
   if (a->m == 0 || a->n == 0) return C3H_OK;
   const int64_t a_bytes = ((a->m - 1) * a->lda + a->k) * 2;
@@ -393,7 +399,9 @@ int c3h_qgemm(const c3h_qgemm_args* a, void* stream) {
   C3H_REQUIRE(!requant_out || a->act_dtype == C3H_F32 || a->act_dtype == C3H_BF16 || a->act_dtype == C3H_F16,
               "qgemm: act_dtype must be fp32, bf16 or fp16");
   C3H_REQUIRE(!requant_out || a->epi.residual == nullptr, "qgemm: no residual into an int8 output");
-  int rc = check_epilogue(a->epi);
+  int rc = check_epilogue(a->epi, a->mode >= 2 && a->out_dtype != C3H_I8);
+  if (rc) return rc;
+  rc = check_row_max(a->epi, a->n, a->ldo, a->out, a->out_dtype, 1);
   if (rc) return rc;
   if (a->m == 0 || a->n == 0) return C3H_OK;
   Problem p;

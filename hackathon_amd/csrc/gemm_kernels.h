@@ -811,6 +811,55 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
+// The value a consumer reads back after the epilogue stores x as TO.
+template <typename TO>
+__device__ __forceinline__ float stored_value(float x) {
+  if constexpr (std::is_same<TO, float>::value) return x;
+  else return Elem<TO>::to_f32(Elem<TO>::from_f32(x));
+}
+
+// Per-row block maxima of the stored values (the epilogue's row_max side
+// output, what an ArgMax of the output finishes from), one tracker per
+// 64-column block of the wave tile (TN / 4 of them) in each lane: the
+// maximum ignoring NaN (v_max_f32), and a NaN witness x * 0 summed in (NaN
+// once the block held a NaN -- or an infinity, which only sends the finish
+// to look at the block's values).  Two VALU operations per element.  The 4
+// lanes of a row then merge the same way.
+struct RowMax {
+  float v, nan;
+  __device__ __forceinline__ void start() { v = -INFINITY; nan = 0.0f; }
+  __device__ __forceinline__ void see(float x) {
+    v = fmaxf(v, x);
+    nan = fmaf(x, 0.0f, nan);
+  }
+  __device__ __forceinline__ void merge(int xaddr) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_bpermute(xaddr, __float_as_int(v))));
+    nan += __int_as_float(__builtin_amdgcn_ds_bpermute(xaddr, __float_as_int(nan)));
+  }
+};
+
+// Merge each row's 4 lanes (lane, lane ^ 16, lane ^ 32, lane ^ 48) and write
+// its blocks from lanes 0-15, which hold rows mrow0 + lane.  Every lane of
+// the wave takes part (ds_bpermute reads the other lanes' registers).
+template <int NB>
+__device__ __forceinline__ void row_max_store(RowMax (&t)[NB], int lane, int64_t mrow0, int64_t nbase) {
+  const KArg<Problem>& p = kernel_arg<Problem>();
+  const int x16 = (lane ^ 16) << 2, x32 = (lane ^ 32) << 2;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    t[b].merge(x16);
+    t[b].merge(x32);
+  }
+  const int64_t m = mrow0 + lane;
+  if (lane < 16 && m < p.m) {
+    c3h_block_max* dst = p.epi.row_max + m * p.epi.row_max_ld + nbase / 64;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      if (nbase + 64 * b < p.n)
+        *reinterpret_cast<uint2*>(dst + b) = uint2{__float_as_uint(t[b].v), t[b].nan != t[b].nan ? 1u : 0u};
+  }
+}
+
 // The 16-bit and fp32 MFMA kernels multiply with the operands swapped, so
 // acc[i][j][r] is C^T: output row m = mbase + 16 i + l16, column
 // n = nbase + 16 j + 4 lg + r.  A lane owns 4 consecutive columns of a row.
@@ -842,12 +891,17 @@ __device__ __forceinline__ void epilogue_direct_impl(const Acc (&acc)[TM][TN], i
       b[j][0] = q.x; b[j][1] = q.y; b[j][2] = q.z; b[j][3] = q.w;
     }
   });
+  static_assert(TN % 4 == 0, "wave tiles of whole 64-column blocks (row_max)");
+  const bool rb = p.epi.row_max != nullptr;
   // Row by row: a row's column tiles share cache lines, so its residual
   // loads and its stores go out back to back (interleaving rows makes L2
   // write partial lines back more than once).
   static_for<TM>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
     const int64_t m = mbase + 16 * i + l16;
+    RowMax best[TN / 4];
+#pragma unroll
+    for (int q = 0; q < TN / 4; ++q) best[q].start();
     if (m < pm) {
       float res[TN][4];
       static_for<TN>([&](auto jc) {
@@ -866,6 +920,7 @@ __device__ __forceinline__ void epilogue_direct_impl(const Acc (&acc)[TM][TN], i
           for (int r = 0; r < 4; ++r) {
             float t = (v[r] + b[j][r]) + res[j][r];
             v[r] = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t);
+            if (rb) best[j / 4].see(stored_value<TO>(v[r]));
           }
           Elem<TO>::store4(outp + m * ldo + n, v);
         } else {
@@ -874,12 +929,15 @@ __device__ __forceinline__ void epilogue_direct_impl(const Acc (&acc)[TM][TN], i
             if (n + r < pn) {
               const int64_t o = m * ldo + n + r;
               float t = (v[r] + (bias ? bias[n + r] : 0.0f)) + (resp ? Elem<TO>::to_f32(resp[o]) : 0.0f);
-              outp[o] = Elem<TO>::from_f32(relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t));
+              const float y = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t);
+              outp[o] = Elem<TO>::from_f32(y);
+              if (rb) best[j / 4].see(stored_value<TO>(y));
             }
           }
         }
       });
     }
+    if (rb) row_max_store(best, lane, mbase + 16 * i, nbase);
   });
 }
 
@@ -888,7 +946,7 @@ __device__ __forceinline__ void epilogue_direct_impl(const Acc (&acc)[TM][TN], i
 // epilogue_direct for a wave tile wholly inside the output: no bounds tests,
 // the activation fixed at compile time (ACT: 0 none, 1 ReLU, 2 GELU).  Same
 // arithmetic: ((acc + b) + res), then the activation.
-template <typename TO, int TM, int TN, int ACT, typename Acc>
+template <typename TO, int TM, int TN, int ACT, bool RB, typename Acc>
 __device__ __forceinline__ void epilogue_direct_interior(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase,
                                                          int lane, TO* outp, const TO* resp, const float* bias) {
 #pragma clang fp contract(off)
@@ -910,6 +968,11 @@ __device__ __forceinline__ void epilogue_direct_interior(const Acc (&acc)[TM][TN
   const TO* rbase = resp ? resp + (mbase + l16) * ldo + nbase + 4 * lg : nullptr;
   static_for<TM>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
+    RowMax best[TN / 4];
+    if constexpr (RB) {
+#pragma unroll
+      for (int q = 0; q < TN / 4; ++q) best[q].start();
+    }
     float res[TN][4];
     static_for<TN>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
@@ -924,9 +987,11 @@ __device__ __forceinline__ void epilogue_direct_interior(const Acc (&acc)[TM][TN
       for (int r = 0; r < 4; ++r) {
         const float t = (acc[i][j][r] + b[j][r]) + res[j][r];
         v[r] = ACT == 1 ? fmaxf(t, 0.0f) : (ACT == 2 ? gelu_erf(t, g0, g1, g2) : t);
+        if constexpr (RB) best[j / 4].see(stored_value<TO>(v[r]));
       }
       Elem<TO>::store4(base + 16 * i * ldo + 16 * j, v);
     });
+    if constexpr (RB) row_max_store(best, lane, mbase + 16 * i, nbase);
   });
 }
 
@@ -935,17 +1000,22 @@ __device__ __forceinline__ void epilogue_direct(const Acc (&acc)[TM][TN], int64_
                                                 TO* outp, const TO* resp, const float* bias, int act) {
   const KArg<Problem>& p = kernel_arg<Problem>();
   if (mbase + 16 * TM <= p.m && nbase + 16 * TN <= p.n) {
+    const bool rb = p.epi.row_max != nullptr;  // host: only with act <= 1
     if (act == 0) {
-      epilogue_direct_interior<TO, TM, TN, 0>(acc, mbase, nbase, lane, outp, resp, bias);
+      if (rb) epilogue_direct_interior<TO, TM, TN, 0, true>(acc, mbase, nbase, lane, outp, resp, bias);
+      else epilogue_direct_interior<TO, TM, TN, 0, false>(acc, mbase, nbase, lane, outp, resp, bias);
       return;
     }
     if (act == 1) {
-      epilogue_direct_interior<TO, TM, TN, 1>(acc, mbase, nbase, lane, outp, resp, bias);
+      if (rb) epilogue_direct_interior<TO, TM, TN, 1, true>(acc, mbase, nbase, lane, outp, resp, bias);
+      else epilogue_direct_interior<TO, TM, TN, 1, false>(acc, mbase, nbase, lane, outp, resp, bias);
       return;
     }
     if constexpr (GELU) {
-      epilogue_direct_interior<TO, TM, TN, 2>(acc, mbase, nbase, lane, outp, resp, bias);
-      return;
+      if (!rb) {
+        epilogue_direct_interior<TO, TM, TN, 2, false>(acc, mbase, nbase, lane, outp, resp, bias);
+        return;
+      }
     }
   }
   if (GELU && act == 2) epilogue_direct_impl<TO, TM, TN, true>(acc, mbase, nbase, lane, outp, resp, bias, act);
@@ -987,10 +1057,16 @@ __device__ __forceinline__ void epilogue_direct_q_impl(const Acc (&acc)[TM][TN],
       mult[j][r] = requant ? (sa * sbv) / sy : sa * sbv;
     }
   });
+  static_assert(TN % 4 == 0, "wave tiles of whole 64-column blocks (row_max)");
+  constexpr bool kFloatOut = !std::is_same<TO, int32_t>::value && !std::is_same<TO, int8_t>::value;
+  const bool rb = kFloatOut && p.epi.row_max != nullptr;
   // Row by row, as epilogue_direct: a row's stores go out back to back.
   static_for<TM>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
     const int64_t m = mbase + 16 * i + l16;
+    RowMax best[TN / 4];
+#pragma unroll
+    for (int q = 0; q < TN / 4; ++q) best[q].start();
     if (m < pm) {
       float res[TN][4];
       static_for<TN>([&](auto jc) {
@@ -1057,6 +1133,7 @@ __device__ __forceinline__ void epilogue_direct_q_impl(const Acc (&acc)[TM][TN],
                 if (resp && !nfull && n + r < pn) rr = Elem<TO>::to_f32(resp[o + r]);
                 const float t = (v[r] + b[j][r]) + rr;
                 v[r] = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t);
+                if (rb && n + r < pn) best[j / 4].see(stored_value<TO>(v[r]));
               }
               if (nfull) {
                 Elem<TO>::store4(outp + o, v);
@@ -1070,6 +1147,7 @@ __device__ __forceinline__ void epilogue_direct_q_impl(const Acc (&acc)[TM][TN],
         }
       });
     }
+    if (rb) row_max_store(best, lane, mbase + 16 * i, nbase);
   });
 }
 
@@ -1115,7 +1193,7 @@ __device__ __forceinline__ void scale_acc(f32x4 (&acc)[TM][TN], int64_t mbase, i
 // output of mode 2 / 3, 4 / 5 int8 output of mode 2 / 3 quantized from the
 // bf16-rounded epilogue value.  ACT: 0 none, 1 ReLU, 2 GELU.  Arithmetic
 // identical to epilogue_direct_q_impl.
-template <typename TO, int TM, int TN, int KIND, int ACT, typename Acc>
+template <typename TO, int TM, int TN, int KIND, int ACT, bool RB, typename Acc>
 __device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
                                                     TO* outp, const TO* resp, const float* bias) {
   // Each product and sum rounds on its own, as in the general form (no
@@ -1169,6 +1247,11 @@ __device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], in
         *reinterpret_cast<int4*>(row + 16 * j) = int4{acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
       });
     } else {
+      RowMax best[TN / 4];
+      if constexpr (RB) {
+#pragma unroll
+        for (int q = 0; q < TN / 4; ++q) best[q].start();
+      }
       float res[TN][4];
       static_for<TN>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
@@ -1195,6 +1278,7 @@ __device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], in
             v[r] = ACT == 1 ? fmaxf(t, 0.0f) : (ACT == 2 ? gelu_erf(t, g0, g1, g2) : t);
           }
           if constexpr (kQuantOut) v[r] = static_cast<float>(qd.code(bf16_bits_to_f32(f32_to_bf16_bits(v[r])), qz));
+          if constexpr (RB) best[j / 4].see(stored_value<TO>(v[r]));
         }
         if constexpr (std::is_same<TO, int8_t>::value) {
           uint32_t w = 0u;
@@ -1205,6 +1289,7 @@ __device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], in
           Elem<TO>::store4(row + 16 * j, v);
         }
       });
+      if constexpr (RB) row_max_store(best, lane, mbase + 16 * i, nbase);
     }
   });
 }
@@ -1218,38 +1303,46 @@ __device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int6
   if (mbase + 16 * TM <= p.m && nbase + 16 * TN <= p.n && act <= (GELU ? 2 : 1)) {
     const int mode = p.qmode;
     if constexpr (std::is_same<TO, int32_t>::value) {
-      epilogue_q_interior<TO, TM, TN, 0, 0>(acc, mbase, nbase, lane, outp, resp, bias);
+      epilogue_q_interior<TO, TM, TN, 0, 0, false>(acc, mbase, nbase, lane, outp, resp, bias);
       return;
     } else if constexpr (std::is_same<TO, int8_t>::value) {
       if (mode == 1) {
-        epilogue_q_interior<TO, TM, TN, 1, 0>(acc, mbase, nbase, lane, outp, resp, bias);
+        epilogue_q_interior<TO, TM, TN, 1, 0, false>(acc, mbase, nbase, lane, outp, resp, bias);
         return;
       }
       if (p.act_dtype == C3H_BF16) {
         const bool m3 = mode == 3;
         if (act == 0) {
-          if (m3) epilogue_q_interior<TO, TM, TN, 5, 0>(acc, mbase, nbase, lane, outp, resp, bias);
-          else epilogue_q_interior<TO, TM, TN, 4, 0>(acc, mbase, nbase, lane, outp, resp, bias);
+          if (m3) epilogue_q_interior<TO, TM, TN, 5, 0, false>(acc, mbase, nbase, lane, outp, resp, bias);
+          else epilogue_q_interior<TO, TM, TN, 4, 0, false>(acc, mbase, nbase, lane, outp, resp, bias);
         } else if (act == 1) {
-          if (m3) epilogue_q_interior<TO, TM, TN, 5, 1>(acc, mbase, nbase, lane, outp, resp, bias);
-          else epilogue_q_interior<TO, TM, TN, 4, 1>(acc, mbase, nbase, lane, outp, resp, bias);
+          if (m3) epilogue_q_interior<TO, TM, TN, 5, 1, false>(acc, mbase, nbase, lane, outp, resp, bias);
+          else epilogue_q_interior<TO, TM, TN, 4, 1, false>(acc, mbase, nbase, lane, outp, resp, bias);
         } else if constexpr (GELU) {
-          if (m3) epilogue_q_interior<TO, TM, TN, 5, 2>(acc, mbase, nbase, lane, outp, resp, bias);
-          else epilogue_q_interior<TO, TM, TN, 4, 2>(acc, mbase, nbase, lane, outp, resp, bias);
+          if (m3) epilogue_q_interior<TO, TM, TN, 5, 2, false>(acc, mbase, nbase, lane, outp, resp, bias);
+          else epilogue_q_interior<TO, TM, TN, 4, 2, false>(acc, mbase, nbase, lane, outp, resp, bias);
         }
         return;
       }
     } else {
       const bool m3 = mode == 3;
-      if (act == 0) {
-        if (m3) epilogue_q_interior<TO, TM, TN, 3, 0>(acc, mbase, nbase, lane, outp, resp, bias);
-        else epilogue_q_interior<TO, TM, TN, 2, 0>(acc, mbase, nbase, lane, outp, resp, bias);
+      if (p.epi.row_max != nullptr) {  // host: only with act <= 1
+        if (act == 0) {
+          if (m3) epilogue_q_interior<TO, TM, TN, 3, 0, true>(acc, mbase, nbase, lane, outp, resp, bias);
+          else epilogue_q_interior<TO, TM, TN, 2, 0, true>(acc, mbase, nbase, lane, outp, resp, bias);
+        } else {
+          if (m3) epilogue_q_interior<TO, TM, TN, 3, 1, true>(acc, mbase, nbase, lane, outp, resp, bias);
+          else epilogue_q_interior<TO, TM, TN, 2, 1, true>(acc, mbase, nbase, lane, outp, resp, bias);
+        }
+      } else if (act == 0) {
+        if (m3) epilogue_q_interior<TO, TM, TN, 3, 0, false>(acc, mbase, nbase, lane, outp, resp, bias);
+        else epilogue_q_interior<TO, TM, TN, 2, 0, false>(acc, mbase, nbase, lane, outp, resp, bias);
       } else if (act == 1) {
-        if (m3) epilogue_q_interior<TO, TM, TN, 3, 1>(acc, mbase, nbase, lane, outp, resp, bias);
-        else epilogue_q_interior<TO, TM, TN, 2, 1>(acc, mbase, nbase, lane, outp, resp, bias);
+        if (m3) epilogue_q_interior<TO, TM, TN, 3, 1, false>(acc, mbase, nbase, lane, outp, resp, bias);
+        else epilogue_q_interior<TO, TM, TN, 2, 1, false>(acc, mbase, nbase, lane, outp, resp, bias);
       } else if constexpr (GELU) {
-        if (m3) epilogue_q_interior<TO, TM, TN, 3, 2>(acc, mbase, nbase, lane, outp, resp, bias);
-        else epilogue_q_interior<TO, TM, TN, 2, 2>(acc, mbase, nbase, lane, outp, resp, bias);
+        if (m3) epilogue_q_interior<TO, TM, TN, 3, 2, false>(acc, mbase, nbase, lane, outp, resp, bias);
+        else epilogue_q_interior<TO, TM, TN, 2, 2, false>(acc, mbase, nbase, lane, outp, resp, bias);
       }
       return;
     }
@@ -2201,7 +2294,12 @@ int launch_w4(Problem p, hipStream_t s) {
   return launch_status("gemm_w4a16");
 }
 
-inline int check_epilogue(const c3h_epilogue& e) {
+// row_max_ok: the entry point can compute the row_max side output (it is
+// refused everywhere else).
+inline int check_epilogue(const c3h_epilogue& e, bool row_max_ok = false) {
+  C3H_REQUIRE(row_max_ok || e.row_max == nullptr,
+              "epilogue: row_max is taken only by c3h_gemm (16-bit inputs), c3h_qgemm (modes 2 / 3), "
+              "c3h_gemm_fp8 and c3h_gemm_w4a16");
   C3H_REQUIRE(e.bias_mode >= 0 && e.bias_mode <= 4, "epilogue: bad bias_mode %d", e.bias_mode);
   C3H_REQUIRE(e.bias_mode == 0 || e.bias != nullptr, "epilogue: bias_mode %d needs a bias pointer", e.bias_mode);
   C3H_REQUIRE(e.act >= 0 && e.act <= 2, "epilogue: bad act %d", e.act);
@@ -2218,6 +2316,28 @@ inline int check_epilogue(const c3h_epilogue& e) {
 }
 
 inline bool aligned(const void* ptr, int bytes) { return (reinterpret_cast<uintptr_t>(ptr) & (bytes - 1)) == 0; }
+
+// The row_max side output is computed by the direct (register) epilogues
+// only; these are the conditions under which every kernel the GEMM entry
+// points select takes one (epilogue_is_simple / epilogue_q_direct_ok, and
+// row-major aligned stores).
+inline int check_row_max(const c3h_epilogue& e, int64_t n, int64_t ldo, const void* out, int out_dtype,
+                         int64_t batch) {
+  if (e.row_max == nullptr) return C3H_OK;
+  C3H_REQUIRE(batch == 1, "row_max: batch 1 only");
+  C3H_REQUIRE(out_dtype == C3H_F32 || out_dtype == C3H_BF16 || out_dtype == C3H_F16,
+              "row_max: float outputs (fp32, bf16, fp16) only");
+  const int es = dtype_size(out_dtype);
+  C3H_REQUIRE(ldo % 4 == 0 && aligned(out, 4 * es) && (e.residual == nullptr || aligned(e.residual, 4 * es)),
+              "row_max: needs ldo %% 4 == 0 and 4-element aligned out / residual");
+  C3H_REQUIRE(e.alpha == 1.0f && e.beta == 1.0f && (e.bias_mode == 0 || (e.bias_mode == 2 && aligned(e.bias, 16))) &&
+                  e.act <= 1 && e.n_inst == 0,
+              "row_max: needs alpha = beta = 1, no bias or a 16-byte aligned per-column bias, act <= 1, no program");
+  C3H_REQUIRE(e.row_max_ld >= ceil_div(n, 64) && aligned(e.row_max, 8),
+              "row_max: row_max_ld must be >= ceil(n / 64) = %lld and the buffer 8-byte aligned",
+              static_cast<long long>(ceil_div(n, 64)));
+  return C3H_OK;
+}
 
 
 // ---------------------------------------------------------------- per-type launchers

@@ -635,6 +635,61 @@ __global__ void __launch_bounds__(kBlock) argmax_kernel(c3h_argmax_args a) {
   if (threadIdx.x == 0) a.out[row] = si[0] < a.cols ? si[0] : 0;
 }
 
+// ArgMax finish from a GEMM epilogue's row_max side output (the maximum of
+// each 64-column block, NaN ignored, and a may-hold-NaN flag): one wave per
+// row.  The largest block maximum mx is the row's largest non-NaN value, and
+// the answer is the first column equal to mx -- in the first block whose
+// maximum equals mx, read once (one column per lane) -- unless the row holds
+// a NaN: then the NaN-flagged blocks are read first, in order (a flag can
+// also come from an infinity; such a block holds no NaN and the search moves
+// on).  c3h_argmax's rule: NaN is the maximum, the first column on ties.
+// Every branch and loop below depends only on wave-wide values (ballots).
+__global__ void __launch_bounds__(kBlock) argmax_finish_kernel(c3h_argmax_finish_args a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
+  if (row >= a.rows) return;  // per wave
+  const c3h_block_max* p = a.parts + row * a.ld;
+  float mx = -INFINITY;
+  int flag = 0;
+  for (int64_t j = lane; j < a.n_parts; j += 64) {
+    const c3h_block_max q = p[j];
+    mx = fmaxf(mx, q.max);
+    flag |= q.nan;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    flag |= __shfl_xor(flag, o, 64);
+  }
+  const int64_t base = row * a.in_ld;
+  int64_t ans = -1;
+  if (flag) {
+    for (int64_t j0 = 0; j0 < a.n_parts && ans < 0; j0 += 64) {
+      uint64_t cand = __ballot(j0 + lane < a.n_parts && p[j0 + lane].nan != 0);
+      while (cand != 0 && ans < 0) {
+        const int64_t blk = j0 + __builtin_ctzll(cand);
+        cand &= cand - 1;
+        const int64_t col = blk * 64 + lane;
+        const float x = col < a.cols ? load_as_f32(a.in, a.in_dtype, base + col) : 0.0f;
+        const uint64_t hit = __ballot(x != x);
+        if (hit != 0) ans = blk * 64 + __builtin_ctzll(hit);
+      }
+    }
+  }
+  for (int64_t j0 = 0; j0 < a.n_parts && ans < 0; j0 += 64) {
+    uint64_t cand = __ballot(j0 + lane < a.n_parts && p[j0 + lane].max == mx);
+    while (cand != 0 && ans < 0) {
+      const int64_t blk = j0 + __builtin_ctzll(cand);
+      cand &= cand - 1;
+      const int64_t col = blk * 64 + lane;
+      const float x = col < a.cols ? load_as_f32(a.in, a.in_dtype, base + col) : NAN;
+      const uint64_t hit = __ballot(x == mx);
+      if (hit != 0) ans = blk * 64 + __builtin_ctzll(hit);
+    }
+  }
+  if (lane == 0) a.out[row] = ans < 0 ? 0 : ans;
+}
+
 // ------------------------------------------------------------------ im2col
 __global__ void __launch_bounds__(kBlock) im2col_kernel(c3h_im2col_args a) {
   const int64_t cols = static_cast<int64_t>(a.c) * a.kh * a.kw;
@@ -1261,6 +1316,22 @@ int c3h_argmax(const c3h_argmax_args* a, void* stream) {
   else
     hipLaunchKernelGGL(argmax_kernel<false>, dim3(static_cast<unsigned>(a->rows)), dim3(kBlock), 0, as_stream(stream), *a);
   return launch_status("argmax");
+}
+
+int c3h_argmax_finish(const c3h_argmax_finish_args* a, void* stream) {
+  C3H_REQUIRE(a && a->rows >= 0 && a->cols >= 1 && a->out, "argmax_finish: bad args");
+  if (a->rows == 0) return C3H_OK;
+  C3H_REQUIRE(a->n_parts == ceil_div(a->cols, 64) && a->ld >= a->n_parts && a->in_ld >= a->cols,
+              "argmax_finish: n_parts must be ceil(cols / 64), ld >= n_parts and in_ld >= cols");
+  C3H_REQUIRE(a->parts != nullptr && (reinterpret_cast<uintptr_t>(a->parts) & 7) == 0 && a->in != nullptr,
+              "argmax_finish: parts (8-byte aligned) and in are required");
+  C3H_REQUIRE(a->in_dtype == C3H_F32 || a->in_dtype == C3H_BF16 || a->in_dtype == C3H_F16,
+              "argmax_finish: in must be fp32, bf16 or fp16");
+  const int64_t blocks = ceil_div(a->rows, kBlock / 64);
+  C3H_REQUIRE(blocks <= 2147483647LL, "argmax_finish: too many rows");
+  hipLaunchKernelGGL(argmax_finish_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, as_stream(stream),
+                     *a);
+  return launch_status("argmax_finish");
 }
 
 int c3h_im2col(const c3h_im2col_args* a, void* stream) {

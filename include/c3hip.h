@@ -337,6 +337,36 @@ typedef struct {
 } c3h_argmax_args;
 int c3h_argmax(const c3h_argmax_args* a, void* stream);
 
+/* One 64-column block of a GEMM output row (the epilogue's row_max side
+ * output): the block's largest stored value ignoring NaN, and whether it may
+ * hold a NaN. */
+typedef struct c3h_block_max {
+  float max;
+  int32_t nan;
+} c3h_block_max;
+
+/* ArgMax of the rows of a GEMM output from its row_max side output: out[m] =
+ * c3h_argmax's result for row m of `in` ([rows, cols], row stride in_ld,
+ * in_dtype fp32 / bf16 / fp16, as stored), found from the n_parts =
+ * ceil(cols / 64) block maxima of the row (row stride ld) and a read of
+ * only the blocks that can hold the answer: those equal to the row's
+ * maximum, or, when a block may hold a NaN, the NaN-flagged ones in order
+ * (NaN is the maximum; first index on ties).  No counterpart in the
+ * reference, whose ArgMax reads the logits (c35/standard_runner.py:409). */
+typedef struct {
+  const c3h_block_max* parts;
+  const void* in;
+  int64_t* out;
+  int64_t rows;
+  int64_t cols;
+  int64_t n_parts;
+  int64_t ld;
+  int64_t in_ld;
+  int32_t in_dtype;
+  int32_t pad_;
+} c3h_argmax_finish_args;
+int c3h_argmax_finish(const c3h_argmax_finish_args* a, void* stream);
+
 /* im2col with the reference's ordering: rows (n, ho, wo), columns (c, kh, kw),
  * zero padding (kernel_registry.py:399-453).  Input NCHW. */
 typedef struct {
@@ -412,6 +442,18 @@ int c3h_maxpool2d(const c3h_pool_args* a, void* stream);
  *                                   1 = the previous instruction's result
  *                                   (x before the first), 2 + j = imm[j];
  *                                   the last result is the output)
+ * Side output (row_max != NULL): for every output row m and every 64-column
+ * block b, row_max[m * row_max_ld + b] = {the largest of the block's values
+ * as stored, ignoring NaN (-inf if there is none); nan != 0 if the block may
+ * hold a NaN (it does, or it holds an infinity)} -- what c3h_argmax_finish
+ * completes an ArgMax of the rows from, reading only the few blocks that
+ * can hold the answer.  It lets a GEMM that produces logits skip re-reading
+ * them for the ArgMax that follows (the harness argmax,
+ * c35/standard_runner.py:409).  Taken by c3h_gemm (16-bit inputs),
+ * c3h_qgemm (modes 2 / 3), c3h_gemm_fp8 and c3h_gemm_w4a16 with batch 1,
+ * a float output (fp32 / bf16 / fp16, row stride a multiple of 4, 4-element
+ * aligned), alpha = beta = 1, bias none or per column, act <= 1 and no
+ * program; refused elsewhere.  row_max_ld >= ceil(n / 64).
  */
 typedef struct {
   const void* bias;      /* fp32 */
@@ -424,6 +466,8 @@ typedef struct {
   int32_t n_inst;
   float imm[8];
   c3h_ew_inst inst[C3H_EW_MAX_INST];
+  struct c3h_block_max* row_max; /* optional side output, see above */
+  int64_t row_max_ld;            /* entries between rows of row_max */
 } c3h_epilogue;
 
 /* General (batched) GEMM: out[b] = epi(op(A[b]) op(B[b])).
@@ -784,7 +828,8 @@ enum c3h_op_kind {
   C3H_OP_GEMM_FP8 = 34,
   C3H_OP_SPLITK = 35,
   C3H_OP_QUANT_MXFP4 = 36,
-  C3H_OP_GEMM_W4A16 = 37
+  C3H_OP_GEMM_W4A16 = 37,
+  C3H_OP_ARGMAX_FINISH = 38
 };
 
 typedef struct {
@@ -818,7 +863,8 @@ int c3h_graph_destroy(void* graph_exec);
  * c3h_gemm_args, c3h_conv_args, c3h_attn_scores_args, c3h_flash_args,
  * c3h_quantize_args, c3h_qgemm_args, c3h_dequantize_args, c3h_op,
  * c3h_pack_args, c3h_conv_pool_args, c3h_fp8_quant_args, c3h_fp8_gemm_args,
- * c3h_splitk_args, c3h_mxfp4_quant_args, c3h_w4a16_gemm_args.
+ * c3h_splitk_args, c3h_mxfp4_quant_args, c3h_w4a16_gemm_args,
+ * c3h_argmax_finish_args.
  * Returns the number of sizes available (host-only; needs no GPU). */
 int32_t c3h_abi_sizes(int64_t* out, int32_t capacity);
 

@@ -148,9 +148,9 @@ def _lower(name, policy):
     ("mlp", "fp32", {"gemm": 3}),
     ("resnet18_cifar", "fp32", {"layout": 1, "conv": 20, "gap": 1, "gemm": 1}),
     ("resnet18_224", "bf16", {"layout": 1, "conv": 20, "maxpool": 1, "gap": 1, "gemm": 1}),
-    ("decoder_fp16", "fp16", {"gather_add": 1, "layernorm": 5, "gemm": 9, "flash": 2, "argmax": 1}),
+    ("decoder_fp16", "fp16", {"gather_add": 1, "layernorm": 5, "gemm": 9, "flash": 2, "argmax_finish": 1}),
     ("decoder_w8a8", "w8a8", {"gather_add": 1, "layernorm_q": 5, "quantize": 2, "qgemm": 9, "flash": 2,
-                              "argmax": 1}),
+                              "argmax_finish": 1}),
 ])
 def test_compiled_lowering_launch_groups(fake_lib, name, policy, expect):
     plan, prog = _lower(name, policy)
