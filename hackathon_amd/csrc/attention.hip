@@ -132,8 +132,15 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
   __shared__ __attribute__((aligned(16))) uint8_t Vt[kD * 128];
 
   const int qtiles = (a.seq_q + kBQ - 1) / kBQ;
-  const int qt = blockIdx.x % qtiles;
-  const int bh = blockIdx.x / qtiles;
+  // Longest first: under the causal mask query tile qt walks qt + 1 key
+  // tiles' worth of work per 64 queries, so the last query tiles of every
+  // (batch, head) are dispatched first and the short ones fill the gaps they
+  // leave (W8A8 decoder layer: 87 -> 55 us against (bh, qt) order).  With
+  // n_bh a multiple of 8 all query tiles of one (batch, head) also land on
+  // one XCD, whose L2 then holds that head's K and V.
+  const int nbh = a.batch * a.heads;
+  const int qt = qtiles - 1 - static_cast<int>(blockIdx.x / nbh);
+  const int bh = blockIdx.x % nbh;
   const int head = bh % a.heads, batch = bh / a.heads;
   // (`wave` is left as a per-lane value: declaring it uniform made the
   // causal checks scalar branches and the kernel measured 17 % slower.)
@@ -271,7 +278,24 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
 #pragma unroll
       for (int u = 0; u < QG; ++u) {
         float tmax = -INFINITY;
-        if (edge) {
+        if (edge && MASK != 2) {
+          // key >= seq_k or (causal) key > q[u]  <=>  key >= lim, taken
+          // relative to this lane's first key so each score costs one
+          // compare against a constant offset.
+          int lim = a.seq_k;
+          if (MASK == 1 && q[u] + 1 < lim) lim = q[u] + 1;
+          lim -= k0 + 4 * g;
+#pragma unroll
+          for (int kt4 = 0; kt4 < 4; ++kt4) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              float sv = s_acc[u][kt4][j];
+              if (16 * kt4 + j >= lim) sv = -INFINITY;
+              s_acc[u][kt4][j] = sv;
+              tmax = fmaxf(tmax, sv);
+            }
+          }
+        } else if (edge) {  // additive mask: every tile
 #pragma unroll
           for (int kt4 = 0; kt4 < 4; ++kt4) {
 #pragma unroll
@@ -279,8 +303,7 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
               const int key = k0 + 16 * kt4 + 4 * g + j;
               float sv = s_acc[u][kt4][j];
               if (key >= a.seq_k) sv = -INFINITY;
-              if (MASK == 1 && key > q[u]) sv = -INFINITY;
-              if (MASK == 2 && q_valid[u] && key < a.seq_k)
+              if (q_valid[u] && key < a.seq_k)
                 sv += mask[static_cast<int64_t>(q[u]) * a.mask_ld + key] * inv_scale;
               s_acc[u][kt4][j] = sv;
               tmax = fmaxf(tmax, sv);
