@@ -247,6 +247,13 @@ struct QuantDiv {
     const float c = fminf(fmaxf(rintf(quotient(x)) + static_cast<float>(zero_point), -128.0f), 127.0f);
     return static_cast<int8_t>(c);
   }
+  // 4 codes packed little-endian into one word.
+  __device__ __forceinline__ uint32_t codes4(const float* x, int zero_point) const {
+    uint32_t w = 0u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w |= (static_cast<uint32_t>(code(x[k], zero_point)) & 0xffu) << (8 * k);
+    return w;
+  }
   // 8 codes packed little-endian into two words.
   __device__ __forceinline__ uint2 codes8(const float* x, int zero_point) const {
     uint32_t w[2] = {0u, 0u};

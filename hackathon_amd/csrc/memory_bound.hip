@@ -410,6 +410,9 @@ struct LnStore {
   static __device__ __forceinline__ void store8(TO* p, const float* y, const QuantDiv&, int) {
     Elem<TO>::store8(p, y);
   }
+  static __device__ __forceinline__ void store4(TO* p, const float* y, const QuantDiv&, int) {
+    Elem<TO>::store4(p, y);
+  }
 };
 template <typename TX>
 struct LnStore<TX, int8_t> {
@@ -419,15 +422,22 @@ struct LnStore<TX, int8_t> {
     for (int e = 0; e < 8; ++e) r[e] = Elem<TX>::to_f32(Elem<TX>::from_f32(y[e]));
     *reinterpret_cast<uint2*>(p) = qd.codes8(r, qz);
   }
+  static __device__ __forceinline__ void store4(int8_t* p, const float* y, const QuantDiv& qd, int qz) {
+    float r[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = Elem<TX>::to_f32(Elem<TX>::from_f32(y[e]));
+    *reinterpret_cast<uint32_t*>(p) = qd.codes4(r, qz);
+  }
 };
 
-template <typename TX, typename TO, int NV, int ROWS>
+template <typename TX, typename TO, int NV, int ROWS, int VW = kLnVec>
 __global__ void __launch_bounds__(kBlock) layernorm_vec_kernel(c3h_layernorm_args a) {
+  static_assert(VW == 8 || VW == 4, "vector width");
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + wave) * ROWS;
   if (row0 >= a.rows) return;
-  const int nvec = static_cast<int>(a.cols / 8);
-  float v[ROWS][NV][8];
+  const int nvec = static_cast<int>(a.cols / VW);
+  float v[ROWS][NV][VW];
 #pragma unroll
   for (int r = 0; r < ROWS; ++r) {
     const int64_t row = row0 + r;
@@ -437,14 +447,16 @@ __global__ void __launch_bounds__(kBlock) layernorm_vec_kernel(c3h_layernorm_arg
     for (int j = 0; j < NV; ++j) {
       const int vi = lane + 64 * j;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[r][j][e] = 0.0f;
+      for (int e = 0; e < VW; ++e) v[r][j][e] = 0.0f;
       if (row < a.rows && vi < nvec) {
-        Elem<TX>::load8(x + vi * 8, v[r][j]);
+        if constexpr (VW == 8) Elem<TX>::load8(x + vi * 8, v[r][j]);
+        else Elem<TX>::load4(x + vi * 4, v[r][j]);
         if (res) {
-          float q[8];
-          Elem<TX>::load8(res + vi * 8, q);
+          float q[VW];
+          if constexpr (VW == 8) Elem<TX>::load8(res + vi * 8, q);
+          else Elem<TX>::load4(res + vi * 4, q);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[r][j][e] += q[e];
+          for (int e = 0; e < VW; ++e) v[r][j][e] += q[e];
         }
       }
     }
@@ -460,14 +472,14 @@ __global__ void __launch_bounds__(kBlock) layernorm_vec_kernel(c3h_layernorm_arg
 #pragma unroll
     for (int j = 0; j < NV; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sum += v[r][j][e];  // out-of-range vectors hold zeros
+      for (int e = 0; e < VW; ++e) sum += v[r][j][e];  // out-of-range vectors hold zeros
     const float mean = wave_sum(sum) / static_cast<float>(a.cols);
     float sq = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       if (lane + 64 * j < nvec) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
+        for (int e = 0; e < VW; ++e) {
           const float d = v[r][j][e] - mean;
           sq += d * d;
         }
@@ -480,16 +492,23 @@ __global__ void __launch_bounds__(kBlock) layernorm_vec_kernel(c3h_layernorm_arg
     for (int j = 0; j < NV; ++j) {
       const int vi = lane + 64 * j;
       if (vi < nvec) {
-        float g[8], y[8];
-        Elem<float>::load8(scale + vi * 8, g);
-        float b[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (bias) Elem<float>::load8(bias + vi * 8, b);
+        float g[VW], y[VW], b[VW];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
+        for (int e = 0; e < VW; ++e) b[e] = 0.0f;
+        if constexpr (VW == 8) {
+          Elem<float>::load8(scale + vi * 8, g);
+          if (bias) Elem<float>::load8(bias + vi * 8, b);
+        } else {
+          Elem<float>::load4(scale + vi * 4, g);
+          if (bias) Elem<float>::load4(bias + vi * 4, b);
+        }
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
           y[e] = (v[r][j][e] - mean) * inv_std * g[e];
           if (bias) y[e] += b[e];
         }
-        LnStore<TX, TO>::store8(out + vi * 8, y, qd, a.out_zero);
+        if constexpr (VW == 8) LnStore<TX, TO>::store8(out + vi * 8, y, qd, a.out_zero);
+        else LnStore<TX, TO>::store4(out + vi * 4, y, qd, a.out_zero);
       }
     }
     if (lane == 0) {
@@ -1058,7 +1077,8 @@ __global__ void __launch_bounds__(kBlock) maxpool_nhwc_vec_kernel(c3h_pool_args 
 
 // Rows per wave: 4 for rows of <= 512 columns, 2 for <= 1024 (measured
 // faster than 4 at 768 columns, where 4 rows keep 64 floats per lane
-// resident), else 1.
+// resident), else 1.  Case 3 is 768 columns as three 4-wide vectors per
+// lane, two rows per wave.
 template <typename TX, typename TO>
 void launch_ln(const c3h_layernorm_args& a, int nv, void* stream) {
   const dim3 b(kBlock);
@@ -1067,6 +1087,7 @@ void launch_ln(const c3h_layernorm_args& a, int nv, void* stream) {
   switch (nv) {
     case 1: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 1, 4>), grid(4), b, 0, st, a); break;
     case 2: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 2, 2>), grid(2), b, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 3, 2, 4>), grid(2), b, 0, st, a); break;
     case 4: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 4, 1>), grid(1), b, 0, st, a); break;
     default: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 8, 1>), grid(1), b, 0, st, a); break;
   }
@@ -1235,7 +1256,9 @@ int c3h_layernorm(const c3h_layernorm_args* a, void* stream) {
               "layernorm: quantized output needs a positive normal out_scale and an int8 zero point");
   if (vec) {
     const int nv = static_cast<int>(ceil_div(a->cols / 8, 64));
-    const int NVsel = nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : 8;
+    // 768 columns: 96 8-wide vectors would leave lanes 32-63 idle for the
+    // second one, so 4-wide vectors, three per lane (launch_ln case 3).
+    const int NVsel = a->cols == 768 ? 3 : nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : 8;
     if (quant) {
       if (a->x_dtype == C3H_F32) launch_ln<float, int8_t>(*a, NVsel, stream);
       else if (a->x_dtype == C3H_BF16) launch_ln<bf16_t, int8_t>(*a, NVsel, stream);
