@@ -156,9 +156,13 @@ def test_conv_nhwc_implicit_gemm(gpu, kind, case):
 
 @pytest.mark.parametrize("kind", ["fp16", "bf16"])
 @pytest.mark.parametrize("mask_kind", [0, 1, 2])
-@pytest.mark.parametrize("b,h,s", [(2, 3, 64), (1, 2, 200), (2, 1, 256)])
+@pytest.mark.parametrize("b,h,s", [(2, 3, 64), (1, 2, 200), (2, 1, 256),
+                                   (3, 5, 520)])  # 5 query tiles, 15 (batch, head) pairs, ragged key tile
 def test_flash_attention(gpu, kind, mask_kind, b, h, s):
-    """softmax(QK^T*scale + mask) V with Q,K,V head-split views of a packed [B,S,3,H,64] buffer."""
+    """softmax(QK^T*scale + mask) V with Q,K,V head-split views of a packed [B,S,3,H,64] buffer.
+    Blocks take the last query tiles of every (batch, head) first; the
+    (3, 5, 520) case has a block count that is no multiple of 8 and several
+    query tiles per head."""
     from hackathon_amd import _lib
     from hackathon_amd.device import DeviceArray
 
