@@ -391,13 +391,12 @@ __global__ void __launch_bounds__(kBlock) layernorm_kernel(c3h_layernorm_args a)
   }
 }
 
-// Vectorized LayerNorm: each wave normalizes ROWS consecutive rows, 8
-// consecutive columns per lane per vector (16-byte loads of 16-bit data), NV
-// vectors per lane per row kept in registers.  Every row's loads are issued
-// before the first reduction, so a wave has ROWS * NV loads in flight (one
-// 1 KB row per wave left HBM latency uncovered: 38-44 % of 8 TB/s at d=512
-// and 768).  Statistics in fp32: mean, then the biased variance of the
-// centred values, as layernorm_kernel.  cols % 8 == 0, cols <= 512 * NV.
+// Vectorized LayerNorm: each wave normalizes ROWS consecutive rows, VW (8
+// or 4) consecutive columns per lane per vector (16- or 8-byte loads of
+// 16-bit data), NV vectors per lane per row kept in registers.  Every row's
+// loads are issued before the first reduction, so a wave has ROWS * NV loads
+// in flight.  Statistics in fp32: mean, then the biased variance of the
+// centred values, as layernorm_kernel.  cols % VW == 0, cols <= 64 * VW * NV.
 //
 // TO = int8_t: the QuantizeLinear that is the LayerNorm's only consumer, in
 // the same pass.  Each output is first rounded to the activation type TX
@@ -1075,19 +1074,20 @@ __global__ void __launch_bounds__(kBlock) maxpool_nhwc_vec_kernel(c3h_pool_args 
   }
 }
 
-// Rows per wave: 4 for rows of <= 512 columns, 2 for <= 1024 (measured
-// faster than 4 at 768 columns, where 4 rows keep 64 floats per lane
-// resident), else 1.  Case 3 is 768 columns as three 4-wide vectors per
-// lane, two rows per wave.
+// Rows per wave: 1, except 2 for the 8-wide form of 513-1024 columns (case
+// 2).  One row per wave measured fastest: 16384 x 512 fp16 9.3 (4 rows) ->
+// 8.1 us, 16384 x 768 bf16 -> int8 14.2 (2 rows) -> 13.0 us; more waves
+// in flight hide the load latency better than more rows per wave.  Case 3
+// is 768 columns as three 4-wide vectors per lane.
 template <typename TX, typename TO>
 void launch_ln(const c3h_layernorm_args& a, int nv, void* stream) {
   const dim3 b(kBlock);
   hipStream_t st = as_stream(stream);
   auto grid = [&](int rows_per_wave) { return dim3(static_cast<unsigned>(ceil_div(a.rows, 4 * rows_per_wave))); };
   switch (nv) {
-    case 1: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 1, 4>), grid(4), b, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 1, 1>), grid(1), b, 0, st, a); break;
     case 2: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 2, 2>), grid(2), b, 0, st, a); break;
-    case 3: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 3, 2, 4>), grid(2), b, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 3, 1, 4>), grid(1), b, 0, st, a); break;
     case 4: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 4, 1>), grid(1), b, 0, st, a); break;
     default: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 8, 1>), grid(1), b, 0, st, a); break;
   }
