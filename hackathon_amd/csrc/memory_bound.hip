@@ -662,6 +662,11 @@ __global__ void __launch_bounds__(kBlock) argmax_kernel(c3h_argmax_args a) {
 // also come from an infinity; such a block holds no NaN and the search moves
 // on).  c3h_argmax's rule: NaN is the maximum, the first column on ties.
 // Every branch and loop below depends only on wave-wide values (ballots).
+// NP > 0: n_parts <= 64 * NP, and lane l keeps blocks l, l + 64, ... in
+// registers: its NP loads are issued together and the parts are read once
+// (a loop with one load per iteration left the load latency exposed per
+// iteration, twice).  NP == 0: any width, the parts are re-read.
+template <int NP>
 __global__ void __launch_bounds__(kBlock) argmax_finish_kernel(c3h_argmax_finish_args a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6);
@@ -669,10 +674,26 @@ __global__ void __launch_bounds__(kBlock) argmax_finish_kernel(c3h_argmax_finish
   const c3h_block_max* p = a.parts + row * a.ld;
   float mx = -INFINITY;
   int flag = 0;
-  for (int64_t j = lane; j < a.n_parts; j += 64) {
-    const c3h_block_max q = p[j];
-    mx = fmaxf(mx, q.max);
-    flag |= q.nan;
+  float pmax[NP > 0 ? NP : 1];
+  uint32_t pnan = 0u;  // bit t: block lane + 64 t may hold a NaN
+  if constexpr (NP > 0) {
+#pragma unroll
+    for (int t = 0; t < NP; ++t) {
+      const int64_t j = lane + 64 * t;
+      c3h_block_max q = {-INFINITY, 0};
+      if (j < a.n_parts) q = p[j];
+      pmax[t] = q.max;
+      pnan |= (q.nan != 0 ? 1u : 0u) << t;
+    }
+#pragma unroll
+    for (int t = 0; t < NP; ++t) mx = fmaxf(mx, pmax[t]);
+    flag = pnan != 0u;
+  } else {
+    for (int64_t j = lane; j < a.n_parts; j += 64) {
+      const c3h_block_max q = p[j];
+      mx = fmaxf(mx, q.max);
+      flag |= q.nan;
+    }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -681,9 +702,24 @@ __global__ void __launch_bounds__(kBlock) argmax_finish_kernel(c3h_argmax_finish
   }
   const int64_t base = row * a.in_ld;
   int64_t ans = -1;
+  // NP > 0: register t holds block 64 t + lane, so candidate round t is j0 = 64 t.
+  auto nan_cand = [&](int64_t j0) -> bool {
+    if constexpr (NP > 0) return j0 + lane < a.n_parts && ((pnan >> (j0 / 64)) & 1u) != 0u;
+    else return j0 + lane < a.n_parts && p[j0 + lane].nan != 0;
+  };
+  auto max_cand = [&](int64_t j0) -> bool {
+    if constexpr (NP > 0) {
+      float v = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < NP; ++t) v = (j0 == 64 * t) ? pmax[t] : v;
+      return j0 + lane < a.n_parts && v == mx;
+    } else {
+      return j0 + lane < a.n_parts && p[j0 + lane].max == mx;
+    }
+  };
   if (flag) {
     for (int64_t j0 = 0; j0 < a.n_parts && ans < 0; j0 += 64) {
-      uint64_t cand = __ballot(j0 + lane < a.n_parts && p[j0 + lane].nan != 0);
+      uint64_t cand = __ballot(nan_cand(j0));
       while (cand != 0 && ans < 0) {
         const int64_t blk = j0 + __builtin_ctzll(cand);
         cand &= cand - 1;
@@ -695,7 +731,7 @@ __global__ void __launch_bounds__(kBlock) argmax_finish_kernel(c3h_argmax_finish
     }
   }
   for (int64_t j0 = 0; j0 < a.n_parts && ans < 0; j0 += 64) {
-    uint64_t cand = __ballot(j0 + lane < a.n_parts && p[j0 + lane].max == mx);
+    uint64_t cand = __ballot(max_cand(j0));
     while (cand != 0 && ans < 0) {
       const int64_t blk = j0 + __builtin_ctzll(cand);
       cand &= cand - 1;
@@ -1352,8 +1388,14 @@ int c3h_argmax_finish(const c3h_argmax_finish_args* a, void* stream) {
               "argmax_finish: in must be fp32, bf16 or fp16");
   const int64_t blocks = ceil_div(a->rows, kBlock / 64);
   C3H_REQUIRE(blocks <= 2147483647LL, "argmax_finish: too many rows");
-  hipLaunchKernelGGL(argmax_finish_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, as_stream(stream),
-                     *a);
+  const dim3 g(static_cast<unsigned>(blocks)), b(kBlock);
+  hipStream_t st = as_stream(stream);
+  const int64_t np = ceil_div(a->n_parts, 64);  // block maxima per lane
+  if (np <= 2) hipLaunchKernelGGL(argmax_finish_kernel<2>, g, b, 0, st, *a);
+  else if (np <= 4) hipLaunchKernelGGL(argmax_finish_kernel<4>, g, b, 0, st, *a);
+  else if (np <= 8) hipLaunchKernelGGL(argmax_finish_kernel<8>, g, b, 0, st, *a);
+  else if (np <= 16) hipLaunchKernelGGL(argmax_finish_kernel<16>, g, b, 0, st, *a);
+  else hipLaunchKernelGGL(argmax_finish_kernel<0>, g, b, 0, st, *a);
   return launch_status("argmax_finish");
 }
 

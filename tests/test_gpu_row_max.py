@@ -120,6 +120,11 @@ def _check(run, m, n, out_kind):
     ("fp16", 1000, 1000, 320, "fp32", 0, False),     # ragged M and N (N % 64 != 0)
     ("fp16", 300, 260, 64, "fp16", 0, False),
     ("fp16", 8192, 8192, 512, "fp32", 0, True),      # the decoder fp16 LM head shape class
+    # wide rows: 192, 625 and 1094 block maxima per row (the finish kernel
+    # keeps up to 4, 16 block maxima per lane in registers, else re-reads)
+    ("fp16", 64, 12288, 64, "fp32", 0, True),
+    ("bf16", 64, 40000, 64, "bf16", 0, True),
+    ("fp16", 32, 70000, 64, "fp32", 0, True),
 ])
 def test_gemm16_row_max(gpu, kind, m, n, k, out_kind, act, bigtile):
     from hackathon_amd import _lib
