@@ -22,6 +22,7 @@ struct Switches {
   bool disable_bigtile = false;  // C3H_DISABLE_BIGTILE: no 256 x 256 tile
   bool disable_buf = false;      // C3H_DISABLE_BUF: no buffer-load GEMM kernel
   bool disable_conv3x3 = false;  // C3H_DISABLE_CONV3X3: no 64-channel band conv
+  bool disable_direct_conv = false;  // C3H_DISABLE_DIRECT_CONV: no direct narrow-input fp32 conv
   int dma_rp = 0;                // C3H_DMA_RP: register-pipelined DMA stages (0 = off)
 };
 const Switches& switches();

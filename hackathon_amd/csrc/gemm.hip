@@ -136,6 +136,8 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
     p.fd_kwpack = make_fastdiv(static_cast<uint32_t>(p.kw_pack));
     p.k = static_cast<int64_t>(a->kh) * a->kw * a->c_pack;
     p.ldb = p.k;
+    const int direct = launch_conv_direct_c4(p, s);  // 4-channel inputs: direct VALU conv
+    if (direct >= 0) return direct;
     return launch_f32_modes(p, 1, s, kConv, true);
   }
   if (a->in_dtype == C3H_BF16 || a->in_dtype == C3H_F16) {

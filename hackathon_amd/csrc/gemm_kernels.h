@@ -2351,6 +2351,7 @@ int launch_i8(Problem p, hipStream_t s, int mode, int out_dtype);  // gemm_i8.hi
 int launch_f8(Problem p, hipStream_t s, int out_dtype);            // gemm_f8.hip
 int launch_w4a16(Problem p, hipStream_t s, int out_dtype);         // gemm_w4.hip
 int launch_f32_modes(Problem p, int64_t batch, hipStream_t s, int am, bool b_kcontig);  // gemm_f32.hip
+int launch_conv_direct_c4(Problem p, hipStream_t s);  // gemm_f32.hip: -1 when not applicable
 
 }  // namespace gk
 }  // namespace c3h

@@ -32,6 +32,7 @@ static Switches read_switches() {
   w.disable_bigtile = getenv("C3H_DISABLE_BIGTILE") != nullptr;
   w.disable_buf = getenv("C3H_DISABLE_BUF") != nullptr;
   w.disable_conv3x3 = getenv("C3H_DISABLE_CONV3X3") != nullptr;
+  w.disable_direct_conv = getenv("C3H_DISABLE_DIRECT_CONV") != nullptr;
   const char* rp = getenv("C3H_DMA_RP");
   w.dma_rp = rp ? atoi(rp) : 0;
   return w;

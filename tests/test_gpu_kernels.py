@@ -154,6 +154,52 @@ def test_conv_nhwc_implicit_gemm(gpu, kind, case):
     np.testing.assert_allclose(got.transpose(0, 3, 1, 2), ref, rtol=tol, atol=tol)
 
 
+@pytest.mark.parametrize("case", [(4, 32, 32, 64, 3, 1, 1, False, 1),    # the CIFAR ResNet's first conv (B = 4)
+                                  (2, 15, 17, 16, 5, 2, 2, True, 0),
+                                  (1, 37, 37, 64, 7, 2, 3, True, 1),     # 50 KB of weights in LDS
+                                  (3, 9, 9, 32, 1, 1, 0, False, 0),
+                                  (2, 11, 13, 256, 3, 2, 1, True, 1)])
+def test_conv_direct_c4_matches_implicit_gemm(gpu, case):
+    """fp32 conv of a 3-channel input (c_pack = c_stride = 4) on the direct VALU
+    kernel: against the implicit-GEMM kernel (C3H_DISABLE_DIRECT_CONV) within
+    fp32 summation-order differences, and against a float64 conv."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import DeviceArray
+
+    n, h, w, o, k, s, p, with_res, act = case
+    rng = np.random.default_rng(sum(case[:7]))
+    x, wt, b, attrs = _conv_case(rng, n, 3, h, w, o, k, k, s, p)
+    ho, wo = (h + 2 * p - k) // s + 1, (w + 2 * p - k) // s + 1
+    xd = E.to_nhwc(_dev(x), 4, out_dtype=np.float32)
+    wp = E.pack_conv_weight(_dev(wt), 4, k, k * k * 4, out_dtype=np.float32)
+    b_dev = _dev(b)
+    resid = rng.standard_normal((n, ho, wo, o), dtype=np.float32)
+    res_dev = _dev(resid) if with_res else None
+
+    def run():
+        out = DeviceArray.empty((n, ho, wo, o), np.float32)
+        a = _lib.ConvArgs()
+        a.x, a.w, a.out = xd.ptr, wp.ptr, out.ptr
+        a.n, a.c, a.h, a.w_, a.c_stride, a.c_pack, a.o = n, 3, h, w, 4, 4, o
+        a.kh, a.kw, a.sh, a.sw, a.pad_top, a.pad_left, a.dh, a.dw, a.ho, a.wo = k, k, s, s, p, p, 1, 1, ho, wo
+        a.out_layout, a.in_dtype, a.out_dtype = 1, _lib.F32, _lib.F32
+        a.epi = E.epilogue(bias=b_dev, bias_mode=2, act=act, residual=res_dev)
+        print(f"conv direct c4 case={case}", flush=True)
+        _lib.launch(a, None)
+        return out.get()
+
+    got = run()
+    gemm = switches.with_switch("C3H_DISABLE_DIRECT_CONV", "1", run)
+    np.testing.assert_allclose(got, gemm, rtol=1e-5, atol=1e-5)
+    ref = R.conv2d(x.astype(np.float64), wt.astype(np.float64), attrs) + b.reshape(1, o, 1, 1)
+    if with_res:
+        ref = ref + resid.transpose(0, 3, 1, 2)
+    if act == 1:
+        ref = np.maximum(ref, 0)
+    np.testing.assert_allclose(got.transpose(0, 3, 1, 2), ref, rtol=1e-4, atol=1e-4)
+
+
 @pytest.mark.parametrize("kind", ["fp16", "bf16"])
 @pytest.mark.parametrize("mask_kind", [0, 1, 2])
 @pytest.mark.parametrize("b,h,s", [(2, 3, 64), (1, 2, 200), (2, 1, 256),
