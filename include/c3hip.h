@@ -106,7 +106,8 @@ int c3h_device_props(int device, c3h_props* out);
 const char* c3h_last_error(void);
 int c3h_device_synchronize(void);
 /* Re-reads the kernel-selection switches (C3H_DISABLE_DMA, C3H_DISABLE_BIGTILE,
- * C3H_DISABLE_BUF, C3H_DISABLE_CONV3X3, C3H_DMA_RP) from the environment.
+ * C3H_DISABLE_BUF, C3H_DISABLE_CONV3X3, C3H_DISABLE_DIRECT_CONV, C3H_DMA_RP)
+ * from the environment.
  * They are read once, at the first launch, otherwise; call this between
  * launches after changing them, never while another thread launches.  No
  * counterpart in the reference (its kernel choice has no switches). */
@@ -504,7 +505,9 @@ int c3h_gemm(const c3h_gemm_args* a, void* stream);
  * NHWC output, width <= 78 and a bias / residual / ReLU epilogue run on a
  * spatially tiled kernel whose results are bit-identical to the
  * implicit-GEMM path (the environment variable C3H_DISABLE_CONV3X3 selects
- * the latter). */
+ * the latter).  fp32 convs with c_pack = c_stride = 4, NHWC output and
+ * o = 16, 32, 64, 128 or 256 run on a direct kernel (VALU FMAs in K order;
+ * C3H_DISABLE_DIRECT_CONV selects the implicit GEMM). */
 typedef struct {
   const void* x;
   const void* w;
