@@ -2142,15 +2142,12 @@ inline bool dma_eligible(const Problem& p, int64_t batch, int am) {
          p.a_bytes < (int64_t{1} << 31) && p.b_bytes < (int64_t{1} << 31);
 }
 
-// Whether the 256 x 256 eight-wave DMA kernel beats 128 x 128 at two blocks
-// per CU: rounds of resident tiles, a 256-tile round costing 1.66 rounds of
-// 128-tiles (measured: 8192^3 GEMM, 1195 vs 994 us), and an epilogue that
-// epilogue_direct(_q) handles (host-side restatement of epilogue_is_simple;
-// plus GELU for int8, which the large-tile instantiation computes in
-// registers).
-// int8 GEMMs writing int32 / int8 (qmode 0 / 1) need only aligned row-major
-// stores (epilogue_q_direct_ok).
-inline bool big_tile_wins(const Problem& p, int cus, size_t out_size, bool int_mma) {
+// Whether an eight-wave (one block per CU) DMA tile can take this GEMM: an
+// epilogue that epilogue_direct(_q) handles (host-side restatement of
+// epilogue_is_simple; plus GELU for int8, which the large-tile instantiation
+// computes in registers).  int8 GEMMs writing int32 / int8 (qmode 0 / 1)
+// need only aligned row-major stores (epilogue_q_direct_ok).
+inline bool big_tile_ok(const Problem& p, size_t out_size, bool int_mma) {
   if (switches().disable_bigtile || p.n <= 128) return false;
   const c3h_epilogue& e = p.epi;
   const uintptr_t al = 4 * out_size - 1;
@@ -2161,11 +2158,35 @@ inline bool big_tile_wins(const Problem& p, int cus, size_t out_size, bool int_m
                       e.act <= max_act && e.n_inst == 0 &&
                       (e.bias_mode == 0 || (reinterpret_cast<uintptr_t>(e.bias) & 15) == 0) &&
                       (reinterpret_cast<uintptr_t>(e.residual) & al) == 0;
-  if (!(int_mma && p.qmode <= 1 ? stores : simple)) return false;
-  const int64_t t128 = ceil_div(p.m, 128) * ceil_div(p.n, 128), t256 = ceil_div(p.m, 256) * ceil_div(p.n, 256);
-  const double r128 = static_cast<double>(ceil_div(t128, 2 * cus));
-  const double r256 = static_cast<double>(ceil_div(t256, cus)) * 1.66;
-  return r256 < 0.9 * r128;  // a clear margin: near-ties measured slower (16384x2304x768 int8)
+  return int_mma && p.qmode <= 1 ? stores : simple;
+}
+
+// Tile cost in rounds of resident tiles, in units of a round of 128 x 128
+// tiles at two blocks per CU: a 256 x 256 round costs 1.66 (measured: 8192^3
+// GEMM, 1195 vs 994 us) and a 256 x 192 round 1.48 (0.89 of a 256 x 256
+// round: int8 16384x768x3072, 45.6 vs 51.2 us).
+inline double rounds_128(const Problem& p, int cus) {
+  return static_cast<double>(ceil_div(ceil_div(p.m, 128) * ceil_div(p.n, 128), 2 * cus));
+}
+inline double rounds_256(const Problem& p, int cus) {
+  return static_cast<double>(ceil_div(ceil_div(p.m, 256) * ceil_div(p.n, 256), cus)) * 1.66;
+}
+
+// Whether the 256 x 256 eight-wave DMA kernel beats 128 x 128 at two blocks
+// per CU by a clear margin (near-ties measured slower: 16384x2304x768 int8).
+inline bool big_tile_wins(const Problem& p, int cus, size_t out_size, bool int_mma) {
+  if (!big_tile_ok(p, out_size, int_mma)) return false;
+  return rounds_256(p, cus) < 0.9 * rounds_128(p, cus);
+}
+
+// Whether the 256 x 192 eight-wave kernel (N a multiple of 192) beats both:
+// the W8A8 QKV (N = 2304: 3 full rounds instead of 2.25 rounds of 256 x 256
+// or 4.5 of 128 x 128) and the N = 768 GEMMs (256 tiles fill the 256 CUs; 192
+// tiles of 256 x 256 leave a quarter idle).
+inline bool tile192_wins(const Problem& p, int cus, size_t out_size, bool int_mma) {
+  if (p.n % 192 != 0 || !big_tile_ok(p, out_size, int_mma)) return false;
+  const double r192 = static_cast<double>(ceil_div(ceil_div(p.m, 256) * (p.n / 192), cus)) * 1.48;
+  return r192 < rounds_256(p, cus) && r192 < rounds_128(p, cus);
 }
 
 // Register-pipelined form of the 4-wave DMA kernel: C3H_DMA_RP = 2, 3 or 4
@@ -2184,6 +2205,15 @@ template <typename Mma, typename TO, int AM>
 int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
   dim3 grid;
   if constexpr (AM == kDenseK || AM == kConvTap) {
+    // 256 x 192: int8 GEMMs with bf16 output only (the W8A8 decoder's QKV,
+    // out projection and FFN2); the same K order as the other tiles.
+    if constexpr (AM == kDenseK && Mma::kInt && std::is_same<TO, bf16_t>::value) {
+      if (dma_eligible(p, batch, AM) && tile192_wins(p, device_cus(), sizeof(TO), Mma::kInt)) {
+        grid_of<256, 192>(p, 1, grid);
+        hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 192, 8, 1, AM, 2, 8>), grid, dim3(512), 0, s, p);
+        return launch_status(what);
+      }
+    }
     if (dma_eligible(p, batch, AM) && big_tile_wins(p, device_cus(), sizeof(TO), Mma::kInt)) {
       grid_of<256, 256>(p, 1, grid);
       hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 256, 4, 2, AM, 2, 8>), grid, dim3(512), 0, s, p);

@@ -695,7 +695,7 @@ def test_layernorm_vec_against_float64(gpu, rows, cols, res, bias, dt):
 
 
 def _bigtile_pair(launch):
-    """Run `launch` with the 256x256 eight-wave kernel allowed, then with it disabled."""
+    """Run `launch` with the eight-wave kernels (256x256, 256x192) allowed, then with them disabled."""
     a = _with_env("C3H_DISABLE_BIGTILE", None, launch)
     b = _with_env("C3H_DISABLE_BIGTILE", "1", launch)
     return a, b
@@ -839,20 +839,25 @@ def test_conv_big_tile_matches_128_tiles(gpu):
         np.testing.assert_allclose(got[b_, y, x_], want, rtol=1e-2, atol=4e-2)
 
 
-@pytest.mark.parametrize("mode,act", [(0, 0), (2, 0), (3, 2)])
-def test_qgemm_big_tile_matches_128_tiles(gpu, mode, act):
-    """int8 GEMM 4096x4096x256 on the 256x256 kernel: int32 accumulators
-    (mode 0) equal the exact integer product; the dequantized bf16 output with
-    bias + residual (mode 2), and requantize -> dequantize + bias + GELU (mode
-    3, computed in registers there and through the staged epilogue by the
+@pytest.mark.parametrize("m,n,k,mode,act", [
+    (4096, 4096, 256, 0, 0), (4096, 4096, 256, 2, 0), (4096, 4096, 256, 3, 2),
+    # N a multiple of 192 with bf16 output: the 256x192 kernel
+    (16384, 768, 768, 2, 0),      # the W8A8 out projection (bias + residual)
+    (4096, 2304, 256, 3, 2),      # QKV-shaped, GELU in registers
+    (16000, 768, 256, 3, 0),      # ragged M (16000 = 62.5 tiles): edge tiles
+])
+def test_qgemm_big_tile_matches_128_tiles(gpu, m, n, k, mode, act):
+    """int8 GEMM on the eight-wave kernels (256x256; 256x192 where N is a
+    multiple of 192 and the output bf16): int32 accumulators (mode 0) equal
+    the exact integer product; the dequantized bf16 output with bias +
+    residual (mode 2), and requantize -> dequantize + bias + GELU (mode 3,
+    computed in registers there and through the staged epilogue by the
     128x128 kernel) are bit-identical to the 128x128 kernel."""
     from hackathon_amd import _lib
     from hackathon_amd.c35 import engine as E
     from hackathon_amd.device import BF16, DeviceArray
 
-    rng = np.random.default_rng(13 + mode)
-    m = n = 4096
-    k = 256
+    rng = np.random.default_rng(13 + mode + n)
     a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
     bt = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
     sb = (rng.random(n) * 0.01 + 0.001).astype(np.float32)
