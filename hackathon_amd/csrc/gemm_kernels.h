@@ -2205,9 +2205,11 @@ template <typename Mma, typename TO, int AM>
 int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
   dim3 grid;
   if constexpr (AM == kDenseK || AM == kConvTap) {
-    // 256 x 192: int8 GEMMs with bf16 output only (the W8A8 decoder's QKV,
-    // out projection and FFN2); the same K order as the other tiles.
-    if constexpr (AM == kDenseK && Mma::kInt && std::is_same<TO, bf16_t>::value) {
+    // 256 x 192: int8 GEMMs with bf16 output (the W8A8 decoder's QKV, out
+    // projection and FFN2) and fp16 GEMMs with fp16 output (the fp16
+    // decoder's QKV); the same K order as the other tiles.
+    if constexpr (AM == kDenseK && ((Mma::kInt && std::is_same<TO, bf16_t>::value) ||
+                                    (std::is_same<Mma, MmaF16>::value && std::is_same<TO, f16_t>::value))) {
       if (dma_eligible(p, batch, AM) && tile192_wins(p, device_cus(), sizeof(TO), Mma::kInt)) {
         grid_of<256, 192>(p, 1, grid);
         hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 192, 8, 1, AM, 2, 8>), grid, dim3(512), 0, s, p);

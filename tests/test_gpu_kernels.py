@@ -701,20 +701,23 @@ def _bigtile_pair(launch):
     return a, b
 
 
-@pytest.mark.parametrize("kind,out_kind,act", [("bf16", "bf16", 1), ("fp16", "fp32", 1), ("fp16", "fp16", 2)])
-def test_gemm_big_tile_matches_128_tiles(gpu, kind, out_kind, act):
-    """4096x4096x192 (enough tiles that the 256x256 eight-wave kernel is
-    chosen) with bias + residual + ReLU or GELU (computed in registers there,
-    through the staged epilogue by the 128x128 kernel): bit-identical to the
-    128x128 kernel (same K order per output and the same epilogue arithmetic)
-    and within the 16-bit GEMM tolerance of float64 on sampled rows."""
+@pytest.mark.parametrize("kind,out_kind,act,m,n,k", [
+    ("bf16", "bf16", 1, 4096, 4096, 192), ("fp16", "fp32", 1, 4096, 4096, 192), ("fp16", "fp16", 2, 4096, 4096, 192),
+    ("fp16", "fp16", 1, 16384, 1536, 512),   # the fp16 decoder's QKV: the 256x192 kernel
+    ("fp16", "fp16", 2, 8192, 1536, 256),    # 256x192 with GELU in registers
+])
+def test_gemm_big_tile_matches_128_tiles(gpu, kind, out_kind, act, m, n, k):
+    """Shapes with enough tiles that an eight-wave kernel is chosen (256x256;
+    256x192 for fp16 output with N a multiple of 192), with bias + residual +
+    ReLU or GELU (computed in registers there, through the staged epilogue by
+    the 128x128 kernel): bit-identical to the 128x128 kernel (same K order
+    per output and the same epilogue arithmetic) and within the 16-bit GEMM
+    tolerance of float64 on sampled rows."""
     from hackathon_amd import _lib
     from hackathon_amd.c35 import engine as E
     from hackathon_amd.device import BF16, DeviceArray
 
-    rng = np.random.default_rng(11)
-    m = n = 4096
-    k = 192
+    rng = np.random.default_rng(11 + n)
     a32 = (rng.standard_normal((m, k)) * 0.5).astype(np.float32)
     b32 = (rng.standard_normal((n, k)) * 0.5).astype(np.float32)
     ab, av = _bits(a32, kind)
