@@ -384,6 +384,143 @@ def _traffic_summary(fetch_dir: str, write_dir: str, meta_path: str) -> int:
     return 0
 
 
+def _profile_path(workload: str, label: str) -> Path:
+    return ROOT / "profiles" / f"{workload}_{label}.md"
+
+
+def _profile_run(meta_path: str, workload: str = HEADLINE, kinds: str = "", reps: int = 10) -> int:
+    """The dispatch stream a `rocprofv3 --kernel-trace --stats` run summarizes.
+
+    The workload's program runs once (realistic buffer contents), then its
+    launches of `kinds` (default: the dominant family) are timed exactly as
+    the bench line's roofline times them: a hipGraph of just those launches,
+    in program order on one stream (so concurrently paired launches run
+    serialized), replayed `reps` times between HIP events after one untimed
+    replay.  Those replays are the run's last dispatches; the HIP-event time
+    and each launch's shape go to `meta_path` for --profile-summary."""
+    from hackathon_amd.device import init, synchronize
+
+    init(0)
+    m, plan, prog = _prepare(workload)
+    kind_list = [k for k in kinds.split(",") if k] or DOMINANT[workload][0]
+    label = "conv" if kind_list == DOMINANT[HEADLINE][0] and workload == HEADLINE else \
+        ("dominant" if kind_list == DOMINANT[workload][0] else "_".join(kind_list))
+    idx = prog.launches_of(kind_list)
+    if not idx:
+        raise ValueError(f"{workload} has no launches of kinds {kind_list}")
+    prog.run(m.inputs)
+    k_ms = prog.time_subset(idx, reps=reps)
+    synchronize()
+    flops, nbytes = prog.work(idx)
+    dtype = DOMINANT[workload][1]
+    meta = {"workload": workload, "label": label, "kinds": kind_list, "reps": reps, "event_ms": k_ms,
+            "peak": PEAK[dtype], "dtype": dtype, "flops": flops, "bytes": nbytes,
+            "launches": [{k: prog.launch_meta[i].get(k) for k in ("kind", "flops", "bytes", "node", "info")}
+                         for i in idx]}
+    with open(meta_path, "w") as f:
+        json.dump(meta, f, indent=1)
+    _log(f"profile run: {workload} {kind_list}: {len(idx)} launches, {k_ms:.4f} ms per pass (HIP events, "
+         f"{reps} replays) = {flops / (k_ms * 1e-3) / 1e12:.1f} TFLOP/s, meta -> {meta_path}")
+    return 0
+
+
+def _trace_rows(run_dir: str):
+    """(kernel name, duration in us) per dispatch, in dispatch order, from a rocprofv3 csv directory."""
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(run_dir, "**", "*kernel_trace.csv"), recursive=True))
+    if not files:
+        raise FileNotFoundError(f"no *kernel_trace.csv under {run_dir}")
+    rows = []
+    for path in files:
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                key = int(r.get("Dispatch_Id") or r.get("Correlation_Id") or 0)
+                rows.append((key, int(r["Start_Timestamp"]), r["Kernel_Name"],
+                             (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    rows.sort()
+    return [(k, d) for _, _, k, d in rows]
+
+
+def _profile_summary(trace_dir: str, meta_path: str, pmc_dir: str = "") -> int:
+    """Per-launch rocprof durations of the --profile-run replays -> profiles/<workload>_<label>.md."""
+    import numpy as np
+
+    with open(meta_path) as f:
+        meta = json.load(f)
+    launches, reps = meta["launches"], meta["reps"]
+    nl = len(launches)
+    rows = _trace_rows(trace_dir)
+    if len(rows) < nl * reps:
+        raise ValueError(f"{len(rows)} dispatches in the trace, need {nl * reps} for the timed replays")
+    sub = rows[-nl * reps:]
+    names = [k for k, _ in sub[:nl]]
+    for r in range(reps):
+        if [k for k, _ in sub[r * nl:(r + 1) * nl]] != names:
+            raise ValueError("the timed replays do not repeat one dispatch sequence")
+    us = np.asarray([d for _, d in sub]).reshape(reps, nl).mean(axis=0)
+    busy = None
+    if pmc_dir:
+        import csv
+        import glob
+        import collections
+
+        d = collections.defaultdict(dict)
+        for path in sorted(glob.glob(os.path.join(pmc_dir, "**", "*counter_collection.csv"), recursive=True)):
+            with open(path) as f:
+                for r in csv.DictReader(f):
+                    d[int(r["Dispatch_Id"])][r["Counter_Name"]] = float(r["Counter_Value"])
+        ids = sorted(d)[-nl * reps:]
+        mb = np.asarray([d[i].get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for i in ids]).reshape(reps, nl).sum(axis=0)
+        cu = np.asarray([d[i].get("SQ_BUSY_CU_CYCLES", 0.0) for i in ids]).reshape(reps, nl).sum(axis=0)
+        busy = mb / np.maximum(cu, 1.0)
+    peak, unit = meta["peak"], "TFLOP/s"
+    wl, label = meta["workload"], meta["label"]
+    kinds = ",".join(meta["kinds"])
+    fl = np.asarray([l["flops"] for l in launches], float)
+    total_us = float(us.sum())
+    frac_table = fl.sum() / (total_us * 1e-6) / 1e12 / peak
+    frac_event = fl.sum() / (meta["event_ms"] * 1e-3) / 1e12 / peak
+    dest = _profile_path(wl, label)
+    lines = [
+        f"# {wl}: per-launch rocprof durations of the {kinds} launches", "",
+        "The launches bench.py's roofline times, replayed as the bench replays them (one hipGraph of just these",
+        "launches, program order, one stream), under the kernel tracer. Commands (repository root, MI355X box):", "",
+        "```",
+        f"cd /tmp && export TMPDIR=/tmp   # then, from the repository root:",
+        f"timeout -s KILL 300 rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_{label} -o run -- \\",
+        f"    python3 bench.py --profile-run gpurun_out/prof_{label}_meta.json --workload {wl} --kinds {kinds}",
+    ]
+    if pmc_dir:
+        lines += [f"timeout -s KILL 120 rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES --output-format csv \\",
+                  f"    -d gpurun_out/prof_{label}_pmc -o run -- python3 bench.py --profile-run \\",
+                  f"    gpurun_out/prof_{label}_pmc_meta.json --workload {wl} --kinds {kinds}"]
+    lines += [f"python3 bench.py --profile-summary gpurun_out/prof_{label} gpurun_out/prof_{label}_meta.json"
+              + (f" gpurun_out/prof_{label}_pmc" if pmc_dir else ""), "```", "",
+              f"Each row is the mean over {reps} timed replays. Peak: {peak:.0f} {unit} ({meta['dtype']} dense MFMA).", ""]
+    head = "| launch | node | shape | kernel | us | GFLOP | TFLOP/s | % of peak |" + (" MFMA busy |" if busy is not None else "")
+    lines += [head, "|---:|---|---|---|---:|---:|---:|---:|" + ("---:|" if busy is not None else "")]
+    for i, l in enumerate(launches):
+        kname = names[i].split("(")[0].replace("void c3h::gk::", "").replace("void c3h::", "")[:70]
+        t = fl[i] / (us[i] * 1e-6) / 1e12 if us[i] > 0 else 0.0
+        row = (f"| {i} | {l.get('node') or ''} | {l.get('info') or ''} | `{kname}` | {us[i]:.1f} | "
+               f"{fl[i] / 1e9:.1f} | {t:.0f} | {100 * t / peak:.1f} |")
+        if busy is not None:
+            row += f" {100 * busy[i]:.1f} |"
+        lines.append(row)
+    lines += ["", f"Sum of per-launch durations: {total_us:.1f} us for {fl.sum() / 1e9:.2f} GFLOP = "
+              f"{fl.sum() / (total_us * 1e-6) / 1e12:.0f} {unit}, {100 * frac_table:.1f} % of peak.",
+              f"HIP events around the same replays (the bench line's kernel_ms_per_step): {meta['event_ms'] * 1e3:.1f} us "
+              f"= {100 * frac_event:.1f} % of peak; rocprof sum / event time = {total_us / (meta['event_ms'] * 1e3):.3f}.",
+              "", f"rocprof_us_per_pass = {total_us:.1f}", f"event_us_per_pass = {meta['event_ms'] * 1e3:.1f}",
+              f"source_commit = {_source_commit()}", ""]
+    dest.write_text("\n".join(lines))
+    _log(f"wrote {dest}: {total_us:.1f} us per pass ({100 * frac_table:.1f} % of peak; events "
+         f"{meta['event_ms'] * 1e3:.1f} us)")
+    return 0
+
+
 def _committed_traffic():
     """(HBM bytes per dominant launch, source note) from the committed pmc summary, or (None, None)."""
     import re
@@ -413,15 +550,24 @@ def main() -> int:
     ap.add_argument("--kinds", default="", help="launch kinds of --traffic-run (default: the dominant family)")
     ap.add_argument("--traffic-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "META_JSON"),
                     help="turn the two pmc passes into the committed traffic summary (no GPU)")
+    ap.add_argument("--profile-run", metavar="META_JSON",
+                    help="dispatch stream for rocprofv3 --kernel-trace: a family's launches replayed as the roofline "
+                         "times them")
+    ap.add_argument("--profile-summary", nargs="+", metavar="DIR",
+                    help="TRACE_DIR META_JSON [PMC_DIR]: per-launch table -> profiles/ (no GPU)")
     args = ap.parse_args()
     if args.traffic_summary:
         return _traffic_summary(*args.traffic_summary)
+    if args.profile_summary:
+        return _profile_summary(*args.profile_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
               "Run with --gpus 1.", file=sys.stderr)
         return 2
     if args.traffic_run:
         return _traffic_run(args.traffic_run, args.workload, args.kinds)
+    if args.profile_run:
+        return _profile_run(args.profile_run, args.workload, args.kinds)
     from hackathon_amd.device import device_props, init
 
     init(0)

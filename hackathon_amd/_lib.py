@@ -105,7 +105,8 @@ class BnFoldArgs(C.Structure):
 class GatherArgs(C.Structure):
     _fields_ = [("data", vp), ("indices", vp), ("out", vp), ("error_flag", vp), ("outer", i64),
                 ("axis_dim", i64), ("inner", i64), ("n_indices", i64), ("elem_bytes", i32),
-                ("dtype", i32), ("addend", vp), ("addend_rows", i64)]
+                ("dtype", i32), ("addend", vp), ("addend_rows", i64), ("addend_dtype", i32),
+                ("pad_", i32)]
 
 
 class ArgmaxArgs(C.Structure):

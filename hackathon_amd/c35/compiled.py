@@ -56,6 +56,19 @@ _POLICY_ACT = {"fp32": np.dtype(np.float32), "bf16": BF16, "fp16": np.dtype(np.f
                "fp8": np.dtype(np.float16), "fp4": np.dtype(np.float16)}
 _MM_CODE = {"fp32": _lib.F32, "bf16": _lib.BF16, "fp16": _lib.F16, "w8a8": _lib.BF16, "fp8": _lib.F16,
             "fp4": _lib.F16}
+# c3h_layernorm's vector path (the only one with an int8 output): 8-wide
+# vectors, at most 8 per lane of one wave (memory_bound.hip: 512 * kLnVec).
+LN_QUANT_MAX_COLS = 4096
+
+
+def quant_scale_ok(scale: float) -> bool:
+    """The C side's quant_scale_ok: the scale, as the fp32 the launch receives,
+    is a positive normal number (2^-126 <= s <= FLT_MAX)."""
+    with np.errstate(over="ignore"):
+        s = np.float32(scale)
+    return bool(np.isfinite(s) and s >= np.float32(2.0 ** -126))
+
+
 _DTYPE_NAME = {np.dtype(np.float32): "fp32", np.dtype(np.float16): "fp16", BF16: "bf16", np.dtype(np.int8): "int8",
                np.dtype(np.int32): "int32", np.dtype(np.int64): "int64", np.dtype(np.uint8): "u8"}
 
@@ -281,13 +294,14 @@ class CompiledPlan:
         raise KeyError(f"compiled plan: value '{name}' is not available")
 
     def _emit(self, kind: str, build, reads: Sequence[Val] = (), writes: Sequence[Val] = (),
-              flops: float = 0.0, skip_bytes: Sequence[Val] = (), extra_bytes: int = 0) -> None:
+              flops: float = 0.0, skip_bytes: Sequence[Val] = (), extra_bytes: int = 0, info: str = "") -> None:
         """Append one launch; records buffer lifetimes and algorithmic work.
 
         `bytes` is the launch's algorithmic HBM traffic: every operand read
         once and every output written once (logical sizes, no padding).  A
         read the launch touches only partly (a gathered table) is named in
-        `skip_bytes` and its touched bytes given as `extra_bytes`.
+        `skip_bytes` and its touched bytes given as `extra_bytes`.  `info`
+        describes the launch's shape for per-launch reports.
         """
         idx = len(self.launches)
         seen = set()
@@ -307,7 +321,8 @@ class CompiledPlan:
         self.launch_rw.append(([v.buf for v in reads if v is not None and v.buf is not None],
                                [v.buf for v in writes if v is not None and v.buf is not None]))
         self.node_kinds.append(kind)
-        self.launch_meta.append({"kind": kind, "flops": float(flops), "bytes": int(nbytes)})
+        self.launch_meta.append({"kind": kind, "flops": float(flops), "bytes": int(nbytes),
+                                 "node": getattr(self, "_cur_node", None), "info": info})
 
     def _ptr(self, v: Val, resolve) -> int:
         return resolve(v.buf) + v.offset * v.dtype.itemsize
@@ -371,7 +386,9 @@ class CompiledPlan:
             handler = getattr(self, f"_op_{node.op_type}", None)
             if handler is None:
                 raise NotImplementedError(f"compiled engine has no lowering for {node.op_type} (node {nid})")
+            self._cur_node = nid
             handler(node)
+        self._cur_node = None
         self.outputs: Dict[str, Val] = {}
         for t in self.graph.outputs:
             v = self.vals[t.name]
@@ -1104,7 +1121,8 @@ class CompiledPlan:
             g.trans_a, g.trans_b, g.in_dtype, g.out_dtype = 0, 1, mm, dtype_code(out.dtype)
             self._fill_epi(g.epi, st, r, alpha, beta, bmode)
             return g
-        self._emit(f"gemm:{node.op_type}", build, [a2, w] + self._epi_reads(st), [out], flops=2.0 * m * n * k)
+        self._emit(f"gemm:{node.op_type}", build, [a2, w] + self._epi_reads(st), [out], flops=2.0 * m * n * k,
+                   info=f"M={m} N={n} K={k}")
         if mm != _lib.F32:
             self._note_row_max_site(st, out, m, n, alpha, beta, bmode)
         self.vals[st.final] = out
@@ -1142,7 +1160,8 @@ class CompiledPlan:
             g.trans_a, g.trans_b, g.in_dtype, g.out_dtype = 0, 1, in_code, _lib.F32
             g.epi.alpha, g.epi.beta = 1.0, 1.0
             return g
-        self._emit(f"gemm:{node.op_type}", gbuild, [a2, w], [part], flops=2.0 * m * n * k)
+        self._emit(f"gemm:{node.op_type}", gbuild, [a2, w], [part], flops=2.0 * m * n * k,
+                   info=f"M={m} N={n} K={k} in {splits} K splits")
 
         def rbuild(r, part=part, out=out, st=st):
             g = _lib.SplitKArgs()
@@ -1278,7 +1297,8 @@ class CompiledPlan:
             self._fill_epi(a.epi, st, r)
             return a
         self._emit("conv", build, [xin, wv] + self._epi_reads(st), [out],
-                   flops=2.0 * n * ho * wo * o * cin * kh * kw)
+                   flops=2.0 * n * ho * wo * o * cin * kh * kw,
+                   info=f"{kh}x{kw}/{sh} {cin}->{o} {ho}x{wo}: M={n * ho * wo} N={o} K={cin * kh * kw}")
         self.vals[st.final] = out
 
     def _stem_pool(self, node, x: Val, wv: Val, bias_name, act, cin, o, kh, kw, sh, sw, dh, dw, pads, ho, wo,
@@ -1324,7 +1344,9 @@ class CompiledPlan:
             a.relu, a.in_dtype, a.mm_dtype = int(act == 1), dtype_code(x.dtype), self.mm_code
             return a
         self._emit("conv:stem_pool", build, [x, wv] + ([bias] if bias is not None else []), [out],
-                   flops=2.0 * n * ho * wo * o * cin * kh * kw)
+                   flops=2.0 * n * ho * wo * o * cin * kh * kw,
+                   info=f"{kh}x{kw}/{sh} {cin}->{o} {ho}x{wo} + pool -> {po}x{qo}: M={n * ho * wo} N={o} "
+                        f"K={cin * kh * kw}")
         self.consumed.add(pool.id)
         if relu_node is not None:
             self.consumed.add(relu_node.id)
@@ -1406,7 +1428,7 @@ class CompiledPlan:
         eps = float(node.attributes.get("epsilon", 1e-5))
         # A QuantizeLinear that is the LayerNorm's only consumer runs in the same
         # launch (W8A8): int8 codes of the activation-type LayerNorm output.
-        quant = self._fusable_quantize(node.outputs[0], cols)
+        quant = self._fusable_quantize(node.outputs[0], cols, max_cols=LN_QUANT_MAX_COLS)
         ln_dtype = self._out_dtype(node.outputs[0])
         if quant is not None and ln_dtype != x.dtype:
             quant = None
@@ -1430,19 +1452,26 @@ class CompiledPlan:
         else:
             self.vals[node.outputs[0]] = out
 
-    def _fusable_quantize(self, tensor: str, cols: int):
+    def _fusable_quantize(self, tensor: str, cols: int, max_cols: Optional[int] = None):
         """(QuantizeLinear node, scale, zero point) when `tensor`'s only consumer
         is a QuantizeLinear with a constant scalar scale and zero point that
-        the fused LayerNorm can apply (not a graph output), else None."""
+        the producing launch can apply (not a graph output), else None.
+
+        Mirrors the C entry points' preconditions, so a fused form that
+        compiles also launches: cols % 8 == 0 (and cols <= max_cols for the
+        LayerNorm form, c3h_layernorm's vector path), a positive normal fp32
+        scale (quant_scale_ok: 2^-126 <= scale <= FLT_MAX) and an int8 zero
+        point.  Anything else keeps the unfused pair."""
         q = self._single_consumer(tensor)
         if q is None or q.op_type != "QuantizeLinear" or q.id in self.consumed or self._is_output(tensor) or \
-                cols % 8 or q.inputs[0] != tensor:
+                cols % 8 or q.inputs[0] != tensor or (max_cols is not None and cols > max_cols):
             return None
         scale = self._scalar_const(q.inputs[1])
-        zero = int(self._scalar_const(q.inputs[2])) if len(q.inputs) > 2 and q.inputs[2] else 0
-        if scale is None or not scale > 0 or not -128 <= zero <= 127:
+        zero = self._scalar_const(q.inputs[2]) if len(q.inputs) > 2 and q.inputs[2] else 0
+        if scale is None or not quant_scale_ok(scale) or zero is None or zero != int(zero) or \
+                not -128 <= int(zero) <= 127:
             return None
-        return q, scale, zero
+        return q, float(np.float32(scale)), int(zero)
 
     def _op_FusedLayerNormalization(self, node):
         self._layernorm(node, self._get(node.inputs[0]), None, node.inputs[1],
@@ -1501,6 +1530,7 @@ class CompiledPlan:
             a.outer, a.axis_dim, a.inner, a.n_indices, a.elem_bytes = outer, adim, inner, idx.size, data.dtype.itemsize
             if addend is not None:
                 a.dtype, a.addend, a.addend_rows = dtype_code(out.dtype), self._ptr(addend, r), addend.size // inner
+                a.addend_dtype = dtype_code(addend.dtype)
             return a
         self._emit("gather_add" if addend is not None else "gather", build,
                    [data, idx] + ([addend] if addend is not None else []), [out],
@@ -1516,8 +1546,10 @@ class CompiledPlan:
 
         The table [rows, inner] must broadcast against [*idx.shape, inner] as
         trailing dims (rows = the product of idx's last dims), the gathered
-        data must be 2-D (outer = 1), and the result is stored in the
-        activation type after one fp32 add, as the unfused Add would round it."""
+        data must be 2-D (outer = 1).  The table is read in fp32, as the
+        unfused Add reads it, and the gathered (stored-type) row plus the
+        table is rounded once to the activation type: bit for bit the
+        unfused Gather then Add."""
         add = self._single_consumer(node.outputs[0])
         if add is None or add.op_type != "Add" or add.id in self.consumed or axis != 0 or len(data.shape) != 2:
             return None, None
@@ -1536,7 +1568,7 @@ class CompiledPlan:
         if data.dtype != od or od not in (np.dtype(np.float32), BF16, np.dtype(np.float16)) or inner % 8 or \
                 w.dtype != np.float32:
             return None, None
-        return add, self._weight_val(others[0], od)
+        return add, self._weight_val(others[0], np.float32)
 
     def _error_flag(self) -> DeviceArray:
         """A device int32 that kernels set to 1 on an invalid index (sticky until read)."""
@@ -1736,6 +1768,12 @@ class CompiledPlan:
         x = x if x.dense else self._dense(x)
         scale = self._scalar_const(node.inputs[1])
         zero = int(self._scalar_const(node.inputs[2])) if len(node.inputs) > 2 and node.inputs[2] else 0
+        # c3h_quantize's precondition, checked here so the plan fails when it
+        # is compiled rather than at its first launch
+        if scale is None:
+            raise NotImplementedError(f"QuantizeLinear '{node.id}': the compiled engine needs a constant scalar scale")
+        if not quant_scale_ok(scale):
+            raise ValueError(f"QuantizeLinear '{node.id}': scale {scale!r} is not a positive normal fp32 number")
         out = self._new(x.shape, np.int8)
 
         def build(r, x=x, out=out):
@@ -1823,7 +1861,8 @@ class CompiledPlan:
                 g.act_dtype, g.q_scale, g.q_zero = quant
             self._fill_epi(g.epi, st, r)
             return g
-        self._emit("qgemm", build, [a, bt, sbv] + self._epi_reads(st), [out], flops=2.0 * m * n * k)
+        self._emit("qgemm", build, [a, bt, sbv] + self._epi_reads(st), [out], flops=2.0 * m * n * k,
+                   info=f"M={m} N={n} K={k}")
 
     def _op_DequantizeLinear(self, node):
         q = self._get(node.inputs[0])

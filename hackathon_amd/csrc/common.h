@@ -24,6 +24,7 @@ struct Switches {
   bool disable_conv3x3 = false;  // C3H_DISABLE_CONV3X3: no 64-channel band conv
   bool disable_direct_conv = false;  // C3H_DISABLE_DIRECT_CONV: no direct narrow-input fp32 conv
   int dma_rp = 0;                // C3H_DMA_RP: register-pipelined DMA stages (0 = off)
+  bool disable_pp = false;       // C3H_DISABLE_PP: no ping-pong schedule for 256 x 256 conv tiles
 };
 const Switches& switches();
 

@@ -136,8 +136,9 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream) {
     p.fd_kwpack = make_fastdiv(static_cast<uint32_t>(p.kw_pack));
     p.k = static_cast<int64_t>(a->kh) * a->kw * a->c_pack;
     p.ldb = p.k;
-    const int direct = launch_conv_direct_c4(p, s);  // 4-channel inputs: direct VALU conv
-    if (direct >= 0) return direct;
+    bool handled = false;
+    rc = launch_conv_direct_c4(p, s, &handled);  // 4-channel inputs: direct VALU conv
+    if (handled) return rc;
     return launch_f32_modes(p, 1, s, kConv, true);
   }
   if (a->in_dtype == C3H_BF16 || a->in_dtype == C3H_F16) {
@@ -241,10 +242,6 @@ int gemm_splitk_into(const c3h_gemm_args* a, int32_t splits, float* partial, hip
 }
 
 }  // namespace
-
-extern "C" {
-
-}  // extern "C"
 
 // ---------------------------------------------------------------------
 // Static split-K scratch for c3h_gemm_splitk_noalloc: fp32 partials live in

@@ -75,17 +75,21 @@ __global__ void __launch_bounds__(256) conv_direct_c4_kernel(Problem p) {
   }
 }
 
-int launch_conv_direct_c4(Problem p, hipStream_t s) {
+// *handled = false (return 0) when the direct kernel does not apply; else
+// the launch's status (0 or a negative C3H_ error).
+int launch_conv_direct_c4(Problem p, hipStream_t s, bool* handled) {
+  *handled = false;
   const int64_t k = static_cast<int64_t>(p.kh) * p.kw * 4;
   const size_t smem = static_cast<size_t>(p.n * k) * sizeof(float);
   const auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
   if (switches().disable_direct_conv || p.c_pack != 4 || p.c_stride != 4 || p.out_nchw || p.ldo != p.n ||
       p.ldb < k || smem > 64 * 1024 || !al16(p.a) || !al16(p.out) || (p.epi.residual && !al16(p.epi.residual)))
-    return -1;
+    return 0;
   const int tpp = static_cast<int>(p.n / 16);
-  if (p.n % 16 != 0 || (tpp != 1 && tpp != 2 && tpp != 4 && tpp != 8 && tpp != 16)) return -1;
+  if (p.n % 16 != 0 || (tpp != 1 && tpp != 2 && tpp != 4 && tpp != 8 && tpp != 16)) return 0;
   const int64_t blocks = ceil_div(p.m, 256 / tpp);
-  if (blocks > 2147483647LL) return -1;
+  if (blocks > 2147483647LL) return 0;
+  *handled = true;
   const dim3 g(static_cast<unsigned>(blocks)), b(256);
   switch (tpp) {
     case 1: hipLaunchKernelGGL(conv_direct_c4_kernel<1>, g, b, smem, s, p); break;

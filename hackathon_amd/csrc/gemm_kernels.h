@@ -1791,7 +1791,15 @@ __device__ __forceinline__ void wait_vmcnt_groups(int64_t n) {
 // the first, and all S stages hold tiles in flight (DMA lead S - 1 tiles).
 // The K order and every accumulation are those of the RP = false kernel, so
 // the two are bit-identical.
-template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, int S, int NW = 4, bool RP = false>
+//
+// PP (ping-pong, eight waves, two stages): waves 0-3 (group A, one per SIMD)
+// and 4-7 (group B, one per SIMD) alternate between a memory phase (issue
+// this wave's DMA share of the next K tile, read its operand fragments of the
+// current one) and an MFMA phase, offset by one workgroup barrier, so on
+// every SIMD one wave multiplies while the other loads.  Same K order and
+// accumulation as the other forms: bit-identical results.
+template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, int S, int NW = 4, bool RP = false,
+          bool PP = false>
 __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
   constexpr bool DIRECT = NW > 4;
   // GELU in registers (epilogue_direct) for 16-bit outputs as well: with the
@@ -1910,7 +1918,64 @@ __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
 
   const int64_t ktiles = ceil_div(p.k, BK);
   const int lrow = lane & 15, lchunk = lane >> 4;
-  if constexpr (RP) {
+  if constexpr (PP) {
+    static_assert(NW == 8 && S == 2 && !RP, "ping-pong: eight waves, two stages");
+    // Barrier pairing.  A executes P, then (X_t, Y_t) per K tile t; B executes
+    // P, E, then (X_t, Y_t) without the last Y.  So A's MFMA phase t (between
+    // X_t and Y_t) runs beside B's memory phase t, and A's memory phase t + 1
+    // beside B's MFMA phase t.  Tile t + 1 is issued in both groups' memory
+    // phase t and complete before A's Y_t / B's X_t (the same barrier), after
+    // which A reads it; its stage last held tile t - 1, whose reads ended
+    // before the barrier that opens each group's memory phase t.
+    const bool grp_b = wave >= 4;  // wave-uniform (readfirstlane): scalar branches
+    auto barrier = [] {
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    };
+    issue(0, 0);
+    wait_vmcnt<0>();
+    barrier();          // P: tile 0 in LDS
+    if (grp_b) barrier();  // E: B runs one phase behind A
+    constexpr int KS = 8 / Mma::kStep;
+    for (int64_t kt = 0; kt < ktiles; ++kt) {
+      // memory phase: this wave's share of tile kt + 1, then tile kt's fragments
+      if (kt + 1 < ktiles) issue(kt + 1, static_cast<int>((kt + 1) & 1));
+      const uint8_t* As = smem + (kt & 1) * STAGE;
+      const uint8_t* Bs = As + BM * RB;
+      vec av[KS][TM], bv[KS][TN];
+#pragma unroll
+      for (int q = 0; q < KS; ++q) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int r = wm * WTM + i * 16 + lrow;
+          av[q][i] = read_operand<Mma>(As + r * RB, r, q * Mma::kStep, lchunk);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int r = wn * WTN + j * 16 + lrow;
+          bv[q][j] = read_operand<Mma>(Bs + r * RB, r, q * Mma::kStep, lchunk);
+        }
+      }
+      // fragments in registers (no read of this stage outlives the barrier);
+      // B's share of tile kt + 1 landed before the barrier A reads it after
+      wait_lgkmcnt0();
+      if (grp_b) wait_vmcnt<0>();
+      __builtin_amdgcn_sched_barrier(0);
+      barrier();  // X_kt
+      if constexpr (kPrio) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int q = 0; q < KS; ++q)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = Mma::mma(bv[q][j], av[q][i], acc[i][j]);
+      if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (!grp_b) wait_vmcnt<0>();  // A's share of tile kt + 1 (issued a phase earlier)
+      if (!grp_b || kt + 1 < ktiles) barrier();  // Y_kt
+    }
+  } else if constexpr (RP) {
     static_assert(LPW * (S - 1) < 64, "vmcnt range");
     constexpr int KS = 8 / Mma::kStep;
     constexpr int N_MFMA = KS * TM * TN;
@@ -2218,6 +2283,16 @@ int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
     }
     if (dma_eligible(p, batch, AM) && big_tile_wins(p, device_cus(), sizeof(TO), Mma::kInt)) {
       grid_of<256, 256>(p, 1, grid);
+      // Convolutions take the ping-pong schedule (layer-3 3x3 convs of
+      // ResNet-18 224: 75 -> 71 us); dense GEMMs measured equal or slower
+      // with it (their K loops are 6-32 tiles; the LM head 246 -> 260 us).
+      if constexpr (AM == kConvTap) {
+        if (!switches().disable_pp) {
+          hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 256, 4, 2, AM, 2, 8, false, true>), grid, dim3(512),
+                             0, s, p);
+          return launch_status(what);
+        }
+      }
       hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 256, 4, 2, AM, 2, 8>), grid, dim3(512), 0, s, p);
       return launch_status(what);
     }
@@ -2383,7 +2458,7 @@ int launch_i8(Problem p, hipStream_t s, int mode, int out_dtype);  // gemm_i8.hi
 int launch_f8(Problem p, hipStream_t s, int out_dtype);            // gemm_f8.hip
 int launch_w4a16(Problem p, hipStream_t s, int out_dtype);         // gemm_w4.hip
 int launch_f32_modes(Problem p, int64_t batch, hipStream_t s, int am, bool b_kcontig);  // gemm_f32.hip
-int launch_conv_direct_c4(Problem p, hipStream_t s);  // gemm_f32.hip: -1 when not applicable
+int launch_conv_direct_c4(Problem p, hipStream_t s, bool* handled);  // gemm_f32.hip
 
 }  // namespace gk
 }  // namespace c3h

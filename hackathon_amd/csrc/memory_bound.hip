@@ -572,15 +572,16 @@ __global__ void __launch_bounds__(kBlock) gather_kernel(c3h_gather_args a, int64
 
 // Gather with a fused per-row addend (token + positional embedding): one
 // thread per 8 elements of a row, 16-byte (16-bit) or 32-byte (fp32) loads
-// of the gathered row and the addend row, fp32 add, one rounding, one vector
-// store.  Consecutive threads take consecutive chunks of a row, so loads and
-// stores are coalesced; the index is read once per chunk from L1.
-template <typename T>
+// of the gathered row and the addend row (TA: fp32, or the data type), fp32
+// add, one rounding, one vector store.  Consecutive threads take consecutive
+// chunks of a row, so loads and stores are coalesced; the index is read once
+// per chunk from L1.
+template <typename T, typename TA>
 __global__ void __launch_bounds__(kBlock) gather_add_kernel(c3h_gather_args a, int64_t row_vecs) {
   const int64_t total = a.n_indices * row_vecs;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   const T* data = static_cast<const T*>(a.data);
-  const T* add = static_cast<const T*>(a.addend);
+  const TA* add = static_cast<const TA*>(a.addend);
   T* out = static_cast<T*>(a.out);
   for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
     const int64_t r = t / row_vecs;
@@ -596,7 +597,7 @@ __global__ void __launch_bounds__(kBlock) gather_add_kernel(c3h_gather_args a, i
       continue;
     }
     Elem<T>::load8(data + idx * a.inner + c, v);
-    Elem<T>::load8(add + (r % a.addend_rows) * a.inner + c, w);
+    Elem<TA>::load8(add + (r % a.addend_rows) * a.inner + c, w);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] += w[e];
     Elem<T>::store8(out + r * a.inner + c, v);
@@ -1338,17 +1339,24 @@ int c3h_gather(const c3h_gather_args* a, void* stream) {
     C3H_REQUIRE((a->dtype == C3H_F32 && a->elem_bytes == 4) ||
                     ((a->dtype == C3H_BF16 || a->dtype == C3H_F16) && a->elem_bytes == 2),
                 "gather: a fused addend needs dtype F32, BF16 or F16 matching elem_bytes");
-    C3H_REQUIRE((reinterpret_cast<uintptr_t>(a->data) | reinterpret_cast<uintptr_t>(a->out) |
-                 reinterpret_cast<uintptr_t>(a->addend)) % vec_bytes == 0,
+    C3H_REQUIRE(a->addend_dtype == C3H_F32 || a->addend_dtype == a->dtype,
+                "gather: the addend must be F32 or of the data dtype");
+    const bool add32 = a->addend_dtype == C3H_F32;
+    C3H_REQUIRE((reinterpret_cast<uintptr_t>(a->data) | reinterpret_cast<uintptr_t>(a->out)) % vec_bytes == 0 &&
+                    reinterpret_cast<uintptr_t>(a->addend) % (add32 ? 32 : vec_bytes) == 0,
                 "gather: a fused addend needs vector-aligned data, addend and out");
     const int64_t rv = a->inner / 8;
     const dim3 grid(grid_for(total_rows * rv));
     if (a->dtype == C3H_F32)
-      hipLaunchKernelGGL(gather_add_kernel<float>, grid, dim3(kBlock), 0, s, *a, rv);
+      hipLaunchKernelGGL((gather_add_kernel<float, float>), grid, dim3(kBlock), 0, s, *a, rv);
+    else if (a->dtype == C3H_BF16 && add32)
+      hipLaunchKernelGGL((gather_add_kernel<bf16_t, float>), grid, dim3(kBlock), 0, s, *a, rv);
     else if (a->dtype == C3H_BF16)
-      hipLaunchKernelGGL(gather_add_kernel<bf16_t>, grid, dim3(kBlock), 0, s, *a, rv);
+      hipLaunchKernelGGL((gather_add_kernel<bf16_t, bf16_t>), grid, dim3(kBlock), 0, s, *a, rv);
+    else if (add32)
+      hipLaunchKernelGGL((gather_add_kernel<f16_t, float>), grid, dim3(kBlock), 0, s, *a, rv);
     else
-      hipLaunchKernelGGL(gather_add_kernel<f16_t>, grid, dim3(kBlock), 0, s, *a, rv);
+      hipLaunchKernelGGL((gather_add_kernel<f16_t, f16_t>), grid, dim3(kBlock), 0, s, *a, rv);
     return launch_status("gather");
   }
   bool aligned16 = (reinterpret_cast<uintptr_t>(a->data) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 15) == 0;

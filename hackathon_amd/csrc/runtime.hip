@@ -35,6 +35,7 @@ static Switches read_switches() {
   w.disable_direct_conv = getenv("C3H_DISABLE_DIRECT_CONV") != nullptr;
   const char* rp = getenv("C3H_DMA_RP");
   w.dma_rp = rp ? atoi(rp) : 0;
+  w.disable_pp = getenv("C3H_DISABLE_PP") != nullptr;
   return w;
 }
 

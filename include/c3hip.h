@@ -307,9 +307,11 @@ int c3h_bn_fold(const c3h_bnfold_args* a, void* stream);
  * Optional fused addend (the decoder's token + positional embedding, the
  * Gather -> Add pair of c35/engine.py:462-481 and :226-244, in one pass):
  * when `addend` is non-NULL, outer must be 1 and `dtype` (F32, BF16 or F16)
- * names the element type of data, out and addend; output row r is
- * data[idx[r]] + addend[r % addend_rows], added in fp32 and rounded once to
- * `dtype`.  `addend` is [addend_rows, inner]. */
+ * names the element type of data and out; `addend_dtype` that of the addend,
+ * either F32 or `dtype`.  Output row r is data[idx[r]] + addend[r %
+ * addend_rows], added in fp32 and rounded once to `dtype` -- with an F32
+ * addend, exactly what a 16-bit Gather followed by an Add of the fp32 table
+ * stores.  `addend` is [addend_rows, inner]. */
 typedef struct {
   const void* data;
   const int64_t* indices;
@@ -323,6 +325,8 @@ typedef struct {
   int32_t dtype;
   const void* addend;
   int64_t addend_rows;
+  int32_t addend_dtype;
+  int32_t pad_;
 } c3h_gather_args;
 int c3h_gather(const c3h_gather_args* a, void* stream);
 

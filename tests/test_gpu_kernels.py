@@ -503,7 +503,8 @@ def test_quantize_every_code_boundary_bit_exact(gpu, kind, zero):
 
 @pytest.mark.parametrize("kind", ["bf16", "fp16"])
 @pytest.mark.parametrize("n,h,w,relu,in_kind", [(2, 64, 64, 1, "fp32"), (3, 70, 57, 1, "fp32"), (1, 45, 83, 0, "fp32"),
-                                                (2, 38, 40, 1, "same")])
+                                                (2, 38, 40, 1, "same"), (2, 224, 224, 1, "fp32"),
+                                                (1, 100, 60, 0, "same"), (1, 61, 92, 1, "fp32")])
 def test_conv_stem_pool_matches_unfused_chain(gpu, kind, n, h, w, relu, in_kind):
     """c3h_conv_stem_pool == layout -> c3h_conv2d (bias, relu) -> c3h_maxpool2d, bit for bit;
     and within 16-bit rounding of a float64 conv + max pool of the rounded operands."""
@@ -804,42 +805,55 @@ def test_gemm_gelu_epilogue_matches_the_chain(gpu):
     assert got[np.isposinf(x)][0] == np.inf
 
 
-def test_conv_big_tile_matches_128_tiles(gpu):
-    """The ResNet layer-3 conv (256 x 14 x 14 x 256, 3x3) takes the 256x256
-    kernel; bit-identical to the 128x128 one, and a float64 spot check."""
+@pytest.mark.parametrize("n,c,h,w,o,stride,resid", [
+    # (each case is large enough for the host to pick the 256x256 tile: its
+    # rounds of resident tiles beat 128x128's by 10 %)
+    (256, 256, 14, 14, 256, 1, False),   # ResNet-18 224 layer 3 (36 K tiles)
+    (200, 256, 14, 14, 256, 1, True),    # ragged M (153.1 tiles of 256 rows), residual
+    (200, 128, 28, 28, 256, 2, False),   # a stride-2 downsampling 3x3 (18 K tiles)
+    (500, 512, 7, 7, 384, 1, True),      # N = 1.5 tiles, 72 K tiles, ragged M
+])
+def test_conv_big_tile_matches_128_tiles(gpu, n, c, h, w, o, stride, resid):
+    """3x3 convs with N > 128 take the 256x256 kernel with the ping-pong
+    schedule; bit-identical to the same tile without it (C3H_DISABLE_PP) and
+    to the 128x128 kernel, and a float64 spot check."""
     from hackathon_amd import _lib
     from hackathon_amd.c35 import engine as E
     from hackathon_amd.device import BF16, DeviceArray
 
-    rng = np.random.default_rng(12)
-    n, c, h, w, o = 256, 256, 14, 14, 256
+    rng = np.random.default_rng(12 + n + o)
+    ho, wo = (h + 2 - 3) // stride + 1, (w + 2 - 3) // stride + 1
     x32 = rng.standard_normal((n, h, w, c)).astype(np.float32)
     w32 = (rng.standard_normal((o, 3, 3, c)) * 0.05).astype(np.float32)
     xb, xv = _bits(x32, "bf16")
     wb, wv = _bits(w32.reshape(o, -1), "bf16")
+    rb, rv = _bits(rng.standard_normal((n, ho, wo, o)).astype(np.float32), "bf16")
     bias = rng.standard_normal(o).astype(np.float32)
-    xd, wd, bd = _dev(xb), _dev(wb), _dev(bias)
-    out = DeviceArray.empty((n, h, w, o), BF16)
+    xd, wd, bd, rd = _dev(xb), _dev(wb), _dev(bias), _dev(rb)
+    out = DeviceArray.empty((n, ho, wo, o), BF16)
 
     def launch():
         a = _lib.ConvArgs()
         a.x, a.w, a.out = xd.ptr, wd.ptr, out.ptr
         a.n, a.c, a.h, a.w_, a.c_stride, a.c_pack, a.o = n, c, h, w, c, c, o
-        a.kh, a.kw, a.sh, a.sw, a.pad_top, a.pad_left, a.dh, a.dw, a.ho, a.wo = 3, 3, 1, 1, 1, 1, 1, 1, h, w
+        a.kh, a.kw, a.sh, a.sw, a.pad_top, a.pad_left, a.dh, a.dw, a.ho, a.wo = 3, 3, stride, stride, 1, 1, 1, 1, ho, wo
         a.out_layout, a.in_dtype, a.out_dtype = 1, _lib.BF16, _lib.BF16
-        a.epi = E.epilogue(bias=bd, bias_mode=2, act=1)
-        print("conv 256x14x14x256 3x3 bf16", flush=True)
+        a.epi = E.epilogue(bias=bd, bias_mode=2, act=1, residual=rd if resid else None)
+        print(f"conv n={n} {c}->{o} {h}x{w}/{stride} resid={resid} 3x3 bf16", flush=True)
+        out.copy_from_host(np.zeros((n, ho, wo, o), np.uint16))
         _lib.launch(a, None)
         return out.get().copy()
     big, small = _bigtile_pair(launch)
+    plain = _with_env("C3H_DISABLE_PP", "1", launch)
     np.testing.assert_array_equal(big.view(np.uint16), small.view(np.uint16))
+    np.testing.assert_array_equal(big.view(np.uint16), plain.view(np.uint16))
     got = _from16(big, "bf16")
     xp = np.pad(xv.astype(np.float64), ((0, 0), (1, 1), (1, 1), (0, 0)))
     wv4 = wv.astype(np.float64).reshape(o, 3, 3, c)
-    for (b_, y, x_) in [(0, 0, 0), (7, 5, 13), (255, 13, 6), (100, 7, 7)]:
-        patch = xp[b_, y:y + 3, x_:x_ + 3, :]
-        want = np.maximum(np.einsum("hwc,ohwc->o", patch, wv4) + bias, 0)
-        np.testing.assert_allclose(got[b_, y, x_], want, rtol=1e-2, atol=4e-2)
+    for (b_, y, x_) in [(0, 0, 0), (n // 3, ho // 2, wo - 1), (n - 1, ho - 1, wo // 2), (n // 2, ho // 2, ho // 2)]:
+        patch = xp[b_, stride * y:stride * y + 3, stride * x_:stride * x_ + 3, :]
+        want = np.einsum("hwc,ohwc->o", patch, wv4) + bias + (rv[b_, y, x_] if resid else 0.0)
+        np.testing.assert_allclose(got[b_, y, x_], np.maximum(want, 0), rtol=1e-2, atol=4e-2)
 
 
 @pytest.mark.parametrize("m,n,k,mode,act", [
@@ -1128,13 +1142,17 @@ def test_flash_attention_config5_shape(gpu, kind, mask_kind):
           f"{float(np.abs(got[b - 1, :, h - 1] - full).max()):.3e}", flush=True)
 
 
-@pytest.mark.parametrize("kind", ["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("kind,addend", [("fp32", "fp32"), ("bf16", "bf16"), ("fp16", "fp16"), ("bf16", "fp32"),
+                                          ("fp16", "fp32")])
 @pytest.mark.parametrize("n_idx,rows,inner", [(64 * 256, 256, 512), (16 * 1024, 1024, 768), (37, 5, 8)])
-def test_gather_fused_addend_bit_exact(gpu, kind, n_idx, rows, inner):
+def test_gather_fused_addend_bit_exact(gpu, kind, addend, n_idx, rows, inner):
     """c3h_gather with an addend: out[r] = data[idx[r]] + addend[r % rows],
     fp32 add of the stored values and one rounding -- what Gather followed by
     the broadcast Add gives -- including negative indices; the decoder
-    embedding shapes of configs 4 and 5 and a ragged small case."""
+    embedding shapes of configs 4 and 5 and a ragged small case.  With an
+    fp32 addend and 16-bit data (the compiled decoders' form) the table is
+    not rounded before the add: the unfused 16-bit Gather then the Add of the
+    fp32 table, bit for bit."""
     from hackathon_amd import _lib
     from hackathon_amd.device import DeviceArray
 
@@ -1144,10 +1162,14 @@ def test_gather_fused_addend_bit_exact(gpu, kind, n_idx, rows, inner):
     pos = rng.standard_normal((rows, inner)).astype(np.float32)
     idx = rng.integers(-vocab, vocab, size=n_idx).astype(np.int64)
     if kind == "fp32":
-        t_st, t_val, p_st, p_val, code = table, table, pos, pos, _lib.F32
+        t_st, t_val, code = table, table, _lib.F32
     else:
-        (t_st, t_val), (p_st, p_val) = _bits(table, kind), _bits(pos, kind)
+        t_st, t_val = _bits(table, kind)
         code = _lib.BF16 if kind == "bf16" else _lib.F16
+    if addend == "fp32":
+        p_st, p_val, acode = pos, pos, _lib.F32
+    else:
+        (p_st, p_val), acode = _bits(pos, addend), code
     want = t_val[idx] + p_val[np.arange(n_idx) % rows]
     want = want if kind == "fp32" else G.round_to(want, kind)
     td, pd, idd = _dev(t_st), _dev(p_st), _dev(idx)
@@ -1156,11 +1178,15 @@ def test_gather_fused_addend_bit_exact(gpu, kind, n_idx, rows, inner):
     a = _lib.GatherArgs()
     a.data, a.indices, a.out, a.error_flag = td.ptr, idd.ptr, out.ptr, flag.ptr
     a.outer, a.axis_dim, a.inner, a.n_indices, a.elem_bytes = 1, vocab, inner, n_idx, t_st.itemsize
-    a.dtype, a.addend, a.addend_rows = code, pd.ptr, rows
+    a.dtype, a.addend, a.addend_rows, a.addend_dtype = code, pd.ptr, rows, acode
     _lib.launch(a, None)
     got = out.get() if kind == "fp32" else _from16(out.get(), kind)
     np.testing.assert_array_equal(got, want)
     assert int(flag.get()[0]) == 0
+    if addend == "fp32" and kind != "fp32":
+        # the table really enters unrounded: rounding it first changes some outputs
+        pre = G.round_to(t_val[idx] + G.round_to(pos, kind)[np.arange(n_idx) % rows], kind)
+        assert n_idx < 100 or not np.array_equal(pre, want)
 
 
 def test_gather_out_of_range_sets_flag_and_zero_rows(gpu):
@@ -1180,7 +1206,7 @@ def test_gather_out_of_range_sets_flag_and_zero_rows(gpu):
         a.data, a.indices, a.out, a.error_flag = td.ptr, idd.ptr, out.ptr, flag.ptr
         a.outer, a.axis_dim, a.inner, a.n_indices, a.elem_bytes = 1, 10, 8, 6, 4
         if fused:
-            a.dtype, a.addend, a.addend_rows = _lib.F32, pos.ptr, 2
+            a.dtype, a.addend, a.addend_rows, a.addend_dtype = _lib.F32, pos.ptr, 2, _lib.F32
         _lib.launch(a, None)
         got = out.get()
         assert int(flag.get()[0]) == 1

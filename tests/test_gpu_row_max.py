@@ -120,6 +120,9 @@ def _check(run, m, n, out_kind):
     ("fp16", 1000, 1000, 320, "fp32", 0, False),     # ragged M and N (N % 64 != 0)
     ("fp16", 300, 260, 64, "fp16", 0, False),
     ("fp16", 8192, 8192, 512, "fp32", 0, True),      # the decoder fp16 LM head shape class
+    # the fp16 decoder's QKV shape: the 256 x 192 tile (tile192_wins), whose
+    # wave tiles keep three 64-column block maxima per lane (TN = 12)
+    ("fp16", 16384, 1536, 512, "fp16", 0, True),
     # wide rows: 192, 625 and 1094 block maxima per row (the finish kernel
     # keeps up to 4, 16 block maxima per lane in registers, else re-reads)
     ("fp16", 64, 12288, 64, "fp32", 0, True),
@@ -166,6 +169,7 @@ def test_gemm16_row_max(gpu, kind, m, n, k, out_kind, act, bigtile):
 
 @pytest.mark.parametrize("m,n,k,mode,out_kind,switch", [
     (4096, 32000, 768, 3, "fp32", None),             # the W8A8 LM head (a quarter of its rows)
+    (16384, 768, 3072, 3, "bf16", None),             # W8A8 FFN2 shape: the 256 x 192 tile (TN = 12)
     (300, 1000, 256, 3, "fp32", "C3H_DISABLE_BIGTILE"),
     (1000, 264, 128, 2, "bf16", "C3H_DISABLE_DMA"),  # register-prefetch kernel, ragged
 ])

@@ -297,3 +297,58 @@ def test_compiled_concurrent_conv_pairs(fake_lib, name, policy, npairs):
             assert seq[j + 1][:2] == (_lib.OP_EVENT_RECORD, 1) and seq[j + 2][:2] == (_lib.OP_EVENT_WAIT, 0)
             assert seq[j + 1][2] == seq[j + 2][2]
     assert sum(1 for k, s, e in seq if s == 1 and k not in (_lib.OP_EVENT_RECORD, _lib.OP_EVENT_WAIT)) == npairs
+
+
+class _ConstScales(_UnitScales):
+    def __init__(self, value):
+        super().__init__()
+        self.value = value
+
+    def __missing__(self, key):
+        return self.value
+
+
+def _lower_model(m, policy):
+    from hackathon_amd.c35.compiled import CompiledPlan
+    from hackathon_amd.c35.executor import PlannedGraphExecutor
+
+    plan = _plan(m, policy)
+    ex = PlannedGraphExecutor(m.graph, m.weights)
+    return CompiledPlan(m.graph, plan, ex.weight_sources(), ex.host_constants, policy=policy)
+
+
+def test_layernorm_quantize_fusion_follows_c_preconditions(fake_lib):
+    """LayerNorm + QuantizeLinear fuse only where c3h_layernorm can write int8
+    (cols % 8 == 0, cols <= 4096): a 5120-column W8A8 model keeps the unfused
+    LayerNorm and quantize launches instead of compiling a launch the library
+    would refuse."""
+    from hackathon_amd import _lib, models
+    from hackathon_amd.c35.compiled import LN_QUANT_MAX_COLS, quant_scale_ok
+
+    assert LN_QUANT_MAX_COLS == 4096
+    assert quant_scale_ok(1.0) and quant_scale_ok(2.0 ** -126) and quant_scale_ok(3.4028235e38)
+    assert not quant_scale_ok(2.0 ** -127) and not quant_scale_ok(0.0) and not quant_scale_ok(-1.0)
+    assert not quant_scale_ok(float("inf")) and not quant_scale_ok(float("nan")) and not quant_scale_ok(1e39)
+    kw = dict(batch=1, seq=8, ffn=64, layers=1, vocab=64, quantized=True, act_scales=_UnitScales())
+    narrow = _lower_model(models.build_decoder(**{**kw, "d_model": 128, "heads": 2}), "w8a8")
+    kinds = collections.Counter(k.split(":")[0] for k in narrow.node_kinds)
+    assert kinds["layernorm_q"] == 3 and kinds["layernorm"] == 0
+    wide = _lower_model(models.build_decoder(**{**kw, "d_model": 5120, "heads": 80}), "w8a8")
+    kinds = collections.Counter(k.split(":")[0] for k in wide.node_kinds)
+    assert kinds["layernorm_q"] == 0 and kinds["layernorm"] == 3
+    assert kinds["quantize"] == 3 + 1  # the three LayerNorm outputs and the attention context
+    for a, k in zip(wide._args, wide.node_kinds):
+        if k == "layernorm":
+            assert a.cols == 5120 and a.out_dtype != _lib.I8
+
+
+def test_subnormal_quantize_scale_fails_at_compile_time(fake_lib):
+    """c3h_quantize and the fused forms accept positive normal scales only: a
+    subnormal activation scale is refused when the plan is compiled, with the
+    node named, not at the first launch."""
+    from hackathon_amd import models
+
+    m = models.build_decoder(batch=1, seq=8, d_model=128, heads=2, ffn=64, layers=1, vocab=64, quantized=True,
+                             act_scales=_ConstScales(1e-39))
+    with pytest.raises(ValueError, match="positive normal"):
+        _lower_model(m, "w8a8")
