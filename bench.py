@@ -136,13 +136,45 @@ def _measure(name: str, steps: int, warmup: int) -> dict:
     for kind, mb in res["memory_bound"].items():
         _log(f"  {name} {kind}: {mb['launches_per_step']} launches, {mb['us_per_launch']:.1f} us, "
              f"{mb['algorithmic_MB_per_launch']:.1f} MB -> {mb['achieved_GBps']:.0f} GB/s "
-             f"({100 * mb['frac_of_hbm_peak']:.1f}% of 8 TB/s)")
+             f"({100 * mb['frac_of_hbm_peak']:.1f}% of 8 TB/s; a copy of the same bytes "
+             f"{mb['copy_same_bytes_GBps']:.0f} GB/s)")
     del prog
     return res
 
 
+def _copy_ms(nbytes: int, count: int, reps: int) -> float:
+    """Milliseconds per device-to-device copy moving `nbytes` (nbytes / 2 read, nbytes / 2 written), timed as
+    `count` copies back to back in one hipGraph on one stream, like a family replay (HIP events)."""
+    import ctypes as C
+
+    from hackathon_amd import _lib
+    from hackathon_amd.device import Buffer, Event, Stream
+
+    half = max(256, (int(nbytes) // 2 + 255) // 256 * 256)
+    src, dst, st = Buffer(half), Buffer(half), Stream()
+    ops = (_lib.Op * count)()
+    for j in range(count):
+        ops[j].kind, ops[j].stream, ops[j].dst, ops[j].src, ops[j].bytes = _lib.OP_COPY, 0, dst.ptr, src.ptr, half
+    streams = (C.c_void_p * 1)(st.handle)
+    g = C.c_void_p()
+    _lib.check(_lib.lib().c3h_program_capture(ops, count, streams, 1, None, 0, C.byref(g)), "c3h_program_capture")
+    try:
+        _lib.check(_lib.lib().c3h_graph_launch(g.value, st.handle), "c3h_graph_launch")
+        e0, e1 = Event(timing=True), Event(timing=True)
+        e0.record(st)
+        for _ in range(reps):
+            _lib.check(_lib.lib().c3h_graph_launch(g.value, st.handle), "c3h_graph_launch")
+        e1.record(st)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) / reps / count
+    finally:
+        _lib.lib().c3h_graph_destroy(g.value)
+
+
 def _memory_bound(prog, reps: int) -> dict:
-    """Achieved HBM bandwidth of each memory-bound kernel family of the program."""
+    """Achieved HBM bandwidth of each memory-bound kernel family of the program, beside the
+    bandwidth a plain device-to-device copy (hipMemcpyAsync in a graph) reaches moving the same
+    bytes per launch, replayed the same way: the practical ceiling for launches of that size."""
     out = {}
     for kind in MEMORY_BOUND:
         idx = prog.launches_of([kind])
@@ -152,10 +184,15 @@ def _memory_bound(prog, reps: int) -> dict:
         ms = prog.time_subset(idx, reps=reps, repeat=repeat)
         _, nbytes = prog.work(idx)
         gbps = nbytes / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+        per = nbytes / len(idx)
+        c_ms = _copy_ms(per, len(idx) * repeat, reps)
+        c_gbps = per / (c_ms * 1e-3) / 1e9 if c_ms > 0 else 0.0
         out[kind] = {"launches_per_step": len(idx), "us_per_launch": ms * 1e3 / len(idx),
-                     "algorithmic_MB_per_launch": nbytes / len(idx) / 1e6, "achieved_GBps": gbps,
+                     "algorithmic_MB_per_launch": per / 1e6, "achieved_GBps": gbps,
                      "peak_GBps": PEAK["hbm"], "frac_of_hbm_peak": gbps / PEAK["hbm"],
-                     "timing": f"hipGraph of the family's launches x{repeat}, HIP events, {reps} replays"}
+                     "copy_same_bytes_GBps": c_gbps, "frac_of_copy": gbps / c_gbps if c_gbps > 0 else None,
+                     "timing": f"hipGraph of the family's launches x{repeat}, HIP events, {reps} replays; copy "
+                               f"reference: hipMemcpyAsync D2D of {per / 2e6:.1f} MB, the same count per graph"}
     return out
 
 

@@ -239,30 +239,47 @@ struct QuantDiv {
     e = ex - 1;
     inv = 1.0f / m;
   }
+  // The same split made on the host (frexpf and an IEEE fp32 division give
+  // the same m, e and inv there), passed to kernels that would otherwise
+  // form it once per wave.
+  __host__ __device__ QuantDiv(float m_, float inv_, int e_) : m(m_), inv(inv_), e(e_) {}
+  static QuantDiv on_host(float scale) {
+    int ex = 0;
+    const float mm = 2.0f * frexpf(scale, &ex);
+    return QuantDiv(mm, 1.0f / mm, ex - 1);
+  }
   __device__ __forceinline__ float quotient(float x) const {
     const float y = ldexpf(x, -e);
     const float q0 = fminf(fmaxf(y * inv, -0x1p20f), 0x1p20f);
     return fmaf(fmaf(-q0, m, y), inv, q0);
   }
-  // saturate(rne(x / scale) + zero_point) as an int8 code
+  // Byte k of `acc` set to saturate(rne(x / scale) + zero_point) + 128: the
+  // integer rne(x / scale) + (zero_point + 128) goes through
+  // v_cvt_pk_u8_f32, which clamps to [0, 255] (a NaN quotient gives 0) and
+  // inserts the byte, so rounding, offset, saturation and packing cost three
+  // instructions.  XOR 0x80 per byte turns the biased byte into the int8 code.
+  __device__ __forceinline__ uint32_t biased_byte(float x, float zp128, uint32_t k, uint32_t acc) const {
+    return __builtin_amdgcn_cvt_pk_u8_f32(rintf(quotient(x)) + zp128, k, acc);
+  }
+  // saturate(rne(x / scale) + zero_point) as an int8 code (NaN -> -128)
   __device__ __forceinline__ int8_t code(float x, int zero_point) const {
-    const float c = fminf(fmaxf(rintf(quotient(x)) + static_cast<float>(zero_point), -128.0f), 127.0f);
-    return static_cast<int8_t>(c);
+    return static_cast<int8_t>(biased_byte(x, static_cast<float>(zero_point + 128), 0u, 0u) ^ 0x80u);
   }
   // 4 codes packed little-endian into one word.
   __device__ __forceinline__ uint32_t codes4(const float* x, int zero_point) const {
+    const float zp128 = static_cast<float>(zero_point + 128);
     uint32_t w = 0u;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) w |= (static_cast<uint32_t>(code(x[k], zero_point)) & 0xffu) << (8 * k);
-    return w;
+    for (int k = 0; k < 4; ++k) w = biased_byte(x[k], zp128, static_cast<uint32_t>(k), w);
+    return w ^ 0x80808080u;
   }
   // 8 codes packed little-endian into two words.
   __device__ __forceinline__ uint2 codes8(const float* x, int zero_point) const {
+    const float zp128 = static_cast<float>(zero_point + 128);
     uint32_t w[2] = {0u, 0u};
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
-      w[k >> 2] |= (static_cast<uint32_t>(code(x[k], zero_point)) & 0xffu) << (8 * (k & 3));
-    return uint2{w[0], w[1]};
+    for (int k = 0; k < 8; ++k) w[k >> 2] = biased_byte(x[k], zp128, static_cast<uint32_t>(k & 3), w[k >> 2]);
+    return uint2{w[0] ^ 0x80808080u, w[1] ^ 0x80808080u};
   }
 };
 

@@ -176,11 +176,16 @@ __device__ __forceinline__ float row16_reduce(float v, Op op) {
   v = op(v, dpp_mov<0x140>(v));  // row_mirror
   return v;
 }
+// Cross-row steps by v_permlane16_swap / v_permlane32_swap (gfx950): with
+// one register as both operands, the pair holds each lane's value and that
+// of lane ^ 16 (^ 32), so each step is one VALU swap and an add -- no LDS
+// round trip as with ds_bpermute -- and the same two addends as before.
 __device__ __forceinline__ float wave_sum(float v) {
   v = row16_reduce(v, [](float a, float b) { return a + b; });
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
 }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -404,6 +409,41 @@ __global__ void __launch_bounds__(kBlock) layernorm_kernel(c3h_layernorm_args a)
 // + out_zero) by the same QuantDiv as quantize_kernel: bit-identical codes.
 constexpr int kLnVec = 8;
 
+// VW consecutive elements of TX as raw 32-bit words (8, 16 or 32 bytes).
+template <typename TX, int VW>
+struct LnRaw {
+  static constexpr int W = VW * static_cast<int>(sizeof(TX)) / 4;
+  uint32_t w[W];
+  __device__ __forceinline__ void load(const TX* p) {
+    if constexpr (W == 2) {
+      const uint2 q = *reinterpret_cast<const uint2*>(p);
+      w[0] = q.x; w[1] = q.y;
+    } else {
+#pragma unroll
+      for (int i = 0; i < W / 4; ++i) {
+        const uint4 q = reinterpret_cast<const uint4*>(p)[i];
+        w[4 * i] = q.x; w[4 * i + 1] = q.y; w[4 * i + 2] = q.z; w[4 * i + 3] = q.w;
+      }
+    }
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < W; ++i) w[i] = 0u;
+  }
+  __device__ __forceinline__ void to_f32(float* v) const {
+    if constexpr (sizeof(TX) == 4) {
+#pragma unroll
+      for (int i = 0; i < W; ++i) v[i] = __uint_as_float(w[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        v[2 * i] = Elem<TX>::to_f32(TX{static_cast<uint16_t>(w[i] & 0xffffu)});
+        v[2 * i + 1] = Elem<TX>::to_f32(TX{static_cast<uint16_t>(w[i] >> 16)});
+      }
+    }
+  }
+};
+
 template <typename TX, typename TO>
 struct LnStore {
   static __device__ __forceinline__ void store8(TO* p, const float* y, const QuantDiv&, int) {
@@ -429,40 +469,84 @@ struct LnStore<TX, int8_t> {
   }
 };
 
-template <typename TX, typename TO, int NV, int ROWS, int VW = kLnVec>
-__global__ void __launch_bounds__(kBlock) layernorm_vec_kernel(c3h_layernorm_args a) {
+// FULL: cols == 64 * VW * NV (512 columns at VW = 8, 768 at three 4-wide
+// vectors): every lane's every vector is in range, so the kernel has no
+// per-vector bounds branches and no zero-filled registers.
+template <typename TX, typename TO, int NV, int ROWS, int VW = kLnVec, bool FULL = false>
+__global__ void __launch_bounds__(kBlock) layernorm_vec_kernel(c3h_layernorm_args a, QuantDiv qd) {
   static_assert(VW == 8 || VW == 4, "vector width");
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + wave) * ROWS;
   if (row0 >= a.rows) return;
-  const int nvec = static_cast<int>(a.cols / VW);
-  float v[ROWS][NV][VW];
+  const int nvec = FULL ? 64 * NV : static_cast<int>(a.cols / VW);
+  // The affine parameters are the same for every row: loaded first, so their
+  // latency overlaps the row loads and reductions instead of following them.
+  const float* scale = static_cast<const float*>(a.scale);
+  const float* bias = static_cast<const float*>(a.bias);
+  float g[NV][VW], b[NV][VW];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int vi = lane + 64 * j;
+    // no bias: -0, the identity of fmaf(t, g, b) (so that t * g is rounded once either way)
+#pragma unroll
+    for (int e = 0; e < VW; ++e) b[j][e] = -0.0f;
+    if constexpr (!FULL) {
+#pragma unroll
+      for (int e = 0; e < VW; ++e) g[j][e] = 0.0f;
+    }
+    if (FULL || vi < nvec) {
+      if constexpr (VW == 8) {
+        Elem<float>::load8(scale + vi * 8, g[j]);
+        if (bias) Elem<float>::load8(bias + vi * 8, b[j]);
+      } else {
+        Elem<float>::load4(scale + vi * 4, g[j]);
+        if (bias) Elem<float>::load4(bias + vi * 4, b[j]);
+      }
+    }
+  }
+  // Every vector of the wave's rows (and of the residual) is loaded as raw
+  // words before any is converted, so all the loads are in flight together
+  // (converting each as it lands put a wait between consecutive loads).
+  typedef LnRaw<TX, VW> Raw;
+  Raw xr[ROWS][NV], rr[ROWS][NV];
+  const bool has_res = a.residual != nullptr;
 #pragma unroll
   for (int r = 0; r < ROWS; ++r) {
     const int64_t row = row0 + r;
     const TX* x = static_cast<const TX*>(a.x) + row * a.cols;
-    const TX* res = a.residual ? static_cast<const TX*>(a.residual) + row * a.cols : nullptr;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int vi = lane + 64 * j;
+      if (row < a.rows && (FULL || vi < nvec)) xr[r][j].load(x + vi * VW);
+      else xr[r][j].zero();
+    }
+  }
+  if (has_res) {
 #pragma unroll
-      for (int e = 0; e < VW; ++e) v[r][j][e] = 0.0f;
-      if (row < a.rows && vi < nvec) {
-        if constexpr (VW == 8) Elem<TX>::load8(x + vi * 8, v[r][j]);
-        else Elem<TX>::load4(x + vi * 4, v[r][j]);
-        if (res) {
-          float q[VW];
-          if constexpr (VW == 8) Elem<TX>::load8(res + vi * 8, q);
-          else Elem<TX>::load4(res + vi * 4, q);
+    for (int r = 0; r < ROWS; ++r) {
+      const int64_t row = row0 + r;
+      const TX* res = static_cast<const TX*>(a.residual) + row * a.cols;
 #pragma unroll
-          for (int e = 0; e < VW; ++e) v[r][j][e] += q[e];
-        }
+      for (int j = 0; j < NV; ++j) {
+        const int vi = lane + 64 * j;
+        if (row < a.rows && (FULL || vi < nvec)) rr[r][j].load(res + vi * VW);
+        else rr[r][j].zero();
       }
     }
   }
-  const float* scale = static_cast<const float*>(a.scale);
-  const float* bias = static_cast<const float*>(a.bias);
-  const QuantDiv qd(std::is_same<TO, int8_t>::value ? a.out_scale : 1.0f);
+  float v[ROWS][NV][VW];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      xr[r][j].to_f32(v[r][j]);
+      if (has_res) {
+        float q[VW];
+        rr[r][j].to_f32(q);
+#pragma unroll
+        for (int e = 0; e < VW; ++e) v[r][j][e] += q[e];
+      }
+    }
 #pragma unroll
   for (int r = 0; r < ROWS; ++r) {
     const int64_t row = row0 + r;
@@ -473,13 +557,15 @@ __global__ void __launch_bounds__(kBlock) layernorm_vec_kernel(c3h_layernorm_arg
 #pragma unroll
       for (int e = 0; e < VW; ++e) sum += v[r][j][e];  // out-of-range vectors hold zeros
     const float mean = wave_sum(sum) / static_cast<float>(a.cols);
+    // The centred values replace the inputs: the affine pass reuses them.
     float sq = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      if (lane + 64 * j < nvec) {
+      if (FULL || lane + 64 * j < nvec) {
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
           const float d = v[r][j][e] - mean;
+          v[r][j][e] = d;
           sq += d * d;
         }
       }
@@ -490,22 +576,10 @@ __global__ void __launch_bounds__(kBlock) layernorm_vec_kernel(c3h_layernorm_arg
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int vi = lane + 64 * j;
-      if (vi < nvec) {
-        float g[VW], y[VW], b[VW];
+      if (FULL || vi < nvec) {
+        float y[VW];
 #pragma unroll
-        for (int e = 0; e < VW; ++e) b[e] = 0.0f;
-        if constexpr (VW == 8) {
-          Elem<float>::load8(scale + vi * 8, g);
-          if (bias) Elem<float>::load8(bias + vi * 8, b);
-        } else {
-          Elem<float>::load4(scale + vi * 4, g);
-          if (bias) Elem<float>::load4(bias + vi * 4, b);
-        }
-#pragma unroll
-        for (int e = 0; e < VW; ++e) {
-          y[e] = (v[r][j][e] - mean) * inv_std * g[e];
-          if (bias) y[e] += b[e];
-        }
+        for (int e = 0; e < VW; ++e) y[e] = fmaf(v[r][j][e] * inv_std, g[j][e], b[j][e]);  // (x - mean) * inv_std * scale + bias
         if constexpr (VW == 8) LnStore<TX, TO>::store8(out + vi * 8, y, qd, a.out_zero);
         else LnStore<TX, TO>::store4(out + vi * 4, y, qd, a.out_zero);
       }
@@ -576,6 +650,10 @@ __global__ void __launch_bounds__(kBlock) gather_kernel(c3h_gather_args a, int64
 // add, one rounding, one vector store.  Consecutive threads take consecutive
 // chunks of a row, so loads and stores are coalesced; the index is read once
 // per chunk from L1.
+// Each thread takes kGatherU chunks per iteration (t0, t0 + stride, ...),
+// issued together: all index loads, then all row and addend loads, then the
+// stores, so a thread has kGatherU independent index -> row chains in flight.
+constexpr int kGatherU = 4;
 template <typename T, typename TA>
 __global__ void __launch_bounds__(kBlock) gather_add_kernel(c3h_gather_args a, int64_t row_vecs) {
   const int64_t total = a.n_indices * row_vecs;
@@ -583,24 +661,40 @@ __global__ void __launch_bounds__(kBlock) gather_add_kernel(c3h_gather_args a, i
   const T* data = static_cast<const T*>(a.data);
   const TA* add = static_cast<const TA*>(a.addend);
   T* out = static_cast<T*>(a.out);
-  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total; t += stride) {
-    const int64_t r = t / row_vecs;
-    const int64_t c = (t - r * row_vecs) * 8;
-    int64_t idx = a.indices[r];
-    if (idx < 0) idx += a.axis_dim;
-    float v[8], w[8];
-    if (idx < 0 || idx >= a.axis_dim) {
-      if (a.error_flag) *a.error_flag = 1;
+  for (int64_t t0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t0 < total;
+       t0 += stride * kGatherU) {
+    int64_t r[kGatherU], c[kGatherU], idx[kGatherU];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = 0.0f;
-      Elem<T>::store8(out + r * a.inner + c, v);
-      continue;
+    for (int u = 0; u < kGatherU; ++u) {
+      const int64_t t = t0 + u * stride;
+      r[u] = t < total ? t / row_vecs : 0;
+      c[u] = (t - r[u] * row_vecs) * 8;
+      idx[u] = t < total ? a.indices[r[u]] : 0;
     }
-    Elem<T>::load8(data + idx * a.inner + c, v);
-    Elem<TA>::load8(add + (r % a.addend_rows) * a.inner + c, w);
+    float v[kGatherU][8], w[kGatherU][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] += w[e];
-    Elem<T>::store8(out + r * a.inner + c, v);
+    for (int u = 0; u < kGatherU; ++u) {
+      if (idx[u] < 0) idx[u] += a.axis_dim;
+      const bool ok = idx[u] >= 0 && idx[u] < a.axis_dim;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[u][e] = w[u][e] = 0.0f;
+      if (t0 + u * stride < total && ok) {
+        Elem<T>::load8(data + idx[u] * a.inner + c[u], v[u]);
+        Elem<TA>::load8(add + (r[u] % a.addend_rows) * a.inner + c[u], w[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kGatherU; ++u) {
+      if (t0 + u * stride >= total) break;
+      if (idx[u] < 0 || idx[u] >= a.axis_dim) {
+        // out-of-range index: a zero row and the error flag
+        if (a.error_flag) *a.error_flag = 1;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[u][e] += w[u][e];
+      }
+      Elem<T>::store8(out + r[u] * a.inner + c[u], v[u]);
+    }
   }
 }
 
@@ -916,10 +1010,14 @@ __global__ void __launch_bounds__(kBlock) quantize_vec_kernel(c3h_quantize_args 
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   const TX* x = static_cast<const TX*>(a.x);
   const QuantDiv qd(a.scale);
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec; i += stride) {
-    float v[8];
+  // two vectors per iteration, both loads issued before either is quantized
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec; i += 2 * stride) {
+    const int64_t i2 = i + stride;
+    float v[8], v2[8];
     Elem<TX>::load8(x + i * 8, v);
+    if (i2 < nvec) Elem<TX>::load8(x + i2 * 8, v2);
     *reinterpret_cast<uint2*>(a.out + i * 8) = qd.codes8(v, a.zero_point);
+    if (i2 < nvec) *reinterpret_cast<uint2*>(a.out + i2 * 8) = qd.codes8(v2, a.zero_point);
   }
 }
 
@@ -1121,12 +1219,16 @@ void launch_ln(const c3h_layernorm_args& a, int nv, void* stream) {
   const dim3 b(kBlock);
   hipStream_t st = as_stream(stream);
   auto grid = [&](int rows_per_wave) { return dim3(static_cast<unsigned>(ceil_div(a.rows, 4 * rows_per_wave))); };
+  const QuantDiv qd = QuantDiv::on_host(std::is_same<TO, int8_t>::value ? a.out_scale : 1.0f);
   switch (nv) {
-    case 1: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 1, 1>), grid(1), b, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 2, 2>), grid(2), b, 0, st, a); break;
-    case 3: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 3, 1, 4>), grid(1), b, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 4, 1>), grid(1), b, 0, st, a); break;
-    default: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 8, 1>), grid(1), b, 0, st, a); break;
+    case 1:
+      if (a.cols == 512) hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 1, 1, 8, true>), grid(1), b, 0, st, a, qd);
+      else hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 1, 1>), grid(1), b, 0, st, a, qd);
+      break;
+    case 2: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 2, 2>), grid(2), b, 0, st, a, qd); break;
+    case 3: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 3, 1, 4, true>), grid(1), b, 0, st, a, qd); break;
+    case 4: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 4, 1>), grid(1), b, 0, st, a, qd); break;
+    default: hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 8, 1>), grid(1), b, 0, st, a, qd); break;
   }
 }
 
@@ -1346,7 +1448,7 @@ int c3h_gather(const c3h_gather_args* a, void* stream) {
                     reinterpret_cast<uintptr_t>(a->addend) % (add32 ? 32 : vec_bytes) == 0,
                 "gather: a fused addend needs vector-aligned data, addend and out");
     const int64_t rv = a->inner / 8;
-    const dim3 grid(grid_for(total_rows * rv));
+    const dim3 grid(grid_for(total_rows * rv, kGatherU));
     if (a->dtype == C3H_F32)
       hipLaunchKernelGGL((gather_add_kernel<float, float>), grid, dim3(kBlock), 0, s, *a, rv);
     else if (a->dtype == C3H_BF16 && add32)
@@ -1484,7 +1586,7 @@ int c3h_quantize(const c3h_quantize_args* a, void* stream) {
   if (a->count % 8 == 0 && (reinterpret_cast<uintptr_t>(a->x) & 15) == 0 &&
       (reinterpret_cast<uintptr_t>(a->out) & 7) == 0 &&
       (a->x_dtype == C3H_F32 || a->x_dtype == C3H_BF16 || a->x_dtype == C3H_F16)) {
-    const dim3 g(grid_for(a->count / 8)), b(kBlock);
+    const dim3 g(grid_for(a->count / 8, 2)), b(kBlock);
     hipStream_t st = as_stream(stream);
     if (a->x_dtype == C3H_F32) hipLaunchKernelGGL(quantize_vec_kernel<float>, g, b, 0, st, *a);
     else if (a->x_dtype == C3H_BF16) hipLaunchKernelGGL(quantize_vec_kernel<bf16_t>, g, b, 0, st, *a);
