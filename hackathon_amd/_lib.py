@@ -34,7 +34,7 @@ OP_NOP, OP_EVENT_RECORD, OP_EVENT_WAIT, OP_COPY = 0, 1, 2, 3
 OP_FILL, OP_CAST, OP_EW, OP_STRIDED_COPY, OP_REDUCE, OP_SOFTMAX, OP_LAYERNORM, OP_BATCHNORM, \
     OP_GATHER, OP_ARGMAX, OP_IM2COL, OP_LAYOUT, OP_MAXPOOL, OP_GEMM, OP_CONV, OP_ATTN_SCORES, \
     OP_FLASH, OP_QUANTIZE, OP_QGEMM, OP_DEQUANTIZE, OP_BNFOLD, OP_PACK, OP_CONV_POOL, OP_QUANT_FP8, \
-    OP_GEMM_FP8, OP_SPLITK, OP_QUANT_MXFP4, OP_GEMM_W4A16, OP_ARGMAX_FINISH = range(10, 39)
+    OP_GEMM_FP8, OP_SPLITK, OP_QUANT_MXFP4, OP_GEMM_W4A16, OP_ARGMAX_FINISH, OP_NONFINITE = range(10, 40)
 
 vp = C.c_void_p
 i32 = C.c_int32
@@ -112,6 +112,10 @@ class GatherArgs(C.Structure):
 class ArgmaxArgs(C.Structure):
     _fields_ = [("in_", vp), ("out", vp), ("rows", i64), ("cols", i64), ("in_dtype", i32),
                 ("pad_", i32)]
+
+
+class NonfiniteArgs(C.Structure):
+    _fields_ = [("x", vp), ("flag", vp), ("count", i64), ("dtype", i32), ("pad_", i32)]
 
 
 class ArgmaxFinishArgs(C.Structure):
@@ -235,7 +239,7 @@ ABI_ORDER = [Props, FillArgs, CastArgs, EwArgs, CopyArgs, ReduceArgs, SoftmaxArg
              BatchNormArgs, BnFoldArgs, GatherArgs, ArgmaxArgs, Im2colArgs, LayoutArgs, PoolArgs,
              Epilogue, GemmArgs, ConvArgs, AttnScoresArgs, FlashArgs, QuantizeArgs, QGemmArgs,
              DequantizeArgs, Op, PackArgs, ConvPoolArgs, Fp8QuantArgs, Fp8GemmArgs,
-             SplitKArgs, Mxfp4QuantArgs, W4A16GemmArgs, ArgmaxFinishArgs]
+             SplitKArgs, Mxfp4QuantArgs, W4A16GemmArgs, ArgmaxFinishArgs, NonfiniteArgs]
 
 # Kernel entry points: name -> args struct (all take (const args*, void* stream)).
 KERNELS = {
@@ -249,7 +253,7 @@ KERNELS = {
     "c3h_pack_conv_weight": PackArgs, "c3h_conv_stem_pool": ConvPoolArgs,
     "c3h_quantize_fp8_rows": Fp8QuantArgs, "c3h_gemm_fp8": Fp8GemmArgs,
     "c3h_gemm_splitk_reduce": SplitKArgs, "c3h_quantize_mxfp4": Mxfp4QuantArgs,
-    "c3h_gemm_w4a16": W4A16GemmArgs, "c3h_argmax_finish": ArgmaxFinishArgs,
+    "c3h_gemm_w4a16": W4A16GemmArgs, "c3h_argmax_finish": ArgmaxFinishArgs, "c3h_nonfinite": NonfiniteArgs,
 }
 
 OP_KIND = {
@@ -262,6 +266,7 @@ OP_KIND = {
     BnFoldArgs: OP_BNFOLD, PackArgs: OP_PACK, ConvPoolArgs: OP_CONV_POOL,
     Fp8QuantArgs: OP_QUANT_FP8, Fp8GemmArgs: OP_GEMM_FP8, SplitKArgs: OP_SPLITK,
     Mxfp4QuantArgs: OP_QUANT_MXFP4, W4A16GemmArgs: OP_GEMM_W4A16, ArgmaxFinishArgs: OP_ARGMAX_FINISH,
+    NonfiniteArgs: OP_NONFINITE,
 }
 
 KERNEL_OF_ARGS = {v: k for k, v in KERNELS.items()}

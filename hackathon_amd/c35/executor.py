@@ -562,6 +562,70 @@ def _run_planned_batches(pipeline, arrays, total, batch, out_name, out_path,
 
 
 _CHUNK_BYTES = 64 << 20
+_COPY_THREADS = 8
+_POOL = None
+
+
+def _copy_pool():
+    """Host threads for the streamed pipeline's large host copies (NumPy copies release the GIL)."""
+    global _POOL
+    if _POOL is None:
+        import concurrent.futures as cf
+
+        _POOL = cf.ThreadPoolExecutor(max_workers=_COPY_THREADS, thread_name_prefix="c3h-copy")
+    return _POOL
+
+
+class _NpyWriter:
+    """A .npy file written by positioned writes from pinned chunks: the header
+    first (NumPy's format), the data region sized up front, then pwrite of
+    each piece from the copy threads -- no memory map whose pages would fault
+    in one at a time."""
+
+    def __init__(self, path: str, dtype, shape: Tuple[int, ...]) -> None:
+        self.dtype = np.dtype(dtype)
+        with open(path, "wb") as f:
+            np.lib.format.write_array_header_1_0(f, {"descr": np.lib.format.dtype_to_descr(self.dtype),
+                                                     "fortran_order": False, "shape": tuple(shape)})
+            self.offset = f.tell()
+            f.truncate(self.offset + math.prod(shape) * self.dtype.itemsize)
+        self.fd = os.open(path, os.O_WRONLY)
+
+    def write(self, elem_offset: int, data: np.ndarray, min_bytes: int = 4 << 20) -> None:
+        """data (contiguous, this file's dtype) at element `elem_offset` of the flat array."""
+        buf = memoryview(np.ascontiguousarray(data)).cast("B")
+        pos = self.offset + elem_offset * self.dtype.itemsize
+        n = len(buf)
+        parts = 1 if n < min_bytes else _COPY_THREADS
+        bounds = [n * i // parts // 4096 * 4096 for i in range(parts)] + [n]
+
+        def one(i):
+            lo, hi = bounds[i], bounds[i + 1]
+            while lo < hi:
+                lo += os.pwrite(self.fd, buf[lo:hi], pos + lo)
+        if parts == 1:
+            one(0)
+        else:
+            list(_copy_pool().map(one, range(parts)))
+
+    def close(self) -> None:
+        if self.fd >= 0:
+            os.close(self.fd)
+            self.fd = -1
+
+
+def _par_copy(dst: np.ndarray, src: np.ndarray, min_bytes: int = 4 << 20) -> None:
+    """dst[...] = src, split over the copy threads along axis 0 when it is large."""
+    n = dst.shape[0] if dst.ndim else 0
+    if dst.nbytes < min_bytes or n < 2:
+        dst[...] = src
+        return
+    parts = min(_COPY_THREADS, n)
+    bounds = [n * i // parts for i in range(parts + 1)]
+
+    def one(i):
+        dst[bounds[i]:bounds[i + 1]] = src[bounds[i]:bounds[i + 1]]
+    list(_copy_pool().map(one, range(parts)))
 
 
 def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path,
@@ -573,22 +637,37 @@ def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path,
     its logits are copied on the device into one of two staging buffers.
     While the GPU runs batch i, the host drains batch i - 1: a copy stream
     moves its staging buffer to the host in 64 MB pinned chunks (two, used in
-    turn), and each chunk is checked for non-finite values and written into
-    the memory-mapped logits.npy.  No whole-output device or host copy is
-    ever built, so C5's 2.1 GB of logits cost one staging buffer per slot.
+    turn), and each chunk is written into logits.npy by positioned writes
+    from the copy threads.  The non-finite check (X:1177) runs on the device over
+    each batch's logits (c3h_nonfinite) and only its flag crosses to the host.
+    No whole-output device or host copy is ever built, so C5's 2.1 GB of
+    logits cost one staging buffer per slot.  The pinned and device staging
+    buffers stay with the pipeline, so a second call with the same batch
+    shape allocates nothing.
     Further graph outputs (`extras`, e.g. the decoders' int64 ArgMax) are
     staged the same way and drained whole into <name>.npy.
     """
     from ..device import Event, PinnedArray, Stream
 
+    cache = pipeline.__dict__.setdefault("_stream_buffers", {})
+
+    def kept(key, make):
+        if key not in cache:
+            cache[key] = make()
+        return cache[key]
+
     names = list(arrays)
-    pin_in = [{n: PinnedArray((batch,) + arrays[n].shape[1:], arrays[n].dtype) for n in names} for _ in range(2)]
-    copy_stream = Stream()
+    pin_in = [{n: kept(("in", n, slot, (batch,) + arrays[n].shape[1:], arrays[n].dtype.str),
+                       lambda n=n: PinnedArray((batch,) + arrays[n].shape[1:], arrays[n].dtype))
+               for n in names} for slot in range(2)]
+    copy_stream = kept("copy_stream", Stream)
     stage: list = [None, None]
     ready = [Event(), Event()]
-    chunks = [PinnedArray((_CHUNK_BYTES // 4,), np.float32) for _ in range(2)]
+    chunks = [kept(("chunk", k), lambda: PinnedArray((_CHUNK_BYTES // 4,), np.float32)) for k in range(2)]
     chunk_done = [Event(), Event()]
     flags = [PinnedArray((1,), np.int32) for _ in range(2)]  # each batch's gather error flag
+    nf_dev = [DeviceArray.empty((1,), np.int32) for _ in range(2)]  # each batch's non-finite flag
+    nf_host = [PinnedArray((1,), np.int32) for _ in range(2)]
     progs: list = [None, None]
     x_stage: list = [{}, {}]   # per slot: extra output name -> device staging buffer
     x_host: list = [{}, {}]    # per slot: extra output name -> pinned host buffer
@@ -601,9 +680,9 @@ def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path,
         copy_stream.wait_event(ready[slot])
         flag = progs[slot]._error_flag()
         _lib.check(_lib.lib().c3h_memcpy_d2h_async(flags[slot].ptr, flag.ptr, 4, copy_stream.handle), "d2h")
+        _lib.check(_lib.lib().c3h_memcpy_d2h_async(nf_host[slot].ptr, nf_dev[slot].ptr, 4, copy_stream.handle), "d2h")
         src = stage[slot]
         row = math.prod(tail)
-        flat = mm.reshape(-1)
         first, last = start * row, end * row
         step = _CHUNK_BYTES // 4
         spans = [(o, min(o + step, last)) for o in range(first, last, step)]
@@ -614,22 +693,24 @@ def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path,
                                                        copy_stream.handle), "d2h")
             chunk_done[k % 2].record(copy_stream)
 
+        def check_flags():
+            if int(flags[slot].array[0]) != 0:
+                progs[slot].check_errors()  # clears the flag and raises IndexError
+            if int(nf_host[slot].array[0]) != 0:
+                raise ValueError("Output contains non-finite values (NaN or Inf)")
+
         if spans:
             issue(0)
         else:
             copy_stream.synchronize()
-        if not spans and int(flags[slot].array[0]) != 0:
-            progs[slot].check_errors()  # clears the flag and raises IndexError
+            check_flags()
         for k, (o0, o1) in enumerate(spans):
             if k + 1 < len(spans):
                 issue(k + 1)
-            chunk_done[k % 2].synchronize()  # the flag copy was queued before chunk 0
-            if k == 0 and int(flags[slot].array[0]) != 0:
-                progs[slot].check_errors()  # clears the flag and raises IndexError
-            host = chunks[k % 2].array[: o1 - o0]
-            if not np.all(np.isfinite(host)):
-                raise ValueError("Output contains non-finite values (NaN or Inf)")
-            flat[o0:o1] = host
+            chunk_done[k % 2].synchronize()  # the flag copies were queued before chunk 0
+            if k == 0:
+                check_flags()
+            mm.write(o0, chunks[k % 2].array[: o1 - o0])
         if extras:
             for n in extras:
                 src_x = x_stage[slot][n]
@@ -640,47 +721,69 @@ def _stream_compiled(pipeline, arrays, total, batch, out_name, out_path,
             for n in extras:
                 x_mm[n][start:end] = x_host[slot][n].array[: end - start]
 
-    for i, start in enumerate(range(0, total, batch)):
-        end = min(start + batch, total)
-        nb = end - start
-        slot = i % 2
-        prog = pipeline.compiled_for_batch(nb)
-        pipeline.last_plan = pipeline._plan_for_batch(nb)
-        feed = {}
-        for n in names:
-            view = pin_in[slot][n].array[:nb]
-            view[...] = arrays[n][start:end]
-            feed[n] = (pin_in[slot][n], view.nbytes)
-        prog.stage_inputs(feed)
-        prog.launch()
-        progs[slot] = prog
-        out = prog.output_arrays[out_name]
-        tail = _check_output(out, out_name, tail)
-        if mm is None:
-            mm = np.lib.format.open_memmap(out_path, mode="w+", dtype=np.float32, shape=(total,) + tail)
-        if stage[slot] is None:
-            stage[slot] = DeviceArray.empty((batch,) + tail, np.float32)
-        _lib.check(_lib.lib().c3h_memcpy_d2d_async(stage[slot].ptr, out.ptr, out.nbytes, prog.stream.handle), "d2d")
-        for n in extras:
-            xo = prog.output_arrays[n]
-            if n not in x_mm:
-                x_mm[n] = np.lib.format.open_memmap(_extra_path(out_path, n), mode="w+", dtype=xo.dtype,
-                                                    shape=(total,) + xo.shape[1:])
-            if n not in x_stage[slot]:
-                x_stage[slot][n] = DeviceArray.empty((batch,) + xo.shape[1:], xo.dtype)
-                x_host[slot][n] = PinnedArray((batch,) + xo.shape[1:], xo.dtype)
-            _lib.check(_lib.lib().c3h_memcpy_d2d_async(x_stage[slot][n].ptr, xo.ptr, xo.nbytes, prog.stream.handle),
-                       "d2d")
-        ready[slot].record(prog.stream)
-        if pending is not None:
-            drain(*pending)
-        pending = (slot, start, end)
-    if pending is None:
-        raise RuntimeError("Inference produced no output batches")
-    drain(*pending)
-    mm.flush()
-    shape = mm.shape
-    del mm
+    try:
+        for i, start in enumerate(range(0, total, batch)):
+            end = min(start + batch, total)
+            nb = end - start
+            slot = i % 2
+            prog = pipeline.compiled_for_batch(nb)
+            pipeline.last_plan = pipeline._plan_for_batch(nb)
+            feed = {}
+            for n in names:
+                view = pin_in[slot][n].array[:nb]
+                _par_copy(view, arrays[n][start:end])
+                feed[n] = (pin_in[slot][n], view.nbytes)
+            prog.stage_inputs(feed)
+            prog.launch()
+            progs[slot] = prog
+            out = prog.output_arrays[out_name]
+            tail = _check_output(out, out_name, tail)
+            # non-finite check of this batch's logits on the device (X:1177)
+            fa = _lib.FillArgs()
+            fa.out, fa.count, fa.dtype, fa.value = nf_dev[slot].ptr, 1, _lib.I32, 0.0
+            _lib.launch(fa, prog.stream.handle)
+            na = _lib.NonfiniteArgs()
+            na.x, na.flag, na.count, na.dtype = out.ptr, nf_dev[slot].ptr, out.size, _lib.F32
+            _lib.launch(na, prog.stream.handle)
+            if mm is None:
+                mm = _NpyWriter(out_path, np.float32, (total,) + tail)
+            if stage[slot] is None:
+                stage[slot] = kept(("stage", slot, (batch,) + tail), lambda: DeviceArray.empty((batch,) + tail, np.float32))
+            _lib.check(_lib.lib().c3h_memcpy_d2d_async(stage[slot].ptr, out.ptr, out.nbytes, prog.stream.handle), "d2d")
+            for n in extras:
+                xo = prog.output_arrays[n]
+                if n not in x_mm:
+                    x_mm[n] = np.lib.format.open_memmap(_extra_path(out_path, n), mode="w+", dtype=xo.dtype,
+                                                        shape=(total,) + xo.shape[1:])
+                if n not in x_stage[slot]:
+                    key = (n, slot, (batch,) + xo.shape[1:], xo.dtype.str)
+                    x_stage[slot][n] = kept(("xstage",) + key, lambda: DeviceArray.empty((batch,) + xo.shape[1:], xo.dtype))
+                    x_host[slot][n] = kept(("xhost",) + key, lambda: PinnedArray((batch,) + xo.shape[1:], xo.dtype))
+                _lib.check(_lib.lib().c3h_memcpy_d2d_async(x_stage[slot][n].ptr, xo.ptr, xo.nbytes, prog.stream.handle),
+                           "d2d")
+            ready[slot].record(prog.stream)
+            if pending is not None:
+                drain(*pending)
+            pending = (slot, start, end)
+        if pending is None:
+            raise RuntimeError("Inference produced no output batches")
+        drain(*pending)
+    except BaseException:
+        # the cached buffers are idle again before the error propagates, and no
+        # partial output file stays behind (the reference raises before it saves, X:1177-1186)
+        copy_stream.synchronize()
+        for p in progs:
+            if p is not None:
+                p.stream.synchronize()
+        if mm is not None:
+            mm.close()
+            os.remove(out_path)
+        for n in list(x_mm):
+            del x_mm[n]
+            os.remove(_extra_path(out_path, n))
+        raise
+    mm.close()
+    shape = (total,) + tail
     for n in extras:
         x_mm[n].flush()
     x_mm.clear()

@@ -698,6 +698,38 @@ __global__ void __launch_bounds__(kBlock) gather_add_kernel(c3h_gather_args a, i
   }
 }
 
+// ------------------------------------------------------------------ finiteness
+// Any NaN / Inf among `count` values: 16-byte loads, an exponent-all-ones
+// test per element, and one plain store of 1 per wave that found one (every
+// writer stores the same value, so no atomic is needed).
+template <typename T>
+__global__ void __launch_bounds__(kBlock) nonfinite_kernel(const T* __restrict__ x, int64_t count,
+                                                           int32_t* __restrict__ flag) {
+  constexpr int PER = 16 / static_cast<int>(sizeof(T));
+  const int64_t nvec = count / PER;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  bool bad = false;
+  for (int64_t i = t0; i < nvec; i += stride) {
+    const uint4 q = reinterpret_cast<const uint4*>(x)[i];
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (sizeof(T) == 4) bad |= (w[k] & 0x7f800000u) == 0x7f800000u;
+      else if constexpr (std::is_same<T, bf16_t>::value)
+        bad |= ((w[k] & 0x7f80u) == 0x7f80u) | ((w[k] & 0x7f800000u) == 0x7f800000u);
+      else bad |= ((w[k] & 0x7c00u) == 0x7c00u) | ((w[k] & 0x7c000000u) == 0x7c000000u);
+    }
+  }
+  for (int64_t i = nvec * PER + t0; i < count; i += stride) {  // the last < PER elements
+    float v;
+    if constexpr (sizeof(T) == 4) v = x[i];
+    else v = Elem<T>::to_f32(x[i]);
+    bad |= !isfinite(v);
+  }
+  if (__ballot(bad) != 0 && (threadIdx.x & 63) == 0) *flag = 1;
+}
+
 // ------------------------------------------------------------------ argmax
 // One 256-thread block per row; NaN counts as the maximum (NumPy rule) and
 // ties resolve to the lowest index.
@@ -1576,6 +1608,24 @@ int c3h_pack_conv_weight(const c3h_pack_args* a, void* stream) {
   hipLaunchKernelGGL(pack_conv_weight_kernel, dim3(grid_for(static_cast<int64_t>(a->o) * a->k_stride)), dim3(kBlock),
                      0, as_stream(stream), *a);
   return launch_status("pack_conv_weight");
+}
+
+int c3h_nonfinite(const c3h_nonfinite_args* a, void* stream) {
+  C3H_REQUIRE(a && a->flag && a->count >= 0 && (a->x || a->count == 0), "nonfinite: bad args");
+  C3H_REQUIRE(a->dtype == C3H_F32 || a->dtype == C3H_BF16 || a->dtype == C3H_F16,
+              "nonfinite: dtype must be F32, BF16 or F16");
+  C3H_REQUIRE((reinterpret_cast<uintptr_t>(a->x) & 15) == 0, "nonfinite: x must be 16-byte aligned");
+  if (a->count == 0) return C3H_OK;
+  const int per = a->dtype == C3H_F32 ? 4 : 8;
+  const dim3 g(grid_for(ceil_div(a->count, per), 4)), b(kBlock);
+  hipStream_t st = as_stream(stream);
+  if (a->dtype == C3H_F32)
+    hipLaunchKernelGGL(nonfinite_kernel<float>, g, b, 0, st, static_cast<const float*>(a->x), a->count, a->flag);
+  else if (a->dtype == C3H_BF16)
+    hipLaunchKernelGGL(nonfinite_kernel<bf16_t>, g, b, 0, st, static_cast<const bf16_t*>(a->x), a->count, a->flag);
+  else
+    hipLaunchKernelGGL(nonfinite_kernel<f16_t>, g, b, 0, st, static_cast<const f16_t*>(a->x), a->count, a->flag);
+  return launch_status("nonfinite");
 }
 
 int c3h_quantize(const c3h_quantize_args* a, void* stream) {

@@ -257,6 +257,7 @@ static int dispatch_op(const c3h_op& op, hipStream_t s, void* const* events, int
       return c3h_quantize_mxfp4(static_cast<const c3h_mxfp4_quant_args*>(op.args), s);
     case C3H_OP_GEMM_W4A16: return c3h_gemm_w4a16(static_cast<const c3h_w4a16_gemm_args*>(op.args), s);
     case C3H_OP_ARGMAX_FINISH: return c3h_argmax_finish(static_cast<const c3h_argmax_finish_args*>(op.args), s);
+    case C3H_OP_NONFINITE: return c3h_nonfinite(static_cast<const c3h_nonfinite_args*>(op.args), s);
     case C3H_OP_SPLITK: return c3h_gemm_splitk_reduce(static_cast<const c3h_splitk_args*>(op.args), s);
     default: return fail(C3H_EINVAL, "unknown op kind %d", op.kind);
   }
@@ -345,7 +346,7 @@ int32_t c3h_abi_sizes(int64_t* out, int32_t capacity) {
       sizeof(c3h_qgemm_args),     sizeof(c3h_dequantize_args), sizeof(c3h_op),
       sizeof(c3h_pack_args),      sizeof(c3h_conv_pool_args), sizeof(c3h_fp8_quant_args),
       sizeof(c3h_fp8_gemm_args), sizeof(c3h_splitk_args), sizeof(c3h_mxfp4_quant_args),
-      sizeof(c3h_w4a16_gemm_args), sizeof(c3h_argmax_finish_args)};
+      sizeof(c3h_w4a16_gemm_args), sizeof(c3h_argmax_finish_args), sizeof(c3h_nonfinite_args)};
   const int32_t n = static_cast<int32_t>(sizeof(sizes) / sizeof(sizes[0]));
   for (int32_t i = 0; i < n && i < capacity && out; ++i) out[i] = sizes[i];
   return n;

@@ -372,6 +372,20 @@ typedef struct {
 } c3h_argmax_finish_args;
 int c3h_argmax_finish(const c3h_argmax_finish_args* a, void* stream);
 
+/* Output check of load_and_infer: writes 1 to *flag when any of the `count`
+ * values at `x` (dtype F32, BF16 or F16) is NaN or +-Inf, and leaves it
+ * untouched otherwise (clear it first).  The device counterpart of
+ * cp.isfinite(final).all() (c35/executor.py:1177); it lets the host drain the
+ * logits without scanning them. */
+typedef struct {
+  const void* x;
+  int32_t* flag;
+  int64_t count;
+  int32_t dtype;
+  int32_t pad_;
+} c3h_nonfinite_args;
+int c3h_nonfinite(const c3h_nonfinite_args* a, void* stream);
+
 /* im2col with the reference's ordering: rows (n, ho, wo), columns (c, kh, kw),
  * zero padding (kernel_registry.py:399-453).  Input NCHW. */
 typedef struct {
@@ -836,7 +850,8 @@ enum c3h_op_kind {
   C3H_OP_SPLITK = 35,
   C3H_OP_QUANT_MXFP4 = 36,
   C3H_OP_GEMM_W4A16 = 37,
-  C3H_OP_ARGMAX_FINISH = 38
+  C3H_OP_ARGMAX_FINISH = 38,
+  C3H_OP_NONFINITE = 39
 };
 
 typedef struct {
@@ -871,7 +886,7 @@ int c3h_graph_destroy(void* graph_exec);
  * c3h_quantize_args, c3h_qgemm_args, c3h_dequantize_args, c3h_op,
  * c3h_pack_args, c3h_conv_pool_args, c3h_fp8_quant_args, c3h_fp8_gemm_args,
  * c3h_splitk_args, c3h_mxfp4_quant_args, c3h_w4a16_gemm_args,
- * c3h_argmax_finish_args.
+ * c3h_argmax_finish_args, c3h_nonfinite_args.
  * Returns the number of sizes available (host-only; needs no GPU). */
 int32_t c3h_abi_sizes(int64_t* out, int32_t capacity);
 

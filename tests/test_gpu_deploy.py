@@ -3,10 +3,11 @@
 ONNX files written by PyTorch's C++ serializer (dynamic batch axis) and by
 this build's writer go through the CLI: manifest + .npy inputs in, logits.npy
 + manifest.json out, ragged last batch included.  fp32 runs are checked
-against PyTorch's fp32 forward (rtol 1e-3); the fp16 policy against the
-workload gate (max |logit diff| 2e-2 after scaling by the logit range, top-1
-agreement); files from this build's writer must give exactly the logits of
-the same graph run in-process.
+against PyTorch's fp32 forward (rtol 1e-3); the fp16 policy against
+north_star's gate (max |logits - fp32| <= 2e-2, argmax equal to fp32's on
+every position whose top-2 margin exceeds 4e-2); files from this build's
+writer must give exactly the logits of the same graph run in-process, up to
+BASELINE config 4 at full size.
 """
 
 from __future__ import annotations
@@ -16,6 +17,8 @@ import os
 
 import numpy as np
 import pytest
+
+import gates
 
 pytestmark = [pytest.mark.gpu, pytest.mark.filterwarnings("ignore::DeprecationWarning")]
 
@@ -73,10 +76,15 @@ def test_deploy_torch_decoder_fp16(gpu, tmp_path):
     with torch.no_grad():
         expect = module(x).numpy()
     got = _deploy(tmp_path, path, in_name, x.numpy(), "--precision", "fp16")
-    scale = max(1.0, float(np.abs(expect).max()))
-    assert float(np.abs(got - expect).max()) <= 2e-2 * scale
-    agree = np.mean(got.argmax(-1) == expect.argmax(-1))
-    assert agree >= 0.99, agree
+    # north_star's 16-bit gate, absolute: max|logits - fp32| <= 2e-2, and the
+    # argmax equal to fp32's wherever the fp32 top-2 margin exceeds 2 * 2e-2
+    err = float(np.abs(got - expect).max())
+    agree, share = gates.margin_agreement(got, expect, 2e-2)
+    print(f"deploy fp16 decoder: max|logits - fp32| {err:.3e} (max|logit| {float(np.abs(expect).max()):.2f}); "
+          f"argmax on decidable positions {agree:.4f} ({share:.1%}), overall {gates.agree(got, expect):.4f}",
+          flush=True)
+    assert err <= 2e-2
+    assert agree == 1.0
 
 
 @pytest.mark.parametrize("name,policy", [("resnet18_cifar", "fp32"), ("resnet18_224", "bf16")])
@@ -111,3 +119,60 @@ def test_deploy_planned_engine_matches_torch(gpu, tmp_path):
         expect = module(x).numpy()
     got = _deploy(tmp_path, path, in_name, x.numpy(), "--engine", "planned", "--batch-size", "2")
     np.testing.assert_allclose(got, expect, rtol=1e-3, atol=1e-4)
+
+
+@pytest.mark.timeout(600)
+def test_deploy_fullsize_decoder_fp16_matches_in_process(gpu, tmp_path):
+    """BASELINE config 4 (decoder fp16, B = 64, S = 256) through the CLI at full
+    size with a ragged batch size (24, 24, 16): logits.npy (537 MB, drained in
+    pinned chunks while the next batch runs), argmax.npy and manifest.json
+    equal, bit for bit, the in-process compiled pipeline run on the same three
+    batches (c35/test_c35.py:22-219 drives the reference's CLI the same way)."""
+    from hackathon_amd import models, onnx_io
+    from hackathon_amd.c35.executor import CrossStageReferencePipeline
+
+    m = models.build("decoder_fp16")
+    path = str(tmp_path / "decoder_fp16.onnx")
+    onnx_io.export_model(m.graph, m.weights, path)
+    (in_name, arr), = m.inputs.items()
+    assert arr.shape == (64, 256)
+    got = _deploy(tmp_path, path, in_name, arr, "--precision", "fp16", "--batch-size", "24")
+    out = str(tmp_path / "out")
+    got_arg = np.load(os.path.join(out, "argmax.npy"))
+    with open(os.path.join(out, "manifest.json")) as f:
+        man = json.load(f)
+    assert man["tensors"] == [{"name": "logits", "file": "logits.npy", "dtype": "float32",
+                               "shape": [64, 256, 8192]}]
+    assert got.shape == (64, 256, 8192) and got_arg.shape == (64, 256) and got_arg.dtype == np.int64
+    pipe = CrossStageReferencePipeline(onnx_io.import_onnx(path), path, engine_kind="compiled", precision="fp16")
+    for start in (0, 24, 48):
+        end = min(start + 24, 64)
+        res = pipe.run({in_name: arr[start:end]})
+        np.testing.assert_array_equal(got[start:end].view(np.uint32), res["logits"].get().view(np.uint32))
+        np.testing.assert_array_equal(got_arg[start:end], res["argmax"].get())
+        print(f"  batch [{start}, {end}): logits and argmax bit-identical to the in-process run", flush=True)
+    # the CLI's own ArgMax output is the first maximum of the logits it wrote
+    np.testing.assert_array_equal(got_arg, np.argmax(got, axis=-1))
+
+
+def test_load_and_infer_rejects_non_finite_logits(gpu, tmp_path):
+    """A batch whose logits hold NaN makes load_and_infer raise ValueError
+    ("Output contains non-finite values", c35/executor.py:1177), found by the
+    device-side check rather than a host scan; a finite run passes."""
+    from hackathon_amd import models, onnx_io
+    from hackathon_amd.c35 import executor
+
+    m = models.build("mlp", batch=8, dims=(784, 10))  # one Gemm, no ReLU to map a NaN to 0
+    path = str(tmp_path / "mlp.onnx")
+    onnx_io.export_model(m.graph, m.weights, path)
+    (in_name, arr), = m.inputs.items()
+    inp = str(tmp_path / "in")
+    _write_inputs(inp, in_name, arr)
+    res = executor.load_and_infer(path, inp, str(tmp_path / "ok"), batch_size=3)
+    assert res["output_shape"] == [8, 10]
+    bad = arr.copy()
+    bad[5, 17] = np.nan  # batch [3, 6) of the ragged 3, 3, 2 split
+    _write_inputs(inp, in_name, bad)
+    with pytest.raises(ValueError, match="non-finite"):
+        executor.load_and_infer(path, inp, str(tmp_path / "bad"), batch_size=3)
+    assert not os.path.exists(tmp_path / "bad" / "logits.npy")  # no partial output

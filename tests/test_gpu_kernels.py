@@ -1415,3 +1415,39 @@ def test_conv_register_pipelined_matches_two_stage(gpu, n, hw, c, o, kh, stride)
     for rp in ("2", "3", "4"):
         got = _with_env("C3H_DISABLE_BIGTILE", "1", lambda: _with_env("C3H_DMA_RP", rp, run))
         np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8), err_msg=f"RP stages {rp}")
+
+
+@pytest.mark.parametrize("kind", ["fp32", "bf16", "fp16"])
+def test_nonfinite_flag(gpu, kind):
+    """c3h_nonfinite: the flag is set by any NaN / +-Inf (vector body and the
+    ragged tail), never by finite values including the largest and subnormals."""
+    from hackathon_amd import _lib
+    from hackathon_amd.device import DeviceArray
+
+    code = {"fp32": _lib.F32, "bf16": _lib.BF16, "fp16": _lib.F16}[kind]
+    big = {"fp32": np.finfo(np.float32).max, "bf16": 3.3895314e38, "fp16": 65504.0}[kind]
+    tiny = {"fp32": 1e-45, "bf16": 1e-39, "fp16": 6e-8}[kind]
+    rng = np.random.default_rng(3)
+    flag = DeviceArray.empty((1,), np.int32)
+
+    def run(x32):
+        host = x32.astype(np.float32) if kind == "fp32" else _bits(x32.astype(np.float32), kind)[0]
+        xd = _dev(host)
+        flag.copy_from_host(np.zeros(1, np.int32))
+        a = _lib.NonfiniteArgs()
+        a.x, a.flag, a.count, a.dtype = xd.ptr, flag.ptr, x32.size, code
+        _lib.launch(a, None)
+        return int(flag.get()[0])
+
+    for n in (1, 7, 8, 1000, 4099, 1 << 20):
+        x = rng.standard_normal(n).astype(np.float32)
+        x[0], x[-1] = big, -big
+        if n > 2:
+            x[n // 2] = tiny
+        print(f"nonfinite {kind} n={n}", flush=True)
+        assert run(x) == 0
+        for pos in sorted({0, n // 3, n - 1}):
+            for bad in (np.nan, np.inf, -np.inf):
+                y = x.copy()
+                y[pos] = bad
+                assert run(y) == 1, (n, pos, bad)

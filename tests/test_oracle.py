@@ -401,6 +401,10 @@ def test_round_bf16_equals_torch_bfloat16_conversion():
     ("resnet18_cifar", dict(batch=2, image=8, widths=(8, 8, 16, 16))),
     ("resnet18_224", dict(batch=1, image=32, widths=(8, 8, 16, 16), classes=20)),
     ("decoder_fp16", dict(batch=2, seq=16, d_model=32, heads=2, ffn=64, layers=2, vocab=50)),
+    # W8A8: QuantizeLinear / QLinearMatMul / DequantizeLinear with calibrated
+    # per-tensor scales (max|x| / 127 of a QDQ-bypassed forward, as the
+    # committed full-size calibration), per-output-channel int8 weights
+    ("decoder_w8a8", dict(batch=2, seq=16, d_model=32, heads=2, ffn=64, layers=2, vocab=50)),
 ])
 def test_plan_decomposition_matches_graph_semantics(name, kw):
     """The fused graph's C3.4 plan, evaluated step by step, equals the unfused ONNX evaluation."""
@@ -411,7 +415,19 @@ def test_plan_decomposition_matches_graph_semantics(name, kw):
     from hackathon_amd.c33.pipeline import GraphPassPipeline
     from hackathon_amd.c34.scheduler import ExecutionScheduler
 
-    m = models.build(name, **kw)
+    if name == "decoder_w8a8":
+        class _Unit(dict):
+            def __missing__(self, key):
+                return 1.0
+
+            def __contains__(self, key):
+                return True
+
+        m = models.build(name, act_scales=_Unit(), **kw)
+        ranges = G.calibration_ranges(m.graph, m.weights, m.inputs)
+        models.apply_activation_scales(m, {n: max(float(ranges[n]), 1e-8) / 127.0 for n in m.meta["quant_scales"]})
+    else:
+        m = models.build(name, **kw)
     base = copy.deepcopy(m.graph)
     want = G.run_graph(base, m.weights, m.inputs)
     GraphPassPipeline().run(m.graph)
