@@ -25,6 +25,7 @@ struct Switches {
   bool disable_direct_conv = false;  // C3H_DISABLE_DIRECT_CONV: no direct narrow-input fp32 conv
   int dma_rp = 0;                // C3H_DMA_RP: register-pipelined DMA stages (0 = off)
   bool disable_pp = false;       // C3H_DISABLE_PP: no ping-pong schedule for 256 x 256 conv tiles
+  bool disable_qmul = false;     // C3H_DISABLE_QMUL: quantize by the division form only
 };
 const Switches& switches();
 
@@ -81,6 +82,10 @@ __device__ __forceinline__ uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
   typedef __attribute__((ext_vector_type(2))) __bf16 b2;
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{lo, hi}, b2));
 }
+// x rounded to bf16 and widened back, bit for bit f32_to_bf16_bits then
+// bf16_bits_to_f32: one v_cvt_pk_bf16_f32 with x in the high half and +0
+// (bf16 0x0000) in the low one.
+__device__ __forceinline__ float bf16_round(float x) { return __uint_as_float(f32x2_to_bf16x2_bits(0.0f, x)); }
 __device__ __forceinline__ uint32_t f32x2_to_f16x2_bits(float lo, float hi) {
   typedef __attribute__((ext_vector_type(2))) float f2;
   typedef __attribute__((ext_vector_type(2))) _Float16 h2;
@@ -206,7 +211,7 @@ __device__ __forceinline__ void store_vec16(T* p, const float* v) {
 // x rounded to the storage type dt (bf16 / fp16; fp32 unchanged) and back:
 // the value a consumer reads after the producer stores x as dt.
 __device__ __forceinline__ float round_to_dtype(float x, int dt) {
-  if (dt == C3H_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
+  if (dt == C3H_BF16) return bf16_round(x);
   if (dt == C3H_F16) return f16_bits_to_f32(f32_to_f16_bits(x));
   return x;
 }
@@ -229,6 +234,17 @@ __device__ __forceinline__ float round_to_dtype(float x, int dt) {
 // Scales QuantDiv serves (and the quantizing entry points accept): positive,
 // normal, finite.
 inline bool quant_scale_ok(float s) { return s >= 0x1p-126f && s <= 3.4028235e38f; }
+
+// Host: a multiplier c such that the int8 code saturate(rne(x * c) +
+// zero) equals saturate(rne(x / scale) + zero) -- the correctly rounded
+// quotient's code, NaN -> -128 on both sides -- for every value x of the
+// 16-bit type `dtype` (C3H_BF16 or C3H_F16: all 65536 encodings are tried).
+// Candidates are fp32(1 / scale) and its neighbours up to 4 ulp away; 0 when
+// none qualifies (or for another dtype, or under C3H_DISABLE_QMUL).  A 16-bit
+// value has at most 11 significant bits, so x / scale lands within an ulp of
+// a rounding boundary (k + 1/2) for few x, and 1 / scale itself qualifies
+// for nearly every scale.  Cached per (scale, zero, dtype).
+float quant_multiplier(float scale, int zero, int dtype);
 
 struct QuantDiv {
   float m, inv;

@@ -410,6 +410,7 @@ int c3h_qgemm(const c3h_qgemm_args* a, void* stream) {
   p.a_scale = a->a_scale; p.y_scale = a->y_scale; p.b_scale = a->b_scale;
   p.y_zero = a->y_zero; p.qmode = a->mode; p.out_dtype = a->out_dtype;
   p.q_scale = requant_out ? a->q_scale : 1.0f; p.q_zero = a->q_zero; p.act_dtype = a->act_dtype;
+  p.q_mul = requant_out ? quant_multiplier(a->q_scale, a->q_zero, a->act_dtype) : 0.0f;
   p.epi = a->epi;
   p.ho = 1; p.wo = 1;
   p.a_bytes = (a->m - 1) * a->lda + a->k;

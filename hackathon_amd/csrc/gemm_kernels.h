@@ -81,6 +81,44 @@ __device__ __forceinline__ float gelu_erf(float x, float c0, float c1, float c2)
   return (x * (erf_cheb(q) + c1)) * c2;
 }
 
+// The chain's constants as every GELU export writes them: c0 = fp32(sqrt 2),
+// c1 = 1, c2 = 0.5.  With these, act 2 evaluates gelu_std.
+__device__ __forceinline__ bool gelu_std_ok(float c0, float c1, float c2) {
+  return c0 == 0x1.6a09e6p+0f && c1 == 1.0f && c2 == 0.5f;
+}
+
+// GELU x Phi(x) for the standard constants, written as
+//   Phi(x) = 1/2 + sign(x) (1/2 - E(|x|)),  E(a) = Phi(-a) = erfc(a / sqrt 2) / 2,
+// with E(a) = 2^P(a): P is a degree-8 polynomial fitted to log2 Phi(-a) on
+// [0, 5.75] by weighted minimax (weight E, so the error is bounded in E
+// itself: 7.6e-9 absolute), |x| clamped at 5.75, where E = 4.1e-9 and
+// 1/2 - E rounds to 1/2 -- as in the chain, where erf rounds to -1 there.
+// One v_exp_f32 and about 13 other VALU operations, against gelu_erf's ~24
+// and two transcendentals.  Evaluated in fp32 it stays within 1.9 |x| 2^-24
+// of x Phi(x) over [-12, 12] (the chain's own roundings: 1.8), and gives the
+// chain's special values: +Inf -> +Inf, -Inf -> NaN, x below -5.5 -> -0,
+// NaN -> NaN.
+__device__ __forceinline__ float gelu_std(float x) {
+  const float a = fminf(fabsf(x), 5.75f);
+  float p = -0x1.740f9ep-19f;
+  p = fmaf(p, a, 0x1.43fa00p-15f);
+  p = fmaf(p, a, -0x1.7ed53ap-13f);
+  p = fmaf(p, a, -0x1.31e784p-13f);
+  p = fmaf(p, a, 0x1.cfb2a2p-8f);
+  p = fmaf(p, a, -0x1.ae1f04p-5f);
+  p = fmaf(p, a, -0x1.d639d0p-2f);
+  p = fmaf(p, a, -0x1.26aedep+0f);
+  p = fmaf(p, a, -1.0f);
+  const float e = __builtin_amdgcn_exp2f(p);  // p in [-27.9, -1]: no range reduction needed
+  return x * (0.5f + __builtin_copysignf(0.5f - e, x));
+}
+
+// act 2 where the constants are only known at run time (uniform `std_form`
+// from gelu_std_ok, hoisted by the caller).
+__device__ __forceinline__ float gelu_act(float x, float c0, float c1, float c2, bool std_form) {
+  return std_form ? gelu_std(x) : gelu_erf(x, c0, c1, c2);
+}
+
 // ---------------------------------------------------------------- epilogue
 // `e` is read straight from the kernel-argument segment (uniform scalar
 // loads); `bias_off` selects the batch's bias slice.
@@ -97,7 +135,7 @@ __device__ __forceinline__ float apply_epilogue(const KArg<c3h_epilogue>& e, flo
   }
   v += res;
   if (e.act == 1) v = fmaxf(v, 0.0f);
-  else if (e.act == 2) v = gelu_erf(v, e.imm[0], e.imm[1], e.imm[2]);
+  else if (e.act == 2) v = gelu_act(v, e.imm[0], e.imm[1], e.imm[2], gelu_std_ok(e.imm[0], e.imm[1], e.imm[2]));
   if (e.n_inst > 0) {
     // Linear program: operand 0 = x (the value entering the program),
     // 1 = previous result, 2 + j = imm[j].  No register file, so the
@@ -159,8 +197,9 @@ __device__ __forceinline__ void apply_epilogue8(const KArg<c3h_epilogue>& e, flo
     for (int c = 0; c < 8; ++c) v[c] = fmaxf(v[c], 0.0f);
   } else if (act == 2) {
     const float c0 = e.imm[0], c1 = e.imm[1], c2 = e.imm[2];
+    const bool sf = gelu_std_ok(c0, c1, c2);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) v[c] = gelu_erf(v[c], c0, c1, c2);
+    for (int c = 0; c < 8; ++c) v[c] = gelu_act(v[c], c0, c1, c2, sf);
   }
   const int ni = e.n_inst;
   if (ni > 0) {
@@ -225,6 +264,10 @@ struct Problem {
   const float* b_scale;
   float q_scale;
   int q_zero, act_dtype;
+  // q_mul != 0: rne(x * q_mul) equals rne(x / q_scale) for every value x of
+  // act_dtype (checked over all 65536 encodings on the host), so the
+  // interior epilogue quantizes with one multiply
+  float q_mul;
   const float* a_rows;  // fp8 GEMM (c3h_gemm_fp8): per-row A scale
   // W4A16 GEMM (c3h_gemm_w4a16): B holds E2M1 codes [n][ldb bytes]; b_blk the
   // E8M0 exponents [n][ldbs] of its 32-element blocks (bs_bytes in all)
@@ -877,6 +920,7 @@ __device__ __forceinline__ void epilogue_direct_impl(const Acc (&acc)[TM][TN], i
   const bool relu = !G && act == 1;
   constexpr bool gelu = G;
   const float g0 = G ? p.epi.imm[0] : 0.0f, g1 = G ? p.epi.imm[1] : 0.0f, g2 = G ? p.epi.imm[2] : 0.0f;
+  const bool gstd = G && gelu_std_ok(g0, g1, g2);
   const int l16 = lane & 15, lg = lane >> 4;
   const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
   // Bias of this lane's columns, for every column tile.
@@ -919,7 +963,7 @@ __device__ __forceinline__ void epilogue_direct_impl(const Acc (&acc)[TM][TN], i
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             float t = (v[r] + b[j][r]) + res[j][r];
-            v[r] = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t);
+            v[r] = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_act(t, g0, g1, g2, gstd) : t);
             if (rb) best[j / 4].see(stored_value<TO>(v[r]));
           }
           Elem<TO>::store4(outp + m * ldo + n, v);
@@ -929,7 +973,7 @@ __device__ __forceinline__ void epilogue_direct_impl(const Acc (&acc)[TM][TN], i
             if (n + r < pn) {
               const int64_t o = m * ldo + n + r;
               float t = (v[r] + (bias ? bias[n + r] : 0.0f)) + (resp ? Elem<TO>::to_f32(resp[o]) : 0.0f);
-              const float y = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t);
+              const float y = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_act(t, g0, g1, g2, gstd) : t);
               outp[o] = Elem<TO>::from_f32(y);
               if (rb) best[j / 4].see(stored_value<TO>(y));
             }
@@ -944,7 +988,8 @@ __device__ __forceinline__ void epilogue_direct_impl(const Acc (&acc)[TM][TN], i
 // GELU: act 2 is computed in registers only by the instantiations that ask
 // for it (the large-tile kernel, which has no staged epilogue).
 // epilogue_direct for a wave tile wholly inside the output: no bounds tests,
-// the activation fixed at compile time (ACT: 0 none, 1 ReLU, 2 GELU).  Same
+// the activation fixed at compile time (ACT: 0 none, 1 ReLU, 2 GELU with
+// run-time constants, 3 GELU with the standard ones, gelu_std).  Same
 // arithmetic: ((acc + b) + res), then the activation.
 template <typename TO, int TM, int TN, int ACT, bool RB, typename Acc>
 __device__ __forceinline__ void epilogue_direct_interior(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase,
@@ -986,7 +1031,7 @@ __device__ __forceinline__ void epilogue_direct_interior(const Acc (&acc)[TM][TN
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float t = (acc[i][j][r] + b[j][r]) + res[j][r];
-        v[r] = ACT == 1 ? fmaxf(t, 0.0f) : (ACT == 2 ? gelu_erf(t, g0, g1, g2) : t);
+        v[r] = ACT == 1 ? fmaxf(t, 0.0f) : (ACT == 3 ? gelu_std(t) : (ACT == 2 ? gelu_erf(t, g0, g1, g2) : t));
         if constexpr (RB) best[j / 4].see(stored_value<TO>(v[r]));
       }
       Elem<TO>::store4(base + 16 * i * ldo + 16 * j, v);
@@ -1012,8 +1057,10 @@ __device__ __forceinline__ void epilogue_direct(const Acc (&acc)[TM][TN], int64_
       return;
     }
     if constexpr (GELU) {
-      if (!rb) {
-        epilogue_direct_interior<TO, TM, TN, 2, false>(acc, mbase, nbase, lane, outp, resp, bias);
+      // GELU interiors for the standard constants only; others take the
+      // general form below
+      if (!rb && gelu_std_ok(p.epi.imm[0], p.epi.imm[1], p.epi.imm[2])) {
+        epilogue_direct_interior<TO, TM, TN, 3, false>(acc, mbase, nbase, lane, outp, resp, bias);
         return;
       }
     }
@@ -1033,6 +1080,7 @@ __device__ __forceinline__ void epilogue_direct_q_impl(const Acc (&acc)[TM][TN],
   const bool relu = !G && act == 1;
   constexpr bool gelu = G;
   const float g0 = G ? p.epi.imm[0] : 0.0f, g1 = G ? p.epi.imm[1] : 0.0f, g2 = G ? p.epi.imm[2] : 0.0f;
+  const bool gstd = G && gelu_std_ok(g0, g1, g2);
   const int l16 = lane & 15, lg = lane >> 4;
   const int64_t pm = p.m, pn = p.n, ldo = p.ldo;
   const int mode = p.qmode;
@@ -1112,7 +1160,7 @@ __device__ __forceinline__ void epilogue_direct_q_impl(const Acc (&acc)[TM][TN],
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                   const float t = v[r] + b[j][r];
-                  const float y = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t);
+                  const float y = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_act(t, g0, g1, g2, gstd) : t);
                   v[r] = static_cast<float>(qd.code(round_to_dtype(y, act_dt), qz));
                 }
               }
@@ -1132,7 +1180,7 @@ __device__ __forceinline__ void epilogue_direct_q_impl(const Acc (&acc)[TM][TN],
                 float rr = res[j][r];
                 if (resp && !nfull && n + r < pn) rr = Elem<TO>::to_f32(resp[o + r]);
                 const float t = (v[r] + b[j][r]) + rr;
-                v[r] = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_erf(t, g0, g1, g2) : t);
+                v[r] = relu ? fmaxf(t, 0.0f) : (gelu ? gelu_act(t, g0, g1, g2, gstd) : t);
                 if (rb && n + r < pn) best[j / 4].see(stored_value<TO>(v[r]));
               }
               if (nfull) {
@@ -1191,8 +1239,17 @@ __device__ __forceinline__ void scale_acc(f32x4 (&acc)[TM][TN], int64_t mbase, i
 // branches made the epilogue cost more VALU issue than a K = 768 main loop).
 // KIND: 0 int32 accumulators (mode 0), 1 int8 codes (mode 1), 2 / 3 float
 // output of mode 2 / 3, 4 / 5 int8 output of mode 2 / 3 quantized from the
-// bf16-rounded epilogue value.  ACT: 0 none, 1 ReLU, 2 GELU.  Arithmetic
-// identical to epilogue_direct_q_impl.
+// bf16-rounded epilogue value by the verified multiplier p.q_mul.  ACT: 0
+// none, 1 ReLU, 2 GELU with run-time constants, 3 GELU with the standard
+// ones (gelu_std).  Same values as epilogue_direct_q_impl, in fewer
+// operations:
+//   requantized y = saturate(rne(a * mult) + zy); mode 3 stores (y - zy) * sy,
+//     which is rne(a * mult) clamped to [-128 - zy, 127 - zy], times sy (all
+//     integers exact in fp32: one v_med3_f32 instead of add, clamp, subtract;
+//     a NaN rne(.) gives the lower bound, as fmaxf then fminf do: v_med3_f32
+//     returns min3 of its operands when one is NaN)
+//   int8 codes are rne(.) + (zero + 128) through v_cvt_pk_u8_f32 (clamp to
+//     [0, 255], NaN -> 0, byte insert), XOR 0x80 per byte
 template <typename TO, int TM, int TN, int KIND, int ACT, bool RB, typename Acc>
 __device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
                                                     TO* outp, const TO* resp, const float* bias) {
@@ -1205,9 +1262,9 @@ __device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], in
   const int l16 = lane & 15, lg = lane >> 4;
   const int64_t ldo = p.ldo;
   const float sa = p.a_scale, sy = p.y_scale, zy = static_cast<float>(p.y_zero);
+  const float lo = -128.0f - zy, hi = 127.0f - zy, zb = zy + 128.0f;
   const float g0 = p.epi.imm[0], g1 = p.epi.imm[1], g2 = p.epi.imm[2];
-  const QuantDiv qd(kQuantOut ? p.q_scale : 1.0f);
-  const int qz = p.q_zero;
+  const float qmul = p.q_mul, qb = static_cast<float>(p.q_zero + 128);
   float mult[TN][4], b[TN][4];
   if constexpr (KIND != 0) {
     // Requantizing, each of the wave tile's 16 TN columns forms its
@@ -1264,27 +1321,26 @@ __device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], in
       static_for<TN>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
         float v[4];
+        uint32_t w = 0u;  // biased int8 codes (KIND 1, 4, 5)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float a = static_cast<float>(acc[i][j][r]);
-          if constexpr (kReq) {
-            const float y = fminf(fmaxf(rintf(a * mult[j][r]) + zy, -128.0f), 127.0f);
-            v[r] = KIND == 1 ? y : (y - zy) * sy;
+          if constexpr (KIND == 1) {
+            w = __builtin_amdgcn_cvt_pk_u8_f32(rintf(a * mult[j][r]) + zb, r, w);
           } else {
-            v[r] = a * mult[j][r];
-          }
-          if constexpr (KIND >= 2) {
+            if constexpr (kReq) {
+              v[r] = __builtin_amdgcn_fmed3f(rintf(a * mult[j][r]), lo, hi) * sy;
+            } else {
+              v[r] = a * mult[j][r];
+            }
             const float t = kQuantOut ? v[r] + b[j][r] : (v[r] + b[j][r]) + res[j][r];
-            v[r] = ACT == 1 ? fmaxf(t, 0.0f) : (ACT == 2 ? gelu_erf(t, g0, g1, g2) : t);
+            v[r] = ACT == 1 ? fmaxf(t, 0.0f) : (ACT == 3 ? gelu_std(t) : (ACT == 2 ? gelu_erf(t, g0, g1, g2) : t));
+            if constexpr (kQuantOut) w = __builtin_amdgcn_cvt_pk_u8_f32(rintf(bf16_round(v[r]) * qmul) + qb, r, w);
+            if constexpr (RB) best[j / 4].see(stored_value<TO>(v[r]));
           }
-          if constexpr (kQuantOut) v[r] = static_cast<float>(qd.code(bf16_bits_to_f32(f32_to_bf16_bits(v[r])), qz));
-          if constexpr (RB) best[j / 4].see(stored_value<TO>(v[r]));
         }
         if constexpr (std::is_same<TO, int8_t>::value) {
-          uint32_t w = 0u;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) w |= (static_cast<uint32_t>(static_cast<int8_t>(v[r])) & 0xffu) << (8 * r);
-          *reinterpret_cast<uint32_t*>(row + 16 * j) = w;
+          *reinterpret_cast<uint32_t*>(row + 16 * j) = w ^ 0x80808080u;
         } else {
           Elem<TO>::store4(row + 16 * j, v);
         }
@@ -1299,8 +1355,10 @@ __device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int6
                                                   TO* outp, const TO* resp, const float* bias, int act) {
   const KArg<Problem>& p = kernel_arg<Problem>();
   // Interior wave tile: the specialized form (int8 outputs of modes 2 / 3
-  // only when rounded through bf16, the W8A8 activation type).
-  if (mbase + 16 * TM <= p.m && nbase + 16 * TN <= p.n && act <= (GELU ? 2 : 1)) {
+  // only when rounded through bf16, the W8A8 activation type, with a
+  // verified multiplier; GELU only with the standard constants).
+  const bool gstd = GELU && act == 2 && gelu_std_ok(p.epi.imm[0], p.epi.imm[1], p.epi.imm[2]);
+  if (mbase + 16 * TM <= p.m && nbase + 16 * TN <= p.n && (act <= 1 || gstd)) {
     const int mode = p.qmode;
     if constexpr (std::is_same<TO, int32_t>::value) {
       epilogue_q_interior<TO, TM, TN, 0, 0, false>(acc, mbase, nbase, lane, outp, resp, bias);
@@ -1310,7 +1368,7 @@ __device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int6
         epilogue_q_interior<TO, TM, TN, 1, 0, false>(acc, mbase, nbase, lane, outp, resp, bias);
         return;
       }
-      if (p.act_dtype == C3H_BF16) {
+      if (p.act_dtype == C3H_BF16 && p.q_mul != 0.0f) {
         const bool m3 = mode == 3;
         if (act == 0) {
           if (m3) epilogue_q_interior<TO, TM, TN, 5, 0, false>(acc, mbase, nbase, lane, outp, resp, bias);
@@ -1319,8 +1377,8 @@ __device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int6
           if (m3) epilogue_q_interior<TO, TM, TN, 5, 1, false>(acc, mbase, nbase, lane, outp, resp, bias);
           else epilogue_q_interior<TO, TM, TN, 4, 1, false>(acc, mbase, nbase, lane, outp, resp, bias);
         } else if constexpr (GELU) {
-          if (m3) epilogue_q_interior<TO, TM, TN, 5, 2, false>(acc, mbase, nbase, lane, outp, resp, bias);
-          else epilogue_q_interior<TO, TM, TN, 4, 2, false>(acc, mbase, nbase, lane, outp, resp, bias);
+          if (m3) epilogue_q_interior<TO, TM, TN, 5, 3, false>(acc, mbase, nbase, lane, outp, resp, bias);
+          else epilogue_q_interior<TO, TM, TN, 4, 3, false>(acc, mbase, nbase, lane, outp, resp, bias);
         }
         return;
       }
@@ -1341,8 +1399,8 @@ __device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int6
         if (m3) epilogue_q_interior<TO, TM, TN, 3, 1, false>(acc, mbase, nbase, lane, outp, resp, bias);
         else epilogue_q_interior<TO, TM, TN, 2, 1, false>(acc, mbase, nbase, lane, outp, resp, bias);
       } else if constexpr (GELU) {
-        if (m3) epilogue_q_interior<TO, TM, TN, 3, 2, false>(acc, mbase, nbase, lane, outp, resp, bias);
-        else epilogue_q_interior<TO, TM, TN, 2, 2, false>(acc, mbase, nbase, lane, outp, resp, bias);
+        if (m3) epilogue_q_interior<TO, TM, TN, 3, 3, false>(acc, mbase, nbase, lane, outp, resp, bias);
+        else epilogue_q_interior<TO, TM, TN, 2, 3, false>(acc, mbase, nbase, lane, outp, resp, bias);
       }
       return;
     }

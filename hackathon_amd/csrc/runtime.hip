@@ -2,8 +2,11 @@
 // logical streams/events, and the native timeline interpreter with hipGraph
 // capture.  Realizes the resource model of c35/executor.py:673-709 and
 // :757-868 in C++ so a compiled plan replays without Python in the loop.
+#include <math.h>
 #include <stdarg.h>
 #include <stdlib.h>
+#include <mutex>
+#include <unordered_map>
 #include <vector>
 #include "common.h"
 
@@ -36,12 +39,71 @@ static Switches read_switches() {
   const char* rp = getenv("C3H_DMA_RP");
   w.dma_rp = rp ? atoi(rp) : 0;
   w.disable_pp = getenv("C3H_DISABLE_PP") != nullptr;
+  w.disable_qmul = getenv("C3H_DISABLE_QMUL") != nullptr;
   return w;
 }
 
 static Switches g_switches = read_switches();
 
 const Switches& switches() { return g_switches; }
+
+float quant_multiplier(float scale, int zero, int dtype) {
+  if (switches().disable_qmul || !quant_scale_ok(scale) || zero < -128 || zero > 127 ||
+      (dtype != C3H_BF16 && dtype != C3H_F16))
+    return 0.0f;
+  static std::mutex mu;
+  static std::unordered_map<uint64_t, float> cache;
+  uint32_t sbits;
+  memcpy(&sbits, &scale, 4);
+  const uint64_t key = (static_cast<uint64_t>(sbits) << 32) | (static_cast<uint64_t>(zero & 0xff) << 8) |
+                       static_cast<uint64_t>(dtype & 0xff);
+  {
+    std::lock_guard<std::mutex> g(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
+  // The code as the kernels form it: rne, + zero_point + 128, v_cvt_pk_u8_f32
+  // (clamp to [0, 255], NaN -> 0), - 128.
+  const float zp128 = static_cast<float>(zero + 128);
+  auto code = [zp128](float q) -> int {
+    const float v = nearbyintf(q) + zp128;
+    if (v != v) return -128;
+    return static_cast<int>(fminf(fmaxf(v, 0.0f), 255.0f)) - 128;
+  };
+  std::vector<float> xs(65536);
+  std::vector<int8_t> want(65536);
+  for (uint32_t u = 0; u < 65536; ++u) {
+    if (dtype == C3H_BF16) {
+      const uint32_t w = u << 16;
+      memcpy(&xs[u], &w, 4);
+    } else {
+      const uint16_t h = static_cast<uint16_t>(u);
+      _Float16 f;
+      memcpy(&f, &h, 2);
+      xs[u] = static_cast<float>(f);
+    }
+    want[u] = static_cast<int8_t>(code(xs[u] / scale));  // IEEE division: the QuantizeLinear code
+  }
+  const float c0 = 1.0f / scale;
+  uint32_t cbits;
+  memcpy(&cbits, &c0, 4);
+  float found = 0.0f;
+  for (int d : {0, 1, -1, 2, -2, 3, -3, 4, -4}) {
+    const uint32_t tb = cbits + static_cast<uint32_t>(d);
+    float c;
+    memcpy(&c, &tb, 4);
+    if (!(c > 0.0f) || c > 3.4028235e38f) continue;
+    bool ok = true;
+    for (uint32_t u = 0; u < 65536 && ok; ++u) ok = code(xs[u] * c) == want[u];
+    if (ok) {
+      found = c;
+      break;
+    }
+  }
+  std::lock_guard<std::mutex> g(mu);
+  cache[key] = found;
+  return found;
+}
 
 }  // namespace c3h
 

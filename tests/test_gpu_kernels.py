@@ -760,10 +760,12 @@ def test_gemm_big_tile_matches_128_tiles(gpu, kind, out_kind, act, m, n, k):
     np.testing.assert_allclose(got, want, rtol=tol, atol=tol * 4)
 
 
-def test_gemm_gelu_epilogue_matches_the_chain(gpu):
+@pytest.mark.parametrize("c0,c1,c2", [(math.sqrt(2.0), 1.0, 0.5),   # the standard constants: gelu_std
+                                      (1.5, 1.0, 0.5)])            # others: the chain form, gelu_erf
+def test_gemm_gelu_epilogue_matches_the_chain(gpu, c0, c1, c2):
     """The GEMM GELU epilogue (act 2) on exact accumulators x (A = [x, 0, 0, 0],
-    B row 0 = 1): equal to the decomposed chain ((x * (erf(x / sqrt 2) + 1)) *
-    0.5) evaluated in fp32 with a correctly rounded erf, within 2^-21 relative
+    B row 0 = 1): equal to the decomposed chain ((x * (erf(x / c0) + c1)) *
+    c2) evaluated in fp32 with a correctly rounded erf, within 2^-21 relative
     plus |x| 2^-22 (two fp32 steps of erf near +-1, where the chain's own
     rounding of erf dominates), over [-12, 12] and the special values."""
     from hackathon_amd import _lib
@@ -786,17 +788,17 @@ def test_gemm_gelu_epilogue_matches_the_chain(gpu):
     g.a, g.b, g.out = ad.ptr, bd.ptr, out.ptr
     g.m, g.n, g.k, g.lda, g.ldb, g.ldo, g.batch = m, n, 4, 4, n, n, 1
     g.trans_a, g.trans_b, g.in_dtype, g.out_dtype = 0, 0, _lib.F32, _lib.F32
-    g.epi = E.epilogue(act=2, imm=[math.sqrt(2.0), 1.0, 0.5])
-    print(f"gemm fp32 gelu epilogue m={m}", flush=True)
+    g.epi = E.epilogue(act=2, imm=[c0, c1, c2])
+    print(f"gemm fp32 gelu epilogue m={m} constants {c0, c1, c2}", flush=True)
     _lib.launch(g, None)
     got = out.get()[: x.size]
     np.testing.assert_array_equal(got, np.repeat(got[:, :1], n, axis=1))
     got = got[:, 0].astype(np.float64)
     f = np.float32
-    q = (x / f(math.sqrt(2.0))).astype(f)
+    q = (x / f(c0)).astype(f)
     e = erf(q.astype(np.float64)).astype(f)
     with np.errstate(invalid="ignore"):
-        ref = ((x * (e + f(1.0))).astype(f) * f(0.5)).astype(f).astype(np.float64)
+        ref = ((x * (e + f(c1))).astype(f) * f(c2)).astype(f).astype(np.float64)
     fin = np.isfinite(ref)
     tol = 2.0 ** -21 * np.abs(ref[fin]) + np.abs(x[fin].astype(np.float64)) * 2.0 ** -22 + 1e-38
     err = np.abs(got[fin] - ref[fin])
@@ -906,19 +908,25 @@ def test_qgemm_big_tile_matches_128_tiles(gpu, m, n, k, mode, act):
         np.testing.assert_array_equal(big[rows], a[rows].astype(np.int64) @ bt.T.astype(np.int64))
 
 
-@pytest.mark.parametrize("m,n,k,mode,act,act_kind,switch", [
-    (4096, 4096, 256, 3, 2, "bf16", None),                      # 256x256 tile, GELU in registers
-    (4096, 4096, 256, 3, 2, "bf16", "C3H_DISABLE_BIGTILE"),     # 128x128 DMA tile, staged GELU epilogue
-    (300, 200, 256, 3, 1, "fp16", None),                        # 128x128, direct epilogue
-    (300, 70, 256, 2, 0, "fp32", None),                         # unaligned rows: staged, partial stores
-    (300, 200, 256, 3, 2, "bf16", "C3H_DISABLE_DMA"),           # register-prefetch kernel
-    (16384, 3072, 768, 3, 2, "bf16", None),                     # W8A8 FFN1
+@pytest.mark.parametrize("m,n,k,mode,act,act_kind,switch,qscale", [
+    (4096, 4096, 256, 3, 2, "bf16", None, 0.0417),                  # 256x256 tile, GELU in registers
+    (4096, 4096, 256, 3, 2, "bf16", "C3H_DISABLE_BIGTILE", 0.0417), # 128x128 DMA tile, staged GELU epilogue
+    (300, 200, 256, 3, 1, "fp16", None, 0.0417),                    # 128x128, direct epilogue
+    (300, 70, 256, 2, 0, "fp32", None, 0.0417),                     # unaligned rows: staged, partial stores
+    (300, 200, 256, 3, 2, "bf16", "C3H_DISABLE_DMA", 0.0417),       # register-prefetch kernel
+    (16384, 3072, 768, 3, 2, "bf16", None, 0.0417),                 # W8A8 FFN1
+    (4096, 4096, 256, 2, 1, "bf16", None, 0.06),                    # multiplier fp32(1 / 0.06) - 1 ulp
+    (4096, 4096, 256, 3, 2, "bf16", "C3H_DISABLE_QMUL", 0.0417),    # division form in the interior tiles too
 ])
-def test_qgemm_int8_output_equals_qgemm_then_quantize(gpu, m, n, k, mode, act, act_kind, switch):
+def test_qgemm_int8_output_equals_qgemm_then_quantize(gpu, m, n, k, mode, act, act_kind, switch, qscale):
     """Modes 2 / 3 with an int8 output (the QuantizeLinear after the epilogue
     in the same launch) give exactly the codes of the two-launch form: the
     float epilogue stored in act_kind, then c3h_quantize -- with saturated
-    codes and a nonzero zero point."""
+    codes and a nonzero zero point.  The interior tiles of a bf16 activation
+    quantize with one multiply by a multiplier the host checked against the
+    division over all 65536 bf16 values: fp32(1 / q_scale) for 0.0417, its
+    neighbour 1 ulp below for 0.06 (where x / 0.06 sits on a rounding tie
+    for some x and fp32(1 / 0.06) rounds those the other way)."""
     from hackathon_amd import _lib
     from hackathon_amd.c35 import engine as E
     from hackathon_amd.device import BF16, DeviceArray
@@ -930,7 +938,7 @@ def test_qgemm_int8_output_equals_qgemm_then_quantize(gpu, m, n, k, mode, act, a
     bias = rng.standard_normal(n).astype(np.float32)
     ad, bd, sbd, biasd = _dev(a), _dev(bt), _dev(sb), _dev(bias)
     code, sdt = {"fp32": (_lib.F32, np.float32), "bf16": (_lib.BF16, BF16), "fp16": (_lib.F16, np.float16)}[act_kind]
-    qscale, qzero = 0.0417, 3
+    qzero = 3
     mid = DeviceArray.empty((m, n), sdt)
     want = DeviceArray.empty((m, n), np.int8)
     got = DeviceArray.empty((m, n), np.int8)
