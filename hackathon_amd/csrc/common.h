@@ -249,6 +249,10 @@ float quant_multiplier(float scale, int zero, int dtype);
 struct QuantDiv {
   float m, inv;
   int e;
+  // quant_multiplier(scale, zero, dtype) when the values codes4 / codes8 see
+  // are all of that 16-bit dtype: their codes are then rne(x * mul), one
+  // multiply, with the same result; 0 = the division form
+  float mul = 0.0f;
   __device__ __forceinline__ explicit QuantDiv(float scale) {
     int ex = 0;
     m = 2.0f * frexpf(scale, &ex);
@@ -258,11 +262,13 @@ struct QuantDiv {
   // The same split made on the host (frexpf and an IEEE fp32 division give
   // the same m, e and inv there), passed to kernels that would otherwise
   // form it once per wave.
-  __host__ __device__ QuantDiv(float m_, float inv_, int e_) : m(m_), inv(inv_), e(e_) {}
-  static QuantDiv on_host(float scale) {
+  __host__ __device__ QuantDiv(float m_, float inv_, int e_, float mul_ = 0.0f) : m(m_), inv(inv_), e(e_), mul(mul_) {}
+  // dtype: the 16-bit type of every value to be quantized (C3H_BF16 /
+  // C3H_F16) for the one-multiply form, or -1
+  static QuantDiv on_host(float scale, int zero = 0, int dtype = -1) {
     int ex = 0;
     const float mm = 2.0f * frexpf(scale, &ex);
-    return QuantDiv(mm, 1.0f / mm, ex - 1);
+    return QuantDiv(mm, 1.0f / mm, ex - 1, dtype >= 0 ? quant_multiplier(scale, zero, dtype) : 0.0f);
   }
   __device__ __forceinline__ float quotient(float x) const {
     const float y = ldexpf(x, -e);
@@ -281,20 +287,32 @@ struct QuantDiv {
   __device__ __forceinline__ int8_t code(float x, int zero_point) const {
     return static_cast<int8_t>(biased_byte(x, static_cast<float>(zero_point + 128), 0u, 0u) ^ 0x80u);
   }
-  // 4 codes packed little-endian into one word.
+  // 4 codes packed little-endian into one word (x of the dtype `mul` was
+  // checked for, when it is nonzero).
   __device__ __forceinline__ uint32_t codes4(const float* x, int zero_point) const {
     const float zp128 = static_cast<float>(zero_point + 128);
     uint32_t w = 0u;
+    if (mul != 0.0f) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) w = biased_byte(x[k], zp128, static_cast<uint32_t>(k), w);
+      for (int k = 0; k < 4; ++k) w = __builtin_amdgcn_cvt_pk_u8_f32(rintf(x[k] * mul) + zp128, k, w);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w = biased_byte(x[k], zp128, static_cast<uint32_t>(k), w);
+    }
     return w ^ 0x80808080u;
   }
   // 8 codes packed little-endian into two words.
   __device__ __forceinline__ uint2 codes8(const float* x, int zero_point) const {
     const float zp128 = static_cast<float>(zero_point + 128);
     uint32_t w[2] = {0u, 0u};
+    if (mul != 0.0f) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) w[k >> 2] = biased_byte(x[k], zp128, static_cast<uint32_t>(k & 3), w[k >> 2]);
+      for (int k = 0; k < 8; ++k)
+        w[k >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(rintf(x[k] * mul) + zp128, k & 3, w[k >> 2]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) w[k >> 2] = biased_byte(x[k], zp128, static_cast<uint32_t>(k & 3), w[k >> 2]);
+    }
     return uint2{w[0] ^ 0x80808080u, w[1] ^ 0x80808080u};
   }
 };

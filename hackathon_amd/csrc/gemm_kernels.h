@@ -1250,12 +1250,18 @@ __device__ __forceinline__ void scale_acc(f32x4 (&acc)[TM][TN], int64_t mbase, i
 //     returns min3 of its operands when one is NaN)
 //   int8 codes are rne(.) + (zero + 128) through v_cvt_pk_u8_f32 (clamp to
 //     [0, 255], NaN -> 0, byte insert), XOR 0x80 per byte
-template <typename TO, int TM, int TN, int KIND, int ACT, bool RB, typename Acc>
+//   NBR (KIND 3, no bias, no residual, sy normal with 255 |sy| finite):
+//     (y - zy) * sy + 0 + 0 as one fma with a +0 addend -- the zero addend
+//     turns -0 into +0 as the additions do, and with |y - zy| >= 1 or 0 the
+//     product never rounds to zero -- and every value is finite (the clamp
+//     maps NaN and +-Inf to its bounds), so row maxima track no NaN.
+template <typename TO, int TM, int TN, int KIND, int ACT, bool RB, bool NBR = false, typename Acc>
 __device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], int64_t mbase, int64_t nbase, int lane,
                                                     TO* outp, const TO* resp, const float* bias) {
   // Each product and sum rounds on its own, as in the general form (no
   // multiply-add contraction of the dequantization with the bias).
 #pragma clang fp contract(off)
+  static_assert(!NBR || (KIND == 3 && ACT == 0), "NBR: mode-3 float output without activation");
   const KArg<Problem>& p = kernel_arg<Problem>();
   constexpr bool kReq = KIND == 1 || KIND == 3 || KIND == 5;
   constexpr bool kQuantOut = KIND >= 4;
@@ -1327,6 +1333,9 @@ __device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], in
           const float a = static_cast<float>(acc[i][j][r]);
           if constexpr (KIND == 1) {
             w = __builtin_amdgcn_cvt_pk_u8_f32(rintf(a * mult[j][r]) + zb, r, w);
+          } else if constexpr (NBR) {
+            v[r] = fmaf(__builtin_amdgcn_fmed3f(rintf(a * mult[j][r]), lo, hi), sy, 0.0f);
+            if constexpr (RB) best[j / 4].v = fmaxf(best[j / 4].v, v[r]);
           } else {
             if constexpr (kReq) {
               v[r] = __builtin_amdgcn_fmed3f(rintf(a * mult[j][r]), lo, hi) * sy;
@@ -1385,7 +1394,10 @@ __device__ __forceinline__ void epilogue_direct_q(const Acc (&acc)[TM][TN], int6
     } else {
       const bool m3 = mode == 3;
       if (p.epi.row_max != nullptr) {  // host: only with act <= 1
-        if (act == 0) {
+        const float asy = fabsf(p.y_scale);
+        if (act == 0 && m3 && !bias && !resp && asy >= 0x1p-126f && asy <= 0x1p119f) {
+          epilogue_q_interior<TO, TM, TN, 3, 0, true, true>(acc, mbase, nbase, lane, outp, resp, bias);
+        } else if (act == 0) {
           if (m3) epilogue_q_interior<TO, TM, TN, 3, 0, true>(acc, mbase, nbase, lane, outp, resp, bias);
           else epilogue_q_interior<TO, TM, TN, 2, 0, true>(acc, mbase, nbase, lane, outp, resp, bias);
         } else {

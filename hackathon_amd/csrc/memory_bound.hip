@@ -455,16 +455,21 @@ struct LnStore {
 };
 template <typename TX>
 struct LnStore<TX, int8_t> {
+  // y rounded to TX, the value c3h_quantize would read back
+  static __device__ __forceinline__ float stored(float y) {
+    if constexpr (std::is_same<TX, bf16_t>::value) return bf16_round(y);
+    else return Elem<TX>::to_f32(Elem<TX>::from_f32(y));
+  }
   static __device__ __forceinline__ void store8(int8_t* p, const float* y, const QuantDiv& qd, int qz) {
     float r[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = Elem<TX>::to_f32(Elem<TX>::from_f32(y[e]));
+    for (int e = 0; e < 8; ++e) r[e] = stored(y[e]);
     *reinterpret_cast<uint2*>(p) = qd.codes8(r, qz);
   }
   static __device__ __forceinline__ void store4(int8_t* p, const float* y, const QuantDiv& qd, int qz) {
     float r[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = Elem<TX>::to_f32(Elem<TX>::from_f32(y[e]));
+    for (int e = 0; e < 4; ++e) r[e] = stored(y[e]);
     *reinterpret_cast<uint32_t*>(p) = qd.codes4(r, qz);
   }
 };
@@ -1037,11 +1042,10 @@ __global__ void quantize_kernel(c3h_quantize_args a) {
 // 8 elements per thread: one 16-byte (16-bit input) or 32-byte (fp32) load,
 // one 8-byte int8 store; the same QuantDiv codes as quantize_kernel.
 template <typename TX>
-__global__ void __launch_bounds__(kBlock) quantize_vec_kernel(c3h_quantize_args a) {
+__global__ void __launch_bounds__(kBlock) quantize_vec_kernel(c3h_quantize_args a, QuantDiv qd) {
   const int64_t nvec = a.count / 8;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   const TX* x = static_cast<const TX*>(a.x);
-  const QuantDiv qd(a.scale);
   // two vectors per iteration, both loads issued before either is quantized
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec; i += 2 * stride) {
     const int64_t i2 = i + stride;
@@ -1251,7 +1255,10 @@ void launch_ln(const c3h_layernorm_args& a, int nv, void* stream) {
   const dim3 b(kBlock);
   hipStream_t st = as_stream(stream);
   auto grid = [&](int rows_per_wave) { return dim3(static_cast<unsigned>(ceil_div(a.rows, 4 * rows_per_wave))); };
-  const QuantDiv qd = QuantDiv::on_host(std::is_same<TO, int8_t>::value ? a.out_scale : 1.0f);
+  // the values quantized are the LayerNorm outputs rounded to TX
+  const QuantDiv qd = std::is_same<TO, int8_t>::value
+                          ? QuantDiv::on_host(a.out_scale, a.out_zero, std::is_same<TX, float>::value ? -1 : a.x_dtype)
+                          : QuantDiv::on_host(1.0f);
   switch (nv) {
     case 1:
       if (a.cols == 512) hipLaunchKernelGGL((layernorm_vec_kernel<TX, TO, 1, 1, 8, true>), grid(1), b, 0, st, a, qd);
@@ -1638,9 +1645,10 @@ int c3h_quantize(const c3h_quantize_args* a, void* stream) {
       (a->x_dtype == C3H_F32 || a->x_dtype == C3H_BF16 || a->x_dtype == C3H_F16)) {
     const dim3 g(grid_for(a->count / 8, 2)), b(kBlock);
     hipStream_t st = as_stream(stream);
-    if (a->x_dtype == C3H_F32) hipLaunchKernelGGL(quantize_vec_kernel<float>, g, b, 0, st, *a);
-    else if (a->x_dtype == C3H_BF16) hipLaunchKernelGGL(quantize_vec_kernel<bf16_t>, g, b, 0, st, *a);
-    else hipLaunchKernelGGL(quantize_vec_kernel<f16_t>, g, b, 0, st, *a);
+    const QuantDiv qd = QuantDiv::on_host(a->scale, a->zero_point, a->x_dtype == C3H_F32 ? -1 : a->x_dtype);
+    if (a->x_dtype == C3H_F32) hipLaunchKernelGGL(quantize_vec_kernel<float>, g, b, 0, st, *a, qd);
+    else if (a->x_dtype == C3H_BF16) hipLaunchKernelGGL(quantize_vec_kernel<bf16_t>, g, b, 0, st, *a, qd);
+    else hipLaunchKernelGGL(quantize_vec_kernel<f16_t>, g, b, 0, st, *a, qd);
     return launch_status("quantize_vec");
   }
   hipLaunchKernelGGL(quantize_kernel, dim3(grid_for(a->count)), dim3(kBlock), 0, as_stream(stream), *a);
