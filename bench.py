@@ -60,6 +60,9 @@ DOMINANT = {
     "decoder_fp4": (["gemm_w4a16"], "fp16", "W4A16 GEMM: MXFP4 weights widened to fp16 in registers "
                     "(fp16 MFMA 16x16x32)"),
 }
+# profiles/<workload>_<label>.md of each workload's dominant family
+PROFILE_LABEL = {"mlp": "gemm", "resnet18_cifar": "conv", "resnet18_224": "conv", "decoder_fp16": "gemm",
+                 "decoder_w8a8": "qgemm", "decoder_fp8": "gemm", "decoder_fp4": "w4a16"}
 BASELINE_INDEX = {"mlp": 0, "resnet18_cifar": 1, "resnet18_224": 2, "decoder_fp16": 3, "decoder_w8a8": 4}
 CPU_SAMPLE = {"mlp": 4096, "resnet18_cifar": 128, "resnet18_224": 48, "decoder_fp16": 16, "decoder_w8a8": 2}
 # smaller samples for the per-config baselines (a few seconds of CPU each)
@@ -404,7 +407,8 @@ def _source_commit() -> str:
         return subprocess.run(["git", "-C", str(ROOT), "rev-parse", "--short=12", "HEAD"], capture_output=True,
                               text=True, check=True).stdout.strip()
     except (OSError, subprocess.CalledProcessError):
-        return "unknown"
+        # a copy of the tree without .git (a GPU box): the commit it was taken at, if the caller names it
+        return os.environ.get("C3H_SOURCE_COMMIT", "unknown")
 
 
 def _traffic_summary(fetch_dir: str, write_dir: str, meta_path: str) -> int:
@@ -483,8 +487,7 @@ def _profile_run(meta_path: str, workload: str = HEADLINE, kinds: str = "", reps
     init(0)
     m, plan, prog = _prepare(workload)
     kind_list = [k for k in kinds.split(",") if k] or DOMINANT[workload][0]
-    label = "conv" if kind_list == DOMINANT[HEADLINE][0] and workload == HEADLINE else \
-        ("dominant" if kind_list == DOMINANT[workload][0] else "_".join(kind_list))
+    label = PROFILE_LABEL[workload] if kind_list == DOMINANT[workload][0] else "_".join(kind_list)
     idx = prog.launches_of(kind_list)
     if not idx:
         raise ValueError(f"{workload} has no launches of kinds {kind_list}")
@@ -553,8 +556,11 @@ def _profile_summary(trace_dir: str, meta_path: str, pmc_dir: str = "") -> int:
                     d[int(r["Dispatch_Id"])][r["Counter_Name"]] = float(r["Counter_Value"])
         ids = sorted(d)[-nl * reps:]
         mb = np.asarray([d[i].get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for i in ids]).reshape(reps, nl).sum(axis=0)
-        cu = np.asarray([d[i].get("SQ_BUSY_CU_CYCLES", 0.0) for i in ids]).reshape(reps, nl).sum(axis=0)
-        busy = mb / np.maximum(cu, 1.0)
+        gr = np.asarray([d[i].get("GRBM_GUI_ACTIVE", 0.0) for i in ids]).reshape(reps, nl).sum(axis=0)
+        # SQ_VALU_MFMA_BUSY_CYCLES sums the busy cycles of all 1024 SIMDs;
+        # GRBM_GUI_ACTIVE sums the dispatch's active cycles over the 8 XCDs:
+        # 1024 SIMDs x cycles = 128 x the GRBM sum
+        busy = mb / np.maximum(128.0 * gr, 1.0)
     peak, unit = meta["peak"], "TFLOP/s"
     wl, label = meta["workload"], meta["label"]
     kinds = ",".join(meta["kinds"])
@@ -569,17 +575,21 @@ def _profile_summary(trace_dir: str, meta_path: str, pmc_dir: str = "") -> int:
         "launches, program order, one stream), under the kernel tracer. Commands (repository root, MI355X box):", "",
         "```",
         f"cd /tmp && export TMPDIR=/tmp   # then, from the repository root:",
-        f"timeout -s KILL 300 rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_{label} -o run -- \\",
-        f"    python3 bench.py --profile-run gpurun_out/prof_{label}_meta.json --workload {wl} --kinds {kinds}",
+        f"timeout -s KILL 300 rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_{wl}_{label} -o run -- \\",
+        f"    python3 bench.py --profile-run gpurun_out/prof_{wl}_{label}_meta.json --workload {wl} --kinds {kinds}",
     ]
     if pmc_dir:
-        lines += [f"timeout -s KILL 120 rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES --output-format csv \\",
-                  f"    -d gpurun_out/prof_{label}_pmc -o run -- python3 bench.py --profile-run \\",
-                  f"    gpurun_out/prof_{label}_pmc_meta.json --workload {wl} --kinds {kinds}"]
-    lines += [f"python3 bench.py --profile-summary gpurun_out/prof_{label} gpurun_out/prof_{label}_meta.json"
-              + (f" gpurun_out/prof_{label}_pmc" if pmc_dir else ""), "```", "",
+        lines += [f"timeout -s KILL 120 rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE --output-format csv \\",
+                  f"    -d gpurun_out/prof_{wl}_{label}_pmc -o run -- python3 bench.py --profile-run \\",
+                  f"    gpurun_out/prof_{wl}_{label}_pmc_meta.json --workload {wl} --kinds {kinds}"]
+    lines += [f"python3 bench.py --profile-summary gpurun_out/prof_{wl}_{label} gpurun_out/prof_{wl}_{label}_meta.json"
+              + (f" gpurun_out/prof_{wl}_{label}_pmc" if pmc_dir else ""), "```", "",
               f"Each row is the mean over {reps} timed replays. Peak: {peak:.0f} {unit} ({meta['dtype']} dense MFMA).", ""]
-    head = "| launch | node | shape | kernel | us | GFLOP | TFLOP/s | % of peak |" + (" MFMA busy |" if busy is not None else "")
+    if busy is not None:
+        lines += ["MFMA busy %: SQ_VALU_MFMA_BUSY_CYCLES / (128 x GRBM_GUI_ACTIVE), the share of SIMD cycles",
+                  "(1024 SIMDs; GRBM_GUI_ACTIVE summed over 8 XCDs) the matrix cores were busy during the launch.", ""]
+    head = "| launch | node | shape | kernel | us | GFLOP | TFLOP/s | % of peak |" + \
+        (" MFMA busy % |" if busy is not None else "")
     lines += [head, "|---:|---|---|---|---:|---:|---:|---:|" + ("---:|" if busy is not None else "")]
     for i, l in enumerate(launches):
         kname = names[i].split("(")[0].replace("void c3h::gk::", "").replace("void c3h::", "")[:70]
