@@ -366,8 +366,7 @@ def _traffic_run(meta_path: str, workload: str = HEADLINE, kinds: str = "", reps
     del src, dst
     m, plan, prog = _prepare(workload)
     kind_list = [k for k in kinds.split(",") if k] or DOMINANT[workload][0]
-    label = "conv" if kind_list == DOMINANT[HEADLINE][0] and workload == HEADLINE else \
-        ("dominant" if kind_list == DOMINANT[workload][0] else "memory_bound")
+    label = PROFILE_LABEL[workload] if kind_list == DOMINANT[workload][0] else "_".join(kind_list)
     idx = prog.launches_of(kind_list)
     if not idx:
         raise ValueError(f"{workload} has no launches of kinds {kind_list}")
@@ -543,7 +542,8 @@ def _profile_summary(trace_dir: str, meta_path: str, pmc_dir: str = "") -> int:
         if [k for k, _ in sub[r * nl:(r + 1) * nl]] != names:
             raise ValueError("the timed replays do not repeat one dispatch sequence")
     us = np.asarray([d for _, d in sub]).reshape(reps, nl).mean(axis=0)
-    busy = None
+    busy = valu = None
+    counters = []
     if pmc_dir:
         import csv
         import glob
@@ -555,12 +555,21 @@ def _profile_summary(trace_dir: str, meta_path: str, pmc_dir: str = "") -> int:
                 for r in csv.DictReader(f):
                     d[int(r["Dispatch_Id"])][r["Counter_Name"]] = float(r["Counter_Value"])
         ids = sorted(d)[-nl * reps:]
-        mb = np.asarray([d[i].get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for i in ids]).reshape(reps, nl).sum(axis=0)
-        gr = np.asarray([d[i].get("GRBM_GUI_ACTIVE", 0.0) for i in ids]).reshape(reps, nl).sum(axis=0)
+        counters = sorted({c for i in ids for c in d[i]})
+
+        def per_launch(name):
+            return np.asarray([d[i].get(name, 0.0) for i in ids]).reshape(reps, nl).mean(axis=0)
+
+        gr = per_launch("GRBM_GUI_ACTIVE")
         # SQ_VALU_MFMA_BUSY_CYCLES sums the busy cycles of all 1024 SIMDs;
         # GRBM_GUI_ACTIVE sums the dispatch's active cycles over the 8 XCDs:
         # 1024 SIMDs x cycles = 128 x the GRBM sum
-        busy = mb / np.maximum(128.0 * gr, 1.0)
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in counters:
+            busy = per_launch("SQ_VALU_MFMA_BUSY_CYCLES") / np.maximum(128.0 * gr, 1.0)
+        # a wave64 VALU instruction occupies its SIMD 4 cycles (more for
+        # transcendentals and 64-bit operations): issue share of all SIMD cycles
+        if "SQ_INSTS_VALU" in counters:
+            valu = per_launch("SQ_INSTS_VALU") * 4.0 / np.maximum(128.0 * gr, 1.0)
     peak, unit = meta["peak"], "TFLOP/s"
     wl, label = meta["workload"], meta["label"]
     kinds = ",".join(meta["kinds"])
@@ -579,7 +588,7 @@ def _profile_summary(trace_dir: str, meta_path: str, pmc_dir: str = "") -> int:
         f"    python3 bench.py --profile-run gpurun_out/prof_{wl}_{label}_meta.json --workload {wl} --kinds {kinds}",
     ]
     if pmc_dir:
-        lines += [f"timeout -s KILL 120 rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE --output-format csv \\",
+        lines += [f"timeout -s KILL 120 rocprofv3 --pmc {' '.join(counters)} --output-format csv \\",
                   f"    -d gpurun_out/prof_{wl}_{label}_pmc -o run -- python3 bench.py --profile-run \\",
                   f"    gpurun_out/prof_{wl}_{label}_pmc_meta.json --workload {wl} --kinds {kinds}"]
     lines += [f"python3 bench.py --profile-summary gpurun_out/prof_{wl}_{label} gpurun_out/prof_{wl}_{label}_meta.json"
@@ -588,21 +597,44 @@ def _profile_summary(trace_dir: str, meta_path: str, pmc_dir: str = "") -> int:
     if busy is not None:
         lines += ["MFMA busy %: SQ_VALU_MFMA_BUSY_CYCLES / (128 x GRBM_GUI_ACTIVE), the share of SIMD cycles",
                   "(1024 SIMDs; GRBM_GUI_ACTIVE summed over 8 XCDs) the matrix cores were busy during the launch.", ""]
-    head = "| launch | node | shape | kernel | us | GFLOP | TFLOP/s | % of peak |" + \
-        (" MFMA busy % |" if busy is not None else "")
-    lines += [head, "|---:|---|---|---|---:|---:|---:|---:|" + ("---:|" if busy is not None else "")]
+    if valu is not None:
+        lines += ["VALU issue %: SQ_INSTS_VALU x 4 cycles / (128 x GRBM_GUI_ACTIVE), the share of SIMD cycles spent",
+                  "issuing VALU instructions (a lower bound: transcendental and 64-bit operations take longer).", ""]
+    mem = not fl.any()  # a memory-bound family: bytes, not flops
+    nb = np.asarray([l.get("bytes") or 0 for l in launches], float)
+    extra = (" MFMA busy % |" if busy is not None else "") + (" VALU issue % |" if valu is not None else "")
+    if mem:
+        head = "| launch | node | shape | kernel | us | algorithmic MB | GB/s | % of 8 TB/s |" + extra
+    else:
+        head = "| launch | node | shape | kernel | us | GFLOP | TFLOP/s | % of peak |" + extra
+    lines += [head, "|---:|---|---|---|---:|---:|---:|---:|" + "---:|" * extra.count("|")]
     for i, l in enumerate(launches):
         kname = names[i].split("(")[0].replace("void c3h::gk::", "").replace("void c3h::", "")[:70]
-        t = fl[i] / (us[i] * 1e-6) / 1e12 if us[i] > 0 else 0.0
-        row = (f"| {i} | {l.get('node') or ''} | {l.get('info') or ''} | `{kname}` | {us[i]:.1f} | "
-               f"{fl[i] / 1e9:.1f} | {t:.0f} | {100 * t / peak:.1f} |")
+        if mem:
+            bw = nb[i] / (us[i] * 1e-6) / 1e9 if us[i] > 0 else 0.0
+            row = (f"| {i} | {l.get('node') or ''} | {l.get('info') or ''} | `{kname}` | {us[i]:.1f} | "
+                   f"{nb[i] / 1e6:.1f} | {bw:.0f} | {100 * bw / 8000.0:.1f} |")
+        else:
+            t = fl[i] / (us[i] * 1e-6) / 1e12 if us[i] > 0 else 0.0
+            row = (f"| {i} | {l.get('node') or ''} | {l.get('info') or ''} | `{kname}` | {us[i]:.1f} | "
+                   f"{fl[i] / 1e9:.1f} | {t:.0f} | {100 * t / peak:.1f} |")
         if busy is not None:
             row += f" {100 * busy[i]:.1f} |"
+        if valu is not None:
+            row += f" {100 * valu[i]:.1f} |"
         lines.append(row)
-    lines += ["", f"Sum of per-launch durations: {total_us:.1f} us for {fl.sum() / 1e9:.2f} GFLOP = "
-              f"{fl.sum() / (total_us * 1e-6) / 1e12:.0f} {unit}, {100 * frac_table:.1f} % of peak.",
-              f"HIP events around the same replays (the bench line's kernel_ms_per_step): {meta['event_ms'] * 1e3:.1f} us "
-              f"= {100 * frac_event:.1f} % of peak; rocprof sum / event time = {total_us / (meta['event_ms'] * 1e3):.3f}.",
+    if mem:
+        lines += ["", f"Sum of per-launch durations: {total_us:.1f} us for {nb.sum() / 1e6:.1f} MB = "
+                  f"{nb.sum() / (total_us * 1e-6) / 1e9:.0f} GB/s, {100 * nb.sum() / (total_us * 1e-6) / 8e12:.1f} % of "
+                  f"8 TB/s.", f"HIP events around the same replays: {meta['event_ms'] * 1e3:.1f} us; rocprof sum / event "
+                  f"time = {total_us / (meta['event_ms'] * 1e3):.3f}."]
+    else:
+        lines += ["", f"Sum of per-launch durations: {total_us:.1f} us for {fl.sum() / 1e9:.2f} GFLOP = "
+                  f"{fl.sum() / (total_us * 1e-6) / 1e12:.0f} {unit}, {100 * frac_table:.1f} % of peak.",
+                  f"HIP events around the same replays (the bench line's kernel_ms_per_step): "
+                  f"{meta['event_ms'] * 1e3:.1f} us = {100 * frac_event:.1f} % of peak; rocprof sum / event time = "
+                  f"{total_us / (meta['event_ms'] * 1e3):.3f}."]
+    lines += [
               "", f"rocprof_us_per_pass = {total_us:.1f}", f"event_us_per_pass = {meta['event_ms'] * 1e3:.1f}",
               f"source_commit = {_source_commit()}", ""]
     dest.write_text("\n".join(lines))

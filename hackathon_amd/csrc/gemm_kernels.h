@@ -87,17 +87,18 @@ __device__ __forceinline__ bool gelu_std_ok(float c0, float c1, float c2) {
   return c0 == 0x1.6a09e6p+0f && c1 == 1.0f && c2 == 0.5f;
 }
 
-// GELU x Phi(x) for the standard constants, written as
-//   Phi(x) = 1/2 + sign(x) (1/2 - E(|x|)),  E(a) = Phi(-a) = erfc(a / sqrt 2) / 2,
-// with E(a) = 2^P(a): P is a degree-8 polynomial fitted to log2 Phi(-a) on
+// GELU for the standard constants as the chain computes it, (x * (erf(q) +
+// 1)) * 0.5 with q = x / sqrt 2, but with erf(q) formed from
+//   E(a) = Phi(-a) = erfc(a / sqrt 2) / 2,  a = |x|:  erf(q) = sign(x) (1 - 2 E),
+// E(a) = 2^P(a).  P is a degree-8 polynomial fitted to log2 Phi(-a) on
 // [0, 5.75] by weighted minimax (weight E, so the error is bounded in E
-// itself: 7.6e-9 absolute), |x| clamped at 5.75, where E = 4.1e-9 and
-// 1/2 - E rounds to 1/2 -- as in the chain, where erf rounds to -1 there.
-// One v_exp_f32 and about 13 other VALU operations, against gelu_erf's ~24
-// and two transcendentals.  Evaluated in fp32 it stays within 1.9 |x| 2^-24
-// of x Phi(x) over [-12, 12] (the chain's own roundings: 1.8), and gives the
-// chain's special values: +Inf -> +Inf, -Inf -> NaN, x below -5.5 -> -0,
-// NaN -> NaN.
+// itself: 1.6e-8 absolute at most, 8e-9 past a = 2), and |x| is clamped at
+// 5.75.  So erf(q) = fl(1 - 2E) lands within about one fp32 step of the
+// correctly rounded erf(q) the chain adds 1 to, and the remaining steps
+// round as the chain's do: x below -5.5 gives -0 (1 - 2E rounds to 1 there,
+// as erf rounds to -1), +Inf gives +Inf, -Inf and NaN give NaN.  One
+// v_exp_f32 and about 14 other VALU operations, against gelu_erf's ~24 and
+// two transcendentals (v_rcp_f32, v_exp_f32).
 __device__ __forceinline__ float gelu_std(float x) {
   const float a = fminf(fabsf(x), 5.75f);
   float p = -0x1.740f9ep-19f;
@@ -110,7 +111,8 @@ __device__ __forceinline__ float gelu_std(float x) {
   p = fmaf(p, a, -0x1.26aedep+0f);
   p = fmaf(p, a, -1.0f);
   const float e = __builtin_amdgcn_exp2f(p);  // p in [-27.9, -1]: no range reduction needed
-  return x * (0.5f + __builtin_copysignf(0.5f - e, x));
+  const float erf_q = __builtin_copysignf(fmaf(-2.0f, e, 1.0f), x);  // 1 - 2E >= 0
+  return (x * (erf_q + 1.0f)) * 0.5f;
 }
 
 // act 2 where the constants are only known at run time (uniform `std_form`

@@ -91,15 +91,24 @@ def test_gemm_16bit_out_and_program_epilogue(gpu, kind):
     ref = 0.5 * v * (1 + erf(v / math.sqrt(2.0)))
     got = _from16(out.get(), kind)
     np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-2)
-    # The compiled GELU activation (act 2) performs the same five operations,
-    # its division and erf within an fp32 ulp or two of the program's
-    # correctly rounded ones: at most one 16-bit step apart, on at most 0.1 %.
+    # The compiled GELU activation (act 2; with these constants gelu_std)
+    # follows the program's roundings with erf within about an fp32 step of
+    # the correctly rounded one: the 16-bit results differ on at most 0.1 %
+    # of elements, by one 16-bit step, or -- in the negative tail, where
+    # both forms carry the chain's quantization of erf + 1 to 2^-24 and the
+    # values are 16-bit subnormals -- by at most |x| 2^-22, the fp32 GELU
+    # bound of test_gemm_gelu_epilogue_matches_the_chain.
     out2 = DeviceArray.empty((m, n), a.dtype)
     e2 = E.epilogue(residual=resd, imm=[math.sqrt(2.0), 1.0, 0.5])
     e2.act = 2
     E.gemm(ad, btd, out2, m, n, k, lda=k, ldb=k, ldo=n, trans_b=1, in_dtype=code, epi=e2)
-    step = np.abs(out2.get().view(np.int16).astype(np.int32) - out.get().view(np.int16).astype(np.int32))
-    assert step.max() <= 1 and np.mean(step != 0) <= 1e-3, (int(step.max()), float(np.mean(step != 0)))
+    g2, g1 = out2.get(), out.get()
+    step = np.abs(g2.view(np.int16).astype(np.int32) - g1.view(np.int16).astype(np.int32))
+    d = np.abs(_from16(g2, kind).astype(np.float64) - _from16(g1, kind).astype(np.float64))
+    ok = (step <= 1) | (d <= np.abs(v) * 2.0 ** -22)
+    print(f"compiled GELU vs program ({kind}): {np.mean(step != 0):.2e} of elements differ, max {int(step.max())} "
+          f"steps", flush=True)
+    assert ok.all() and np.mean(step != 0) <= 1e-3, (int(step.max()), float(np.mean(step != 0)))
 
 
 def _conv_case(rng, n, c, h, w, o, kh, kw, s, p):
