@@ -454,7 +454,7 @@ def _traffic_summary(fetch_dir: str, write_dir: str, meta_path: str) -> int:
         "|---:|---|---|---:|---:|---:|---:|",
     ]
     for i in range(nl):
-        kname = names[i].split("(")[0][:60]
+        kname = names[i].replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")[:60]
         lines.append(f"| {i} | {launches[i]['kind']} | `{kname}` | {alg[i] / 1e6:.1f} | {fetch[i] / 1e6:.1f} | "
                      f"{write[i] / 1e6:.1f} | {traffic[i] / alg[i]:.2f} |")
     lines += ["", f"Per step: algorithmic {alg.sum() / 1e9:.3f} GB, measured {traffic.sum() / 1e9:.3f} GB "
@@ -542,7 +542,7 @@ def _profile_summary(trace_dir: str, meta_path: str, pmc_dir: str = "") -> int:
         if [k for k, _ in sub[r * nl:(r + 1) * nl]] != names:
             raise ValueError("the timed replays do not repeat one dispatch sequence")
     us = np.asarray([d for _, d in sub]).reshape(reps, nl).mean(axis=0)
-    busy = valu = None
+    busy = valu = waves = None
     counters = []
     if pmc_dir:
         import csv
@@ -570,6 +570,8 @@ def _profile_summary(trace_dir: str, meta_path: str, pmc_dir: str = "") -> int:
         # transcendentals and 64-bit operations): issue share of all SIMD cycles
         if "SQ_INSTS_VALU" in counters:
             valu = per_launch("SQ_INSTS_VALU") * 4.0 / np.maximum(128.0 * gr, 1.0)
+        if "SQ_WAVES" in counters:
+            waves = per_launch("SQ_WAVES")
     peak, unit = meta["peak"], "TFLOP/s"
     wl, label = meta["workload"], meta["label"]
     kinds = ",".join(meta["kinds"])
@@ -593,7 +595,8 @@ def _profile_summary(trace_dir: str, meta_path: str, pmc_dir: str = "") -> int:
                   f"    gpurun_out/prof_{wl}_{label}_pmc_meta.json --workload {wl} --kinds {kinds}"]
     lines += [f"python3 bench.py --profile-summary gpurun_out/prof_{wl}_{label} gpurun_out/prof_{wl}_{label}_meta.json"
               + (f" gpurun_out/prof_{wl}_{label}_pmc" if pmc_dir else ""), "```", "",
-              f"Each row is the mean over {reps} timed replays. Peak: {peak:.0f} {unit} ({meta['dtype']} dense MFMA).", ""]
+              f"Each row is the mean over {reps} timed replays. Peak: " +
+              (f"{peak:.0f} {unit} ({meta['dtype']} dense MFMA)." if fl.any() else "8 TB/s (HBM3E)."), ""]
     if busy is not None:
         lines += ["MFMA busy %: SQ_VALU_MFMA_BUSY_CYCLES / (128 x GRBM_GUI_ACTIVE), the share of SIMD cycles",
                   "(1024 SIMDs; GRBM_GUI_ACTIVE summed over 8 XCDs) the matrix cores were busy during the launch.", ""]
@@ -602,14 +605,16 @@ def _profile_summary(trace_dir: str, meta_path: str, pmc_dir: str = "") -> int:
                   "issuing VALU instructions (a lower bound: transcendental and 64-bit operations take longer).", ""]
     mem = not fl.any()  # a memory-bound family: bytes, not flops
     nb = np.asarray([l.get("bytes") or 0 for l in launches], float)
-    extra = (" MFMA busy % |" if busy is not None else "") + (" VALU issue % |" if valu is not None else "")
+    extra = (" MFMA busy % |" if busy is not None else "") + (" VALU issue % |" if valu is not None else "") + \
+        (" waves |" if waves is not None else "")
     if mem:
         head = "| launch | node | shape | kernel | us | algorithmic MB | GB/s | % of 8 TB/s |" + extra
     else:
         head = "| launch | node | shape | kernel | us | GFLOP | TFLOP/s | % of peak |" + extra
     lines += [head, "|---:|---|---|---|---:|---:|---:|---:|" + "---:|" * extra.count("|")]
     for i, l in enumerate(launches):
-        kname = names[i].split("(")[0].replace("void c3h::gk::", "").replace("void c3h::", "")[:70]
+        kname = names[i].replace("(anonymous namespace)::", "").split("(")[0]
+        kname = kname.replace("void c3h::gk::", "").replace("void c3h::", "").replace("void ", "")[:70]
         if mem:
             bw = nb[i] / (us[i] * 1e-6) / 1e9 if us[i] > 0 else 0.0
             row = (f"| {i} | {l.get('node') or ''} | {l.get('info') or ''} | `{kname}` | {us[i]:.1f} | "
@@ -622,6 +627,8 @@ def _profile_summary(trace_dir: str, meta_path: str, pmc_dir: str = "") -> int:
             row += f" {100 * busy[i]:.1f} |"
         if valu is not None:
             row += f" {100 * valu[i]:.1f} |"
+        if waves is not None:
+            row += f" {waves[i]:.0f} |"
         lines.append(row)
     if mem:
         lines += ["", f"Sum of per-launch durations: {total_us:.1f} us for {nb.sum() / 1e6:.1f} MB = "
