@@ -226,6 +226,65 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(c3h_reduce_args a) 
   }
 }
 
+// Short reduce axis (GlobalAveragePool's 16 or 49 positions), inner % 8 ==
+// 0, 16-byte aligned: a block covers one outer index and 16 vectors of 8
+// inner elements (128 channels); its 256 threads are 16 position groups x 16
+// vectors (thread t: group p = t / 16, vector t % 16), group p summing
+// positions p, p + 16, ... two loads in flight, and the 16 partials of each
+// vector are combined through LDS in group order.  Per 512 channels that is
+// four blocks where reduce_cols_vec_kernel has one: its one block per outer
+// index left the ResNet pools (256 images) with one wave per SIMD, too few
+// loads in flight to cover HBM latency.
+template <typename T>
+__global__ void __launch_bounds__(kBlock) reduce_cols_vec16_kernel(c3h_reduce_args a) {
+  __shared__ float part[16][16][9];
+  const int t = threadIdx.x, p = t >> 4, v = t & 15;
+  const int64_t o = blockIdx.x;
+  const int64_t c8 = static_cast<int64_t>(blockIdx.y) * 16 + v;
+  const bool live = c8 * 8 < a.inner;
+  const T* in = static_cast<const T*>(a.in) + o * a.reduce * a.inner + c8 * 8;
+  const bool mx = a.kind == 0;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = mx ? -INFINITY : 0.0f;
+  if (live) {
+    int64_t i = p;
+    for (; i + 16 < a.reduce; i += 32) {
+      float x0[8], x1[8];
+      load_vec16(in + i * a.inner, x0);
+      load_vec16(in + (i + 16) * a.inner, x1);
+      if constexpr (sizeof(T) == 4) {
+        load_vec16(in + i * a.inner + 4, x0 + 4);
+        load_vec16(in + (i + 16) * a.inner + 4, x1 + 4);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = mx ? fmaxf(acc[e], x0[e]) : acc[e] + x0[e];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = mx ? fmaxf(acc[e], x1[e]) : acc[e] + x1[e];
+    }
+    if (i < a.reduce) {
+      float x0[8];
+      load_vec16(in + i * a.inner, x0);
+      if constexpr (sizeof(T) == 4) load_vec16(in + i * a.inner + 4, x0 + 4);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = mx ? fmaxf(acc[e], x0[e]) : acc[e] + x0[e];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) part[p][v][e] = acc[e];
+  __syncthreads();
+  if (t < 16 && live) {  // group 0: t == v
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float r = part[0][v][e];
+#pragma unroll
+      for (int q = 1; q < 16; ++q) r = mx ? fmaxf(r, part[q][v][e]) : r + part[q][v][e];
+      if (a.kind == 2) r = r / static_cast<float>(a.reduce);
+      store_from_f32(a.out, a.out_dtype, o * a.inner + c8 * 8 + e, r);
+    }
+  }
+}
+
 // inner % 8 == 0, 16-byte aligned (channels-last GlobalAveragePool): a block
 // covers one outer index and 64 vectors of 8 inner elements; its four waves
 // split the reduce axis (positions w, w + 4, ...), each thread keeping 8
@@ -1393,8 +1452,17 @@ int c3h_reduce(const c3h_reduce_args* a, void* stream) {
     hipLaunchKernelGGL(reduce_rows_kernel, dim3(blocks), dim3(kBlock), 0, as_stream(stream), *a);
   } else if (a->inner % 8 == 0 && (reinterpret_cast<uintptr_t>(a->in) & 15) == 0 && a->outer < (int64_t{1} << 31) &&
              (a->in_dtype == C3H_F32 || a->in_dtype == C3H_BF16 || a->in_dtype == C3H_F16)) {
-    const dim3 g(static_cast<unsigned>(a->outer), static_cast<unsigned>(ceil_div(a->inner / 8, 64)));
     hipStream_t st = as_stream(stream);
+    if (a->reduce <= 64) {
+      const dim3 g(static_cast<unsigned>(a->outer), static_cast<unsigned>(ceil_div(a->inner / 8, 16)));
+      C3H_REQUIRE(g.y <= 65535, "reduce: inner too large");
+      if (a->in_dtype == C3H_F32) hipLaunchKernelGGL(reduce_cols_vec16_kernel<float>, g, dim3(kBlock), 0, st, *a);
+      else if (a->in_dtype == C3H_BF16)
+        hipLaunchKernelGGL(reduce_cols_vec16_kernel<bf16_t>, g, dim3(kBlock), 0, st, *a);
+      else hipLaunchKernelGGL(reduce_cols_vec16_kernel<f16_t>, g, dim3(kBlock), 0, st, *a);
+      return launch_status("reduce");
+    }
+    const dim3 g(static_cast<unsigned>(a->outer), static_cast<unsigned>(ceil_div(a->inner / 8, 64)));
     C3H_REQUIRE(g.y <= 65535, "reduce: inner too large");
     if (a->in_dtype == C3H_F32) hipLaunchKernelGGL(reduce_cols_vec_kernel<float>, g, dim3(kBlock), 0, st, *a);
     else if (a->in_dtype == C3H_BF16) hipLaunchKernelGGL(reduce_cols_vec_kernel<bf16_t>, g, dim3(kBlock), 0, st, *a);

@@ -632,10 +632,12 @@ def test_splitk_reduce_fixed_order_bit_exact(gpu, out_kind):
 
 
 @pytest.mark.parametrize("kind_name,dt", [("fp32", "fp32"), ("bf16", "bf16"), ("fp16", "fp16")])
-@pytest.mark.parametrize("outer,red,inner", [(3, 49, 512), (2, 13, 8), (5, 3, 1024), (1, 64, 136)])
+@pytest.mark.parametrize("outer,red,inner", [(3, 49, 512), (2, 13, 8), (5, 3, 1024), (1, 64, 136), (256, 16, 512),
+                                             (256, 49, 512), (2, 65, 256), (3, 200, 64)])
 def test_reduce_channels_last_vec(gpu, kind_name, dt, outer, red, inner):
-    """Channels-last reductions (inner % 8 == 0: GlobalAveragePool over NHWC):
-    max exact, sum / mean within float32 summation error of float64."""
+    """Channels-last reductions (inner % 8 == 0: GlobalAveragePool over NHWC;
+    reduce <= 64 on the 16-position-group kernel, longer on the four-wave
+    one): max exact, sum / mean within float32 summation error of float64."""
     from hackathon_amd import _lib
     from hackathon_amd.device import DeviceArray
 
