@@ -273,14 +273,17 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_vec16_kernel(c3h_reduce_ar
 #pragma unroll
   for (int e = 0; e < 8; ++e) part[p][v][e] = acc[e];
   __syncthreads();
-  if (t < 16 && live) {  // group 0: t == v
+  // 128 threads, one output each (vector t / 8, element t % 8: consecutive
+  // threads store consecutive channels), sum the 16 groups in group order.
+  if (t < 128) {
+    const int ov = t >> 3, oe = t & 7;
+    const int64_t oc8 = static_cast<int64_t>(blockIdx.y) * 16 + ov;
+    if (oc8 * 8 < a.inner) {
+      float r = part[0][ov][oe];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float r = part[0][v][e];
-#pragma unroll
-      for (int q = 1; q < 16; ++q) r = mx ? fmaxf(r, part[q][v][e]) : r + part[q][v][e];
+      for (int q = 1; q < 16; ++q) r = mx ? fmaxf(r, part[q][ov][oe]) : r + part[q][ov][oe];
       if (a.kind == 2) r = r / static_cast<float>(a.reduce);
-      store_from_f32(a.out, a.out_dtype, o * a.inner + c8 * 8 + e, r);
+      store_from_f32(a.out, a.out_dtype, o * a.inner + oc8 * 8 + oe, r);
     }
   }
 }
