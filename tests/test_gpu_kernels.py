@@ -209,6 +209,28 @@ def test_conv_direct_c4_matches_implicit_gemm(gpu, case):
     np.testing.assert_allclose(got.transpose(0, 3, 1, 2), ref, rtol=1e-4, atol=1e-4)
 
 
+def test_flash_attention_host_checks(gpu):
+    """A head whose K (or V) rows span 2 GiB or more is refused before any
+    launch: the kernel stages K and V with 32-bit buffer offsets."""
+    from hackathon_amd import _lib
+    from hackathon_amd.device import DeviceArray
+
+    buf = DeviceArray.empty((4096,), np.uint16)
+    a = _lib.FlashArgs()
+    a.q = a.k = a.v = a.mask = a.out = buf.ptr
+    a.batch, a.heads, a.seq_q, a.seq_k, a.head_dim, a.dtype = 1, 1, 16, 9, 64, _lib.F16
+    a.q_sb = a.k_sb = a.v_sb = a.o_sb = 0
+    a.q_sh = a.k_sh = a.v_sh = a.o_sh = 0
+    a.q_ss = a.o_ss = 64
+    a.k_ss, a.v_ss = 1 << 27, 64  # 8 rows x 2^27 elements x 2 bytes = 2 GiB
+    a.mask_ld, a.scale, a.mask_kind = 0, 0.125, 0
+    with pytest.raises(_lib.C3HError, match="2 GiB"):
+        _lib.launch(a, None)
+    a.k_ss, a.v_ss = 64, 1 << 27
+    with pytest.raises(_lib.C3HError, match="2 GiB"):
+        _lib.launch(a, None)
+
+
 @pytest.mark.parametrize("kind", ["fp16", "bf16"])
 @pytest.mark.parametrize("mask_kind", [0, 1, 2])
 @pytest.mark.parametrize("b,h,s", [(2, 3, 64), (1, 2, 200), (2, 1, 256),
