@@ -595,7 +595,8 @@ int c3h_attention_scores(const c3h_attn_scores_args* a, void* stream);
  * stride along D, so head-split views of a packed QKV buffer and a
  * [B,S,H*D] output need no copies.  mask_kind: 0 none, 1 causal (key > query
  * masked), 2 additive fp32 mask [Sq,Sk] (row stride mask_ld).  D must be 64;
- * dtype F16 or BF16 (fp32 scores and softmax state). */
+ * dtype F16 or BF16 (fp32 scores and softmax state).  One head's K rows
+ * ((seq_k - 1) * k_ss + 64 elements) and V rows must each span under 2 GiB. */
 typedef struct {
   const void* q;
   const void* k;
