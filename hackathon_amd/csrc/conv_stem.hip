@@ -8,12 +8,12 @@
 // unfused sequence: inputs are rounded to 16 bits exactly as the layout
 // kernel does, the conv uses the same MFMA (16x16x32, K chunk order and
 // accumulation order of c3h_conv2d's narrow-channel packing), the epilogue
-// performs the same float operations, and the maximum of 16-bit-rounded
+// pools before the epilogue (below), and the maximum of 16-bit-rounded
 // values equals the rounding of the maximum.
 //
-// Work decomposition: a tile is 4 x 8 pooled pixels x 64 channels of one
-// image.  It needs a 9 x 17 conv-output tile (153 pixels, 10 MFMA column
-// tiles), which needs a 23 x 40 x 4 input patch.  A persistent workgroup
+// Work decomposition: a tile is 7 x 8 pooled pixels x 64 channels of one
+// image.  It needs a 15 x 17 conv-output tile (255 pixels, 16 MFMA column
+// tiles, four per wave), which needs a 35 x 40 x 4 input patch.  A persistent workgroup
 // (4 waves) walks a contiguous range of tiles: the next tile's patch is
 // loaded into registers while the current tile's MFMAs run, so global
 // latency hides behind compute, and neighbouring tiles share their input
@@ -21,10 +21,16 @@
 // MFMA fragments) in registers for the kernel's life.
 //
 // The MFMA computes C^T = W . X^T, so a lane's four accumulators are four
-// consecutive channels of one conv pixel: bias, ReLU and the 16-bit
-// rounding run on them in registers and leave as one 8-byte LDS store.
-// After ReLU every value is +0 or positive, whose 16-bit patterns order like
-// the values, so the pool takes packed unsigned 16-bit maxima.
+// consecutive channels of one conv pixel; they go to the fp32 conv tile in
+// LDS as they are, one 16-byte store.  The pool takes the maximum of the raw
+// accumulators and only then adds the bias, applies ReLU and rounds to 16
+// bits, once per pooled value instead of once per conv value.  That is
+// exact: v -> round(relu(v + b)) is monotone non-decreasing, so the maximum
+// of its values is its value at the maximum.  NaN accumulators agree too:
+// fmaxf skips them, and the unfused chain maps them to +0 under ReLU, which
+// the maximum of the non-negative others absorbs (all-NaN windows give +0
+// either way).  Without ReLU the same holds for a finite bias, with all-NaN
+// windows mapped to the unfused pool's -inf.
 #include "common.h"
 
 using namespace c3h;
@@ -34,27 +40,30 @@ namespace {
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
-typedef __attribute__((ext_vector_type(2))) unsigned short u16x2;
 
 constexpr int kThreads = 256;
 constexpr int KH = 7, KWP = 8, CP = 4;  // filter rows, packed filter columns, packed channels
 constexpr int KSTRIDE = KH * KWP * CP;  // 224: packed K per output channel
 constexpr int O = 64;                   // output channels
-constexpr int PH = 4, PW = 8;           // pooled tile (rows, columns)
-constexpr int CTH = 2 * PH + 1;         // 9 conv tile rows
+constexpr int PH = 7, PW = 8;           // pooled tile (rows, columns)
+constexpr int CTH = 2 * PH + 1;         // 15 conv tile rows
 constexpr int CTW = 2 * PW + 1;         // 17 conv tile columns
-constexpr int CPIX = CTH * CTW;         // 153 conv pixels per tile
-constexpr int MT = (CPIX + 15) / 16;    // 10 MFMA pixel tiles
-constexpr int PR = 2 * (CTH - 1) + KH;  // 23 patch rows
+constexpr int CPIX = CTH * CTW;         // 255 conv pixels per tile
+constexpr int MT = (CPIX + 15) / 16;    // 16 MFMA pixel tiles
+constexpr int PR = 2 * (CTH - 1) + KH;  // 35 patch rows
 constexpr int PC = 2 * (CTW - 1) + KWP; // 40 patch columns
 constexpr int PROW = PC * CP * 2;       // 320 bytes per patch row
-constexpr int PATCH_BYTES = PR * PROW;  // 7360
-constexpr int CS = 136;                 // conv-tile pixel stride (128 used): conflict-free 8-byte stores
-constexpr int CT_BYTES = CPIX * CS;     // 20808
-constexpr int SLOTS = (PR * PC + kThreads - 1) / kThreads;  // 4 patch pixels per thread
-constexpr int TPW = (MT + 3) / 4;       // 3 pixel tiles per wave (waves 2 and 3 have 2)
+constexpr int PATCH_BYTES = PR * PROW;  // 11200
+constexpr int CS = 272;                 // fp32 conv-tile pixel stride (256 used): conflict-free 16-byte stores
+constexpr int CT_BYTES = CPIX * CS;     // 69360
+constexpr int SLOTS = (PR * PC + kThreads - 1) / kThreads;  // 6 patch pixels per thread
+constexpr int TPW = MT / 4;             // 4 pixel tiles per wave
+static_assert(MT == 4 * TPW, "the pixel tiles split evenly over the four waves");
+constexpr int POOL_ITEMS = PH * PW * 8; // 448 (pooled pixel, 8-channel group) items, two rounds
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset past num_records: reads 0
-static_assert(PH * PW * 8 == kThreads, "one pooled item (8 channels) per thread");
+static_assert(kThreads % 8 == 0 && POOL_ITEMS <= 2 * kThreads, "two pool rounds; a thread keeps its 8 channels");
+// Two workgroups per CU must fit the 160 KiB of LDS.
+static_assert(2 * (PATCH_BYTES + CT_BYTES + O * 4) <= 160 * 1024, "LDS for two workgroups per CU");
 
 template <typename T> struct In;
 template <> struct In<float> {
@@ -94,6 +103,16 @@ template <> struct Mm<f16_t> {
   static __device__ __forceinline__ float f32(uint32_t b) { return f16_bits_to_f32(static_cast<uint16_t>(b)); }
 };
 
+// Maximum of three accumulators as one v_max3_f32.  fmaxf on values loaded
+// from LDS would first canonicalize each operand (one more VALU operation
+// apiece).  The accumulators are MFMA results, which hold no signalling NaN,
+// and the IEEE-mode maximum skips quiet NaN operands as fmaxf does.
+__device__ __forceinline__ float max3_f32(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 struct StemGeom {
   int64_t tiles;
   int n, c, h, w, ho, wo, po, qo, tq, tpi;
@@ -101,19 +120,17 @@ struct StemGeom {
   uint32_t image_bytes;  // c * h * w * sizeof(input element)
 };
 
-__device__ __forceinline__ uint32_t umax16x2(uint32_t a, uint32_t b) {
-  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
-                                                                __builtin_bit_cast(u16x2, b)));
-}
-
 template <typename TI, typename T16>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp, const float* __restrict__ bias,
                       uint16_t* __restrict__ out, StemGeom g) {
   typedef Mm<T16> MM;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[PATCH_BYTES + CT_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[PATCH_BYTES + CT_BYTES + O * 4];
   uint8_t* patch = smem;
   uint8_t* ctile = smem + PATCH_BYTES;
+  // The bias lives in LDS and is read per pooled item: eight registers held
+  // for the kernel's life would push the register budget into spills.
+  float* bias_s = reinterpret_cast<float*>(smem + PATCH_BYTES + CT_BYTES);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -126,12 +143,7 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       bw[kh][j] = *reinterpret_cast<const uint4*>(wp + (16 * j + l16) * KSTRIDE + 32 * kh + 8 * lg);
-  // Bias of the lane's accumulator channels 16 j + 4 lg + r.
-  float bv[4][4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) bv[j][r] = bias ? bias[16 * j + 4 * lg + r] : 0.0f;
+  if (tid < O) bias_s[tid] = bias ? bias[tid] : 0.0f;  // read after the first barrier
   // Retire the weight and bias loads here (s_waitcnt vmcnt(0)).  Left
   // pending, the compiler's wait insertion carries them into the tile loop's
   // header state and waits on vmcnt before the MFMAs of every tile, which
@@ -150,13 +162,13 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
     const int r = m / CTW, c = m - r * CTW;
     aoff[t] = 2 * r * PROW + (2 * c + 2 * lg) * (CP * 2);
   }
-  // This thread's patch slots: fixed (row, col) inside every tile.
-  int s_row[SLOTS], s_col[SLOTS];
+  // This thread's patch slots: fixed (row, col) inside every tile, packed
+  // as row << 8 | col; a slot past the patch gets column 255 (never loaded).
+  int s_rc[SLOTS];
 #pragma unroll
   for (int s = 0; s < SLOTS; ++s) {
     const int slot = tid + s * kThreads;
-    s_row[s] = slot / PC;
-    s_col[s] = slot - s_row[s] * PC;
+    s_rc[s] = slot < PR * PC ? (slot / PC) << 8 | (slot % PC) : 0xff;
   }
   const uint32_t plane_bytes = static_cast<uint32_t>(g.h) * g.w * sizeof(TI);
 
@@ -175,8 +187,9 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
     const int hi0 = 4 * PH * f_pt - 5, wi0 = 4 * PW * f_qt - 5;
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
-      const int hi = hi0 + s_row[s], wi = wi0 + s_col[s];
-      const bool ok = tid + s * kThreads < PR * PC && s_col[s] < PC - 1 &&
+      const int col = s_rc[s] & 0xff;
+      const int hi = hi0 + (s_rc[s] >> 8), wi = wi0 + col;
+      const bool ok = col < PC - 1 &&
                       static_cast<unsigned>(hi) < static_cast<unsigned>(g.h) &&
                       static_cast<unsigned>(wi) < static_cast<unsigned>(g.w);
       const uint32_t off = ok ? static_cast<uint32_t>((hi * g.w + wi) * static_cast<int>(sizeof(TI))) : kOob;
@@ -217,117 +230,105 @@ conv_stem_pool_kernel(const TI* __restrict__ x, const uint16_t* __restrict__ wp,
     }
     if (t + 1 < t_end) fetch(n_img, n_pt, n_qt);
 
+    // The kh = 0 MFMAs take a zero C operand (an inline constant), so the
+    // accumulators need no zeroing moves.
     f32x4 acc[TPW][4];
-#pragma unroll
-    for (int i = 0; i < TPW; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     __builtin_amdgcn_s_setprio(1);  // MFMA section at raised wave priority
 #pragma unroll
     for (int kh = 0; kh < KH; ++kh) {
 #pragma unroll
       for (int i = 0; i < TPW; ++i) {
-        if (wave + 4 * i < MT) {
-          uint4 a = *reinterpret_cast<const uint4*>(patch + aoff[i] + kh * PROW);
-          a.z &= kw7_mask;
-          a.w &= kw7_mask;
+        uint4 a = *reinterpret_cast<const uint4*>(patch + aoff[i] + kh * PROW);
+        a.z &= kw7_mask;
+        a.w &= kw7_mask;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = MM::mma(bw[kh][j], a, acc[i][j]);
-        }
+        for (int j = 0; j < 4; ++j) acc[i][j] = MM::mma(bw[kh][j], a, kh == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j]);
       }
     }
     __builtin_amdgcn_s_setprio(0);
-    // bias (+ the absent residual's +0, as c3h_conv2d) + ReLU, rounded, into the conv tile [pixel][channel].
+    // Raw accumulators into the fp32 conv tile [pixel][channel].
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int m = 16 * (wave + 4 * i) + l16;
-      if (wave + 4 * i < MT && m < CPIX) {
+      if (m < CPIX) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float v[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            // With ReLU the zero residual's "+ 0" changes nothing (it only
-            // turns -0 into +0, and the select maps both zeros and NaN to
-            // +0), so it is added only without ReLU.
-            const float t = acc[i][j][r] + bv[j][r];
-            v[r] = g.relu ? (t > 0.0f ? t : 0.0f) : t + 0.0f;
-          }
-          *reinterpret_cast<uint2*>(ctile + m * CS + (16 * j + 4 * lg) * 2) =
-              uint2{MM::pack(v[0], v[1]), MM::pack(v[2], v[3])};
-        }
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<f32x4*>(ctile + m * CS + (16 * j + 4 * lg) * 4) = acc[i][j];
       }
     }
     __syncthreads();
     if (t + 1 < t_end) stash();  // every wave is past its patch reads
-    // 3x3 / stride 2 max over the valid conv pixels of each pooled pixel, 8 channels per thread.
+    // 3x3 / stride 2 max over the valid conv pixels of each pooled pixel, 8
+    // channels per thread, then bias (+ the absent residual's +0, as
+    // c3h_conv2d), ReLU and the 16-bit rounding.
     {
       // Whether every window of the tile lies inside the conv output (uniform).
       const bool interior = pt > 0 && qt > 0 && 2 * (PH * pt + PH - 1) + 1 < g.ho && 2 * (PW * qt + PW - 1) + 1 < g.wo;
-      const int px = tid >> 3, cg = tid & 7;
-      const int pr = px / PW, qc = px - pr * PW;
-      const int P = PH * pt + pr, Q = PW * qt + qc;
-      if (P < g.po && Q < g.qo) {
-        uint4 res;
-        if (g.relu && interior) {
-          // Every window position is a conv pixel of the image: constant
-          // offsets from the window's corner, no checks.
-          const uint8_t* c0 = ctile + ((2 * pr) * CTW + 2 * qc) * CS + cg * 16;
-          uint32_t mx[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-          for (int dr = 0; dr < 3; ++dr)
-#pragma unroll
-            for (int dc = 0; dc < 3; ++dc) {
-              const uint4 v = *reinterpret_cast<const uint4*>(c0 + (dr * CTW + dc) * CS);
-              mx[0] = umax16x2(mx[0], v.x);
-              mx[1] = umax16x2(mx[1], v.y);
-              mx[2] = umax16x2(mx[2], v.z);
-              mx[3] = umax16x2(mx[3], v.w);
-            }
-          res = uint4{mx[0], mx[1], mx[2], mx[3]};
-        } else if (g.relu) {
-          // Every window holds the valid pixel (2 pr + 1, 2 qc + 1); invalid
-          // positions re-read it, which leaves the maximum unchanged.
-          uint32_t mx[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-          for (int dr = 0; dr < 3; ++dr) {
-            const bool rok = static_cast<unsigned>(2 * P - 1 + dr) < static_cast<unsigned>(g.ho);
-#pragma unroll
-            for (int dc = 0; dc < 3; ++dc) {
-              const bool ok = rok && static_cast<unsigned>(2 * Q - 1 + dc) < static_cast<unsigned>(g.wo);
-              const int m = ok ? (2 * pr + dr) * CTW + 2 * qc + dc : (2 * pr + 1) * CTW + 2 * qc + 1;
-              const uint4 v = *reinterpret_cast<const uint4*>(ctile + m * CS + cg * 16);
-              mx[0] = umax16x2(mx[0], v.x);
-              mx[1] = umax16x2(mx[1], v.y);
-              mx[2] = umax16x2(mx[2], v.z);
-              mx[3] = umax16x2(mx[3], v.w);
-            }
-          }
-          res = uint4{mx[0], mx[1], mx[2], mx[3]};
-        } else {
+      for (int round = 0; round < 2; ++round) {
+        const int item = tid + round * kThreads;
+        const int px = item >> 3, cg = item & 7;
+        const int pr = px / PW, qc = px - pr * PW;
+        const int P = PH * pt + pr, Q = PW * qt + qc;
+        if (item < POOL_ITEMS && P < g.po && Q < g.qo) {
+          const uint8_t* c0 = ctile + ((2 * pr) * CTW + 2 * qc) * CS + cg * 32;
           float mx[8];
+          // Row maxima first (three positions each), then the maximum of the rows.
+          auto pool = [&](auto offset) {
+            float rm[3][8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) mx[e] = -__builtin_huge_valf();
+            for (int dr = 0; dr < 3; ++dr) {
+              f32x4 lo[3], hi[3];
 #pragma unroll
-          for (int dr = 0; dr < 3; ++dr) {
-            if (static_cast<unsigned>(2 * P - 1 + dr) >= static_cast<unsigned>(g.ho)) continue;
-#pragma unroll
-            for (int dc = 0; dc < 3; ++dc) {
-              if (static_cast<unsigned>(2 * Q - 1 + dc) >= static_cast<unsigned>(g.wo)) continue;
-              const int m = (2 * pr + dr) * CTW + 2 * qc + dc;
-              const uint4 v = *reinterpret_cast<const uint4*>(ctile + m * CS + cg * 16);
-              const uint32_t wds[4] = {v.x, v.y, v.z, v.w};
+              for (int dc = 0; dc < 3; ++dc) {
+                lo[dc] = *reinterpret_cast<const f32x4*>(c0 + offset(dr, dc));
+                hi[dc] = *reinterpret_cast<const f32x4*>(c0 + offset(dr, dc) + 16);
+              }
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
-                mx[2 * e] = fmaxf(mx[2 * e], MM::f32(wds[e] & 0xffffu));
-                mx[2 * e + 1] = fmaxf(mx[2 * e + 1], MM::f32(wds[e] >> 16));
+                rm[dr][e] = max3_f32(lo[0][e], lo[1][e], lo[2][e]);
+                rm[dr][4 + e] = max3_f32(hi[0][e], hi[1][e], hi[2][e]);
               }
             }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx[e] = max3_f32(rm[0][e], rm[1][e], rm[2][e]);
+          };
+          if (interior) {
+            pool([](int dr, int dc) { return (dr * CTW + dc) * CS; });
+          } else {
+            // Outside the conv output a window position re-reads the window's
+            // centre (2 pr + 1, 2 qc + 1), which every window holds and which
+            // leaves the maximum unchanged.
+            bool rok[3], cok[3];
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+              rok[k] = static_cast<unsigned>(2 * P - 1 + k) < static_cast<unsigned>(g.ho);
+              cok[k] = static_cast<unsigned>(2 * Q - 1 + k) < static_cast<unsigned>(g.wo);
+            }
+            pool([&](int dr, int dc) { return (rok[dr] & cok[dc]) ? (dr * CTW + dc) * CS : (CTW + 1) * CS; });
           }
-          res = uint4{MM::pack(mx[0], mx[1]), MM::pack(mx[2], mx[3]), MM::pack(mx[4], mx[5]), MM::pack(mx[6], mx[7])};
+          float bv[8];
+          *reinterpret_cast<f32x4*>(bv) = *reinterpret_cast<const f32x4*>(bias_s + 8 * cg);
+          *reinterpret_cast<f32x4*>(bv + 4) = *reinterpret_cast<const f32x4*>(bias_s + 8 * cg + 4);
+          float v[8];
+          // With ReLU the zero residual's "+ 0" changes nothing (it only turns
+          // -0 into +0, and the select maps both zeros and NaN to +0), so it is
+          // added only without ReLU.
+          if (g.relu) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float t = mx[e] + bv[e];
+              v[e] = t > 0.0f ? t : 0.0f;
+            }
+          } else {
+            // A window of NaN conv values only pools to -inf, as the unfused
+            // max pool (fmaxf from -inf) gives.
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = mx[e] == mx[e] ? (mx[e] + bv[e]) + 0.0f : -__builtin_huge_valf();
+          }
+          const uint4 res{MM::pack(v[0], v[1]), MM::pack(v[2], v[3]), MM::pack(v[4], v[5]), MM::pack(v[6], v[7])};
+          const int64_t o = ((static_cast<int64_t>(img) * g.po + P) * g.qo + Q) * O + cg * 8;
+          *reinterpret_cast<uint4*>(out + o) = res;
         }
-        const int64_t o = ((static_cast<int64_t>(img) * g.po + P) * g.qo + Q) * O + cg * 8;
-        *reinterpret_cast<uint4*>(out + o) = res;
       }
     }
     __syncthreads();

@@ -535,16 +535,28 @@ def test_quantize_every_code_boundary_bit_exact(gpu, kind, zero):
 @pytest.mark.parametrize("kind", ["bf16", "fp16"])
 @pytest.mark.parametrize("n,h,w,relu,in_kind", [(2, 64, 64, 1, "fp32"), (3, 70, 57, 1, "fp32"), (1, 45, 83, 0, "fp32"),
                                                 (2, 38, 40, 1, "same"), (2, 224, 224, 1, "fp32"),
-                                                (1, 100, 60, 0, "same"), (1, 61, 92, 1, "fp32")])
+                                                (1, 100, 60, 0, "same"), (1, 61, 92, 1, "fp32"),
+                                                (2, 64, 64, 1, "fp32 nonfinite"), (2, 64, 64, 0, "fp32 nonfinite")])
 def test_conv_stem_pool_matches_unfused_chain(gpu, kind, n, h, w, relu, in_kind):
     """c3h_conv_stem_pool == layout -> c3h_conv2d (bias, relu) -> c3h_maxpool2d, bit for bit;
-    and within 16-bit rounding of a float64 conv + max pool of the rounded operands."""
+    and within 16-bit rounding of a float64 conv + max pool of the rounded operands.
+
+    The fused kernel pools the raw accumulators before bias, ReLU and rounding; the
+    "nonfinite" cases put NaN and +-inf inputs in (NaN and +-inf conv values, whole
+    windows of NaN, inf - inf) so that the NaN rules of the two orders are compared too."""
     from hackathon_amd import _lib
     from hackathon_amd.c35 import engine as E
     from hackathon_amd.device import BF16, DeviceArray
 
     rng = np.random.default_rng(h * w + n)
     x, wt, b, attrs = _conv_case(rng, n, 3, h, w, 64, 7, 7, 2, 3)
+    nonfinite = in_kind.endswith("nonfinite")
+    if nonfinite:
+        in_kind = "fp32"
+        x[0, 0, 10:12, 10:12] = np.nan  # conv rows / columns 4-7 NaN: pooled (3, 3) sees only NaN
+        for (i, c, r, q), v in {(0, 1, 30, 40): np.inf, (1, 2, 50, 5): -np.inf, (1, 0, 33, 33): np.inf,
+                                (1, 1, 34, 35): -np.inf, (0, 0, 0, 63): np.nan, (1, 2, 63, 0): np.inf}.items():
+            x[i, c, r, q] = v
     code = {"bf16": _lib.BF16, "fp16": _lib.F16}[kind]
     sdt = {"bf16": BF16, "fp16": np.float16}[kind]
     ho, wo = (h + 6 - 7) // 2 + 1, (w + 6 - 7) // 2 + 1
@@ -580,6 +592,11 @@ def test_conv_stem_pool_matches_unfused_chain(gpu, kind, n, h, w, relu, in_kind)
     _lib.launch(f, None)
     got = fused.get()
     np.testing.assert_array_equal(got.view(np.uint16), pooled.get().view(np.uint16))
+    if nonfinite:
+        g = _from16(got, kind)
+        assert not np.isnan(g).any() and (g == np.inf).any()
+        assert (g[0, 3, 3] == (0.0 if relu else -np.inf)).all()
+        return
     xr, wr = G.round_to(x, kind), G.round_to(wt, kind)
     ref = R.conv2d(xr.astype(np.float64), wr.astype(np.float64), attrs) + b.reshape(1, 64, 1, 1)
     ref = np.maximum(ref, 0) if relu else ref
