@@ -7,18 +7,17 @@
 // fused, the conv output never leaves LDS.  Results are identical to the
 // unfused sequence: inputs are rounded to 16 bits exactly as the layout
 // kernel does, the conv uses the same MFMA (16x16x32, K chunk order and
-// accumulation order of c3h_conv2d's narrow-channel packing), the epilogue
-// pools before the epilogue (below), and the maximum of 16-bit-rounded
-// values equals the rounding of the maximum.
+// accumulation order of c3h_conv2d's narrow-channel packing), and the pool
+// runs before the bias / ReLU / rounding, which commutes with it (below).
 //
 // Work decomposition: a tile is 7 x 8 pooled pixels x 64 channels of one
 // image.  It needs a 15 x 17 conv-output tile (255 pixels, 16 MFMA column
-// tiles, four per wave), which needs a 35 x 40 x 4 input patch.  A persistent workgroup
-// (4 waves) walks a contiguous range of tiles: the next tile's patch is
-// loaded into registers while the current tile's MFMAs run, so global
-// latency hides behind compute, and neighbouring tiles share their input
-// halo in L2.  Every wave keeps the whole packed weight (64 x 224, as 28
-// MFMA fragments) in registers for the kernel's life.
+// tiles, four per wave), which needs a 35 x 40 x 4 input patch.  A
+// persistent workgroup (4 waves, two per CU) walks a contiguous range of
+// tiles: the next tile's patch is loaded into registers while the current
+// tile's MFMAs run, so global latency hides behind compute, and neighbouring
+// tiles share their input halo in L2.  Every wave keeps the whole packed
+// weight (64 x 224, as 28 MFMA fragments) in registers for the kernel's life.
 //
 // The MFMA computes C^T = W . X^T, so a lane's four accumulators are four
 // consecutive channels of one conv pixel; they go to the fp32 conv tile in
