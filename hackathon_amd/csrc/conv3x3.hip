@@ -193,7 +193,14 @@ __global__ void __launch_bounds__(kWaves * 64, 2) conv3x3_c64_kernel(Conv3x3Args
   // the compiler's wait insertion merges them into the loop header's state
   // and emits a vmcnt wait before every weight use in every band, which
   // also waits for the next band's patch DMA and serializes it with the MFMAs.
+  // The wait alone does not pin the loads: the scheduler sinks them past it
+  // to the loop entry.  An empty asm that takes every weight register as an
+  // operand right after the wait keeps them above it.
   wait_vm<0>();
+#pragma unroll
+  for (int j = 0; j < kTN; ++j)
+#pragma unroll
+    for (int s = 0; s < 18; ++s) asm volatile("" : "+v"(bw[j][s]));
 
   // Bands [t_begin, t_end) of this block: a contiguous, balanced range.
   const int t_begin = static_cast<int>(static_cast<int64_t>(blockIdx.x) * p.tiles / gridDim.x);
