@@ -49,11 +49,12 @@ constexpr int kWaves = 4;              // 2 (pixels) x 2 (channels)
 constexpr int kWavePix = 64;           // 4 row tiles per wave (the band padded to 128 pixels)
 constexpr int kTM = kWavePix / 16;     // 4
 constexpr int kTN = 2;                 // 32 channels per wave
-constexpr int kPatchGroups = 30;                         // DMA groups of 8 patch pixels
-constexpr int kMaxPatch = kPatchGroups * 8;              // 240 patch pixels
-constexpr int kGroups = kPatchGroups;                    // 30 KB per stage
-constexpr int kSlots = (kGroups + kWaves - 1) / kWaves;  // 19 DMA slots per wave
-constexpr int kStage = kGroups * 1024;
+constexpr int kMaxPatch = 240;                           // patch pixels per stage
+constexpr int kPitch = 144;                              // LDS bytes per patch pixel: 128 of channels + 16 of padding
+constexpr int kGroups = (kMaxPatch * kPitch + 1023) / 1024;  // 34 DMA instructions of 1 KB per stage
+constexpr int kSlots = (kGroups + kWaves - 1) / kWaves;  // 9 DMA slots per wave
+constexpr int kStage = kGroups * 1024;                   // 34816 bytes: the last DMA stays inside its stage
+static_assert(kMaxPatch * kPitch <= kStage, "patch fits a stage");
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset past num_records: reads zeros
 
 struct Conv3x3Args {
@@ -130,56 +131,64 @@ __global__ void __launch_bounds__(kWaves * 64, 2) conv3x3_c64_kernel(Conv3x3Args
         bw[j][s] = *reinterpret_cast<const vec*>(w + (wn * 32 + 16 * j + l16) * kK + s * 32 + lg * 8);
   }
 
-  // DMA slot j of this wave moves patch pixels 8 g .. 8 g + 7, g = wave + 4 j;
-  // a lane moves one 16-byte chunk of pixel 8 g + (lane >> 3).
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.x), 0, p.x_bytes, 0x00020000);
-  const int chunk = (lane & 7) ^ (lane >> 3);  // logical 16-byte chunk stored at physical chunk lane & 7
   // out and residual have x's extent (NHWC, 64 channels): below 2^31 bytes.
   const __amdgpu_buffer_rsrc_t rs_out = __builtin_amdgcn_make_buffer_rsrc(p.out, 0, p.x_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs_res =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.residual), 0, p.x_bytes, 0x00020000);
-  // DMA slot j of this wave: patch pixel pix = g * 8 + (lane >> 3),
-  // g = wave + 4 j, at patch row pr = pix / pw, column pix - pr * pw.  Its
-  // input pixel, relative to (h0 - 1, -1), is pr * W + (pix - pr * pw) =
-  // pix - 2 pr (pw = W + 2).  Only the row is kept per slot (far out of
-  // range for pixels past the patch or in its padding columns, so the row
-  // check fails); a band then costs a few adds, a compare and a select.
-  int spr[kSlots];
+  // LDS layout: patch pixel pix at byte pix * 144 (its 64 channels, then 16
+  // bytes of padding).  Sixteen consecutive pixels then start on sixteen
+  // different 16-byte bank groups, so fragment reads are conflict-free
+  // without a swizzle, and a fragment's address is a per-lane base plus
+  // constants.  DMA instruction g (slot j = (g - wave) / 4) fills stage
+  // bytes [1024 g, 1024 g + 1024): lane l writes 16 bytes at 1024 g + 16 l,
+  // which is chunk c = (byte % 144) / 16 of patch pixel byte / 144 (c = 8 is
+  // the padding: read out of range, as are pixels past the patch and its
+  // zero columns).  The pixel's patch row pr and its input offset relative
+  // to (h0 - 1, 0) do not depend on the band; they are kept per slot as
+  // pr << 16 | offset (pr = 0x7fff when the lane loads nothing, so the row
+  // check fails), and a band costs an add, a mask, a compare and a select.
+  int sdma[kSlots];
 #pragma unroll
   for (int j = 0; j < kSlots; ++j) {
-    const int pix = (wave + kWaves * j) * 8 + (lane >> 3);
+    const int byte = (wave + kWaves * j) * 1024 + lane * 16;
+    const int pix = byte / kPitch, c = (byte - pix * kPitch) >> 4;
     const int pr = static_cast<int>((static_cast<uint32_t>(pix) * p.pw_magic) >> 20);
     const int wi = pix - pr * pw - 1;
-    const bool ok = pix < p.npix && static_cast<unsigned>(wi) < static_cast<unsigned>(W);
-    spr[j] = ok ? pr : -0x10000000;  // 2 * spr stays within int
+    const bool ok = wave + kWaves * j < kGroups && c < 8 && pix < p.npix &&
+                    static_cast<unsigned>(wi) < static_cast<unsigned>(W);
+    sdma[j] = ok ? (pr << 16) | ((pr * W + wi) * (kC * 2) + c * 16) : 0x7fff << 16;
   }
   auto issue = [&](int t, int buf) {
     const int img = t / p.bands, h0 = (t - img * p.bands) * p.rows;
-    // byte offset of input pixel (h0 - 1, -1) of image img, plus this lane's pixel and chunk
-    const int lane_base = ((img * H + h0 - 1) * W - 1) * (kC * 2) + (lane >> 3) * (kC * 2) + chunk * 16;
+    // byte offset of input pixel (h0 - 1, 0) of image img
+    const int band_base = (img * H + h0 - 1) * W * (kC * 2);
 #pragma unroll
     for (int j = 0; j < kSlots; ++j) {
       const int g = wave + kWaves * j;
       uint8_t* dst = smem + buf * kStage + g * 1024;
-      if (g < kPatchGroups) {
-        const int hi = h0 - 1 + spr[j];
-        const int off = lane_base + (g * 8 - 2 * spr[j]) * (kC * 2);
+      if (g < kGroups) {
+        const int hi = h0 - 1 + (sdma[j] >> 16);
+        const int off = band_base + (sdma[j] & 0xffff);
         const uint32_t voff = static_cast<unsigned>(hi) < static_cast<unsigned>(H) ? static_cast<uint32_t>(off) : kOob;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_ptr)dst, 16, voff, 0, 0, 0);
       }
     }
   };
 
-  // Patch index of output pixel q = wm * 64 + 16 i + l16 of the band at tap
-  // (0, 0); pixels past the band (the padding to 128, or a band shorter than
-  // 112 pixels) read the band's last pixel and are never stored.
-  int p0[kTM];
+  // LDS byte of output pixel q = wm * 64 + 16 i + l16's fragment chunk lg at
+  // tap (0, 0) of stage 0; pixels past the band (the padding to 128, or a
+  // band shorter than 112 pixels) read the band's last pixel and are never
+  // stored.  A tap (kh, kw), K half ks and stage add (kh * pw + kw) * 144 +
+  // 64 ks + stage * 34816: kh's part per band in a scalar register, the rest
+  // as the read's immediate offset.
+  uint32_t a0[kTM];
   const int band_pix = p.band_pix;
 #pragma unroll
   for (int i = 0; i < kTM; ++i) {
     const int q = min(wm * kWavePix + 16 * i + l16, band_pix - 1);
     const int r = q / W;
-    p0[i] = r * pw + (q - r * W);
+    a0[i] = static_cast<uint32_t>((r * pw + (q - r * W)) * kPitch + lg * 16);
   }
 
   float bias[kTN][4];
@@ -244,11 +253,6 @@ __global__ void __launch_bounds__(kWaves * 64, 2) conv3x3_c64_kernel(Conv3x3Args
     }
     if (t + 1 < t_end) issue(t + 1, buf ^ 1);
 
-    const uint8_t* base = smem + buf * kStage;
-    // Likewise for the 126 LDS addresses derived from p0 (7 fragments x 18
-    // K steps): recomputed per tile, a few VALU per read.
-#pragma unroll
-    for (int i = 0; i < kTM; ++i) asm volatile("" : "+v"(p0[i]));
     f32x4 acc[kTM][kTN];
 #pragma unroll
     for (int i = 0; i < kTM; ++i)
@@ -259,24 +263,19 @@ __global__ void __launch_bounds__(kWaves * 64, 2) conv3x3_c64_kernel(Conv3x3Args
     // sub-step ahead, and a scheduling barrier between sub-steps keeps the
     // compiler from hoisting more reads (the weights hold 144 registers).
     vec av[2][kTM];
-    // Byte address of a fragment row's K chunks 4 ks + lg: pp * 128 +
-    // ((4 ks + lg) ^ (pp & 7)) * 16; the ks = 1 address is the ks = 0 one
-    // with bit 6 flipped, so each (tap, fragment) costs one address.
-    uint32_t aaddr[kTM];
+    // One address per (filter row, fragment): a0 + stage + kh * pw * 144
+    // (a wave-uniform add); kw and ks are immediate offsets of the reads.
+    uint32_t arow[kTM];
     auto load_a = [&](auto uc, vec (&dst)[kTM]) {
       constexpr int u = decltype(uc)::value;
-      constexpr int tap = u / 2, ks = u & 1;
-      if constexpr (ks == 0) {
-        const int toff = (tap / 3) * pw + (tap % 3);
+      constexpr int tap = u / 2, ks = u & 1, kh = tap / 3, kw = tap % 3;
+      if constexpr (kw == 0 && ks == 0) {
+        const uint32_t row = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(buf * kStage + kh * pw * kPitch));
 #pragma unroll
-        for (int i = 0; i < kTM; ++i) {
-          const int pp = p0[i] + toff;
-          aaddr[i] = static_cast<uint32_t>(pp * 128 + ((lg ^ (pp & 7)) << 4));
-        }
+        for (int i = 0; i < kTM; ++i) arow[i] = a0[i] + row;
       }
 #pragma unroll
-      for (int i = 0; i < kTM; ++i)
-        dst[i] = *reinterpret_cast<const vec*>(base + (ks ? (aaddr[i] ^ 64u) : aaddr[i]));
+      for (int i = 0; i < kTM; ++i) dst[i] = *reinterpret_cast<const vec*>(smem + arow[i] + (kw * kPitch + ks * 64));
     };
     load_a(std::integral_constant<int, 0>{}, av[0]);
     // MFMA section at raised wave priority (the other block on this CU's
@@ -355,7 +354,7 @@ int conv3x3_c64_launch(const c3h_conv_args* a, hipStream_t s, bool* handled) {
                    (reinterpret_cast<uintptr_t>(a->x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->w) & 15) == 0;
   if (!shape || !epi) return C3H_OK;
   const int64_t x_bytes = static_cast<int64_t>(a->n) * a->h * a->w_ * kC * 2;
-  if (x_bytes >= (int64_t{1} << 31) - 16) return C3H_OK;
+  if (x_bytes >= (int64_t{1} << 31) - 16 || a->h >= 0x7fff) return C3H_OK;  // the DMA row sentinel is 0x7fff
   const int rows = band_rows(a->h, a->w_);
   if (rows < 1) return C3H_OK;
   Conv3x3Args p;
