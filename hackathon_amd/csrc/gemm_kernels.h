@@ -351,6 +351,40 @@ __device__ __forceinline__ void store_strip(const Problem& p, const float* stage
     const int c0 = (lane & 3) * (WTN / 4);
     const int64_t m = mrow0 + row;
     if (m >= p.m) return;
+    if constexpr (std::is_same<TO, float>::value && WTN == 64) {
+      // fp32 rows with all 16 columns inside N, 16-byte aligned: the lane's
+      // residual comes in as four vector loads issued together (one memory
+      // round trip per strip instead of one per column) and the results
+      // leave as vector stores.  Same per-element arithmetic.
+      const int64_t o0 = m * p.ldo + ncol0 + c0;
+      const bool vec = ncol0 + c0 + 16 <= p.n && (p.ldo & 3) == 0 && (o0 & 3) == 0 &&
+                       (reinterpret_cast<uintptr_t>(outp) & 15) == 0 &&
+                       (resp == nullptr || (reinterpret_cast<uintptr_t>(resp) & 15) == 0);
+      if (vec) {
+        const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 r0 = resp ? *reinterpret_cast<const float4*>(resp + o0) : zero;
+        const float4 r1 = resp ? *reinterpret_cast<const float4*>(resp + o0 + 4) : zero;
+        const float4 r2 = resp ? *reinterpret_cast<const float4*>(resp + o0 + 8) : zero;
+        const float4 r3 = resp ? *reinterpret_cast<const float4*>(resp + o0 + 12) : zero;
+        const float* srow = stage + row * SS + c0;
+        const KArg<c3h_epilogue>& e = kernel_arg<Problem>().epi;
+        // A rolled loop (four epilogue copies, not sixteen) keeps the
+        // caller's strip loop small enough to unroll, so the accumulators
+        // stay in registers.
+#pragma unroll 1
+        for (int v = 0; v < 4; ++v) {
+          const float4 r = v == 0 ? r0 : v == 1 ? r1 : v == 2 ? r2 : r3;
+          const int c = 4 * v;
+          const int64_t n = ncol0 + c0 + c;
+          *reinterpret_cast<float4*>(outp + o0 + c) =
+              make_float4(apply_epilogue(e, srow[c], m, n, p.n, r.x, bias_off),
+                          apply_epilogue(e, srow[c + 1], m, n + 1, p.n, r.y, bias_off),
+                          apply_epilogue(e, srow[c + 2], m, n + 2, p.n, r.z, bias_off),
+                          apply_epilogue(e, srow[c + 3], m, n + 3, p.n, r.w, bias_off));
+        }
+        return;
+      }
+    }
     for (int c = 0; c < WTN / 4; ++c) {
       const int64_t n = ncol0 + c0 + c;
       if (n >= p.n) break;
