@@ -351,28 +351,29 @@ __device__ __forceinline__ void store_strip(const Problem& p, const float* stage
     const int c0 = (lane & 3) * (WTN / 4);
     const int64_t m = mrow0 + row;
     if (m >= p.m) return;
-    if constexpr (std::is_same<TO, float>::value && WTN == 64) {
-      // fp32 rows with all 16 columns inside N, 16-byte aligned: the lane's
-      // residual comes in as four vector loads issued together (one memory
-      // round trip per strip instead of one per column) and the results
-      // leave as vector stores.  Same per-element arithmetic.
+    if constexpr (std::is_same<TO, float>::value && (WTN == 64 || WTN == 32)) {
+      // fp32 rows with all WTN / 4 columns inside N, 16-byte aligned: the
+      // lane's residual comes in as WTN / 16 vector loads issued together
+      // (one memory round trip per strip instead of one per column) and the
+      // results leave as vector stores.  Same per-element arithmetic.
+      constexpr int NV = WTN / 16;
       const int64_t o0 = m * p.ldo + ncol0 + c0;
-      const bool vec = ncol0 + c0 + 16 <= p.n && (p.ldo & 3) == 0 && (o0 & 3) == 0 &&
+      const bool vec = ncol0 + c0 + WTN / 4 <= p.n && (p.ldo & 3) == 0 && (o0 & 3) == 0 &&
                        (reinterpret_cast<uintptr_t>(outp) & 15) == 0 &&
                        (resp == nullptr || (reinterpret_cast<uintptr_t>(resp) & 15) == 0);
       if (vec) {
         const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
         const float4 r0 = resp ? *reinterpret_cast<const float4*>(resp + o0) : zero;
         const float4 r1 = resp ? *reinterpret_cast<const float4*>(resp + o0 + 4) : zero;
-        const float4 r2 = resp ? *reinterpret_cast<const float4*>(resp + o0 + 8) : zero;
-        const float4 r3 = resp ? *reinterpret_cast<const float4*>(resp + o0 + 12) : zero;
+        const float4 r2 = NV == 4 && resp ? *reinterpret_cast<const float4*>(resp + o0 + 8) : zero;
+        const float4 r3 = NV == 4 && resp ? *reinterpret_cast<const float4*>(resp + o0 + 12) : zero;
         const float* srow = stage + row * SS + c0;
         const KArg<c3h_epilogue>& e = kernel_arg<Problem>().epi;
         // A rolled loop (four epilogue copies, not sixteen) keeps the
         // caller's strip loop small enough to unroll, so the accumulators
         // stay in registers.
 #pragma unroll 1
-        for (int v = 0; v < 4; ++v) {
+        for (int v = 0; v < NV; ++v) {
           const float4 r = v == 0 ? r0 : v == 1 ? r1 : v == 2 ? r2 : r3;
           const int c = 4 * v;
           const int64_t n = ncol0 + c0 + c;
