@@ -551,7 +551,9 @@ int c3h_conv2d(const c3h_conv_args* a, void* stream);
  * ([64][kh][kw_pack = 8][c_pack = 4], k_stride 224); out is NHWC
  * [n, po, qo, 64] in mm_dtype (each pooled window's centre conv pixel must
  * lie inside [ho, wo]).  Bit-identical to layout -> c3h_conv2d
- * (bias, relu) -> c3h_maxpool2d; replaces that chain for the Conv
+ * (bias, relu) -> c3h_maxpool2d (without ReLU: for a finite bias; the
+ * kernel pools before the bias, which commutes with the pool for every
+ * finite bias); replaces that chain for the Conv
  * (+BatchNormalization) + Relu + MaxPool nodes of c32/decompositions.py
  * :300-375 and the MaxPool that the reference registry lacks. */
 typedef struct {
