@@ -26,6 +26,7 @@ struct Switches {
   int dma_rp = 0;                // C3H_DMA_RP: register-pipelined DMA stages (0 = off)
   bool disable_pp = false;       // C3H_DISABLE_PP: no ping-pong schedule for 256 x 256 conv tiles
   bool disable_qmul = false;     // C3H_DISABLE_QMUL: quantize by the division form only
+  bool disable_tile160 = false;  // C3H_DISABLE_TILE160: no 160 x 128 conv tile
 };
 const Switches& switches();
 

@@ -1909,6 +1909,10 @@ template <typename Mma, typename TO, int BM, int BN, int WM, int WN, int AM, int
           bool PP = false>
 __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
   constexpr bool DIRECT = NW > 4;
+  // The 160-row tile has no staged epilogue: its LDS stage would not fit two
+  // blocks per CU, and the host takes it only for epilogues epilogue_direct
+  // computes (tile160_wins).
+  constexpr bool STAGED = !DIRECT && BM != 160;
   // GELU in registers (epilogue_direct) for 16-bit outputs as well: with the
   // branch-free erf it beats the staged epilogue.
   constexpr bool DIRECT_GELU = DIRECT || !Mma::kInt;
@@ -1924,7 +1928,7 @@ __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
   static_assert(WM * WN == NW && GROUPS % NW == 0 && BM % 8 == 0, "shape");
   static_assert(AM == kDenseK || AM == kConvTap, "dma kernel: dense or tap-uniform conv only");
   static_assert(S >= 2 && S <= 4 && LPW * (S - 2) < 64, "stages");
-  constexpr int kStageBytes = DIRECT ? 0 : NW * WTM * (WTN + 4) * 4;
+  constexpr int kStageBytes = STAGED ? NW * WTM * (WTN + 4) * 4 : 0;
   constexpr int kSmem = S * STAGE > kStageBytes ? S * STAGE : kStageBytes;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmem];
   typedef typename Mma::vec vec;
@@ -2224,12 +2228,12 @@ __global__ void __launch_bounds__(NW * 64) mfma_gemm_dma_kernel(Problem p) {
         epilogue_direct_q<TO, TM, TN, DIRECT_GELU>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act);
         return;
       }
-    } else if (DIRECT || epilogue_is_simple(kernel_arg<Problem>(), vec4, DIRECT_GELU)) {
+    } else if (!STAGED || epilogue_is_simple(kernel_arg<Problem>(), vec4, DIRECT_GELU)) {
       epilogue_direct<TO, TM, TN, DIRECT_GELU>(acc, m0 + wm * WTM, n0 + wn * WTN, lane, outp, resp, bias, p.epi.act);
       return;
     }
   }
-  if constexpr (!DIRECT) {
+  if constexpr (STAGED) {
   const bool vec_ok = !p.out_nchw && (p.ldo % 8 == 0) && ((reinterpret_cast<uintptr_t>(p.out) & 15) == 0) &&
                       ((reinterpret_cast<uintptr_t>(p.epi.residual) & 15) == 0);
   __syncthreads();
@@ -2361,6 +2365,27 @@ inline bool tile192_wins(const Problem& p, int cus, size_t out_size, bool int_mm
   return r192 < rounds_256(p, cus) && r192 < rounds_128(p, cus);
 }
 
+// Whether the 160 x 128 four-wave tile (wave tiles 80 x 64, two blocks per
+// CU) beats 128 x 128 on a 16-bit implicit-GEMM conv: its rounds cost 1.25
+// rounds of 128 x 128 tiles (the rows per tile), so it wins where it removes
+// a mostly empty last round (ResNet-18 224 layer 2: 1255 tiles are 3 rounds
+// of 512 slots, against 4 for the 1568 tiles of 128 x 128).  Its epilogue
+// must be one epilogue_direct computes (it has no staged form): row-major
+// aligned stores, alpha = beta = 1, no or per-column bias, ReLU or none.
+inline bool tile160_wins(const Problem& p, int cus, size_t out_size) {
+  if (switches().disable_tile160 || p.n <= 64 || p.n % 128 != 0) return false;
+  const c3h_epilogue& e = p.epi;
+  const uintptr_t al = 4 * out_size - 1;
+  const bool simple = !p.out_nchw && p.ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(p.out) & al) == 0 &&
+                      e.alpha == 1.0f && e.beta == 1.0f && (e.bias_mode == 0 || e.bias_mode == 2) && e.act <= 1 &&
+                      e.n_inst == 0 && e.row_max == nullptr &&
+                      (e.bias_mode == 0 || (reinterpret_cast<uintptr_t>(e.bias) & 15) == 0) &&
+                      (reinterpret_cast<uintptr_t>(e.residual) & al) == 0;
+  if (!simple) return false;
+  const double r160 = static_cast<double>(ceil_div(ceil_div(p.m, 160) * (p.n / 128), 2 * cus)) * 1.25;
+  return r160 < 0.97 * rounds_128(p, cus);
+}
+
 // Register-pipelined form of the 4-wave DMA kernel: C3H_DMA_RP = 2, 3 or 4
 // LDS stages (0: the two-stage kernel without register pipelining).
 inline int dma_rp_stages() { return switches().dma_rp; }
@@ -2414,6 +2439,13 @@ int launch_mfma(Problem p, int64_t batch, hipStream_t s, const char* what) {
         else
           hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 256, 64, 4, 1, AM, 2>), grid, dim3(kThreads), 0, s, p);
       } else {
+        if constexpr (AM == kConvTap && !Mma::kInt) {
+          if (rp == 0 && tile160_wins(p, device_cus(), sizeof(TO))) {
+            grid_of<160, 128>(p, 1, grid);
+            hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 160, 128, 2, 2, AM, 2>), grid, dim3(kThreads), 0, s, p);
+            return launch_status(what);
+          }
+        }
         grid_of<128, 128>(p, 1, grid);
         if (rp == 2)
           hipLaunchKernelGGL((mfma_gemm_dma_kernel<Mma, TO, 128, 128, 2, 2, AM, 2, 4, true>), grid, dim3(kThreads), 0, s,

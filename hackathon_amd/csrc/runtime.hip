@@ -40,6 +40,7 @@ static Switches read_switches() {
   w.dma_rp = rp ? atoi(rp) : 0;
   w.disable_pp = getenv("C3H_DISABLE_PP") != nullptr;
   w.disable_qmul = getenv("C3H_DISABLE_QMUL") != nullptr;
+  w.disable_tile160 = getenv("C3H_DISABLE_TILE160") != nullptr;
   return w;
 }
 

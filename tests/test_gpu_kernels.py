@@ -908,6 +908,74 @@ def test_conv_big_tile_matches_128_tiles(gpu, n, c, h, w, o, stride, resid):
         np.testing.assert_allclose(got[b_, y, x_], np.maximum(want, 0), rtol=1e-2, atol=4e-2)
 
 
+@pytest.mark.parametrize("n,c,h,w,o,ksz,stride,resid,dt,out_dt", [
+    (256, 128, 28, 28, 128, 3, 1, True, "bf16", "bf16"),   # ResNet-18 224 layer 2 (1255 tiles of 160 rows)
+    (256, 64, 56, 56, 128, 3, 2, False, "bf16", "bf16"),   # its stride-2 entry conv
+    (256, 64, 56, 56, 128, 1, 2, False, "bf16", "bf16"),   # its 1x1 downsampling shortcut
+    (200, 128, 28, 28, 128, 3, 1, True, "fp16", "f32"),    # ragged M (980 tiles), fp16 in, fp32 out
+    (203, 128, 28, 28, 128, 3, 1, False, "bf16", "bf16"),  # ragged last tile (159152 rows)
+])
+def test_conv_tile160_matches_128_tiles(gpu, n, c, h, w, o, ksz, stride, resid, dt, out_dt):
+    """16-bit implicit-GEMM convs whose 160 x 128 tiles fill fewer rounds of
+    the chip than 128 x 128 ones take the 160-row kernel: bit-identical to the
+    128 x 128 kernel (C3H_DISABLE_TILE160; same K order per element), and a
+    float64 spot check."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import BF16, DeviceArray
+
+    pad = ksz // 2
+    ho, wo = (h + 2 * pad - ksz) // stride + 1, (w + 2 * pad - ksz) // stride + 1
+    m = n * ho * wo
+    # the host's choice for a 256-CU device: 160-row rounds cost 1.25 rounds of 128 x 128
+    r128 = -(-(-(-m // 128) * -(-o // 128)) // 512)
+    r160 = -(-(-(-m // 160) * (o // 128)) // 512) * 1.25
+    assert r160 < 0.97 * r128, (r160, r128)
+    rng = np.random.default_rng(31 + n + o + ksz)
+    x32 = rng.standard_normal((n, h, w, c)).astype(np.float32)
+    w32 = (rng.standard_normal((o, ksz, ksz, c)) * 0.05).astype(np.float32)
+    xb, xv = _bits(x32, dt)
+    wb, wv = _bits(w32.reshape(o, -1), dt)
+    r32 = rng.standard_normal((n, ho, wo, o)).astype(np.float32)
+    if out_dt == "f32":
+        rb, rv = r32, r32
+    else:
+        rb, rv = _bits(r32, out_dt)
+    bias = rng.standard_normal(o).astype(np.float32)
+    xd, wd, bd, rd = _dev(xb), _dev(wb), _dev(bias), _dev(rb)
+    out = DeviceArray.empty((n, ho, wo, o), np.float32 if out_dt == "f32" else BF16)
+    in_code = _lib.BF16 if dt == "bf16" else _lib.F16
+    out_code = _lib.F32 if out_dt == "f32" else _lib.BF16
+
+    def launch():
+        a = _lib.ConvArgs()
+        a.x, a.w, a.out = xd.ptr, wd.ptr, out.ptr
+        a.n, a.c, a.h, a.w_, a.c_stride, a.c_pack, a.o = n, c, h, w, c, c, o
+        a.kh, a.kw, a.sh, a.sw, a.pad_top, a.pad_left, a.dh, a.dw, a.ho, a.wo = (
+            ksz, ksz, stride, stride, pad, pad, 1, 1, ho, wo)
+        a.out_layout, a.in_dtype, a.out_dtype = 1, in_code, out_code
+        a.epi = E.epilogue(bias=bd, bias_mode=2, act=1, residual=rd if resid else None)
+        print(f"conv n={n} {c}->{o} {h}x{w} k{ksz}/{stride} resid={resid} {dt}->{out_dt}", flush=True)
+        out.copy_from_host(np.zeros(out.nbytes, np.uint8))
+        _lib.launch(a, None)
+        return out.get().copy()
+    got160 = launch()
+    got128 = _with_env("C3H_DISABLE_TILE160", "1", launch)
+    if out_dt == "f32":
+        np.testing.assert_array_equal(got160.view(np.uint32), got128.view(np.uint32))
+        got = got160
+    else:
+        np.testing.assert_array_equal(got160.view(np.uint16), got128.view(np.uint16))
+        got = _from16(got160, out_dt)
+    assert np.any(got != 0)
+    xp = np.pad(xv.astype(np.float64), ((0, 0), (pad, pad), (pad, pad), (0, 0)))
+    wv4 = wv.astype(np.float64).reshape(o, ksz, ksz, c)
+    for (b_, y, x_) in [(0, 0, 0), (n // 3, ho // 2, wo - 1), (n - 1, ho - 1, wo - 1), (n // 2, ho // 2, ho // 2)]:
+        patch = xp[b_, stride * y:stride * y + ksz, stride * x_:stride * x_ + ksz, :]
+        want = np.einsum("hwc,ohwc->o", patch, wv4) + bias + (rv[b_, y, x_] if resid else 0.0)
+        np.testing.assert_allclose(got[b_, y, x_], np.maximum(want, 0), rtol=1e-2, atol=4e-2)
+
+
 @pytest.mark.parametrize("m,n,k,mode,act", [
     (4096, 4096, 256, 0, 0), (4096, 4096, 256, 2, 0), (4096, 4096, 256, 3, 2),
     # N a multiple of 192 with bf16 output: the 256x192 kernel
