@@ -21,8 +21,12 @@
 //     128) x 32 channels each, so every A fragment read from LDS feeds two
 //     MFMAs;
 //   * the band's residual is loaded into registers before the MFMAs, and a
-//     band's kTM * kTN output stores per wave stay in flight while the next
-//     band is multiplied.
+//     band's kTM output stores per wave stay in flight while the next band
+//     is multiplied;
+//   * residual loads and output stores move 16 bytes per lane, 8 channels
+//     of one pixel (each wave's 64 bytes of a pixel in one access): two lane
+//     swaps (permlane32 / permlane16) convert between that layout and the
+//     MFMA accumulators' 4 channels per lane.
 // The K order (tap-major, then channel chunks 0-31 and 32-63 with lane group
 // g supplying chunk g) and the epilogue arithmetic ((acc + bias) + residual,
 // then max 0) are those of the tap-uniform implicit-GEMM kernel, so the
@@ -36,7 +40,7 @@ namespace c3h {
 namespace {
 
 typedef __attribute__((ext_vector_type(4))) float f32x4;
-typedef __attribute__((ext_vector_type(2))) int i32x2;
+typedef __attribute__((ext_vector_type(4))) int i32x4;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
@@ -221,10 +225,10 @@ __global__ void __launch_bounds__(kWaves * 64, 2) conv3x3_c64_kernel(Conv3x3Args
   for (bool first = true; t < t_end; ++t, first = false) {
     // This wave's DMAs of band t are complete (vector-memory operations
     // retire in issue order; the only later ones are the previous band's
-    // kTM * kTN stores, which may stay in flight); the barrier makes every
+    // kTM stores, which may stay in flight); the barrier makes every
     // wave's complete and retires all reads of the other stage.
     if (first) wait_vm<0>();
-    else wait_vm<kTM * kTN>();
+    else wait_vm<kTM>();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -232,24 +236,21 @@ __global__ void __launch_bounds__(kWaves * 64, 2) conv3x3_c64_kernel(Conv3x3Args
     const int img = t / p.bands, h0 = (t - img * p.bands) * p.rows;
     const int valid = min(p.rows, H - h0) * W;
     const uint32_t band_off = static_cast<uint32_t>((img * H + h0) * W) * (kO * 2);
-    const uint32_t col_off = static_cast<uint32_t>(wn * 32 + 4 * lg) * 2;
+    // lane's 16 bytes of a pixel: channels wn * 32 + 8 lg .. + 7
+    const uint32_t col_off = static_cast<uint32_t>(wn * 32 + 8 * lg) * 2;
     uint32_t roff[kTM];
 #pragma unroll
     for (int i = 0; i < kTM; ++i) {
       const int q = wm * kWavePix + 16 * i + l16;
       roff[i] = q < valid ? band_off + static_cast<uint32_t>(q) * (kO * 2) + col_off : kOob;
     }
-    i32x2 rraw[kTM][kTN];
+    i32x4 rraw[kTM];
     if (p.residual) {
 #pragma unroll
-      for (int i = 0; i < kTM; ++i)
-#pragma unroll
-        for (int j = 0; j < kTN; ++j) rraw[i][j] = __builtin_amdgcn_raw_buffer_load_b64(rs_res, roff[i] + 32 * j, 0, 0);
+      for (int i = 0; i < kTM; ++i) rraw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_res, roff[i], 0, 0);
     } else {
 #pragma unroll
-      for (int i = 0; i < kTM; ++i)
-#pragma unroll
-        for (int j = 0; j < kTN; ++j) rraw[i][j] = i32x2{0, 0};
+      for (int i = 0; i < kTM; ++i) rraw[i] = i32x4{0, 0, 0, 0};
     }
     if (t + 1 < t_end) issue(t + 1, buf ^ 1);
 
@@ -293,28 +294,66 @@ __global__ void __launch_bounds__(kWaves * 64, 2) conv3x3_c64_kernel(Conv3x3Args
     __builtin_amdgcn_s_setprio(0);
 
     // Epilogue from the C^T accumulators: acc[i][j][r] is output pixel
-    // q = wm * 64 + 16 i + l16 of the band, channel wn * 32 + 16 j + 4 lg + r.
-    // The residual was loaded into rraw at the top of the band (zeros past it).
+    // q = wm * 64 + 16 i + l16 of the band, channel wn * 32 + 16 j + 4 lg + r,
+    // and the 16-bit pair (r = 2h, 2h + 1) is dword d[j][h] of the lane.  The
+    // 16-byte layout gives lane row lg (lanes 16 lg .. 16 lg + 15) channels
+    // 8 lg .. 8 lg + 7 of the wave's 32, dword k = 2 k1 + h holding channels
+    // 8 lg + 4 k1 + 2 h, + 1: the pair that d[j = lg >> 1][h] holds in lane
+    // row 2 (lg & 1) + k1.  Between the two, the index bits (j, lane row bit
+    // 1, lane row bit 0) become (lane row bit 1, lane row bit 0, k1): a
+    // permlane32 swap exchanges the register bit with lane row bit 1 (the
+    // upper 32 lanes of the first operand with the lower 32 of the second),
+    // then a permlane16 swap exchanges it with lane row bit 0 (odd rows of
+    // the first with even rows of the second).  Lanes of one pixel (same l16)
+    // trade values, so a pixel's validity is uniform over its lanes.
+    // The residual, loaded in the 16-byte layout at the top of the band
+    // (zeros past it), goes the inverse way (permlane16, then permlane32).
     // Stores are buffer stores at 32-bit byte offsets: rows past the band get
     // an offset past num_records and are dropped, so every wave issues
-    // exactly kTM * kTN stores per band (the wait at the top of the loop
-    // counts them).
+    // exactly kTM stores per band (the wait at the top of the loop counts
+    // them).
 #pragma unroll
-    for (int i = 0; i < kTM; ++i)
+    for (int i = 0; i < kTM; ++i) {
+      uint32_t rd[kTN][2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (p.residual) {
+          const auto e = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(rraw[i][h]),
+                                                          static_cast<uint32_t>(rraw[i][2 + h]), false, false);
+          const auto d = __builtin_amdgcn_permlane32_swap(e[0], e[1], false, false);
+          rd[0][h] = d[0];
+          rd[1][h] = d[1];
+        } else {
+          rd[0][h] = 0u;
+          rd[1][h] = 0u;
+        }
+      }
+      uint32_t pk[kTN][2];
 #pragma unroll
       for (int j = 0; j < kTN; ++j) {
-        const uint32_t r01 = static_cast<uint32_t>(rraw[i][j][0]), r23 = static_cast<uint32_t>(rraw[i][j][1]);
-        const float res[4] = {to_f32<F16>(r01 & 0xffffu), to_f32<F16>(r01 >> 16), to_f32<F16>(r23 & 0xffffu),
-                              to_f32<F16>(r23 >> 16)};
+        const float res[4] = {to_f32<F16>(rd[j][0] & 0xffffu), to_f32<F16>(rd[j][0] >> 16),
+                              to_f32<F16>(rd[j][1] & 0xffffu), to_f32<F16>(rd[j][1] >> 16)};
         float v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float s = (acc[i][j][r] + bias[j][r]) + res[r];
           v[r] = p.relu ? fmaxf(s, 0.0f) : s;
         }
-        const i32x2 packed{static_cast<int>(pack2<F16>(v[0], v[1])), static_cast<int>(pack2<F16>(v[2], v[3]))};
-        __builtin_amdgcn_raw_buffer_store_b64(packed, rs_out, roff[i] + 32 * j, 0, 0);
+        pk[j][0] = pack2<F16>(v[0], v[1]);
+        pk[j][1] = pack2<F16>(v[2], v[3]);
       }
+      uint32_t z[2][2];  // [k1][h]
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const auto e = __builtin_amdgcn_permlane32_swap(pk[0][h], pk[1][h], false, false);
+        const auto zz = __builtin_amdgcn_permlane16_swap(e[0], e[1], false, false);
+        z[0][h] = zz[0];
+        z[1][h] = zz[1];
+      }
+      const i32x4 packed{static_cast<int>(z[0][0]), static_cast<int>(z[0][1]), static_cast<int>(z[1][0]),
+                         static_cast<int>(z[1][1])};
+      __builtin_amdgcn_raw_buffer_store_b128(packed, rs_out, roff[i], 0, 0);
+    }
     buf ^= 1;
   }
 }
