@@ -186,9 +186,66 @@ struct Elem16 {
   static __device__ __forceinline__ void store4(T* p, const float* v) {
     *reinterpret_cast<uint2*>(p) = uint2{Pack2(v[0], v[1]), Pack2(v[2], v[3])};
   }
+  // Two elements as one dword (the first in the low half), and back.
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) { return Pack2(lo, hi); }
+  static __device__ __forceinline__ void unpack2(uint32_t w, float* v) {
+    v[0] = ToF(static_cast<uint16_t>(w & 0xffffu));
+    v[1] = ToF(static_cast<uint16_t>(w >> 16));
+  }
 };
 template <> struct Elem<bf16_t> : Elem16<bf16_t, bf16_bits_to_f32, f32_to_bf16_bits, f32x2_to_bf16x2_bits> {};
 template <> struct Elem<f16_t> : Elem16<f16_t, f16_bits_to_f32, f32_to_f16_bits, f32x2_to_f16x2_bits> {};
+
+// 16-bit outputs of the MFMA C^T accumulator layout, 16 bytes per lane.  A
+// 16 x 16 output tile j of a 16x16 MFMA leaves lane (l16, lg = lane / 16)
+// with row l16's columns 16 j + 4 lg .. + 3, as dwords d[j][h] (columns
+// 4 lg + 2 h, + 1).  For a pair of adjacent tiles (j = 0, 1: 32 columns),
+// the row layout gives lane row lg columns 8 lg .. 8 lg + 7 instead, as one
+// 16-byte vector whose dword k = 2 k1 + h holds columns 8 lg + 4 k1 + 2 h,
+// + 1 -- the pair that d[lg >> 1][h] holds in lane row 2 (lg & 1) + k1.  So
+// the index bits (tile j, lane row bit 1, lane row bit 0) of a pair become
+// (lane row bit 1, lane row bit 0, k1): a permlane32 swap exchanges the
+// register index with lane row bit 1 (the upper 32 lanes of its first
+// operand with the lower 32 of its second), a permlane16 swap then
+// exchanges it with lane row bit 0 (odd lane rows of the first operand with
+// even rows of the second).  Only lanes with the same l16 (the same output
+// row) trade values.
+__device__ __forceinline__ uint4 ct_pair_to_rows(const uint32_t (&d0)[2], const uint32_t (&d1)[2]) {
+  uint32_t z[2][2];  // [k1][h]
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const auto e = __builtin_amdgcn_permlane32_swap(d0[h], d1[h], false, false);
+    const auto f = __builtin_amdgcn_permlane16_swap(e[0], e[1], false, false);
+    z[0][h] = f[0];
+    z[1][h] = f[1];
+  }
+  return uint4{z[0][0], z[0][1], z[1][0], z[1][1]};
+}
+// int8 outputs: tile j of a group of four (64 columns) leaves lane (l16, lg)
+// with row l16's columns 16 j + 4 lg .. + 3 as the dword w[j]; the row
+// layout gives lane row lg the group's columns 16 lg .. 16 lg + 15, whose
+// dword k is w[lg] of lane row k -- a transpose of (tile, lane row): tile
+// bit 1 <-> lane row bit 1 (permlane32 swaps of tiles 0, 2 and 1, 3), then
+// tile bit 0 <-> lane row bit 0 (permlane16 swaps of 0, 1 and 2, 3).
+__device__ __forceinline__ uint4 ct_quad_to_rows(const uint32_t (&w)[4]) {
+  const auto a = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  return uint4{c[0], c[1], d[0], d[1]};
+}
+// The inverse of ct_pair_to_rows: a row-layout vector back to the dwords d0
+// (tile j = 0) and d1.
+__device__ __forceinline__ void rows_to_ct_pair(const uint4 q, uint32_t (&d0)[2], uint32_t (&d1)[2]) {
+  const uint32_t z[2][2] = {{q.x, q.y}, {q.z, q.w}};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const auto e = __builtin_amdgcn_permlane16_swap(z[0][h], z[1][h], false, false);
+    const auto f = __builtin_amdgcn_permlane32_swap(e[0], e[1], false, false);
+    d0[h] = f[0];
+    d1[h] = f[1];
+  }
+}
 
 // 16 bytes of T <-> fp32 values (8 for 16-bit types, 4 for fp32).
 template <typename T>

@@ -294,40 +294,23 @@ __global__ void __launch_bounds__(kWaves * 64, 2) conv3x3_c64_kernel(Conv3x3Args
     __builtin_amdgcn_s_setprio(0);
 
     // Epilogue from the C^T accumulators: acc[i][j][r] is output pixel
-    // q = wm * 64 + 16 i + l16 of the band, channel wn * 32 + 16 j + 4 lg + r,
-    // and the 16-bit pair (r = 2h, 2h + 1) is dword d[j][h] of the lane.  The
-    // 16-byte layout gives lane row lg (lanes 16 lg .. 16 lg + 15) channels
-    // 8 lg .. 8 lg + 7 of the wave's 32, dword k = 2 k1 + h holding channels
-    // 8 lg + 4 k1 + 2 h, + 1: the pair that d[j = lg >> 1][h] holds in lane
-    // row 2 (lg & 1) + k1.  Between the two, the index bits (j, lane row bit
-    // 1, lane row bit 0) become (lane row bit 1, lane row bit 0, k1): a
-    // permlane32 swap exchanges the register bit with lane row bit 1 (the
-    // upper 32 lanes of the first operand with the lower 32 of the second),
-    // then a permlane16 swap exchanges it with lane row bit 0 (odd rows of
-    // the first with even rows of the second).  Lanes of one pixel (same l16)
-    // trade values, so a pixel's validity is uniform over its lanes.
-    // The residual, loaded in the 16-byte layout at the top of the band
-    // (zeros past it), goes the inverse way (permlane16, then permlane32).
+    // q = wm * 64 + 16 i + l16 of the band, channel wn * 32 + 16 j + 4 lg + r.
+    // The packed outputs go to the 16-byte row layout (lane row lg: the
+    // wave's channels 8 lg .. 8 lg + 7 of the pixel) by ct_pair_to_rows, and
+    // the residual, loaded in that layout at the top of the band (zeros past
+    // it), comes back by rows_to_ct_pair.  Only lanes of one pixel trade
+    // values, so a pixel's validity is uniform over them.
     // Stores are buffer stores at 32-bit byte offsets: rows past the band get
     // an offset past num_records and are dropped, so every wave issues
     // exactly kTM stores per band (the wait at the top of the loop counts
     // them).
 #pragma unroll
     for (int i = 0; i < kTM; ++i) {
-      uint32_t rd[kTN][2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if (p.residual) {
-          const auto e = __builtin_amdgcn_permlane16_swap(static_cast<uint32_t>(rraw[i][h]),
-                                                          static_cast<uint32_t>(rraw[i][2 + h]), false, false);
-          const auto d = __builtin_amdgcn_permlane32_swap(e[0], e[1], false, false);
-          rd[0][h] = d[0];
-          rd[1][h] = d[1];
-        } else {
-          rd[0][h] = 0u;
-          rd[1][h] = 0u;
-        }
-      }
+      uint32_t rd[kTN][2] = {{0u, 0u}, {0u, 0u}};
+      if (p.residual)
+        rows_to_ct_pair(uint4{static_cast<uint32_t>(rraw[i][0]), static_cast<uint32_t>(rraw[i][1]),
+                              static_cast<uint32_t>(rraw[i][2]), static_cast<uint32_t>(rraw[i][3])},
+                        rd[0], rd[1]);
       uint32_t pk[kTN][2];
 #pragma unroll
       for (int j = 0; j < kTN; ++j) {
@@ -342,16 +325,8 @@ __global__ void __launch_bounds__(kWaves * 64, 2) conv3x3_c64_kernel(Conv3x3Args
         pk[j][0] = pack2<F16>(v[0], v[1]);
         pk[j][1] = pack2<F16>(v[2], v[3]);
       }
-      uint32_t z[2][2];  // [k1][h]
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const auto e = __builtin_amdgcn_permlane32_swap(pk[0][h], pk[1][h], false, false);
-        const auto zz = __builtin_amdgcn_permlane16_swap(e[0], e[1], false, false);
-        z[0][h] = zz[0];
-        z[1][h] = zz[1];
-      }
-      const i32x4 packed{static_cast<int>(z[0][0]), static_cast<int>(z[0][1]), static_cast<int>(z[1][0]),
-                         static_cast<int>(z[1][1])};
+      const uint4 z = ct_pair_to_rows(pk[0], pk[1]);
+      const i32x4 packed{static_cast<int>(z.x), static_cast<int>(z.y), static_cast<int>(z.z), static_cast<int>(z.w)};
       __builtin_amdgcn_raw_buffer_store_b128(packed, rs_out, roff[i], 0, 0);
     }
     buf ^= 1;

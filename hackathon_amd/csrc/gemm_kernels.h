@@ -1046,6 +1046,63 @@ __device__ __forceinline__ void epilogue_direct_interior(const Acc (&acc)[TM][TN
       b[j][0] = q.x; b[j][1] = q.y; b[j][2] = q.z; b[j][3] = q.w;
     }
   });
+  if constexpr (sizeof(TO) == 2 && TN % 2 == 0 && ACT <= 1) {
+    // 16-bit output rows 16-byte aligned: residual loads and stores of 16
+    // bytes per lane (a lane row's 8 columns of each pair of column tiles),
+    // converted from / to the accumulators' 4 columns per lane by lane swaps
+    // (rows_to_ct_pair, ct_pair_to_rows).  Same values, wider accesses.
+    // (GELU interiors keep the 8-byte form: measured faster there, the
+    // fp16 decoder's FFN1 54 against 56-57 us.)
+    if ((ldo & 7) == 0 && (reinterpret_cast<uintptr_t>(outp) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(resp) & 15) == 0) {
+      TO* base = outp + (mbase + l16) * ldo + nbase + 8 * lg;
+      const TO* rbase = resp ? resp + (mbase + l16) * ldo + nbase + 8 * lg : nullptr;
+      static_for<TM>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        RowMax best[TN / 4];
+        if constexpr (RB) {
+#pragma unroll
+          for (int q = 0; q < TN / 4; ++q) best[q].start();
+        }
+        float res[TN][4];
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) res[j][r] = 0.0f;
+        if (rbase) {
+          static_for<TN / 2>([&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            uint32_t d0[2], d1[2];
+            rows_to_ct_pair(*reinterpret_cast<const uint4*>(rbase + 16 * i * ldo + 32 * q), d0, d1);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              Elem<TO>::unpack2(d0[h], &res[2 * q][2 * h]);
+              Elem<TO>::unpack2(d1[h], &res[2 * q + 1][2 * h]);
+            }
+          });
+        }
+        uint32_t pk[TN][2];
+        static_for<TN>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float t = (acc[i][j][r] + b[j][r]) + res[j][r];
+            v[r] = ACT == 1 ? fmaxf(t, 0.0f) : (ACT == 3 ? gelu_std(t) : (ACT == 2 ? gelu_erf(t, g0, g1, g2) : t));
+            if constexpr (RB) best[j / 4].see(stored_value<TO>(v[r]));
+          }
+          pk[j][0] = Elem<TO>::pack2(v[0], v[1]);
+          pk[j][1] = Elem<TO>::pack2(v[2], v[3]);
+        });
+        static_for<TN / 2>([&](auto qc) {
+          constexpr int q = decltype(qc)::value;
+          *reinterpret_cast<uint4*>(base + 16 * i * ldo + 32 * q) = ct_pair_to_rows(pk[2 * q], pk[2 * q + 1]);
+        });
+        if constexpr (RB) row_max_store(best, lane, mbase + 16 * i, nbase);
+      });
+      return;
+    }
+  }
   TO* base = outp + (mbase + l16) * ldo + nbase + 4 * lg;
   const TO* rbase = resp ? resp + (mbase + l16) * ldo + nbase + 4 * lg : nullptr;
   static_for<TM>([&](auto ic) {
@@ -1338,6 +1395,19 @@ __device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], in
   }
   TO* base = outp + (mbase + l16) * ldo + nbase + 4 * lg;
   const TO* rbase = resp ? resp + (mbase + l16) * ldo + nbase + 4 * lg : nullptr;
+  // 16-byte accesses where rows are 16-byte aligned: 16-bit outputs and
+  // residuals (KIND 2 / 3 without GELU) by pairs of column tiles
+  // (ct_pair_to_rows, rows_to_ct_pair), int8 outputs by groups of four
+  // (ct_quad_to_rows); a lane row then covers 8 / 16 consecutive columns.
+  constexpr bool kW16 = sizeof(TO) == 2 && TN % 2 == 0 && ACT <= 1 && (KIND == 2 || KIND == 3);
+  constexpr bool kW8 = std::is_same<TO, int8_t>::value && TN % 4 == 0;
+  bool wide = false;
+  if constexpr (kW16 || kW8)
+    wide = (ldo & (kW8 ? 15 : 7)) == 0 && (reinterpret_cast<uintptr_t>(outp) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(resp) & 15) == 0;
+  constexpr int kWideCols = kW8 ? 16 : 8;
+  TO* wbase = outp + (mbase + l16) * ldo + nbase + kWideCols * lg;
+  const TO* wrbase = resp ? resp + (mbase + l16) * ldo + nbase + kWideCols * lg : nullptr;
   static_for<TM>([&](auto ic) {
     constexpr int i = decltype(ic)::value;
     TO* row = base + 16 * i * ldo;
@@ -1352,19 +1422,11 @@ __device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], in
 #pragma unroll
         for (int q = 0; q < TN / 4; ++q) best[q].start();
       }
-      float res[TN][4];
-      static_for<TN>([&](auto jc) {
+      // Column tile j's four values v (float outputs) and int8 codes (the
+      // return value: KIND 1, 4, 5), given its residual values res.
+      auto tile = [&](auto jc, const float (&res)[4], float (&v)[4]) -> uint32_t {
         constexpr int j = decltype(jc)::value;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) res[j][r] = 0.0f;
-        if constexpr (KIND == 2 || KIND == 3) {
-          if (rbase) Elem<TO>::load4(rbase + 16 * i * ldo + 16 * j, res[j]);
-        }
-      });
-      static_for<TN>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        float v[4];
-        uint32_t w = 0u;  // biased int8 codes (KIND 1, 4, 5)
+        uint32_t w = 0u;  // biased int8 codes
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float a = static_cast<float>(acc[i][j][r]);
@@ -1379,18 +1441,81 @@ __device__ __forceinline__ void epilogue_q_interior(const Acc (&acc)[TM][TN], in
             } else {
               v[r] = a * mult[j][r];
             }
-            const float t = kQuantOut ? v[r] + b[j][r] : (v[r] + b[j][r]) + res[j][r];
+            const float t = kQuantOut ? v[r] + b[j][r] : (v[r] + b[j][r]) + res[r];
             v[r] = ACT == 1 ? fmaxf(t, 0.0f) : (ACT == 3 ? gelu_std(t) : (ACT == 2 ? gelu_erf(t, g0, g1, g2) : t));
             if constexpr (kQuantOut) w = __builtin_amdgcn_cvt_pk_u8_f32(rintf(bf16_round(v[r]) * qmul) + qb, r, w);
             if constexpr (RB) best[j / 4].see(stored_value<TO>(v[r]));
           }
         }
-        if constexpr (std::is_same<TO, int8_t>::value) {
-          *reinterpret_cast<uint32_t*>(row + 16 * j) = w ^ 0x80808080u;
-        } else {
-          Elem<TO>::store4(row + 16 * j, v);
+        return w ^ 0x80808080u;
+      };
+      bool done = false;
+      if constexpr (kW16) {
+        if (wide) {
+          // the row block's residual, packed (all loads first), then a pair
+          // of column tiles at a time
+          uint4 rq[TN / 2];
+#pragma unroll
+          for (int q = 0; q < TN / 2; ++q)
+            rq[q] = wrbase ? *reinterpret_cast<const uint4*>(wrbase + 16 * i * ldo + 32 * q) : uint4{0u, 0u, 0u, 0u};
+          static_for<TN / 2>([&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            uint32_t d0[2], d1[2];
+            rows_to_ct_pair(rq[q], d0, d1);
+            float r0[4], r1[4], v0[4], v1[4];
+            Elem<TO>::unpack2(d0[0], &r0[0]);
+            Elem<TO>::unpack2(d0[1], &r0[2]);
+            Elem<TO>::unpack2(d1[0], &r1[0]);
+            Elem<TO>::unpack2(d1[1], &r1[2]);
+            tile(std::integral_constant<int, 2 * q>{}, r0, v0);
+            tile(std::integral_constant<int, 2 * q + 1>{}, r1, v1);
+            const uint32_t p0[2] = {Elem<TO>::pack2(v0[0], v0[1]), Elem<TO>::pack2(v0[2], v0[3])};
+            const uint32_t p1[2] = {Elem<TO>::pack2(v1[0], v1[1]), Elem<TO>::pack2(v1[2], v1[3])};
+            *reinterpret_cast<uint4*>(wbase + 16 * i * ldo + 32 * q) = ct_pair_to_rows(p0, p1);
+          });
+          done = true;
         }
-      });
+      }
+      if constexpr (kW8) {
+        if (wide) {
+          static_for<TN / 4>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            const float z[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            float v[4];
+            const uint32_t w4[4] = {tile(std::integral_constant<int, 4 * g>{}, z, v),
+                                    tile(std::integral_constant<int, 4 * g + 1>{}, z, v),
+                                    tile(std::integral_constant<int, 4 * g + 2>{}, z, v),
+                                    tile(std::integral_constant<int, 4 * g + 3>{}, z, v)};
+            *reinterpret_cast<uint4*>(wbase + 16 * i * ldo + 64 * g) = ct_quad_to_rows(w4);
+          });
+          done = true;
+        }
+      }
+      if (!done) {
+        float res[TN][4];
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) res[j][r] = 0.0f;
+        if constexpr (KIND == 2 || KIND == 3) {
+          if (rbase) {
+            static_for<TN>([&](auto jc) {
+              constexpr int j = decltype(jc)::value;
+              Elem<TO>::load4(rbase + 16 * i * ldo + 16 * j, res[j]);
+            });
+          }
+        }
+        static_for<TN>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          float v[4];
+          const uint32_t w = tile(jc, res[j], v);
+          if constexpr (std::is_same<TO, int8_t>::value) {
+            *reinterpret_cast<uint32_t*>(row + 16 * j) = w;
+          } else {
+            Elem<TO>::store4(row + 16 * j, v);
+          }
+        });
+      }
       if constexpr (RB) row_max_store(best, lane, mbase + 16 * i, nbase);
     }
   });
