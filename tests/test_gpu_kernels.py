@@ -920,17 +920,23 @@ def test_conv_tile160_matches_128_tiles(gpu, n, c, h, w, o, ksz, stride, resid, 
     the chip than 128 x 128 ones take the 160-row kernel: bit-identical to the
     128 x 128 kernel (C3H_DISABLE_TILE160; same K order per element), and a
     float64 spot check."""
+    m = n * ((h + 2 * (ksz // 2) - ksz) // stride + 1) * ((w + 2 * (ksz // 2) - ksz) // stride + 1)
+    # the host's choice for a 256-CU device: 160-row rounds cost 1.25 rounds of 128 x 128
+    r128 = -(-(-(-m // 128) * -(-o // 128)) // 512)
+    r160 = -(-(-(-m // 160) * (o // 128)) // 512) * 1.25
+    assert r160 < 0.97 * r128, (r160, r128)
+    _conv_alt_tile_check(n, c, h, w, o, ksz, stride, resid, dt, out_dt, ["C3H_DISABLE_TILE160"])
+
+
+def _conv_alt_tile_check(n, c, h, w, o, ksz, stride, resid, dt, out_dt, switches_off):
+    """Runs a conv with the default kernel choice and with each switch in
+    switches_off set; all outputs bit-identical; float64 spot check."""
     from hackathon_amd import _lib
     from hackathon_amd.c35 import engine as E
     from hackathon_amd.device import BF16, DeviceArray
 
     pad = ksz // 2
     ho, wo = (h + 2 * pad - ksz) // stride + 1, (w + 2 * pad - ksz) // stride + 1
-    m = n * ho * wo
-    # the host's choice for a 256-CU device: 160-row rounds cost 1.25 rounds of 128 x 128
-    r128 = -(-(-(-m // 128) * -(-o // 128)) // 512)
-    r160 = -(-(-(-m // 160) * (o // 128)) // 512) * 1.25
-    assert r160 < 0.97 * r128, (r160, r128)
     rng = np.random.default_rng(31 + n + o + ksz)
     x32 = rng.standard_normal((n, h, w, c)).astype(np.float32)
     w32 = (rng.standard_normal((o, ksz, ksz, c)) * 0.05).astype(np.float32)
@@ -959,14 +965,12 @@ def test_conv_tile160_matches_128_tiles(gpu, n, c, h, w, o, ksz, stride, resid, 
         out.copy_from_host(np.zeros(out.nbytes, np.uint8))
         _lib.launch(a, None)
         return out.get().copy()
-    got160 = launch()
-    got128 = _with_env("C3H_DISABLE_TILE160", "1", launch)
-    if out_dt == "f32":
-        np.testing.assert_array_equal(got160.view(np.uint32), got128.view(np.uint32))
-        got = got160
-    else:
-        np.testing.assert_array_equal(got160.view(np.uint16), got128.view(np.uint16))
-        got = _from16(got160, out_dt)
+    got_default = launch()
+    view = np.uint32 if out_dt == "f32" else np.uint16
+    for var in switches_off:
+        other = _with_env(var, "1", launch)
+        np.testing.assert_array_equal(got_default.view(view), other.view(view), err_msg=var)
+    got = got_default if out_dt == "f32" else _from16(got_default, out_dt)
     assert np.any(got != 0)
     xp = np.pad(xv.astype(np.float64), ((0, 0), (pad, pad), (pad, pad), (0, 0)))
     wv4 = wv.astype(np.float64).reshape(o, ksz, ksz, c)
