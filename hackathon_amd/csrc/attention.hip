@@ -379,17 +379,31 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
     __syncthreads();
   }
 
+  // O rows 16-byte aligned: each pair of dim tiles leaves as one 16-byte
+  // store per lane (lane row g: dims 32 pair + 8 g .. + 7 of its query, by
+  // the lane swaps of ct_pair_to_rows, which trade values only between
+  // lanes of one query); otherwise 8 bytes per lane and tile.
+  const bool wide = ((a.o_ss | a.o_sh | a.o_sb) & 7) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0;
 #pragma unroll
   for (int u = 0; u < QG; ++u) {
     const float l_tot = l_acc[u][0];
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (q_valid[u]) {
+    uint32_t pk[4][2];
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const uint2 w = {pack2<T>(o_acc[u][d][0] * inv, o_acc[u][d][1] * inv),
-                         pack2<T>(o_acc[u][d][2] * inv, o_acc[u][d][3] * inv)};
-        *reinterpret_cast<uint2*>(O + q[u] * a.o_ss + 16 * d + 4 * g) = w;
+    for (int d = 0; d < 4; ++d) {
+      pk[d][0] = pack2<T>(o_acc[u][d][0] * inv, o_acc[u][d][1] * inv);
+      pk[d][1] = pack2<T>(o_acc[u][d][2] * inv, o_acc[u][d][3] * inv);
+    }
+    if (wide) {
+      const uint4 w0 = ct_pair_to_rows(pk[0], pk[1]), w1 = ct_pair_to_rows(pk[2], pk[3]);
+      if (q_valid[u]) {
+        *reinterpret_cast<uint4*>(O + q[u] * a.o_ss + 8 * g) = w0;
+        *reinterpret_cast<uint4*>(O + q[u] * a.o_ss + 32 + 8 * g) = w1;
       }
+    } else if (q_valid[u]) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        *reinterpret_cast<uint2*>(O + q[u] * a.o_ss + 16 * d + 4 * g) = uint2{pk[d][0], pk[d][1]};
     }
   }
 }
