@@ -217,7 +217,9 @@ __global__ void __launch_bounds__(256) flash_kernel(c3h_flash_args a) {
   // slower (613 -> 711 us): 172 VGPRs leave two waves per SIMD instead of
   // three.
   const int k_row = tid >> 3, k_chunk = tid & 7;
-  const int kq = 4 * (tid & 15), d0 = 4 * (tid >> 4);
+  // (lanes along dims: one V load instruction reads four whole 128-byte key
+  // rows, 16 lanes x 8 bytes each)
+  const int d0 = 4 * (tid & 15), kq = 4 * (tid >> 4);
   constexpr uint32_t kOob = 0x80000000u;
   const int k_bytes = static_cast<int>(((a.seq_k - 1) * a.k_ss + kD) * 2);
   const int v_bytes = static_cast<int>(((a.seq_k - 1) * a.v_ss + kD) * 2);
