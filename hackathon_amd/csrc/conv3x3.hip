@@ -364,7 +364,7 @@ int conv3x3_c64_launch(const c3h_conv_args* a, hipStream_t s, bool* handled) {
                      a->c_pack == kC && a->c_stride == kC && a->o == kO && a->out_layout == 1 && a->n >= 1;
   const bool epi = e.alpha == 1.0f && e.beta == 1.0f && (e.bias_mode == 0 || e.bias_mode == 2) && e.act <= 1 &&
                    e.n_inst == 0 && (e.bias_mode == 0 || (reinterpret_cast<uintptr_t>(e.bias) & 15) == 0) &&
-                   (reinterpret_cast<uintptr_t>(e.residual) & 7) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 7) == 0 &&
+                   (reinterpret_cast<uintptr_t>(e.residual) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->out) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(a->x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a->w) & 15) == 0;
   if (!shape || !epi) return C3H_OK;
   const int64_t x_bytes = static_cast<int64_t>(a->n) * a->h * a->w_ * kC * 2;

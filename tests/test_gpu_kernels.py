@@ -67,6 +67,35 @@ def test_gemm_16bit_matches_float64(gpu, kind, m, n, k):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "fp16"])
+@pytest.mark.parametrize("n", [260, 264])
+def test_gemm_16bit_out_bias_residual_relu(gpu, kind, n):
+    """16-bit output + per-column bias + residual + ReLU through the register
+    epilogue: rows of 264 elements are 16-byte aligned (16-byte stores and
+    residual loads, lane-swapped from the accumulator layout), rows of 260
+    are not (8-byte form); both against float64 of the rounded operands."""
+    from hackathon_amd import _lib
+    from hackathon_amd.c35 import engine as E
+    from hackathon_amd.device import DeviceArray
+
+    rng = np.random.default_rng(7 + n)
+    m, k = 1000, 256
+    a, af = _bits(rng.standard_normal((m, k), dtype=np.float32) * 0.5, kind)
+    bt, bf = _bits(rng.standard_normal((n, k), dtype=np.float32) * 0.1, kind)
+    res, resf = _bits(rng.standard_normal((m, n), dtype=np.float32), kind)
+    bias = rng.standard_normal(n).astype(np.float32)
+    code = _lib.BF16 if kind == "bf16" else _lib.F16
+    out = DeviceArray.empty((m, n), a.dtype)
+    ad, btd, resd, bd = _dev(a), _dev(bt), _dev(res), _dev(bias)
+    out.copy_from_host(np.zeros((m, n), a.dtype))
+    E.gemm(ad, btd, out, m, n, k, lda=k, ldb=k, ldo=n, trans_b=1, in_dtype=code,
+           epi=E.epilogue(bias=bd, bias_mode=2, act=1, residual=resd))
+    ref = np.maximum(af.astype(np.float64) @ bf.astype(np.float64).T + bias + resf, 0)
+    got = _from16(out.get(), kind)
+    np.testing.assert_allclose(got, ref, rtol=1e-2, atol=2e-2)
+    assert np.count_nonzero(got) > got.size // 4
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
 def test_gemm_16bit_out_and_program_epilogue(gpu, kind):
     """16-bit output with a GELU program epilogue and a residual."""
     from hackathon_amd import _lib
@@ -350,9 +379,12 @@ def test_program_run_and_graph_replay(gpu):
 
 
 @pytest.mark.parametrize("mode,n,out_kind", [(2, 200, "fp32"), (3, 200, "fp32"), (3, 200, "bf16"), (3, 70, "fp32"),
-                                              (2, 96, "fp16")])
+                                              (2, 96, "fp16"), (2, 260, "bf16"), (3, 196, "fp16"), (3, 264, "bf16")])
 def test_qgemm_fused_dequant_epilogue_bit_exact(gpu, mode, n, out_kind):
-    """Modes 2/3 (dequantize / QLinearMatMul->DequantizeLinear) + bias + residual + relu, float32 order."""
+    """Modes 2/3 (dequantize / QLinearMatMul->DequantizeLinear) + bias + residual + relu, float32 order.
+    16-bit rows of 8k + 4 elements (n = 260, 196) take the interior epilogue's
+    8-byte stores and residual loads, 16-byte aligned ones (n = 200, 264)
+    the 16-byte form."""
     from hackathon_amd import _lib
     from hackathon_amd.c35 import engine as E
     from hackathon_amd.device import BF16, DeviceArray
